@@ -1,0 +1,195 @@
+/*
+ * nert_hip.h -- C-ABI of the gfx950 (MI355X) device layer for NERT.
+ *
+ * Two levels:
+ *  1. Node level: nert_hip_run_node() runs one row of the HIP kernel table
+ *     from a plain-C node description (nert_abi.h). It is the C form of the
+ *     reference seam call `HipDevice().kernels().find(op)(node, in, out)`
+ *     (include/nert/device.hpp:30-31,53-57,96; executor call site
+ *     src/executor.cpp:534). The C++ seam itself, `nert::HipDevice()`, is
+ *     exported from the same library with the reference's C++ signature.
+ *  2. Kernel level: one entry point per kernel family with plain pointers,
+ *     sizes and a stream. Each replaces the compute of the reference rows it
+ *     names (the oracle in src/kernels/, the reference HIP layer in src/hip/).
+ *
+ * Conventions: every function returns 0 on success and non-zero on failure,
+ * with the message in nert_hip_last_error() (thread-local). Tensor pointers are
+ * device pointers unless stated otherwise. `stream` is a hipStream_t; NULL
+ * selects the layer's own stream, on which all seam rows and transfers run.
+ * Kernel-level calls are asynchronous: they return once the work is queued.
+ * Element types use the nert_dtype codes of nert_abi.h.
+ */
+#ifndef NERT_HIP_H
+#define NERT_HIP_H
+
+#include <stdint.h>
+
+#include "nert_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------- runtime --- */
+
+/* Selects device 0 and creates the layer stream; replaces EnsureDevice
+ * (src/hip_device.cpp:33-44). Non-zero when no HIP device is usable. */
+int nert_hip_init(void);
+const char* nert_hip_last_error(void);
+int nert_hip_device_count(int* count);
+
+/* Device memory; replaces HIPAllocator (src/hip_device.cpp:46-68).
+ * bytes <= 0 returns NULL. nert_hip_free(NULL) is a no-op. */
+void* nert_hip_malloc(int64_t bytes);
+int nert_hip_free(void* ptr);
+
+/* Blocking transfers on the layer stream; replace HIPTransfer
+ * (src/hip_device.cpp:70-89). bytes == 0 is a no-op. */
+int nert_hip_memcpy_h2d(void* dst, const void* src, int64_t bytes);
+int nert_hip_memcpy_d2h(void* dst, const void* src, int64_t bytes);
+/* Asynchronous device-to-device copy (Identity/Reshape/Flatten payloads). */
+int nert_hip_memcpy_d2d(void* dst, const void* src, int64_t bytes, void* stream);
+
+void* nert_hip_default_stream(void);
+int nert_hip_stream_sync(void* stream);
+void* nert_hip_event_create(void);
+int nert_hip_event_record(void* event, void* stream);
+/* Waits for `stop`, then writes the elapsed milliseconds start -> stop. */
+int nert_hip_event_elapsed_ms(void* start, void* stop, float* ms);
+int nert_hip_event_destroy(void* event);
+
+/* Reads (and clears when set) the device error word that rows with
+ * data-dependent failures raise: bit 0 = integer division by zero,
+ * bit 1 = index out of range. Synchronises `stream`. */
+int nert_hip_take_error_flags(int32_t* flags_out, void* stream);
+
+/* ---------------------------------------------------------- node level --- */
+
+/* Runs one row of the HIP table on device tensors. Returns a nert_status;
+ * on error `err` receives the row's message ("<Op> (node '<name>'): ...",
+ * the reference convention, e.g. src/kernels/gemm.cpp:60). The row's work is
+ * queued on the layer stream; results are visible after the next blocking
+ * transfer or nert_hip_stream_sync(NULL). */
+int nert_hip_run_node(const char* op_type, const char* node_name, int64_t schema_version,
+                      const nert_attr_desc* attrs, int n_attrs, const nert_tensor_desc* inputs, int n_inputs,
+                      const nert_tensor_desc* outputs, int n_outputs, char* err, int err_len);
+
+/* 1 when the HIP table has a row for op_type (KernelTable::find != null). */
+int nert_hip_has_row(const char* op_type);
+
+/* ------------------------------------------------------ GEMM on MFMA --- */
+
+/* Y[M,N] = alpha * op(A) * op(B) + beta * C. A is [M,K] (trans_a = 0) or
+ * [K,M]; B is [K,N] (trans_b = 0) or [N,K]; C is absent (c_rank = 0 or
+ * c = NULL), [N] (c_rank = 1) or [M,N] (c_rank = 2).
+ * Replaces Gemm: src/kernels/gemm.cpp:59-137, src/hip/gemm.cu:75-158. */
+int nert_hip_gemm_f32(const float* a, const float* b, const float* c, float* y, int64_t m, int64_t n, int64_t k,
+                      int trans_a, int trans_b, float alpha, float beta, int c_rank, void* stream);
+
+/* Batched Y[b][M,N] = A[b][M,K] * B[b][K,N] with up to four broadcast batch
+ * axes: batch b decomposes over batch_dims (row-major) and each operand
+ * advances by its own per-axis element stride (0 = broadcast). Y is dense.
+ * Replaces MatMul: src/kernels/mat_mul.cpp:79-169, src/hip/mat_mul.cu:86-193. */
+int nert_hip_matmul_f32(const float* a, const float* b, float* y, int64_t m, int64_t n, int64_t k, int batch_rank,
+                        const int64_t* batch_dims, const int64_t* a_batch_strides, const int64_t* b_batch_strides,
+                        void* stream);
+
+/* Convolution geometry, lifted to three spatial axes (depth, height, width)
+ * with unit leading extents for 1-D/2-D, as src/kernels/conv.cpp:233-249. */
+typedef struct nert_conv_desc {
+    int64_t batch, in_channels, out_channels, group;
+    int64_t in[3];
+    int64_t kernel[3];
+    int64_t out[3];
+    int64_t stride[3];
+    int64_t dilation[3];
+    int64_t pad[3]; /* leading pads; trailing pads are implied by out[] */
+} nert_conv_desc;
+
+/* NCHW (or NCDHW) implicit-GEMM convolution, optional bias [M].
+ * Replaces Conv: src/kernels/conv.cpp:138-295, src/hip/conv.cu:159-338. */
+int nert_hip_conv_f32(const float* x, const float* w, const float* bias, float* y, const nert_conv_desc* d,
+                      void* stream);
+
+/* ---------------------------------------------------------- elementwise --- */
+
+enum nert_unary_op {
+    NERT_UN_RELU = 0,   /* src/kernels/relu.cpp:51-53      std::max(0, x) */
+    NERT_UN_SIGMOID,    /* src/kernels/sigmoid.cpp:52      1/(1+exp(-x)) */
+    NERT_UN_TANH,       /* src/kernels/tanh.cpp */
+    NERT_UN_EXP,        /* src/kernels/exp.cpp:48 */
+    NERT_UN_LOG,        /* src/kernels/log.cpp */
+    NERT_UN_SQRT,       /* src/kernels/sqrt.cpp:48 */
+    NERT_UN_SIN,        /* src/kernels/sin.cpp */
+    NERT_UN_COS,        /* src/kernels/cos.cpp */
+    NERT_UN_FLOOR,      /* src/kernels/floor.cpp:48 */
+    NERT_UN_ABS,        /* src/kernels/abs.cpp (f32, i64) */
+    NERT_UN_NEG,        /* src/kernels/neg.cpp (f32, i64) */
+    NERT_UN_SIGN,       /* src/kernels/sign.cpp:26-33 (f32, i64; NaN kept) */
+    NERT_UN_ERF,        /* src/kernels/erf.cpp:48 */
+    NERT_UN_ELU,        /* src/kernels/elu.cpp:62-66, p0 = alpha */
+    NERT_UN_CLIP,       /* src/kernels/clip.cpp:49-75, p0 = lo, p1 = hi (f32) */
+    NERT_UN_ISNAN,      /* src/kernels/is_nan.cpp, f32 -> bool */
+    NERT_UN_NOT         /* src/kernels/not.cpp, bool -> bool */
+};
+
+/* y[i] = op(x[i]) over `count` elements of `dtype` (F32 or I64). */
+int nert_hip_unary(int op, int dtype, const void* x, void* y, int64_t count, double p0, double p1, void* stream);
+/* int64 Clip with exact 64-bit bounds (src/kernels/clip.cpp:92-95). */
+int nert_hip_clip_i64(const int64_t* x, int64_t* y, int64_t count, int64_t lo, int64_t hi, void* stream);
+
+enum nert_binary_op {
+    NERT_BIN_ADD = 0,      /* src/kernels/add.cpp:96-131 (f32, i64) */
+    NERT_BIN_SUB,          /* src/kernels/sub.cpp */
+    NERT_BIN_MUL,          /* src/kernels/mul.cpp */
+    NERT_BIN_DIV,          /* src/kernels/div.cpp (i64 truncates; zero divisor sets flag bit 0) */
+    NERT_BIN_POW,          /* src/kernels/pow.cpp (f32; exponent 2 is x*x) */
+    NERT_BIN_MOD,          /* src/kernels/mod.cpp (i64 truncating remainder) */
+    NERT_BIN_MAX,          /* src/kernels/max.cpp (std::max NaN order) */
+    NERT_BIN_MIN,          /* src/kernels/min.cpp */
+    NERT_BIN_EQUAL,        /* -> bool, src/kernels/equal.cpp */
+    NERT_BIN_GREATER,
+    NERT_BIN_LESS,
+    NERT_BIN_GREATER_EQUAL,
+    NERT_BIN_LESS_EQUAL,
+    NERT_BIN_AND,          /* bool x bool -> bool */
+    NERT_BIN_OR,
+    NERT_BIN_WHERE         /* three operands: bool cond, x, y (f32 or i64) */
+};
+
+/* NumPy multidirectional broadcast of 2 (or 3 for WHERE) operands into
+ * `out` of rank out_rank and dims out_dims. Operand k has input_ranks[k]
+ * dims input_dims[k], right-aligned against out_dims. `dtype` is the
+ * operands' element type (for WHERE, of operands 1 and 2). Shared form of the
+ * reference's AlignedStrides walk (src/kernels/add.cpp:55-93). */
+int nert_hip_broadcast(int op, int dtype, int n_inputs, const void* const* inputs, const int64_t* const* input_dims,
+                       const int* input_ranks, void* out, int out_rank, const int64_t* out_dims, void* stream);
+
+/* Element conversion (src/kernels/cast.cpp). to_int32 = 1 emulates ONNX
+ * INT32 on int64 lanes (saturating, NaN -> 0). */
+int nert_hip_cast(int src_dtype, int dst_dtype, int to_int32, const void* x, void* y, int64_t count, void* stream);
+/* Fills `count` elements: F32 takes fvalue, I64 and BOOL take ivalue. */
+int nert_hip_fill(int dtype, void* y, int64_t count, double fvalue, int64_t ivalue, void* stream);
+
+/* ---------------------------------------------------------------- pools --- */
+
+typedef struct nert_pool_desc {
+    int64_t batch, channels;
+    int64_t in[2], out[2], kernel[2], stride[2], dilation[2];
+    int64_t pad_begin[2], pad_end[2];
+    int64_t count_include_pad; /* AveragePool only */
+} nert_pool_desc;
+
+/* src/kernels/max_pool.cpp:138-239 (primary output). */
+int nert_hip_maxpool2d_f32(const float* x, float* y, const nert_pool_desc* d, void* stream);
+/* src/kernels/average_pool.cpp. */
+int nert_hip_avgpool2d_f32(const float* x, float* y, const nert_pool_desc* d, void* stream);
+/* Mean of each of `planes` contiguous runs of `spatial` elements;
+ * src/kernels/global_average_pool.cpp:32-69. */
+int nert_hip_global_avgpool_f32(const float* x, float* y, int64_t planes, int64_t spatial, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NERT_HIP_H */

@@ -1,0 +1,82 @@
+#pragma once
+// Shared helpers for the gfx950 kernels and the C-ABI wrappers.
+//
+// Every C-ABI entry point returns 0 on success or a non-zero status with a
+// message retrievable through nert_hip_last_error(); internal code reports
+// failures by throwing nert_hip::Error, which the wrappers convert.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace nert_hip {
+
+struct Error : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+void SetLastError(const std::string& message);
+
+inline void Check(hipError_t status, const char* what) {
+    if (status != hipSuccess) {
+        throw Error(std::string(what) + " failed: " + hipGetErrorString(status));
+    }
+}
+
+// The launch stream every entry point uses when the caller passes null.
+hipStream_t DefaultStream();
+
+inline hipStream_t StreamOr(void* stream) {
+    return stream != nullptr ? static_cast<hipStream_t>(stream) : DefaultStream();
+}
+
+// Reusable device workspace on the default device: grows on demand (a
+// stream-synchronised reallocation), never shrinks. Kernels that need
+// scratch (split-K partials, TopK candidates, error flags) take it from here.
+void* Workspace(int64_t bytes, hipStream_t stream);
+
+// A 64-byte device flag block (zeroed at creation) used by rows that must
+// report data-dependent errors (out-of-range indices, integer division by
+// zero) back to the host.
+int32_t* ErrorFlags();
+
+// Host shadows of small host-to-device uploads (<= 64 KiB), keyed by device
+// address. nert_hip_memcpy_h2d records them; device-side writes that go
+// through the runtime (d2d copies, frees, seam row outputs) drop overlapping
+// entries. Rows use them to read control operands without a D2H round trip.
+void ShadowPut(const void* dst, const void* src, int64_t bytes);
+void ShadowDrop(const void* dst, int64_t bytes);
+bool ShadowGet(const void* src, int64_t bytes, void* out);
+
+inline unsigned GridFor(int64_t work, int per_block, int64_t cap = 1 << 20) {
+    int64_t blocks = (work + per_block - 1) / per_block;
+    if (blocks < 1) {
+        blocks = 1;
+    }
+    if (blocks > cap) {
+        blocks = cap;
+    }
+    return static_cast<unsigned>(blocks);
+}
+
+// Runs `body` and converts exceptions into a C status code.
+template <typename F>
+int Guard(F&& body) {
+    try {
+        body();
+        return 0;
+    } catch (const std::exception& e) {
+        SetLastError(e.what());
+        return 1;
+    }
+}
+
+inline void CheckLaunch(const char* what) { Check(hipGetLastError(), what); }
+
+} // namespace nert_hip
+
+// Device-side vector types for the MFMA builtins.
+typedef float nert_floatx4 __attribute__((ext_vector_type(4)));
+typedef float nert_floatx16 __attribute__((ext_vector_type(16)));

@@ -1,0 +1,282 @@
+// Conv as an implicit GEMM on fp32 MFMA.
+//
+// Per group g:  Y_g[m, n] = sum_k W_g[m, k] * X_col[k, n] + bias[m]
+//   m = output channel within the group        (M_g = M / group)
+//   k = (c, kd, kh, kw), c within the group     (K_g = C/group * kD*kH*kW)
+//   n = (b, od, oh, ow)                         (N = batch * OD*OH*OW)
+// W is already [M, K_g] row-major (ONNX OIHW), so it loads like a row-major
+// GEMM operand. X_col is never materialised: the B loader gathers each
+// element from NCHW X with the stride/dilation/pad arithmetic and writes zero
+// for padding taps, exactly the taps the reference skips
+// (src/kernels/conv.cpp:267-285). 1-D and 2-D convolutions arrive lifted to
+// three spatial axes with unit leading extents, as the reference lifts them
+// (src/kernels/conv.cpp:233-249).
+
+#include "mfma_tile.hpp"
+#include "../../include/nert_hip.h"
+
+namespace nert_hip {
+namespace {
+
+struct ConvArgs {
+    const float* x;
+    const float* w;
+    const float* bias;
+    float* y;
+    int64_t batch, c, m, group;
+    int64_t cg, mg, kg; // channels per group, outputs per group, K per group
+    int32_t in_d, in_h, in_w;
+    int32_t k_d, k_h, k_w;
+    int32_t out_d, out_h, out_w;
+    int32_t s_d, s_h, s_w;
+    int32_t d_d, d_h, d_w;
+    int32_t p_d, p_h, p_w;
+    int64_t plane_out; // OD*OH*OW
+    int64_t plane_in;  // ID*IH*IW
+    int64_t n_total;   // batch * plane_out
+    int64_t k_per_split;
+    float* partial; // [splits][group][M_g][N] when split
+};
+
+// Gathers B(k, n) = X_col for one K tile. Thread t owns column nn = t % BN
+// for every pass, so the column decode (b, od, oh, ow) happens once per block.
+template <int BN, int BK, int THREADS, int PITCH>
+struct ConvBLoader {
+    static_assert(THREADS % BN == 0, "threads must cover whole B rows");
+    static constexpr int kRowsPerPass = THREADS / BN;
+    static constexpr int kPer = BK / kRowsPerPass;
+    struct Stage {
+        float v[kPer];
+    };
+    const ConvArgs* p;
+    const float* xb; // X at (b, g*C_g, 0, 0, 0)
+    int32_t id0, ih0, iw0; // od*s - pad for this thread's column
+    bool col_ok;
+    int32_t kvol, khw;
+    int64_t k_total;
+
+    __device__ void init(const ConvArgs& args, int64_t col0, int g) {
+        p = &args;
+        const int nn = threadIdx.x % BN;
+        const int64_t n = col0 + nn;
+        col_ok = n < args.n_total;
+        const int64_t nc = col_ok ? n : 0;
+        const int64_t b = nc / args.plane_out;
+        int64_t rem = nc - b * args.plane_out;
+        const int32_t hw = args.out_h * args.out_w;
+        const int32_t od = static_cast<int32_t>(rem / hw);
+        rem -= static_cast<int64_t>(od) * hw;
+        const int32_t oh = static_cast<int32_t>(rem / args.out_w);
+        const int32_t ow = static_cast<int32_t>(rem - static_cast<int64_t>(oh) * args.out_w);
+        id0 = od * args.s_d - args.p_d;
+        ih0 = oh * args.s_h - args.p_h;
+        iw0 = ow * args.s_w - args.p_w;
+        xb = args.x + (b * args.c + static_cast<int64_t>(g) * args.cg) * args.plane_in;
+        kvol = args.k_d * args.k_h * args.k_w;
+        khw = args.k_h * args.k_w;
+    }
+
+    __device__ void load(int64_t k0, Stage& s) const {
+        const int kk0 = threadIdx.x / BN;
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int64_t k = k0 + kk0 + q * kRowsPerPass;
+            float val = 0.f;
+            if (col_ok && k < k_total) {
+                const int32_t kc = static_cast<int32_t>(k);
+                const int32_t c = kc / kvol;
+                int32_t r = kc - c * kvol;
+                const int32_t kd = r / khw;
+                r -= kd * khw;
+                const int32_t kh = r / p->k_w;
+                const int32_t kw = r - kh * p->k_w;
+                const int32_t id = id0 + kd * p->d_d;
+                const int32_t ih = ih0 + kh * p->d_h;
+                const int32_t iw = iw0 + kw * p->d_w;
+                if (static_cast<uint32_t>(id) < static_cast<uint32_t>(p->in_d) &&
+                    static_cast<uint32_t>(ih) < static_cast<uint32_t>(p->in_h) &&
+                    static_cast<uint32_t>(iw) < static_cast<uint32_t>(p->in_w)) {
+                    val = xb[static_cast<int64_t>(c) * p->plane_in +
+                             (static_cast<int64_t>(id) * p->in_h + ih) * p->in_w + iw];
+                }
+            }
+            s.v[q] = val;
+        }
+    }
+    __device__ void store(const Stage& s, float* lds) const {
+        const int nn = threadIdx.x % BN;
+        const int kk0 = threadIdx.x / BN;
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            lds[(kk0 + q * kRowsPerPass) * PITCH + nn] = s.v[q];
+        }
+    }
+};
+
+template <class Shape>
+__global__ __launch_bounds__(Shape::kThreads) void ConvKernel(ConvArgs p) {
+    __shared__ __attribute__((aligned(16))) float lds[2 * (Shape::kLdsA + Shape::kLdsB)];
+    const int64_t tiles_m = (p.mg + Shape::kBM - 1) / Shape::kBM;
+    const int64_t tile = blockIdx.x;
+    const int64_t tm = tile % tiles_m;
+    const int64_t tn = tile / tiles_m;
+    const int64_t row0 = tm * Shape::kBM;
+    const int64_t col0 = tn * Shape::kBN;
+    const int g = blockIdx.y;
+    const int split = blockIdx.z;
+
+    const int64_t k_begin = static_cast<int64_t>(split) * p.k_per_split;
+    int64_t k_end = k_begin + p.k_per_split;
+    if (k_end > p.kg) {
+        k_end = p.kg;
+    }
+
+    KContigLoader<Shape::kBM, Shape::kBK, Shape::kThreads, Shape::kPitchA> aload;
+    aload.base = p.w + (static_cast<int64_t>(g) * p.mg + row0) * p.kg;
+    aload.row_stride = p.kg;
+    aload.rows_left = p.mg - row0;
+    aload.k_total = k_end;
+    aload.vec_ok = (p.kg % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.w) & 15) == 0);
+
+    ConvBLoader<Shape::kBN, Shape::kBK, Shape::kThreads, Shape::kPitchB> bload;
+    bload.init(p, col0, g);
+    bload.k_total = k_end;
+
+    Accum<Shape> acc;
+    MainLoop<Shape>(aload, bload, k_begin, k_end, lds, acc);
+
+    if (p.partial != nullptr) {
+        float* out = p.partial + (static_cast<int64_t>(split) * p.group + g) * p.mg * p.n_total;
+        ForEachAccum<Shape>(acc, [&](int r, int c, float v) {
+            const int64_t gr = row0 + r;
+            const int64_t gc = col0 + c;
+            if (gr < p.mg && gc < p.n_total) {
+                out[gr * p.n_total + gc] = v;
+            }
+        });
+        return;
+    }
+    ForEachAccum<Shape>(acc, [&](int r, int c, float v) {
+        const int64_t gr = row0 + r;
+        const int64_t gc = col0 + c;
+        if (gr < p.mg && gc < p.n_total) {
+            const int64_t oc = static_cast<int64_t>(g) * p.mg + gr;
+            const int64_t b = gc / p.plane_out;
+            const int64_t pix = gc - b * p.plane_out;
+            const float value = p.bias != nullptr ? v + p.bias[oc] : v;
+            p.y[(b * p.m + oc) * p.plane_out + pix] = value;
+        }
+    });
+}
+
+__global__ void ConvSplitReduceKernel(ConvArgs p, int splits) {
+    const int64_t per_split = p.group * p.mg * p.n_total;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < per_split;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        float sum = 0.f;
+        for (int s = 0; s < splits; ++s) {
+            sum += p.partial[s * per_split + i];
+        }
+        const int64_t gc = i % p.n_total;
+        const int64_t oc = i / p.n_total; // g * mg + m
+        const int64_t b = gc / p.plane_out;
+        const int64_t pix = gc - b * p.plane_out;
+        p.y[(b * p.m + oc) * p.plane_out + pix] = p.bias != nullptr ? sum + p.bias[oc] : sum;
+    }
+}
+
+using ConvShapeL = TileShape<128, 128, 16, 2, 2>;
+using ConvShapeM = TileShape<64, 128, 16, 2, 2>;
+using ConvShapeS = TileShape<32, 128, 16, 1, 4>;
+
+template <class Shape>
+int64_t ConvTiles(const ConvArgs& p) {
+    return ((p.mg + Shape::kBM - 1) / Shape::kBM) * ((p.n_total + Shape::kBN - 1) / Shape::kBN) * p.group;
+}
+
+template <class Shape>
+void LaunchConv(ConvArgs p, hipStream_t stream) {
+    const int64_t k_tiles = (p.kg + Shape::kBK - 1) / Shape::kBK;
+    const int64_t tiles = ConvTiles<Shape>(p);
+    int splits = 1;
+    while (tiles * splits < 256 && k_tiles / (splits * 2) >= 8 && splits < 16) {
+        splits *= 2;
+    }
+    p.k_per_split = ((k_tiles + splits - 1) / splits) * Shape::kBK;
+    p.partial = nullptr;
+    if (splits > 1) {
+        p.partial =
+            static_cast<float*>(Workspace(static_cast<int64_t>(splits) * p.group * p.mg * p.n_total * 4, stream));
+    }
+    const int64_t tiles_mn = ((p.mg + Shape::kBM - 1) / Shape::kBM) * ((p.n_total + Shape::kBN - 1) / Shape::kBN);
+    dim3 grid(static_cast<unsigned>(tiles_mn), static_cast<unsigned>(p.group), static_cast<unsigned>(splits));
+    ConvKernel<Shape><<<grid, Shape::kThreads, 0, stream>>>(p);
+    CheckLaunch("ConvKernel launch");
+    if (splits > 1) {
+        const int64_t total = p.group * p.mg * p.n_total;
+        ConvSplitReduceKernel<<<GridFor(total, 256, 4096), 256, 0, stream>>>(p, splits);
+        CheckLaunch("ConvSplitReduceKernel launch");
+    }
+}
+
+} // namespace
+} // namespace nert_hip
+
+extern "C" int nert_hip_conv_f32(const float* x, const float* w, const float* bias, float* y, const nert_conv_desc* d,
+                                 void* stream) {
+    return nert_hip::Guard([&] {
+        nert_hip::ConvArgs p{};
+        p.x = x;
+        p.w = w;
+        p.bias = bias;
+        p.y = y;
+        p.batch = d->batch;
+        p.c = d->in_channels;
+        p.m = d->out_channels;
+        p.group = d->group;
+        if (p.group <= 0 || p.c % p.group != 0 || p.m % p.group != 0) {
+            throw nert_hip::Error("conv: invalid group");
+        }
+        if (p.group > 65535) {
+            throw nert_hip::Error("conv: more than 65535 groups");
+        }
+        p.cg = p.c / p.group;
+        p.mg = p.m / p.group;
+        p.in_d = static_cast<int32_t>(d->in[0]);
+        p.in_h = static_cast<int32_t>(d->in[1]);
+        p.in_w = static_cast<int32_t>(d->in[2]);
+        p.k_d = static_cast<int32_t>(d->kernel[0]);
+        p.k_h = static_cast<int32_t>(d->kernel[1]);
+        p.k_w = static_cast<int32_t>(d->kernel[2]);
+        p.out_d = static_cast<int32_t>(d->out[0]);
+        p.out_h = static_cast<int32_t>(d->out[1]);
+        p.out_w = static_cast<int32_t>(d->out[2]);
+        p.s_d = static_cast<int32_t>(d->stride[0]);
+        p.s_h = static_cast<int32_t>(d->stride[1]);
+        p.s_w = static_cast<int32_t>(d->stride[2]);
+        p.d_d = static_cast<int32_t>(d->dilation[0]);
+        p.d_h = static_cast<int32_t>(d->dilation[1]);
+        p.d_w = static_cast<int32_t>(d->dilation[2]);
+        p.p_d = static_cast<int32_t>(d->pad[0]);
+        p.p_h = static_cast<int32_t>(d->pad[1]);
+        p.p_w = static_cast<int32_t>(d->pad[2]);
+        p.kg = p.cg * p.k_d * p.k_h * p.k_w;
+        p.plane_out = static_cast<int64_t>(p.out_d) * p.out_h * p.out_w;
+        p.plane_in = static_cast<int64_t>(p.in_d) * p.in_h * p.in_w;
+        p.n_total = p.batch * p.plane_out;
+        if (p.kg >= (int64_t{1} << 31)) {
+            throw nert_hip::Error("conv: reduction length exceeds 2^31");
+        }
+        if (p.n_total == 0 || p.mg == 0) {
+            return;
+        }
+        hipStream_t s = nert_hip::StreamOr(stream);
+        if (p.mg <= 32) {
+            nert_hip::LaunchConv<nert_hip::ConvShapeS>(p, s);
+        } else if (p.mg <= 64 || nert_hip::ConvTiles<nert_hip::ConvShapeL>(p) < 256) {
+            nert_hip::LaunchConv<nert_hip::ConvShapeM>(p, s);
+        } else {
+            nert_hip::LaunchConv<nert_hip::ConvShapeL>(p, s);
+        }
+    });
+}

@@ -1,0 +1,405 @@
+// Gemm, MatMul and Conv rows: host validation mirroring the reference CPU
+// rows, then one MFMA launch (plus a split-K reduction for small grids).
+
+#include "rows.hpp"
+
+#include <algorithm>
+
+namespace nert_hip {
+namespace rows {
+
+using namespace seam;
+
+// Validation follows src/kernels/gemm.cpp:59-117.
+void Gemm(const Node& node, const Views& inputs, const Views& outputs) {
+    const std::string context = "Gemm (node '" + node.name + "')";
+    if (inputs.size() < 2 || inputs.size() > 3 || outputs.size() != 1) {
+        throw InferenceException(context + ": expected two or three inputs and one output");
+    }
+    const TensorView& a = inputs[0];
+    const TensorView& b = inputs[1];
+    const TensorView& out = outputs[0];
+    const bool has_c = inputs.size() == 3;
+    if (a.dtype != DataType::Float32 || b.dtype != DataType::Float32 || out.dtype != DataType::Float32) {
+        throw InferenceException(context + ": tensors must be float32");
+    }
+    if (has_c && inputs[2].dtype != DataType::Float32) {
+        throw InferenceException(context + ": bias tensor must be float32");
+    }
+    if (a.dims.size() != 2 || b.dims.size() != 2) {
+        throw InferenceException(context + ": A and B must be rank-2");
+    }
+    (void)ElementCount(a.dims, context);
+    (void)ElementCount(b.dims, context);
+    const int64_t trans_a = IntAttr(node, "transA", 0, "Gemm");
+    const int64_t trans_b = IntAttr(node, "transB", 0, "Gemm");
+    const float alpha = FloatAttr(node, "alpha", 1.0f, "Gemm");
+    const float beta = FloatAttr(node, "beta", 1.0f, "Gemm");
+    const int64_t m = trans_a == 0 ? a.dims[0] : a.dims[1];
+    const int64_t k = trans_a == 0 ? a.dims[1] : a.dims[0];
+    const int64_t bk = trans_b == 0 ? b.dims[0] : b.dims[1];
+    const int64_t n = trans_b == 0 ? b.dims[1] : b.dims[0];
+    if (k != bk) {
+        throw InferenceException(context + ": contraction dimension mismatch");
+    }
+    if (out.dims != std::vector<int64_t>{m, n}) {
+        throw InferenceException(context + ": output shape does not match the operands");
+    }
+    (void)ElementCount(out.dims, context);
+    const float* bias = nullptr;
+    int bias_rank = 0;
+    if (has_c) {
+        const TensorView& c = inputs[2];
+        const bool rank_one = c.dims.size() == 1 && c.dims[0] == n;
+        const bool rank_two = c.dims.size() == 2 && c.dims[0] == m && c.dims[1] == n;
+        if (!rank_one && !rank_two) {
+            throw InferenceException(context + ": bias shape must be [N] or [M,N]");
+        }
+        (void)ElementCount(c.dims, context);
+        bias = static_cast<const float*>(c.data);
+        bias_rank = static_cast<int>(c.dims.size());
+    }
+    if (a.data == nullptr || b.data == nullptr || out.data == nullptr || (has_c && bias == nullptr)) {
+        throw InferenceException(context + ": null buffer");
+    }
+    CheckStatus(nert_hip_gemm_f32(static_cast<const float*>(a.data), static_cast<const float*>(b.data), bias,
+                                  static_cast<float*>(out.data), m, n, k, trans_a != 0 ? 1 : 0, trans_b != 0 ? 1 : 0,
+                                  alpha, beta, bias_rank, Stream()),
+                context);
+    AfterRow(outputs, context);
+}
+
+namespace {
+
+std::vector<int64_t> BroadcastBatch(const std::vector<int64_t>& a, const std::vector<int64_t>& b,
+                                    const std::string& context) {
+    const size_t rank = std::max(a.size(), b.size());
+    std::vector<int64_t> out(rank, 1);
+    for (size_t i = 0; i < rank; ++i) {
+        const int64_t da = i < rank - a.size() ? 1 : a[i - (rank - a.size())];
+        const int64_t db = i < rank - b.size() ? 1 : b[i - (rank - b.size())];
+        if (da != db && da != 1 && db != 1) {
+            throw InferenceException(context + ": batch dimensions are not broadcast-compatible");
+        }
+        out[i] = std::max(da, db);
+    }
+    return out;
+}
+
+// Per-output-batch-axis element strides of one operand's batch (0 where the
+// operand broadcasts), in units of whole matrices times `mat`.
+std::vector<int64_t> BatchStrides(const std::vector<int64_t>& in, const std::vector<int64_t>& out, int64_t mat) {
+    std::vector<int64_t> strides(out.size(), 0);
+    int64_t s = mat;
+    for (size_t j = out.size(); j-- > 0;) {
+        const size_t off = out.size() - in.size();
+        if (j < off) {
+            continue;
+        }
+        const int64_t d = in[j - off];
+        strides[j] = d == 1 ? 0 : s;
+        s *= d;
+    }
+    return strides;
+}
+
+} // namespace
+
+// Validation follows src/kernels/mat_mul.cpp:79-139.
+void MatMul(const Node& node, const Views& inputs, const Views& outputs) {
+    const std::string context = "MatMul (node '" + node.name + "')";
+    if (inputs.size() != 2 || outputs.size() != 1) {
+        throw InferenceException(context + ": expected two inputs and one output");
+    }
+    const TensorView& a = inputs[0];
+    const TensorView& b = inputs[1];
+    const TensorView& out = outputs[0];
+    if (a.dtype != DataType::Float32 || b.dtype != DataType::Float32 || out.dtype != DataType::Float32) {
+        throw InferenceException(context + ": tensors must be float32");
+    }
+    if (a.dims.empty() || b.dims.empty()) {
+        throw InferenceException(context + ": operands must have at least one dimension");
+    }
+    std::vector<int64_t> a_dims = a.dims;
+    std::vector<int64_t> b_dims = b.dims;
+    const bool a_promoted = a_dims.size() == 1;
+    const bool b_promoted = b_dims.size() == 1;
+    if (a_promoted) {
+        a_dims.insert(a_dims.begin(), 1);
+    }
+    if (b_promoted) {
+        b_dims.push_back(1);
+    }
+    (void)ElementCount(a_dims, context);
+    (void)ElementCount(b_dims, context);
+    const size_t a_rank = a_dims.size();
+    const size_t b_rank = b_dims.size();
+    const int64_t m = a_dims[a_rank - 2];
+    const int64_t k = a_dims[a_rank - 1];
+    const int64_t bk = b_dims[b_rank - 2];
+    const int64_t n = b_dims[b_rank - 1];
+    if (k != bk) {
+        throw InferenceException(context + ": contraction dimension mismatch");
+    }
+    const std::vector<int64_t> batch_a(a_dims.begin(), a_dims.end() - 2);
+    const std::vector<int64_t> batch_b(b_dims.begin(), b_dims.end() - 2);
+    const std::vector<int64_t> batch_out = BroadcastBatch(batch_a, batch_b, context);
+    std::vector<int64_t> full = batch_out;
+    full.push_back(m);
+    full.push_back(n);
+    std::vector<int64_t> expected = full;
+    if (a_promoted) {
+        expected.erase(expected.begin() + static_cast<std::ptrdiff_t>(batch_out.size()));
+    }
+    if (b_promoted) {
+        const size_t n_index = a_promoted ? batch_out.size() : batch_out.size() + 1;
+        expected.erase(expected.begin() + static_cast<std::ptrdiff_t>(n_index));
+    }
+    if (out.dims != expected) {
+        throw InferenceException(context + ": output shape does not match the operands");
+    }
+    (void)ElementCount(full, context);
+    if (a.data == nullptr || b.data == nullptr || out.data == nullptr) {
+        throw InferenceException(context + ": null buffer");
+    }
+
+    const auto* ap = static_cast<const float*>(a.data);
+    const auto* bp = static_cast<const float*>(b.data);
+    auto* yp = static_cast<float*>(out.data);
+    std::vector<int64_t> a_strides = BatchStrides(batch_a, batch_out, m * k);
+    std::vector<int64_t> b_strides = BatchStrides(batch_b, batch_out, k * n);
+    std::vector<int64_t> dims = batch_out;
+
+    // A dense A batch against one shared B is a single tall GEMM: fold the
+    // batch into M (the ViT projections [16,197,768] x [768,N]).
+    bool b_shared = true;
+    for (int64_t s : b_strides) {
+        b_shared = b_shared && s == 0;
+    }
+    bool a_dense = true;
+    {
+        int64_t expect = m * k;
+        for (size_t j = dims.size(); j-- > 0;) {
+            if (dims[j] == 1) {
+                continue;
+            }
+            a_dense = a_dense && a_strides[j] == expect;
+            expect *= dims[j];
+        }
+    }
+    int64_t batches = Count(dims);
+    if (b_shared && a_dense && batches > 1) {
+        CheckStatus(nert_hip_matmul_f32(ap, bp, yp, m * batches, n, k, 0, nullptr, nullptr, nullptr, Stream()),
+                    context);
+        AfterRow(outputs, context);
+        return;
+    }
+    // Drop unit batch axes; merge neighbours both operands walk densely.
+    std::vector<int64_t> cd, ca, cb;
+    for (size_t j = 0; j < dims.size(); ++j) {
+        if (dims[j] == 1) {
+            continue;
+        }
+        if (!cd.empty() && ca.back() == a_strides[j] * dims[j] && cb.back() == b_strides[j] * dims[j]) {
+            cd.back() *= dims[j];
+            ca.back() = a_strides[j];
+            cb.back() = b_strides[j];
+            continue;
+        }
+        if (!cd.empty() && ca.back() == 0 && a_strides[j] == 0 && cb.back() == b_strides[j] * dims[j]) {
+            cd.back() *= dims[j];
+            cb.back() = b_strides[j];
+            continue;
+        }
+        if (!cd.empty() && cb.back() == 0 && b_strides[j] == 0 && ca.back() == a_strides[j] * dims[j]) {
+            cd.back() *= dims[j];
+            ca.back() = a_strides[j];
+            continue;
+        }
+        cd.push_back(dims[j]);
+        ca.push_back(a_strides[j]);
+        cb.push_back(b_strides[j]);
+    }
+    if (cd.size() > 4) {
+        throw InferenceException(context + ": more than four non-mergeable batch axes");
+    }
+    CheckStatus(nert_hip_matmul_f32(ap, bp, yp, m, n, k, static_cast<int>(cd.size()), cd.data(), ca.data(), cb.data(),
+                                    Stream()),
+                context);
+    AfterRow(outputs, context);
+}
+
+namespace {
+
+// src/kernels/conv.cpp:78-119.
+void ResolvePads(const std::string& context, const std::string& auto_pad, const std::vector<int64_t>& in_spatial,
+                 const std::vector<int64_t>& kernel, const std::vector<int64_t>& dilations,
+                 const std::vector<int64_t>& strides, const std::vector<int64_t>& pads_attr,
+                 std::vector<int64_t>& pad_begin, std::vector<int64_t>& pad_end) {
+    const size_t rank = in_spatial.size();
+    pad_begin.assign(rank, 0);
+    pad_end.assign(rank, 0);
+    if (auto_pad == "VALID") {
+        return;
+    }
+    if (auto_pad == "SAME_UPPER" || auto_pad == "SAME_LOWER") {
+        for (size_t i = 0; i < rank; ++i) {
+            const int64_t out = (in_spatial[i] + strides[i] - 1) / strides[i];
+            const int64_t effective = dilations[i] * (kernel[i] - 1) + 1;
+            const int64_t total = std::max<int64_t>(0, (out - 1) * strides[i] + effective - in_spatial[i]);
+            if (auto_pad == "SAME_UPPER") {
+                pad_begin[i] = total / 2;
+                pad_end[i] = total - pad_begin[i];
+            } else {
+                pad_end[i] = total / 2;
+                pad_begin[i] = total - pad_end[i];
+            }
+        }
+        return;
+    }
+    if (pads_attr.empty()) {
+        return;
+    }
+    if (pads_attr.size() != 2 * rank) {
+        throw InferenceException(context + ": pads must have two entries per spatial dimension");
+    }
+    for (size_t i = 0; i < rank; ++i) {
+        pad_begin[i] = pads_attr[i];
+        pad_end[i] = pads_attr[rank + i];
+    }
+}
+
+} // namespace
+
+void ResolveWindowPads(const std::string& context, const std::string& auto_pad, const std::vector<int64_t>& in_spatial,
+                       const std::vector<int64_t>& kernel, const std::vector<int64_t>& dilations,
+                       const std::vector<int64_t>& strides, const std::vector<int64_t>& pads_attr,
+                       std::vector<int64_t>& pad_begin, std::vector<int64_t>& pad_end) {
+    ResolvePads(context, auto_pad, in_spatial, kernel, dilations, strides, pads_attr, pad_begin, pad_end);
+}
+
+int64_t WindowOutput(const std::string& context, int64_t in, int64_t kernel, int64_t dilation, int64_t pad_begin,
+                     int64_t pad_end, int64_t stride, bool ceil_mode) {
+    const int64_t effective = dilation * (kernel - 1) + 1;
+    const int64_t numer = in + pad_begin + pad_end - effective;
+    if (numer < 0) {
+        throw InferenceException(context + ": window is larger than the padded input");
+    }
+    const int64_t out = (ceil_mode ? (numer + stride - 1) / stride : numer / stride) + 1;
+    if (out <= 0) {
+        throw InferenceException(context + ": computes a non-positive output dimension");
+    }
+    return out;
+}
+
+// Validation follows src/kernels/conv.cpp:138-231.
+void Conv(const Node& node, const Views& inputs, const Views& outputs) {
+    const std::string context = "Conv (node '" + node.name + "')";
+    if (inputs.size() < 2 || inputs.size() > 3 || outputs.size() != 1) {
+        throw InferenceException(context + ": expected two or three inputs and one output");
+    }
+    const TensorView& x = inputs[0];
+    const TensorView& w = inputs[1];
+    const TensorView& out = outputs[0];
+    const bool has_bias = inputs.size() == 3;
+    if (x.dtype != DataType::Float32 || w.dtype != DataType::Float32 || out.dtype != DataType::Float32) {
+        throw InferenceException(context + ": tensors must be float32");
+    }
+    if (has_bias && inputs[2].dtype != DataType::Float32) {
+        throw InferenceException(context + ": bias tensor must be float32");
+    }
+    const size_t rank = x.dims.size();
+    if (rank < 3 || rank > 5) {
+        throw InferenceException(context + ": input must be rank 3, 4, or 5 (1-D, 2-D, or 3-D convolution)");
+    }
+    if (w.dims.size() != rank) {
+        throw InferenceException(context + ": weight rank must match the input rank");
+    }
+    (void)ElementCount(x.dims, context);
+    (void)ElementCount(w.dims, context);
+    (void)ElementCount(out.dims, context);
+    const size_t spatial = rank - 2;
+    const int64_t batch = x.dims[0];
+    const int64_t in_channels = x.dims[1];
+    const int64_t out_channels = w.dims[0];
+    const int64_t group = IntAttr(node, "group", 1, "Conv");
+    if (group <= 0) {
+        throw InferenceException(context + ": group must be positive");
+    }
+    if (in_channels % group != 0) {
+        throw InferenceException(context + ": input channels are not divisible by group");
+    }
+    if (w.dims[1] != in_channels / group) {
+        throw InferenceException(context + ": weight channel dimension does not match input/group");
+    }
+    if (out_channels % group != 0) {
+        throw InferenceException(context + ": output channels are not divisible by group");
+    }
+    std::vector<int64_t> strides = IntsAttr(node, "strides", "Conv");
+    std::vector<int64_t> dilations = IntsAttr(node, "dilations", "Conv");
+    if (strides.empty()) {
+        strides.assign(spatial, 1);
+    }
+    if (dilations.empty()) {
+        dilations.assign(spatial, 1);
+    }
+    if (strides.size() != spatial || dilations.size() != spatial) {
+        throw InferenceException(context + ": stride and dilation must have one entry per spatial dimension");
+    }
+    const std::vector<int64_t> in_spatial(x.dims.begin() + 2, x.dims.end());
+    const std::vector<int64_t> kernel(w.dims.begin() + 2, w.dims.end());
+    for (size_t i = 0; i < spatial; ++i) {
+        if (strides[i] <= 0 || dilations[i] <= 0) {
+            throw InferenceException(context + ": stride and dilation must be positive");
+        }
+        if (kernel[i] <= 0) {
+            throw InferenceException(context + ": kernel dimensions must be positive");
+        }
+    }
+    std::vector<int64_t> pad_begin;
+    std::vector<int64_t> pad_end;
+    ResolvePads(context, StringAttr(node, "auto_pad", "NOTSET", "Conv"), in_spatial, kernel, dilations, strides,
+                IntsAttr(node, "pads", "Conv"), pad_begin, pad_end);
+    std::vector<int64_t> expected = {batch, out_channels};
+    for (size_t i = 0; i < spatial; ++i) {
+        expected.push_back(
+            WindowOutput(context, in_spatial[i], kernel[i], dilations[i], pad_begin[i], pad_end[i], strides[i], false));
+    }
+    if (out.dims != expected) {
+        throw InferenceException(context + ": output shape does not match the convolution");
+    }
+    const float* bias = nullptr;
+    if (has_bias) {
+        const std::vector<int64_t>& bias_dims = inputs[2].dims;
+        if (bias_dims.size() != 1 || bias_dims[0] != out_channels) {
+            throw InferenceException(context + ": bias must be rank-1 of length M");
+        }
+        bias = static_cast<const float*>(inputs[2].data);
+    }
+    if (x.data == nullptr || w.data == nullptr || out.data == nullptr || (has_bias && bias == nullptr)) {
+        throw InferenceException(context + ": null buffer");
+    }
+    nert_conv_desc d{};
+    d.batch = batch;
+    d.in_channels = in_channels;
+    d.out_channels = out_channels;
+    d.group = group;
+    const size_t lift = 3 - spatial;
+    for (size_t i = 0; i < 3; ++i) {
+        const bool real = i >= lift;
+        const size_t s = real ? i - lift : 0;
+        d.in[i] = real ? in_spatial[s] : 1;
+        d.kernel[i] = real ? kernel[s] : 1;
+        d.out[i] = real ? expected[2 + s] : 1;
+        d.stride[i] = real ? strides[s] : 1;
+        d.dilation[i] = real ? dilations[s] : 1;
+        d.pad[i] = real ? pad_begin[s] : 0;
+    }
+    CheckStatus(nert_hip_conv_f32(static_cast<const float*>(x.data), static_cast<const float*>(w.data), bias,
+                                  static_cast<float*>(out.data), &d, Stream()),
+                context);
+    AfterRow(outputs, context);
+}
+
+} // namespace rows
+} // namespace nert_hip

@@ -1,0 +1,297 @@
+// Gemm and MatMul on fp32 MFMA (v_mfma_f32_32x32x2_f32).
+//
+// One kernel serves both rows: Y[b] = alpha * op(A[b]) * op(B[b]) + beta * C,
+// where b runs over up to four broadcast batch axes (MatMul) or is absent
+// (Gemm). Transposes are expressed as operand strides, so Gemm's four
+// (transA, transB) cases and MatMul's broadcast batches are the same code with
+// different loaders. Small problems that cannot fill 256 CUs are split along
+// K into a workspace and summed by a second kernel in a fixed order, so the
+// result does not depend on scheduling.
+
+#include "mfma_tile.hpp"
+#include "../../include/nert_hip.h"
+
+namespace nert_hip {
+namespace {
+
+struct GemmArgs {
+    const float* a;
+    const float* b;
+    float* y;
+    const float* bias;
+    int64_t m, n, k;
+    int64_t a_sm, a_sk; // A(m,k) = a[m*a_sm + k*a_sk]
+    int64_t b_sk, b_sn; // B(k,n) = b[k*b_sk + n*b_sn]
+    int64_t bias_sm, bias_sn;
+    float alpha, beta;
+    int has_bias;
+    int batch_rank;
+    int64_t bdims[4];
+    int64_t a_bs[4];
+    int64_t b_bs[4];
+    int64_t k_per_split; // multiple of BK
+    float* partial;      // [splits][batch][m][n] when split
+};
+
+template <class Shape, bool A_KCONTIG, bool B_NCONTIG>
+__global__ __launch_bounds__(Shape::kThreads) void GemmKernel(GemmArgs p) {
+    __shared__ __attribute__((aligned(16))) float lds[2 * (Shape::kLdsA + Shape::kLdsB)];
+    const int64_t tiles_m = (p.m + Shape::kBM - 1) / Shape::kBM;
+    const int64_t tile = blockIdx.x;
+    const int64_t tm = tile % tiles_m;
+    const int64_t tn = tile / tiles_m;
+    const int64_t row0 = tm * Shape::kBM;
+    const int64_t col0 = tn * Shape::kBN;
+    const int64_t batch = blockIdx.y;
+    const int split = blockIdx.z;
+
+    // Batch offsets from the broadcast strides (innermost axis last).
+    int64_t a_off = 0;
+    int64_t b_off = 0;
+    int64_t rem = batch;
+    for (int d = p.batch_rank - 1; d >= 0; --d) {
+        const int64_t idx = rem % p.bdims[d];
+        rem /= p.bdims[d];
+        a_off += idx * p.a_bs[d];
+        b_off += idx * p.b_bs[d];
+    }
+    const float* a = p.a + a_off;
+    const float* b = p.b + b_off;
+
+    const int64_t k_begin = static_cast<int64_t>(split) * p.k_per_split;
+    int64_t k_end = k_begin + p.k_per_split;
+    if (k_end > p.k) {
+        k_end = p.k;
+    }
+
+    using ALoad = typename std::conditional<A_KCONTIG, KContigLoader<Shape::kBM, Shape::kBK, Shape::kThreads, Shape::kPitchA>,
+                                            RowContigLoader<Shape::kBM, Shape::kBK, Shape::kThreads, Shape::kPitchA>>::type;
+    using BLoad = typename std::conditional<B_NCONTIG, RowContigLoader<Shape::kBN, Shape::kBK, Shape::kThreads, Shape::kPitchB>,
+                                            KContigLoader<Shape::kBN, Shape::kBK, Shape::kThreads, Shape::kPitchB>>::type;
+    ALoad aload;
+    BLoad bload;
+    if constexpr (A_KCONTIG) {
+        aload.base = a + row0 * p.a_sm;
+        aload.row_stride = p.a_sm;
+        aload.vec_ok = (p.a_sm % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.a) & 15) == 0) && (a_off % 4 == 0);
+    } else {
+        aload.base = a + row0;
+        aload.k_stride = p.a_sk;
+        aload.vec_ok = (p.a_sk % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.a) & 15) == 0) && (a_off % 4 == 0) &&
+                       (row0 % 4 == 0);
+    }
+    aload.rows_left = p.m - row0;
+    aload.k_total = k_end;
+    if constexpr (B_NCONTIG) {
+        bload.base = b + col0;
+        bload.k_stride = p.b_sk;
+        bload.vec_ok = (p.b_sk % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.b) & 15) == 0) && (b_off % 4 == 0) &&
+                       (col0 % 4 == 0);
+    } else {
+        bload.base = b + col0 * p.b_sn;
+        bload.row_stride = p.b_sn;
+        bload.vec_ok = (p.b_sn % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.b) & 15) == 0) && (b_off % 4 == 0);
+    }
+    bload.rows_left = p.n - col0;
+    bload.k_total = k_end;
+
+    Accum<Shape> acc;
+    MainLoop<Shape>(aload, bload, k_begin, k_end, lds, acc);
+
+    const int64_t plane = p.m * p.n;
+    if (p.partial != nullptr) {
+        float* out = p.partial + (static_cast<int64_t>(split) * gridDim.y + batch) * plane;
+        ForEachAccum<Shape>(acc, [&](int r, int c, float v) {
+            const int64_t gr = row0 + r;
+            const int64_t gc = col0 + c;
+            if (gr < p.m && gc < p.n) {
+                out[gr * p.n + gc] = v;
+            }
+        });
+        return;
+    }
+    float* out = p.y + batch * plane;
+    ForEachAccum<Shape>(acc, [&](int r, int c, float v) {
+        const int64_t gr = row0 + r;
+        const int64_t gc = col0 + c;
+        if (gr < p.m && gc < p.n) {
+            float value = p.alpha * v;
+            if (p.has_bias) {
+                value += p.beta * p.bias[gr * p.bias_sm + gc * p.bias_sn];
+            }
+            out[gr * p.n + gc] = value;
+        }
+    });
+}
+
+// Sums the split-K partials in split order and applies the epilogue.
+__global__ void SplitReduceKernel(GemmArgs p, int splits, int64_t batches) {
+    const int64_t plane = p.m * p.n;
+    const int64_t total = plane * batches;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        float sum = 0.f;
+        for (int s = 0; s < splits; ++s) {
+            sum += p.partial[s * total + i];
+        }
+        const int64_t e = i % plane;
+        const int64_t r = e / p.n;
+        const int64_t c = e % p.n;
+        float value = p.alpha * sum;
+        if (p.has_bias) {
+            value += p.beta * p.bias[r * p.bias_sm + c * p.bias_sn];
+        }
+        p.y[i] = value;
+    }
+}
+
+using ShapeL = TileShape<128, 128, 16, 2, 2>; // 4 waves, 64x64 per wave
+using ShapeM = TileShape<64, 64, 16, 2, 2>;   // 4 waves, 32x32 per wave
+using ShapeS = TileShape<32, 64, 32, 1, 2>;   // 2 waves, skinny M
+
+template <class Shape>
+void LaunchShape(GemmArgs p, int64_t batches, int splits, hipStream_t stream) {
+    const int64_t tiles = ((p.m + Shape::kBM - 1) / Shape::kBM) * ((p.n + Shape::kBN - 1) / Shape::kBN);
+    dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(batches), static_cast<unsigned>(splits));
+    dim3 block(Shape::kThreads);
+    const bool a_k = p.a_sk == 1;
+    const bool b_n = p.b_sn == 1;
+    if (a_k && b_n) {
+        GemmKernel<Shape, true, true><<<grid, block, 0, stream>>>(p);
+    } else if (a_k) {
+        GemmKernel<Shape, true, false><<<grid, block, 0, stream>>>(p);
+    } else if (b_n) {
+        GemmKernel<Shape, false, true><<<grid, block, 0, stream>>>(p);
+    } else {
+        GemmKernel<Shape, false, false><<<grid, block, 0, stream>>>(p);
+    }
+    CheckLaunch("GemmKernel launch");
+}
+
+constexpr int64_t kTargetBlocks = 512; // two blocks per CU on 256 CUs
+
+template <class Shape>
+int64_t TileCount(const GemmArgs& p, int64_t batches) {
+    return ((p.m + Shape::kBM - 1) / Shape::kBM) * ((p.n + Shape::kBN - 1) / Shape::kBN) * batches;
+}
+
+void Launch(GemmArgs p, int64_t batches, hipStream_t stream) {
+    if (p.m == 0 || p.n == 0 || batches == 0) {
+        return;
+    }
+    // Operand strides must make one of each pair unit (contiguous tensors).
+    if (!(p.a_sk == 1 || p.a_sm == 1) || !(p.b_sn == 1 || p.b_sk == 1)) {
+        throw Error("gemm: operands must be contiguous in one index");
+    }
+    int shape = 0; // 0 = L, 1 = M, 2 = S
+    int64_t tiles = TileCount<ShapeL>(p, batches);
+    if (p.m <= 32) {
+        shape = 2;
+        tiles = TileCount<ShapeS>(p, batches);
+    } else if (tiles < kTargetBlocks / 2) {
+        shape = 1;
+        tiles = TileCount<ShapeM>(p, batches);
+    }
+    const int bk = shape == 2 ? ShapeS::kBK : ShapeL::kBK;
+    // Split K while the grid is under one block per CU and each split keeps
+    // at least 8 K tiles of work.
+    int splits = 1;
+    const int64_t k_tiles = (p.k + bk - 1) / bk;
+    while (tiles * splits < 256 && k_tiles / (splits * 2) >= 8 && splits < 32) {
+        splits *= 2;
+    }
+    p.k_per_split = ((k_tiles + splits - 1) / splits) * bk;
+    if (p.k == 0) {
+        p.k_per_split = 0;
+        splits = 1;
+    }
+    p.partial = nullptr;
+    if (splits > 1) {
+        p.partial = static_cast<float*>(Workspace(static_cast<int64_t>(splits) * batches * p.m * p.n * 4, stream));
+    }
+    switch (shape) {
+    case 0:
+        LaunchShape<ShapeL>(p, batches, splits, stream);
+        break;
+    case 1:
+        LaunchShape<ShapeM>(p, batches, splits, stream);
+        break;
+    default:
+        LaunchShape<ShapeS>(p, batches, splits, stream);
+        break;
+    }
+    if (splits > 1) {
+        const int64_t total = batches * p.m * p.n;
+        SplitReduceKernel<<<GridFor(total, 256, 4096), 256, 0, stream>>>(p, splits, batches);
+        CheckLaunch("SplitReduceKernel launch");
+    }
+}
+
+} // namespace
+} // namespace nert_hip
+
+extern "C" {
+
+int nert_hip_gemm_f32(const float* a, const float* b, const float* c, float* y, int64_t m, int64_t n, int64_t k,
+                      int trans_a, int trans_b, float alpha, float beta, int c_rank, void* stream) {
+    return nert_hip::Guard([&] {
+        nert_hip::GemmArgs p{};
+        p.a = a;
+        p.b = b;
+        p.y = y;
+        p.m = m;
+        p.n = n;
+        p.k = k;
+        // A is stored [M,K] (trans_a = 0) or [K,M]; B is [K,N] or [N,K].
+        p.a_sm = trans_a ? 1 : k;
+        p.a_sk = trans_a ? m : 1;
+        p.b_sk = trans_b ? 1 : n;
+        p.b_sn = trans_b ? k : 1;
+        p.alpha = alpha;
+        p.beta = beta;
+        p.has_bias = (c != nullptr && c_rank > 0) ? 1 : 0;
+        p.bias = c;
+        p.bias_sm = c_rank == 2 ? n : 0;
+        p.bias_sn = 1;
+        p.batch_rank = 0;
+        nert_hip::Launch(p, 1, nert_hip::StreamOr(stream));
+    });
+}
+
+int nert_hip_matmul_f32(const float* a, const float* b, float* y, int64_t m, int64_t n, int64_t k, int batch_rank,
+                        const int64_t* batch_dims, const int64_t* a_batch_strides, const int64_t* b_batch_strides,
+                        void* stream) {
+    return nert_hip::Guard([&] {
+        if (batch_rank < 0 || batch_rank > 4) {
+            throw nert_hip::Error("matmul: at most four batch axes are supported");
+        }
+        nert_hip::GemmArgs p{};
+        p.a = a;
+        p.b = b;
+        p.y = y;
+        p.m = m;
+        p.n = n;
+        p.k = k;
+        p.a_sm = k;
+        p.a_sk = 1;
+        p.b_sk = n;
+        p.b_sn = 1;
+        p.alpha = 1.0f;
+        p.beta = 0.0f;
+        p.has_bias = 0;
+        p.batch_rank = batch_rank;
+        int64_t batches = 1;
+        for (int d = 0; d < batch_rank; ++d) {
+            p.bdims[d] = batch_dims[d];
+            p.a_bs[d] = a_batch_strides[d];
+            p.b_bs[d] = b_batch_strides[d];
+            batches *= batch_dims[d];
+        }
+        if (batches > 65535) {
+            throw nert_hip::Error("matmul: more than 65535 batches");
+        }
+        nert_hip::Launch(p, batches, nert_hip::StreamOr(stream));
+    });
+}
+
+} // extern "C"

@@ -1,0 +1,189 @@
+// Pooling rows: MaxPool (2-D), AveragePool (2-D) and GlobalAveragePool.
+//
+// MaxPool keeps the reference's comparison exactly: a tap replaces the
+// running best only when `x > best`, starting from -inf and skipping padded
+// taps (src/kernels/max_pool.cpp:210-238), so NaN inputs never win.
+// GlobalAveragePool gives each (n, c) plane to one wave: lanes stride the
+// plane with coalesced loads, accumulate in double like the reference
+// (src/kernels/global_average_pool.cpp:62-68) and combine with a shuffle tree.
+
+#include "common.hpp"
+#include "../../include/nert_hip.h"
+
+namespace nert_hip {
+namespace {
+
+struct PoolArgs {
+    const float* x;
+    float* y;
+    int64_t planes; // N*C
+    int32_t in_h, in_w, out_h, out_w;
+    int32_t k_h, k_w, s_h, s_w, d_h, d_w, p_h, p_w;
+    int32_t pad_end_h, pad_end_w;
+    int32_t count_include_pad;
+};
+
+__global__ void MaxPool2dKernel(PoolArgs p) {
+    const int64_t total = p.planes * p.out_h * p.out_w;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total; i += stride) {
+        const int32_t ow = static_cast<int32_t>(i % p.out_w);
+        const int64_t t = i / p.out_w;
+        const int32_t oh = static_cast<int32_t>(t % p.out_h);
+        const int64_t plane = t / p.out_h;
+        const float* xp = p.x + plane * p.in_h * p.in_w;
+        const int32_t h0 = oh * p.s_h - p.p_h;
+        const int32_t w0 = ow * p.s_w - p.p_w;
+        float best = -__builtin_huge_valf();
+        for (int32_t kh = 0; kh < p.k_h; ++kh) {
+            const int32_t ih = h0 + kh * p.d_h;
+            if (static_cast<uint32_t>(ih) >= static_cast<uint32_t>(p.in_h)) {
+                continue;
+            }
+            const float* row = xp + static_cast<int64_t>(ih) * p.in_w;
+            for (int32_t kw = 0; kw < p.k_w; ++kw) {
+                const int32_t iw = w0 + kw * p.d_w;
+                if (static_cast<uint32_t>(iw) >= static_cast<uint32_t>(p.in_w)) {
+                    continue;
+                }
+                const float v = row[iw];
+                if (v > best) {
+                    best = v;
+                }
+            }
+        }
+        p.y[i] = best;
+    }
+}
+
+// AveragePool, exactly as src/kernels/average_pool.cpp:196-223: a float sum
+// over the window clipped to the input, in row-major tap order, divided once
+// by either the clipped tap count or (count_include_pad) the window clipped to
+// the padded extent. Same operations in the same order, so the result is
+// bit-identical to the reference.
+__global__ void AvgPool2dKernel(PoolArgs p) {
+    const int64_t total = p.planes * p.out_h * p.out_w;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total; i += stride) {
+        const int32_t ow = static_cast<int32_t>(i % p.out_w);
+        const int64_t t = i / p.out_w;
+        const int32_t oh = static_cast<int32_t>(t % p.out_h);
+        const int64_t plane = t / p.out_h;
+        const float* xp = p.x + plane * p.in_h * p.in_w;
+        const int32_t h_start = oh * p.s_h - p.p_h;
+        const int32_t h_end = min(h_start + p.k_h, p.in_h + p.pad_end_h);
+        const int32_t h0 = max(h_start, 0);
+        const int32_t h1 = min(h_end, p.in_h);
+        const int32_t w_start = ow * p.s_w - p.p_w;
+        const int32_t w_end = min(w_start + p.k_w, p.in_w + p.pad_end_w);
+        const int32_t w0 = max(w_start, 0);
+        const int32_t w1 = min(w_end, p.in_w);
+        float sum = 0.0f;
+        for (int32_t ih = h0; ih < h1; ++ih) {
+            const float* row = xp + static_cast<int64_t>(ih) * p.in_w;
+            for (int32_t iw = w0; iw < w1; ++iw) {
+                sum = __fadd_rn(sum, row[iw]);
+            }
+        }
+        const int64_t divisor = p.count_include_pad ? static_cast<int64_t>(h_end - h_start) * (w_end - w_start)
+                                                    : static_cast<int64_t>(h1 - h0) * (w1 - w0);
+        p.y[i] = divisor > 0 ? __fdiv_rn(sum, static_cast<float>(divisor)) : 0.0f;
+    }
+}
+
+__device__ __forceinline__ double WaveSum(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        v += __shfl_xor(v, off, 64);
+    }
+    return v;
+}
+
+// One wave per plane; `waves` planes per 256-thread block.
+__global__ __launch_bounds__(256) void GlobalAvgPoolKernel(const float* __restrict__ x, float* __restrict__ y,
+                                                           int64_t planes, int64_t spatial) {
+    const int lane = threadIdx.x & 63;
+    const int64_t plane = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (plane >= planes) {
+        return;
+    }
+    const float* xp = x + plane * spatial;
+    double sum = 0.0;
+    for (int64_t k = lane; k < spatial; k += 64) {
+        sum += static_cast<double>(xp[k]);
+    }
+    sum = WaveSum(sum);
+    if (lane == 0) {
+        y[plane] = static_cast<float>(sum / static_cast<double>(spatial));
+    }
+}
+
+PoolArgs MakeArgs(const float* x, float* y, const nert_pool_desc* d) {
+    PoolArgs p{};
+    p.x = x;
+    p.y = y;
+    p.planes = d->batch * d->channels;
+    p.in_h = static_cast<int32_t>(d->in[0]);
+    p.in_w = static_cast<int32_t>(d->in[1]);
+    p.out_h = static_cast<int32_t>(d->out[0]);
+    p.out_w = static_cast<int32_t>(d->out[1]);
+    p.k_h = static_cast<int32_t>(d->kernel[0]);
+    p.k_w = static_cast<int32_t>(d->kernel[1]);
+    p.s_h = static_cast<int32_t>(d->stride[0]);
+    p.s_w = static_cast<int32_t>(d->stride[1]);
+    p.d_h = static_cast<int32_t>(d->dilation[0]);
+    p.d_w = static_cast<int32_t>(d->dilation[1]);
+    p.p_h = static_cast<int32_t>(d->pad_begin[0]);
+    p.p_w = static_cast<int32_t>(d->pad_begin[1]);
+    p.pad_end_h = static_cast<int32_t>(d->pad_end[0]);
+    p.pad_end_w = static_cast<int32_t>(d->pad_end[1]);
+    p.count_include_pad = static_cast<int32_t>(d->count_include_pad);
+    return p;
+}
+
+} // namespace
+} // namespace nert_hip
+
+using namespace nert_hip;
+
+extern "C" {
+
+int nert_hip_maxpool2d_f32(const float* x, float* y, const nert_pool_desc* d, void* stream) {
+    return Guard([&] {
+        PoolArgs p = MakeArgs(x, y, d);
+        const int64_t total = p.planes * p.out_h * p.out_w;
+        if (total <= 0) {
+            return;
+        }
+        MaxPool2dKernel<<<GridFor(total, 256, 16384), 256, 0, StreamOr(stream)>>>(p);
+        CheckLaunch("MaxPool2dKernel launch");
+    });
+}
+
+int nert_hip_avgpool2d_f32(const float* x, float* y, const nert_pool_desc* d, void* stream) {
+    return Guard([&] {
+        PoolArgs p = MakeArgs(x, y, d);
+        const int64_t total = p.planes * p.out_h * p.out_w;
+        if (total <= 0) {
+            return;
+        }
+        AvgPool2dKernel<<<GridFor(total, 256, 16384), 256, 0, StreamOr(stream)>>>(p);
+        CheckLaunch("AvgPool2dKernel launch");
+    });
+}
+
+int nert_hip_global_avgpool_f32(const float* x, float* y, int64_t planes, int64_t spatial, void* stream) {
+    return Guard([&] {
+        if (planes <= 0 || spatial <= 0) {
+            return;
+        }
+        const int64_t blocks = (planes + 3) / 4;
+        if (blocks > 0x7FFFFFFF) {
+            throw Error("global_avgpool: too many planes");
+        }
+        GlobalAvgPoolKernel<<<static_cast<unsigned>(blocks), 256, 0, StreamOr(stream)>>>(x, y, planes, spatial);
+        CheckLaunch("GlobalAvgPoolKernel launch");
+    });
+}
+
+} // extern "C"

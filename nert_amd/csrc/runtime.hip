@@ -1,0 +1,285 @@
+// Device runtime behind the C-ABI: device selection, the launch stream,
+// memory, transfers, events, workspace and the last-error string.
+//
+// One process-lifetime context on device 0, as NERT's seam expects
+// (src/hip_device.cpp:33-44 pins ordinal 0). All kernels and transfers are
+// ordered on one stream, created at default priority, so the only host/device
+// synchronisation points are blocking transfers and explicit syncs.
+
+#include "common.hpp"
+#include "../../include/nert_hip.h"
+
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace nert_hip {
+namespace {
+
+thread_local std::string g_last_error;
+
+struct Context {
+    bool ready = false;
+    hipStream_t stream = nullptr;
+    void* workspace = nullptr;
+    int64_t workspace_bytes = 0;
+    int32_t* flags = nullptr;
+};
+
+Context& Ctx() {
+    static Context ctx;
+    return ctx;
+}
+
+std::mutex& Mutex() {
+    static std::mutex m;
+    return m;
+}
+
+void EnsureReady() {
+    Context& ctx = Ctx();
+    if (ctx.ready) {
+        return;
+    }
+    std::lock_guard<std::mutex> lock(Mutex());
+    if (ctx.ready) {
+        return;
+    }
+    int count = 0;
+    Check(hipGetDeviceCount(&count), "hipGetDeviceCount");
+    if (count <= 0) {
+        throw Error("no HIP device found");
+    }
+    Check(hipSetDevice(0), "hipSetDevice");
+    Check(hipStreamCreateWithFlags(&ctx.stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+    Check(hipMalloc(reinterpret_cast<void**>(&ctx.flags), 64), "hipMalloc(flags)");
+    Check(hipMemsetAsync(ctx.flags, 0, 64, ctx.stream), "hipMemsetAsync(flags)");
+    Check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
+    ctx.ready = true;
+}
+
+} // namespace
+
+void SetLastError(const std::string& message) { g_last_error = message; }
+
+hipStream_t DefaultStream() {
+    EnsureReady();
+    return Ctx().stream;
+}
+
+void* Workspace(int64_t bytes, hipStream_t stream) {
+    EnsureReady();
+    Context& ctx = Ctx();
+    if (bytes <= ctx.workspace_bytes) {
+        return ctx.workspace;
+    }
+    // Grow geometrically; the old buffer may still be read by queued work.
+    int64_t want = ctx.workspace_bytes * 2;
+    if (want < bytes) {
+        want = bytes;
+    }
+    want = (want + 0xFFFFF) & ~static_cast<int64_t>(0xFFFFF);
+    if (ctx.workspace != nullptr) {
+        Check(hipStreamSynchronize(stream), "hipStreamSynchronize(workspace)");
+        Check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize(workspace)");
+        Check(hipFree(ctx.workspace), "hipFree(workspace)");
+        ctx.workspace = nullptr;
+        ctx.workspace_bytes = 0;
+    }
+    Check(hipMalloc(&ctx.workspace, static_cast<size_t>(want)), "hipMalloc(workspace)");
+    ctx.workspace_bytes = want;
+    return ctx.workspace;
+}
+
+int32_t* ErrorFlags() {
+    EnsureReady();
+    return Ctx().flags;
+}
+
+namespace {
+
+constexpr int64_t kShadowMaxBytes = 64 * 1024;
+
+struct ShadowStore {
+    std::mutex mutex;
+    std::map<uintptr_t, std::vector<uint8_t>> entries;
+
+    // Removes every entry overlapping [addr, addr + bytes). Caller holds mutex.
+    void DropLocked(uintptr_t addr, int64_t bytes) {
+        if (entries.empty() || bytes <= 0) {
+            return;
+        }
+        auto it = entries.upper_bound(addr);
+        if (it != entries.begin()) {
+            auto prev = std::prev(it);
+            if (prev->first + prev->second.size() > addr) {
+                it = prev;
+            }
+        }
+        while (it != entries.end() && it->first < addr + static_cast<uintptr_t>(bytes)) {
+            it = entries.erase(it);
+        }
+    }
+};
+
+ShadowStore& Shadows() {
+    static ShadowStore store;
+    return store;
+}
+
+} // namespace
+
+void ShadowPut(const void* dst, const void* src, int64_t bytes) {
+    ShadowStore& s = Shadows();
+    std::lock_guard<std::mutex> lock(s.mutex);
+    s.DropLocked(reinterpret_cast<uintptr_t>(dst), bytes);
+    if (bytes <= 0 || bytes > kShadowMaxBytes) {
+        return;
+    }
+    const auto* p = static_cast<const uint8_t*>(src);
+    s.entries[reinterpret_cast<uintptr_t>(dst)] = std::vector<uint8_t>(p, p + bytes);
+}
+
+void ShadowDrop(const void* dst, int64_t bytes) {
+    ShadowStore& s = Shadows();
+    std::lock_guard<std::mutex> lock(s.mutex);
+    s.DropLocked(reinterpret_cast<uintptr_t>(dst), bytes);
+}
+
+bool ShadowGet(const void* src, int64_t bytes, void* out) {
+    ShadowStore& s = Shadows();
+    std::lock_guard<std::mutex> lock(s.mutex);
+    const auto it = s.entries.find(reinterpret_cast<uintptr_t>(src));
+    if (it == s.entries.end() || static_cast<int64_t>(it->second.size()) < bytes) {
+        return false;
+    }
+    std::memcpy(out, it->second.data(), static_cast<size_t>(bytes));
+    return true;
+}
+
+} // namespace nert_hip
+
+using nert_hip::Guard;
+
+extern "C" {
+
+const char* nert_hip_last_error(void) { return nert_hip::g_last_error.c_str(); }
+
+int nert_hip_init(void) {
+    return Guard([] { nert_hip::EnsureReady(); });
+}
+
+int nert_hip_device_count(int* count) {
+    return Guard([&] {
+        int n = 0;
+        const hipError_t status = hipGetDeviceCount(&n);
+        *count = status == hipSuccess ? n : 0;
+    });
+}
+
+void* nert_hip_malloc(int64_t bytes) {
+    if (bytes <= 0) {
+        return nullptr;
+    }
+    void* ptr = nullptr;
+    const int rc = Guard([&] {
+        nert_hip::EnsureReady();
+        nert_hip::Check(hipMalloc(&ptr, static_cast<size_t>(bytes)), "hipMalloc");
+    });
+    return rc == 0 ? ptr : nullptr;
+}
+
+int nert_hip_free(void* ptr) {
+    if (ptr == nullptr) {
+        return 0;
+    }
+    return Guard([&] {
+        nert_hip::Check(hipStreamSynchronize(nert_hip::DefaultStream()), "hipStreamSynchronize");
+        hipDeviceptr_t base = nullptr;
+        size_t size = 0;
+        if (hipMemGetAddressRange(&base, &size, ptr) == hipSuccess) {
+            nert_hip::ShadowDrop(ptr, static_cast<int64_t>(size));
+        } else {
+            (void)hipGetLastError();
+        }
+        nert_hip::Check(hipFree(ptr), "hipFree");
+    });
+}
+
+int nert_hip_memcpy_h2d(void* dst, const void* src, int64_t bytes) {
+    if (bytes == 0) {
+        return 0;
+    }
+    return Guard([&] {
+        hipStream_t s = nert_hip::DefaultStream();
+        nert_hip::Check(hipMemcpyAsync(dst, src, static_cast<size_t>(bytes), hipMemcpyHostToDevice, s),
+                        "hipMemcpyAsync(H2D)");
+        nert_hip::Check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        nert_hip::ShadowPut(dst, src, bytes);
+    });
+}
+
+int nert_hip_memcpy_d2h(void* dst, const void* src, int64_t bytes) {
+    if (bytes == 0) {
+        return 0;
+    }
+    return Guard([&] {
+        hipStream_t s = nert_hip::DefaultStream();
+        nert_hip::Check(hipMemcpyAsync(dst, src, static_cast<size_t>(bytes), hipMemcpyDeviceToHost, s),
+                        "hipMemcpyAsync(D2H)");
+        nert_hip::Check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    });
+}
+
+int nert_hip_memcpy_d2d(void* dst, const void* src, int64_t bytes, void* stream) {
+    if (bytes == 0) {
+        return 0;
+    }
+    return Guard([&] {
+        nert_hip::ShadowDrop(dst, bytes);
+        nert_hip::Check(hipMemcpyAsync(dst, src, static_cast<size_t>(bytes), hipMemcpyDeviceToDevice,
+                                       nert_hip::StreamOr(stream)),
+                        "hipMemcpyAsync(D2D)");
+    });
+}
+
+void* nert_hip_default_stream(void) {
+    void* s = nullptr;
+    (void)Guard([&] { s = nert_hip::DefaultStream(); });
+    return s;
+}
+
+int nert_hip_stream_sync(void* stream) {
+    return Guard([&] { nert_hip::Check(hipStreamSynchronize(nert_hip::StreamOr(stream)), "hipStreamSynchronize"); });
+}
+
+void* nert_hip_event_create(void) {
+    hipEvent_t e = nullptr;
+    const int rc = Guard([&] {
+        nert_hip::EnsureReady();
+        nert_hip::Check(hipEventCreate(&e), "hipEventCreate");
+    });
+    return rc == 0 ? static_cast<void*>(e) : nullptr;
+}
+
+int nert_hip_event_record(void* event, void* stream) {
+    return Guard([&] {
+        nert_hip::Check(hipEventRecord(static_cast<hipEvent_t>(event), nert_hip::StreamOr(stream)), "hipEventRecord");
+    });
+}
+
+int nert_hip_event_elapsed_ms(void* start, void* stop, float* ms) {
+    return Guard([&] {
+        nert_hip::Check(hipEventSynchronize(static_cast<hipEvent_t>(stop)), "hipEventSynchronize");
+        nert_hip::Check(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)),
+                        "hipEventElapsedTime");
+    });
+}
+
+int nert_hip_event_destroy(void* event) {
+    return Guard([&] { nert_hip::Check(hipEventDestroy(static_cast<hipEvent_t>(event)), "hipEventDestroy"); });
+}
+
+} // extern "C"

@@ -1,0 +1,183 @@
+"""GPU parity: Gemm, MatMul and Conv rows against the reference CpuDevice and
+the numpy restatement, from the reference's own known-answer cases up to the
+BASELINE.json configs at full size."""
+
+import numpy as np
+import pytest
+
+from nert_amd.device import DeviceArray, run_node
+from oracle import restate
+from rowcheck import assert_parity, assert_same_error, compare, randn, uniform
+
+pytestmark = pytest.mark.gpu
+
+F = np.float32
+
+
+def _hip(op, inputs, out_shape, attrs=None):
+    dev_in = [None if x is None else DeviceArray.from_host(x) for x in inputs]
+    out = DeviceArray(out_shape, F)
+    run_node(op, dev_in, [out], attrs)
+    return out.to_host()
+
+
+# --- known answers from test/hip_kernels_test.cpp -------------------------
+
+def test_gemm_small_exact(gpu):
+    a = np.array([[1, 2, 3], [4, 5, 6]], F)
+    b = np.array([[7, 8], [9, 10], [11, 12]], F)
+    got = assert_parity("Gemm", [a, b], [((2, 2), F)], name="gemm0")
+    assert np.array_equal(got[0], np.array([[58, 64], [139, 154]], F))  # hip_kernels_test.cpp:97-98
+
+
+def test_gemm_transposed_with_bias(gpu):
+    a = np.array([1, 2, 3, 4, 5, 6], F).reshape(3, 2)
+    b = np.array([1, 0, 0, 1, 2, 1, 0, 2, 1, 1, 0, 1], F).reshape(4, 3)
+    c = np.array([0.5, -0.5, 1.0, 2.0], F)
+    attrs = {"transA": 1, "transB": 1, "alpha": 2.0, "beta": 0.5}
+    assert_parity("Gemm", [a, b, c], [((2, 4), F)], attrs, name="gemm1")
+
+
+def test_gemm_rejects_mismatch(gpu):
+    msg = assert_same_error("Gemm", [np.ones((2, 3), F), np.ones((2, 2), F)], [((2, 2), F)], name="gemm_bad")
+    assert "contraction dimension mismatch" in msg
+
+
+def test_matmul_batched_broadcast(gpu):
+    a = np.array([1, 2, 3, 4, 5, 6], F).reshape(2, 3)
+    b = np.array([1, 0, 0, 1, 1, 1, 2, 0, 0, 2, 1, 0], F).reshape(2, 3, 2)
+    got = assert_parity("MatMul", [a, b], [((2, 2, 2), F)], name="mm0")
+    assert np.array_equal(got[0].ravel(), np.array([4, 5, 10, 11, 5, 4, 14, 10], F))
+
+
+def test_matmul_promoted_vector(gpu):
+    a = np.array([1, 2, 3], F)
+    b = np.array([[1, 2], [3, 4], [5, 6]], F)
+    got = assert_parity("MatMul", [a, b], [((2,), F)], name="mm1")
+    assert np.array_equal(got[0], np.array([22, 28], F))
+
+
+def test_conv_pointwise_no_bias(gpu):
+    x = np.arange(1, 9, dtype=F).reshape(1, 2, 2, 2)
+    w = np.array([1, 0, 0, 1, 1, 1], F).reshape(3, 2, 1, 1)
+    got = assert_parity("Conv", [x, w], [((1, 3, 2, 2), F)], name="cv0")
+    assert np.array_equal(got[0].ravel(), np.array([1, 2, 3, 4, 5, 6, 7, 8, 6, 8, 10, 12], F))
+
+
+def test_conv_padded_3x3_with_bias(gpu):
+    x = np.arange(1, 10, dtype=F).reshape(1, 1, 3, 3)
+    w = np.ones((1, 1, 3, 3), F)
+    b = np.array([10], F)
+    got = assert_parity("Conv", [x, w, b], [((1, 1, 3, 3), F)], {"pads": [1, 1, 1, 1]}, name="cv1")
+    assert np.array_equal(got[0].ravel(), np.array([22, 31, 26, 37, 55, 43, 34, 49, 38], F))
+
+
+def test_conv_depthwise_with_bias(gpu):
+    x = np.arange(1, 9, dtype=F).reshape(1, 2, 2, 2)
+    w = np.array([2, 3], F).reshape(2, 1, 1, 1)
+    b = np.array([1, -1], F)
+    got = assert_parity("Conv", [x, w, b], [((1, 2, 2, 2), F)], {"group": 2}, name="cv2")
+    assert np.array_equal(got[0].ravel(), np.array([3, 5, 7, 9, 14, 17, 20, 23], F))
+
+
+def test_conv_same_upper_asymmetric(gpu):
+    x = ((np.arange(18) % 13) - 6).astype(F).reshape(1, 2, 3, 3) * F(0.5)
+    w = ((np.arange(16) % 7) - 3).astype(F).reshape(2, 2, 2, 2) * F(0.25)
+    b = np.array([1.5, -2.5], F)
+    assert_parity("Conv", [x, w, b], [((1, 2, 3, 3), F)], {"auto_pad": "SAME_UPPER"}, name="cv_same")
+
+
+# --- randomized parity against the reference rows -------------------------
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (7, 13, 5), (33, 65, 17), (130, 97, 301), (256, 128, 64)])
+def test_gemm_trans_random(gpu, ta, tb, m, n, k):
+    a = uniform((k, m) if ta else (m, k), seed=m)
+    b = uniform((n, k) if tb else (k, n), seed=n + 1)
+    c = uniform((n,), seed=k + 2)
+    assert_parity("Gemm", [a, b, c], [((m, n), F)], {"transA": ta, "transB": tb, "alpha": 0.75, "beta": -1.25})
+
+
+def test_gemm_rank2_bias_and_no_bias(gpu):
+    a = uniform((40, 70), seed=1)
+    b = uniform((70, 90), seed=2)
+    c = uniform((40, 90), seed=3)
+    assert_parity("Gemm", [a, b, c], [((40, 90), F)])
+    assert_parity("Gemm", [a, b], [((40, 90), F)], {"alpha": 3.0})
+
+
+@pytest.mark.parametrize("ashape,bshape,oshape", [
+    ((3, 4, 5), (5, 6), (3, 4, 6)),
+    ((2, 1, 4, 5), (3, 5, 7), (2, 3, 4, 7)),
+    ((5,), (2, 5, 3), (2, 3)),
+    ((2, 3, 4), (4,), (2, 3)),
+    ((4,), (4,), ()),
+    ((2, 12, 33, 16), (2, 12, 16, 33), (2, 12, 33, 33)),
+    ((1, 9, 130, 70), (70, 64), (1, 9, 130, 64)),
+])
+def test_matmul_shapes(gpu, ashape, bshape, oshape):
+    a = uniform(ashape, seed=len(ashape))
+    b = uniform(bshape, seed=len(bshape) + 7)
+    assert_parity("MatMul", [a, b], [(oshape, F)])
+
+
+CONV_CASES = [
+    # x shape, w shape, attrs
+    ((2, 3, 17, 19), (8, 3, 3, 3), {"pads": [1, 1, 1, 1]}),
+    ((1, 4, 15, 15), (6, 4, 5, 3), {"strides": [2, 1], "pads": [2, 1, 2, 1]}),
+    ((2, 6, 12, 12), (6, 2, 3, 3), {"group": 3, "dilations": [2, 2], "pads": [2, 2, 2, 2]}),
+    ((1, 3, 32, 32), (16, 3, 7, 7), {"strides": [2, 2], "pads": [3, 3, 3, 3]}),
+    ((2, 16, 14, 14), (32, 16, 1, 1), {"strides": [2, 2]}),
+    ((1, 4, 9, 9), (5, 4, 2, 2), {"auto_pad": "SAME_LOWER", "strides": [2, 2]}),
+    ((1, 4, 9, 9), (5, 4, 3, 3), {"auto_pad": "VALID"}),
+    ((2, 3, 20), (4, 3, 5), {"pads": [2, 2]}),                   # 1-D
+    ((1, 2, 5, 6, 7), (3, 2, 2, 3, 3), {"pads": [1, 0, 1, 1, 1, 1]}),  # 3-D
+    ((1, 8, 10, 10), (8, 1, 3, 3), {"group": 8, "pads": [1, 1, 1, 1]}),  # depthwise
+    ((4, 64, 14, 14), (128, 64, 3, 3), {"pads": [1, 1, 1, 1], "strides": [2, 2]}),
+]
+
+
+@pytest.mark.parametrize("xs,ws,attrs", CONV_CASES)
+def test_conv_random(gpu, xs, ws, attrs):
+    x = randn(xs, seed=sum(xs))
+    w = randn(ws, seed=sum(ws), scale=0.2)
+    b = randn((ws[0],), seed=3, scale=0.1)
+    ref = restate.conv(x, w, b, attrs.get("strides"), attrs.get("dilations"), attrs.get("pads"),
+                       attrs.get("group", 1), attrs.get("auto_pad", "NOTSET"))
+    got = assert_parity("Conv", [x, w, b], [(ref.shape, F)], attrs)
+    compare(got[0], ref, what="conv vs restatement")
+
+
+# --- BASELINE.json configs at full size -----------------------------------
+
+def test_config0_conv_3x3(gpu):
+    """X[1,64,56,56], W[64,64,3,3], B[64], pad 1 -> [1,64,56,56]."""
+    x = randn((1, 64, 56, 56), seed=0)
+    w = randn((64, 64, 3, 3), seed=1, scale=np.sqrt(2 / 576))
+    b = randn((64,), seed=2, scale=0.01)
+    assert_parity("Conv", [x, w, b], [((1, 64, 56, 56), F)], {"pads": [1, 1, 1, 1]})
+
+
+def test_config1a_batched_matmul(gpu):
+    """configs[1](a): [8,1024,1024] x [8,1024,1024] against the restatement."""
+    a = uniform((8, 1024, 1024), seed=10)
+    b = uniform((8, 1024, 1024), seed=11)
+    got = _hip("MatMul", [a, b], (8, 1024, 1024))
+    compare(got, restate.matmul(a, b), what="cfg1a")
+
+
+def test_config1b_gemm_transb(gpu):
+    """configs[1](b): A[2048,4096] x B[1024,4096]^T + C[1024]."""
+    a = uniform((2048, 4096), seed=12)
+    b = uniform((1024, 4096), seed=13)
+    c = uniform((1024,), seed=14)
+    got = _hip("Gemm", [a, b, c], (2048, 1024), {"transB": 1, "alpha": 1.0, "beta": 1.0})
+    compare(got, restate.gemm(a, b, c, trans_b=1), what="cfg1b")
+
+
+def test_config1c_skinny_gemm(gpu):
+    """configs[1](c): A[32,512] x B[1000,512]^T + bias, against the reference row."""
+    a = uniform((32, 512), seed=15)
+    b = uniform((1000, 512), seed=16)
+    c = uniform((1000,), seed=17)
+    assert_parity("Gemm", [a, b, c], [((32, 1000), F)], {"transB": 1})
