@@ -58,6 +58,18 @@ int nert_hip_event_record(void* event, void* stream);
 int nert_hip_event_elapsed_ms(void* start, void* stop, float* ms);
 int nert_hip_event_destroy(void* event);
 
+/* HIP-graph capture of the layer stream. Everything queued on the layer
+ * stream between begin and end (kernel launches of any rows, device-to-device
+ * copies) becomes one replayable graph; rows that must synchronise (control
+ * reads without a host shadow, data-dependent error checks) cannot be
+ * captured and fail the capture. Workspace growth must happen before capture
+ * (run the sequence once eagerly first). No reference counterpart: the
+ * reference executor launches rows one by one (src/executor.cpp:480-535). */
+int nert_hip_capture_begin(void);
+int nert_hip_capture_end(void** graph_exec);
+int nert_hip_graph_launch(void* graph_exec, void* stream);
+int nert_hip_graph_destroy(void* graph_exec);
+
 /* Reads (and clears when set) the device error word that rows with
  * data-dependent failures raise: bit 0 = integer division by zero,
  * bit 1 = index out of range. Synchronises `stream`. */

@@ -282,4 +282,40 @@ int nert_hip_event_destroy(void* event) {
     return Guard([&] { nert_hip::Check(hipEventDestroy(static_cast<hipEvent_t>(event)), "hipEventDestroy"); });
 }
 
+int nert_hip_capture_begin(void) {
+    return Guard([&] {
+        nert_hip::Check(hipStreamBeginCapture(nert_hip::DefaultStream(), hipStreamCaptureModeThreadLocal),
+                        "hipStreamBeginCapture");
+    });
+}
+
+int nert_hip_capture_end(void** graph_exec) {
+    return Guard([&] {
+        *graph_exec = nullptr;
+        hipGraph_t graph = nullptr;
+        nert_hip::Check(hipStreamEndCapture(nert_hip::DefaultStream(), &graph), "hipStreamEndCapture");
+        hipGraphExec_t exec = nullptr;
+        const hipError_t status = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        nert_hip::Check(status, "hipGraphInstantiate");
+        *graph_exec = exec;
+    });
+}
+
+int nert_hip_graph_launch(void* graph_exec, void* stream) {
+    return Guard([&] {
+        nert_hip::Check(hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec), nert_hip::StreamOr(stream)),
+                        "hipGraphLaunch");
+    });
+}
+
+int nert_hip_graph_destroy(void* graph_exec) {
+    if (graph_exec == nullptr) {
+        return 0;
+    }
+    return Guard([&] {
+        nert_hip::Check(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)), "hipGraphExecDestroy");
+    });
+}
+
 } // extern "C"

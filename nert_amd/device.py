@@ -63,6 +63,9 @@ def lib() -> C.CDLL:
     L.nert_hip_matmul_f32.argtypes = [vp, vp, vp, i64, i64, i64, i32, vp, vp, vp, vp]
     L.nert_hip_conv_f32.argtypes = [vp, vp, vp, vp, vp, vp]
     L.nert_hip_unary.argtypes = [i32, i32, vp, vp, i64, C.c_double, C.c_double, vp]
+    L.nert_hip_capture_end.argtypes = [C.POINTER(C.c_void_p)]
+    L.nert_hip_graph_launch.argtypes = [vp, vp]
+    L.nert_hip_graph_destroy.argtypes = [vp]
     _lib = L
     return L
 

@@ -1,0 +1,182 @@
+"""Runs a Graph on the gfx950 layer with every tensor resident in HBM.
+
+Plays the role the reference executor plays for a device
+(src/executor.cpp:202-225 construct, :422-560 Execute): plan one arena for the
+intermediates, upload initializers once, then call each node's row through the
+seam's C form (nert_hip_run_node) in graph order. Two things differ, both
+MI355X-side choices: graph inputs are bound once and stay in HBM (the timed
+region never stages host data), and the whole node sequence can be captured
+into one HIP graph and replayed, which removes per-row host overhead.
+
+The arena plan is a first-fit over definition/last-use intervals with 256-byte
+alignment, so intermediates whose lifetimes do not overlap share memory and
+the working set stays small enough to live in the 256 MB Infinity Cache where
+possible.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from typing import Any, Iterable
+
+import numpy as np
+
+from . import abi
+from .device import DeviceArray, Event, NertError, check, lib
+from .graph import Graph
+
+ALIGN = 256
+
+
+def plan_arena(g: Graph) -> tuple[dict[str, int], int]:
+    """Offsets for every node output that is not a graph input/initializer."""
+    produced: dict[str, int] = {}
+    last_use: dict[str, int] = {}
+    for idx, n in enumerate(g.nodes):
+        for t in n.inputs:
+            if t:
+                last_use[t] = idx
+        for t in n.outputs:
+            produced.setdefault(t, idx)
+            last_use.setdefault(t, idx)
+    end = len(g.nodes)
+    for t in g.outputs:
+        last_use[t] = end
+    live: list[tuple[int, int, int]] = []  # (offset, size, last_use)
+    offsets: dict[str, int] = {}
+    arena = 0
+    for t, start in sorted(produced.items(), key=lambda kv: kv[1]):
+        dtype, shape = g.tensors[t]
+        size = max(1, int(np.prod(shape)) * np.dtype(dtype).itemsize)
+        size = (size + ALIGN - 1) // ALIGN * ALIGN
+        # Only tensors still live at this node's definition block memory; a
+        # node's inputs stay live through the node (inclusive intervals).
+        live = [e for e in live if e[2] >= start]
+        cursor = 0
+        for off, sz, _ in sorted(live):
+            if cursor + size <= off:
+                break
+            cursor = max(cursor, off + sz)
+        offsets[t] = cursor
+        live.append((cursor, size, last_use[t]))
+        arena = max(arena, cursor + size)
+    return offsets, arena
+
+
+class _PackedNode:
+    __slots__ = ("op", "name", "attrs", "ins", "outs", "err")
+
+    def __init__(self, op: str, name: str, attrs: abi.AttrPack, ins: abi.TensorPack, outs: abi.TensorPack):
+        self.op = op.encode()
+        self.name = name.encode()
+        self.attrs = attrs
+        self.ins = ins
+        self.outs = outs
+        self.err = C.create_string_buffer(1024)
+
+
+class Program:
+    def __init__(self, g: Graph):
+        self.graph = g
+        self.offsets, self.arena_bytes = plan_arena(g)
+        self.arena = DeviceArray((max(self.arena_bytes, 1),), np.uint8)
+        self.resident: dict[str, DeviceArray] = {}
+        for name, value in g.initializers.items():
+            self.resident[name] = DeviceArray.from_host(value)
+        for name in g.inputs:
+            dtype, shape = g.tensors[name]
+            self.resident[name] = DeviceArray(shape, dtype)
+        self.nodes = [self._pack(n) for n in g.nodes]
+        self.exec_graph = None
+        self._events: list[Event] = []
+
+    def ptr(self, name: str) -> int:
+        if name in self.resident:
+            return self.resident[name].ptr or 0
+        return (self.arena.ptr or 0) + self.offsets[name]
+
+    def _entry(self, name: str):
+        if not name:
+            return None
+        dtype, shape = self.graph.tensors[name]
+        return (self.ptr(name), abi.dtype_code(dtype), shape)
+
+    def _pack(self, n) -> _PackedNode:
+        return _PackedNode(n.op, n.name, abi.AttrPack(n.attrs), abi.TensorPack([self._entry(t) for t in n.inputs]),
+                           abi.TensorPack([self._entry(t) for t in n.outputs]))
+
+    def set_input(self, name: str, value: np.ndarray) -> None:
+        d = self.resident[name]
+        a = np.asarray(value, dtype=d.dtype, order="C")
+        if a.shape != d.shape:
+            raise ValueError(f"input {name}: shape {a.shape} != {d.shape}")
+        check(lib().nert_hip_memcpy_h2d(d.ptr, a.ctypes.data, d.nbytes), "h2d")
+
+    def output(self, name: str) -> np.ndarray:
+        dtype, shape = self.graph.tensors[name]
+        out = np.empty(shape, dtype)
+        if out.nbytes:
+            check(lib().nert_hip_memcpy_d2h(out.ctypes.data, self.ptr(name), out.nbytes), "d2h")
+        return out
+
+    def _call(self, p: _PackedNode) -> None:
+        rc = lib().nert_hip_run_node(p.op, p.name, 0, p.attrs.array, p.attrs.count, p.ins.array, p.ins.count,
+                                     p.outs.array, p.outs.count, p.err, len(p.err))
+        if rc != abi.OK:
+            raise NertError(rc, p.err.value.decode())
+
+    def run(self) -> None:
+        """Queues every node once (asynchronous; the layer stream orders it)."""
+        for p in self.nodes:
+            self._call(p)
+
+    def run_timed(self, ops: Iterable[str]) -> dict[int, float]:
+        """Runs once with HIP events around each node whose op is in `ops`;
+        returns {node index: milliseconds} measured on the layer stream."""
+        wanted = {o.encode() for o in ops}
+        marks: list[tuple[int, Event, Event]] = []
+        need = sum(1 for p in self.nodes if p.op in wanted)
+        while len(self._events) < 2 * need:
+            self._events.append(Event())
+        k = 0
+        for idx, p in enumerate(self.nodes):
+            if p.op in wanted:
+                e0, e1 = self._events[k], self._events[k + 1]
+                k += 2
+                e0.record()
+                self._call(p)
+                e1.record()
+                marks.append((idx, e0, e1))
+            else:
+                self._call(p)
+        return {idx: e0.elapsed_ms(e1) for idx, e0, e1 in marks}
+
+    def capture(self) -> None:
+        """Captures the node sequence into one HIP graph (after a warm run so
+        every workspace has reached its size)."""
+        self.run()
+        check(lib().nert_hip_stream_sync(None), "sync")
+        check(lib().nert_hip_capture_begin(), "capture begin")
+        try:
+            self.run()
+        finally:
+            handle = C.c_void_p()
+            rc = lib().nert_hip_capture_end(C.byref(handle))
+        check(rc, "capture end")
+        self.exec_graph = handle
+
+    def replay(self) -> None:
+        if self.exec_graph is None:
+            raise NertError(abi.OTHER_ERROR, "replay before capture")
+        check(lib().nert_hip_graph_launch(self.exec_graph, None), "graph launch")
+
+    def close(self) -> None:
+        if self.exec_graph is not None:
+            lib().nert_hip_graph_destroy(self.exec_graph)
+            self.exec_graph = None
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -39,8 +39,32 @@ def lib() -> C.CDLL:
                                          C.POINTER(abi.TensorDesc), C.POINTER(C.c_double), C.c_char_p, C.c_int]
         L.nert_ref_infer_shape.argtypes = [C.c_void_p, C.c_int, C.POINTER(abi.TensorDesc), C.c_char_p,
                                            C.POINTER(C.c_int64), C.POINTER(C.c_int), C.c_char_p, C.c_int]
+        L.nert_ref_load_graph.restype = C.c_void_p
+        L.nert_ref_load_graph.argtypes = [C.c_char_p, C.c_char_p, C.c_int]
+        L.nert_ref_free_graph.argtypes = [C.c_void_p]
         _lib = L
     return _lib
+
+
+class LoadedGraph:
+    """A nert::Graph loaded from an ONNX file by the reference loader."""
+
+    def __init__(self, path: str):
+        err = C.create_string_buffer(4096)
+        self.handle = lib().nert_ref_load_graph(str(path).encode(), err, len(err))
+        if not self.handle:
+            raise RefError(abi.OTHER_ERROR, err.value.decode())
+
+    def close(self) -> None:
+        if self.handle:
+            lib().nert_ref_free_graph(self.handle)
+            self.handle = None
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def has_row(op_type: str) -> bool:

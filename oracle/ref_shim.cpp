@@ -11,6 +11,7 @@
 #include "nert/device.hpp"
 #include "nert/executor.hpp"
 #include "nert/graph.hpp"
+#include "nert/model_loader.hpp"
 #include "nert/shapes.hpp"
 
 #include <chrono>
@@ -27,6 +28,19 @@ int nert_ref_run_node(const char* op_type, const char* name, int64_t schema_vers
     return nert_abi::RunNode(nert::CpuDevice(), op_type, name, schema_version, attrs, n_attrs, inputs, n_inputs,
                              outputs, n_outputs, err, err_len);
 }
+
+// Loads an ONNX file with the reference loader (src/model_loader.cpp:2278);
+// returns an owned nert::Graph* or null with the message in `err`.
+void* nert_ref_load_graph(const char* path, char* err, int err_len) {
+    try {
+        return new nert::Graph(nert::LoadGraphFromFile(path != nullptr ? path : ""));
+    } catch (const std::exception& e) {
+        nert_abi::CopyMessage(e.what(), err, err_len);
+        return nullptr;
+    }
+}
+
+void nert_ref_free_graph(void* graph) { delete static_cast<nert::Graph*>(graph); }
 
 // True (1) when the CPU table has a row for `op_type`.
 int nert_ref_has_row(const char* op_type) {

@@ -1,0 +1,96 @@
+"""GPU end-to-end: the seeded ResNet-18 on the gfx950 layer.
+
+Three ways to run the same ONNX model, all checked against the reference
+executor on CpuDevice (oracle/_ref):
+  * nert_amd.runner.Program, eager rows and HIP-graph replay (the bench path);
+  * the reference's own executor nert::Model on nert::HipDevice() -- the
+    drop-in: unchanged caller, new device (tests/cpp/dropin.cpp).
+Logits must agree within |d| <= 2e-4 * (1 + |ref|) (north_star: rel 2e-4
+end-to-end on logits). At the full batch of 32, per-image independence is
+the size-independent property: images 0-1 of the batch-32 run must match the
+oracle's batch-2 run of the same two images.
+"""
+
+import ctypes as C
+import os
+import tempfile
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from nert_amd import abi, graph, workloads
+from nert_amd.runner import Program
+from oracle import ref
+from rowcheck import compare
+
+pytestmark = pytest.mark.gpu
+
+ROOT = Path(__file__).resolve().parent.parent
+DROPIN = ROOT / "tests" / "_build" / "libnert_dropin.so"
+RTOL = 2e-4
+
+
+@pytest.fixture(scope="module")
+def resnet(gpu):
+    g, inputs = workloads.resnet18(batch=32)
+    tmp = tempfile.mkdtemp()
+    path = os.path.join(tmp, "resnet18.onnx")
+    Path(path).write_bytes(graph.to_onnx(g))
+    lg = ref.LoadedGraph(path)
+    x = inputs["input"]
+    want = np.zeros((2, 1000), np.float32)
+    ref.model_run(lg.handle, [np.ascontiguousarray(x[:2])], [want])
+    yield g, x, lg, want
+    lg.close()
+
+
+def _dropin_run(lg, x, runs=2):
+    L = C.CDLL(str(DROPIN))
+    L.dropin_model_run.argtypes = [C.c_void_p, C.c_int, C.POINTER(abi.TensorDesc), C.c_int,
+                                   C.POINTER(abi.TensorDesc), C.c_int, C.POINTER(C.c_double),
+                                   C.POINTER(C.c_int64), C.c_char_p, C.c_int]
+    out = np.zeros((x.shape[0], 1000), np.float32)
+    ip = abi.TensorPack(abi.host_entries([x]))
+    op = abi.TensorPack(abi.host_entries([out]))
+    secs, arena = C.c_double(), C.c_int64()
+    err = C.create_string_buffer(4096)
+    rc = L.dropin_model_run(lg.handle, 1, ip.array, 1, op.array, runs, C.byref(secs), C.byref(arena), err, len(err))
+    assert rc == abi.OK, err.value.decode()
+    return out, secs.value, arena.value
+
+
+def test_program_eager_and_graph_match_oracle(resnet):
+    g, x, lg, want = resnet
+    g2, _ = workloads.resnet18(batch=2)
+    prog = Program(g2)
+    prog.set_input("input", np.ascontiguousarray(x[:2]))
+    prog.run()
+    eager = prog.output("logits")
+    compare(eager, want, rtol=RTOL, atol=RTOL, what="eager logits")
+    prog.capture()
+    for _ in range(3):
+        prog.replay()
+    replayed = prog.output("logits")
+    assert np.array_equal(replayed, eager), "graph replay differs from eager rows"
+    prog.close()
+
+
+def test_batch32_images_match_oracle(resnet):
+    g, x, lg, want = resnet
+    prog = Program(g)
+    prog.set_input("input", x)
+    prog.capture()
+    prog.replay()
+    logits = prog.output("logits")
+    assert logits.shape == (32, 1000) and np.all(np.isfinite(logits))
+    compare(logits[:2], want, rtol=RTOL, atol=RTOL, what="bs32 images 0-1")
+    prog.close()
+
+
+def test_reference_executor_on_hipdevice(resnet):
+    """nert::Model(graph, dims, HipDevice()) -- the drop-in swap."""
+    g, x, lg, want = resnet
+    got, secs, arena = _dropin_run(lg, np.ascontiguousarray(x[:2]))
+    assert arena > 0
+    compare(got, want, rtol=RTOL, atol=RTOL, what="drop-in logits")
