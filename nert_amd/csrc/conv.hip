@@ -11,12 +11,46 @@
 // (src/kernels/conv.cpp:267-285). 1-D and 2-D convolutions arrive lifted to
 // three spatial axes with unit leading extents, as the reference lifts them
 // (src/kernels/conv.cpp:233-249).
+//
+// The gather is arranged so almost all index arithmetic is scalar: every
+// lane of a wave loads the same k row of the B tile (consecutive n across the
+// lanes), so the (c, kd, kh, kw) decode of k is wave-uniform and runs on the
+// SALU, with compile-time divisors for 1x1, 3x3 and 7x7 kernels and
+// multiply-shift division otherwise. Per gathered element a lane does two
+// adds, a bounds test and one load. Pointwise stride-1 unpadded convolutions
+// skip the gather and run as a batched GEMM on the same engine.
 
+#include "gemm_engine.hpp"
 #include "mfma_tile.hpp"
 #include "../../include/nert_hip.h"
 
 namespace nert_hip {
 namespace {
+
+// Unsigned division by a runtime divisor via multiply-high and shift
+// (Granlund & Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994): q = (umulhi(n, m) + n) >> s, exact for all
+// 32-bit n when evaluated in 64 bits.
+struct FastDiv {
+    uint32_t d;
+    uint32_t m;
+    uint32_t s;
+    static FastDiv Make(uint32_t d) {
+        FastDiv f{d, 0, 0};
+        if (d > 1) {
+            uint32_t l = 0;
+            while ((uint64_t{1} << l) < d) {
+                ++l;
+            }
+            f.s = l;
+            f.m = static_cast<uint32_t>(((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1);
+        }
+        return f;
+    }
+    __device__ __forceinline__ uint32_t Div(uint32_t n) const {
+        return static_cast<uint32_t>((static_cast<uint64_t>(__umulhi(n, m)) + n) >> s);
+    }
+};
 
 struct ConvArgs {
     const float* x;
@@ -34,30 +68,34 @@ struct ConvArgs {
     int64_t plane_out; // OD*OH*OW
     int64_t plane_in;  // ID*IH*IW
     int64_t n_total;   // batch * plane_out
+    FastDiv div_kvol, div_khw, div_kw;
     int64_t k_per_split;
     float* partial; // [splits][group][M_g][N] when split
 };
 
-// Gathers B(k, n) = X_col for one K tile. Thread t owns column nn = t % BN
-// for every pass, so the column decode (b, od, oh, ow) happens once per block.
-template <int BN, int BK, int THREADS, int PITCH>
+// Gathers B(k, n) = X_col for one K tile. Thread t owns column nn = t % BN for
+// every pass (the column decode happens once per block); rows are assigned
+// so that each wave's lanes share one k.
+template <int BN, int BK, int THREADS, int PITCH, int KH, int KW, bool CHECKED>
 struct ConvBLoader {
-    static_assert(THREADS % BN == 0, "threads must cover whole B rows");
+    static_assert(THREADS % BN == 0 && BN % 64 == 0, "a wave must cover part of one B row");
     static constexpr int kRowsPerPass = THREADS / BN;
     static constexpr int kPer = BK / kRowsPerPass;
     struct Stage {
         float v[kPer];
     };
     const ConvArgs* p;
-    const float* xb; // X at (b, g*C_g, 0, 0, 0)
-    int32_t id0, ih0, iw0; // od*s - pad for this thread's column
+    const float* xb;       // X at (b, g*C_g, 0, 0, 0) for this thread's column
+    int64_t col_off;       // (id0*IH + ih0)*IW + iw0, may be negative
+    int32_t id0, ih0, iw0; // window origin of this thread's output position
     bool col_ok;
-    int32_t kvol, khw;
+    int32_t kk0; // this wave's first row within a tile (wave-uniform)
     int64_t k_total;
 
-    __device__ void init(const ConvArgs& args, int64_t col0, int g) {
+    __device__ __forceinline__ void init(const ConvArgs& args, int64_t col0, int g) {
         p = &args;
         const int nn = threadIdx.x % BN;
+        kk0 = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(threadIdx.x / BN));
         const int64_t n = col0 + nn;
         col_ok = n < args.n_total;
         const int64_t nc = col_ok ? n : 0;
@@ -71,41 +109,53 @@ struct ConvBLoader {
         id0 = od * args.s_d - args.p_d;
         ih0 = oh * args.s_h - args.p_h;
         iw0 = ow * args.s_w - args.p_w;
+        col_off = (static_cast<int64_t>(id0) * args.in_h + ih0) * args.in_w + iw0;
         xb = args.x + (b * args.c + static_cast<int64_t>(g) * args.cg) * args.plane_in;
-        kvol = args.k_d * args.k_h * args.k_w;
-        khw = args.k_h * args.k_w;
     }
 
-    __device__ void load(int64_t k0, Stage& s) const {
-        const int kk0 = threadIdx.x / BN;
+    // Wave-uniform decode of k into the channel and the tap displacement.
+    __device__ __forceinline__ void Decode(int32_t k, int32_t& c, int32_t& dd, int32_t& dh, int32_t& dw) const {
+        int32_t kd = 0, kh, kw;
+        if constexpr (KH > 0) {
+            c = k / (KH * KW);
+            const int32_t r = k - c * (KH * KW);
+            kh = r / KW;
+            kw = r - kh * KW;
+        } else {
+            c = static_cast<int32_t>(p->div_kvol.Div(static_cast<uint32_t>(k)));
+            int32_t r = k - c * static_cast<int32_t>(p->div_kvol.d);
+            kd = static_cast<int32_t>(p->div_khw.Div(static_cast<uint32_t>(r)));
+            r -= kd * static_cast<int32_t>(p->div_khw.d);
+            kh = static_cast<int32_t>(p->div_kw.Div(static_cast<uint32_t>(r)));
+            kw = r - kh * static_cast<int32_t>(p->div_kw.d);
+        }
+        dd = kd * p->d_d;
+        dh = kh * p->d_h;
+        dw = kw * p->d_w;
+    }
+
+    // Padding taps read a clamped in-bounds address and select zero, so the
+    // gather has no branches and all of a thread's loads stay in flight.
+    __device__ __forceinline__ void load(int64_t k0, Stage& s) const {
 #pragma unroll
         for (int q = 0; q < kPer; ++q) {
-            const int64_t k = k0 + kk0 + q * kRowsPerPass;
-            float val = 0.f;
-            if (col_ok && k < k_total) {
-                const int32_t kc = static_cast<int32_t>(k);
-                const int32_t c = kc / kvol;
-                int32_t r = kc - c * kvol;
-                const int32_t kd = r / khw;
-                r -= kd * khw;
-                const int32_t kh = r / p->k_w;
-                const int32_t kw = r - kh * p->k_w;
-                const int32_t id = id0 + kd * p->d_d;
-                const int32_t ih = ih0 + kh * p->d_h;
-                const int32_t iw = iw0 + kw * p->d_w;
-                if (static_cast<uint32_t>(id) < static_cast<uint32_t>(p->in_d) &&
-                    static_cast<uint32_t>(ih) < static_cast<uint32_t>(p->in_h) &&
-                    static_cast<uint32_t>(iw) < static_cast<uint32_t>(p->in_w)) {
-                    val = xb[static_cast<int64_t>(c) * p->plane_in +
-                             (static_cast<int64_t>(id) * p->in_h + ih) * p->in_w + iw];
-                }
-            }
-            s.v[q] = val;
+            int64_t k = k0 + kk0 + q * kRowsPerPass; // wave-uniform
+            const bool k_ok = !CHECKED || k < k_total;
+            k = k_ok ? k : 0;
+            int32_t c, dd, dh, dw;
+            Decode(static_cast<int32_t>(k), c, dd, dh, dw);
+            const int64_t koff =
+                static_cast<int64_t>(c) * p->plane_in + (static_cast<int64_t>(dd) * p->in_h + dh) * p->in_w + dw;
+            const bool in = k_ok && (!CHECKED || col_ok) &&
+                            static_cast<uint32_t>(ih0 + dh) < static_cast<uint32_t>(p->in_h) &&
+                            static_cast<uint32_t>(iw0 + dw) < static_cast<uint32_t>(p->in_w) &&
+                            (KH > 0 || static_cast<uint32_t>(id0 + dd) < static_cast<uint32_t>(p->in_d));
+            const float v = xb[in ? col_off + koff : 0];
+            s.v[q] = in ? v : 0.f;
         }
     }
-    __device__ void store(const Stage& s, float* lds) const {
+    __device__ __forceinline__ void store(const Stage& s, float* lds) const {
         const int nn = threadIdx.x % BN;
-        const int kk0 = threadIdx.x / BN;
 #pragma unroll
         for (int q = 0; q < kPer; ++q) {
             lds[(kk0 + q * kRowsPerPass) * PITCH + nn] = s.v[q];
@@ -113,7 +163,7 @@ struct ConvBLoader {
     }
 };
 
-template <class Shape>
+template <class Shape, int KH, int KW>
 __global__ __launch_bounds__(Shape::kThreads) void ConvKernel(ConvArgs p) {
     __shared__ __attribute__((aligned(16))) float lds[2 * (Shape::kLdsA + Shape::kLdsB)];
     const int64_t tiles_m = (p.mg + Shape::kBM - 1) / Shape::kBM;
@@ -131,19 +181,36 @@ __global__ __launch_bounds__(Shape::kThreads) void ConvKernel(ConvArgs p) {
         k_end = p.kg;
     }
 
-    KContigLoader<Shape::kBM, Shape::kBK, Shape::kThreads, Shape::kPitchA> aload;
-    aload.base = p.w + (static_cast<int64_t>(g) * p.mg + row0) * p.kg;
-    aload.row_stride = p.kg;
-    aload.rows_left = p.mg - row0;
-    aload.k_total = k_end;
-    aload.vec_ok = (p.kg % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.w) & 15) == 0);
-
-    ConvBLoader<Shape::kBN, Shape::kBK, Shape::kThreads, Shape::kPitchB> bload;
-    bload.init(p, col0, g);
-    bload.k_total = k_end;
-
     Accum<Shape> acc;
-    MainLoop<Shape>(aload, bload, k_begin, k_end, lds, acc);
+    acc.zero();
+    const float* wg = p.w + (static_cast<int64_t>(g) * p.mg + row0) * p.kg;
+    // Interior tiles (full rows and columns, 16-byte aligned weight rows) run
+    // every full K tile unchecked; the rest, and the K remainder, run checked.
+    const bool interior = p.kg % 4 == 0 && ((reinterpret_cast<uintptr_t>(p.w) & 15) == 0) &&
+                          row0 + Shape::kBM <= p.mg && col0 + Shape::kBN <= p.n_total;
+    const int64_t k_full = interior ? k_begin + (k_end - k_begin) / Shape::kBK * Shape::kBK : k_begin;
+    if (k_full > k_begin) {
+        KContigLoader<Shape::kBM, Shape::kBK, Shape::kThreads, Shape::kPitchA, false> aload;
+        aload.base = wg;
+        aload.row_stride = p.kg;
+        aload.rows_left = p.mg - row0;
+        aload.k_total = k_full;
+        ConvBLoader<Shape::kBN, Shape::kBK, Shape::kThreads, Shape::kPitchB, KH, KW, false> bload;
+        bload.init(p, col0, g);
+        bload.k_total = k_full;
+        MainLoop<Shape>(aload, bload, k_begin, k_full, lds, acc);
+    }
+    if (k_full < k_end) {
+        KContigLoader<Shape::kBM, Shape::kBK, Shape::kThreads, Shape::kPitchA, true> aload;
+        aload.base = wg;
+        aload.row_stride = p.kg;
+        aload.rows_left = p.mg - row0;
+        aload.k_total = k_end;
+        ConvBLoader<Shape::kBN, Shape::kBK, Shape::kThreads, Shape::kPitchB, KH, KW, true> bload;
+        bload.init(p, col0, g);
+        bload.k_total = k_end;
+        MainLoop<Shape>(aload, bload, k_full, k_end, lds, acc);
+    }
 
     if (p.partial != nullptr) {
         float* out = p.partial + (static_cast<int64_t>(split) * p.group + g) * p.mg * p.n_total;
@@ -198,8 +265,10 @@ template <class Shape>
 void LaunchConv(ConvArgs p, hipStream_t stream) {
     const int64_t k_tiles = (p.kg + Shape::kBK - 1) / Shape::kBK;
     const int64_t tiles = ConvTiles<Shape>(p);
+    // Split K until there are at least two blocks per CU, keeping each split
+    // at least 8 K tiles deep.
     int splits = 1;
-    while (tiles * splits < 256 && k_tiles / (splits * 2) >= 8 && splits < 16) {
+    while (tiles * splits < 512 && k_tiles / (splits * 2) >= 8 && splits < 16) {
         splits *= 2;
     }
     p.k_per_split = ((k_tiles + splits - 1) / splits) * Shape::kBK;
@@ -210,13 +279,54 @@ void LaunchConv(ConvArgs p, hipStream_t stream) {
     }
     const int64_t tiles_mn = ((p.mg + Shape::kBM - 1) / Shape::kBM) * ((p.n_total + Shape::kBN - 1) / Shape::kBN);
     dim3 grid(static_cast<unsigned>(tiles_mn), static_cast<unsigned>(p.group), static_cast<unsigned>(splits));
-    ConvKernel<Shape><<<grid, Shape::kThreads, 0, stream>>>(p);
+    if (p.k_d == 1 && p.k_h == 3 && p.k_w == 3) {
+        ConvKernel<Shape, 3, 3><<<grid, Shape::kThreads, 0, stream>>>(p);
+    } else if (p.k_d == 1 && p.k_h == 1 && p.k_w == 1) {
+        ConvKernel<Shape, 1, 1><<<grid, Shape::kThreads, 0, stream>>>(p);
+    } else if (p.k_d == 1 && p.k_h == 7 && p.k_w == 7) {
+        ConvKernel<Shape, 7, 7><<<grid, Shape::kThreads, 0, stream>>>(p);
+    } else {
+        ConvKernel<Shape, 0, 0><<<grid, Shape::kThreads, 0, stream>>>(p);
+    }
     CheckLaunch("ConvKernel launch");
     if (splits > 1) {
         const int64_t total = p.group * p.mg * p.n_total;
         ConvSplitReduceKernel<<<GridFor(total, 256, 4096), 256, 0, stream>>>(p, splits);
         CheckLaunch("ConvSplitReduceKernel launch");
     }
+}
+
+// A 1x1, stride-1, unpadded, ungrouped convolution is Y[b] = W[M,C] * X[b][C,P]
+// with P = D*H*W: a batched GEMM whose B batches are the images.
+bool TryPointwise(const ConvArgs& p, hipStream_t stream) {
+    const bool unit = p.k_d == 1 && p.k_h == 1 && p.k_w == 1 && p.s_d == 1 && p.s_h == 1 && p.s_w == 1 &&
+                      p.p_d == 0 && p.p_h == 0 && p.p_w == 0 && p.group == 1 && p.plane_in == p.plane_out;
+    if (!unit || p.batch > 65535) {
+        return false;
+    }
+    GemmArgs g{};
+    g.a = p.w;
+    g.b = p.x;
+    g.y = p.y;
+    g.m = p.m;
+    g.n = p.plane_out;
+    g.k = p.c;
+    g.a_sm = p.c;
+    g.a_sk = 1;
+    g.b_sk = p.plane_in;
+    g.b_sn = 1;
+    g.alpha = 1.0f;
+    g.beta = 1.0f;
+    g.has_bias = p.bias != nullptr ? 1 : 0;
+    g.bias = p.bias;
+    g.bias_sm = 1;
+    g.bias_sn = 0;
+    g.batch_rank = 1;
+    g.bdims[0] = p.batch;
+    g.a_bs[0] = 0;
+    g.b_bs[0] = p.c * p.plane_in;
+    LaunchGemm(g, p.batch, stream);
+    return true;
 }
 
 } // namespace
@@ -264,16 +374,22 @@ extern "C" int nert_hip_conv_f32(const float* x, const float* w, const float* bi
         p.plane_out = static_cast<int64_t>(p.out_d) * p.out_h * p.out_w;
         p.plane_in = static_cast<int64_t>(p.in_d) * p.in_h * p.in_w;
         p.n_total = p.batch * p.plane_out;
-        if (p.kg >= (int64_t{1} << 31)) {
+        if (p.kg >= (int64_t{1} << 31) || p.plane_in * p.cg >= (int64_t{1} << 40)) {
             throw nert_hip::Error("conv: reduction length exceeds 2^31");
         }
+        p.div_kvol = nert_hip::FastDiv::Make(static_cast<uint32_t>(p.k_d * p.k_h * p.k_w));
+        p.div_khw = nert_hip::FastDiv::Make(static_cast<uint32_t>(p.k_h * p.k_w));
+        p.div_kw = nert_hip::FastDiv::Make(static_cast<uint32_t>(p.k_w));
         if (p.n_total == 0 || p.mg == 0) {
             return;
         }
         hipStream_t s = nert_hip::StreamOr(stream);
+        if (nert_hip::TryPointwise(p, s)) {
+            return;
+        }
         if (p.mg <= 32) {
             nert_hip::LaunchConv<nert_hip::ConvShapeS>(p, s);
-        } else if (p.mg <= 64 || nert_hip::ConvTiles<nert_hip::ConvShapeL>(p) < 256) {
+        } else if (p.mg <= 64) {
             nert_hip::LaunchConv<nert_hip::ConvShapeM>(p, s);
         } else {
             nert_hip::LaunchConv<nert_hip::ConvShapeL>(p, s);

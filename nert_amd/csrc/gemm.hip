@@ -8,30 +8,34 @@
 // K into a workspace and summed by a second kernel in a fixed order, so the
 // result does not depend on scheduling.
 
+#include "gemm_engine.hpp"
 #include "mfma_tile.hpp"
 #include "../../include/nert_hip.h"
 
 namespace nert_hip {
 namespace {
 
-struct GemmArgs {
-    const float* a;
-    const float* b;
-    float* y;
-    const float* bias;
-    int64_t m, n, k;
-    int64_t a_sm, a_sk; // A(m,k) = a[m*a_sm + k*a_sk]
-    int64_t b_sk, b_sn; // B(k,n) = b[k*b_sk + n*b_sn]
-    int64_t bias_sm, bias_sn;
-    float alpha, beta;
-    int has_bias;
-    int batch_rank;
-    int64_t bdims[4];
-    int64_t a_bs[4];
-    int64_t b_bs[4];
-    int64_t k_per_split; // multiple of BK
-    float* partial;      // [splits][batch][m][n] when split
-};
+// Builds the loader of one operand. `row_stride`/`k_stride` are the element
+// strides of the operand's non-K and K index; K_CONTIG selects which is 1.
+template <int ROWS, int BK, int THREADS, int PITCH, bool K_CONTIG, bool CHECKED>
+__device__ __forceinline__ auto MakeOperand(const float* base, int64_t row0, int64_t row_stride, int64_t k_stride,
+                                            int64_t rows, int64_t k_total) {
+    if constexpr (K_CONTIG) {
+        KContigLoader<ROWS, BK, THREADS, PITCH, CHECKED> l;
+        l.base = base + row0 * row_stride;
+        l.row_stride = row_stride;
+        l.rows_left = rows - row0;
+        l.k_total = k_total;
+        return l;
+    } else {
+        RowContigLoader<ROWS, BK, THREADS, PITCH, CHECKED> l;
+        l.base = base + row0;
+        l.k_stride = k_stride;
+        l.rows_left = rows - row0;
+        l.k_total = k_total;
+        return l;
+    }
+}
 
 template <class Shape, bool A_KCONTIG, bool B_NCONTIG>
 __global__ __launch_bounds__(Shape::kThreads) void GemmKernel(GemmArgs p) {
@@ -64,39 +68,28 @@ __global__ __launch_bounds__(Shape::kThreads) void GemmKernel(GemmArgs p) {
         k_end = p.k;
     }
 
-    using ALoad = typename std::conditional<A_KCONTIG, KContigLoader<Shape::kBM, Shape::kBK, Shape::kThreads, Shape::kPitchA>,
-                                            RowContigLoader<Shape::kBM, Shape::kBK, Shape::kThreads, Shape::kPitchA>>::type;
-    using BLoad = typename std::conditional<B_NCONTIG, RowContigLoader<Shape::kBN, Shape::kBK, Shape::kThreads, Shape::kPitchB>,
-                                            KContigLoader<Shape::kBN, Shape::kBK, Shape::kThreads, Shape::kPitchB>>::type;
-    ALoad aload;
-    BLoad bload;
-    if constexpr (A_KCONTIG) {
-        aload.base = a + row0 * p.a_sm;
-        aload.row_stride = p.a_sm;
-        aload.vec_ok = (p.a_sm % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.a) & 15) == 0) && (a_off % 4 == 0);
-    } else {
-        aload.base = a + row0;
-        aload.k_stride = p.a_sk;
-        aload.vec_ok = (p.a_sk % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.a) & 15) == 0) && (a_off % 4 == 0) &&
-                       (row0 % 4 == 0);
-    }
-    aload.rows_left = p.m - row0;
-    aload.k_total = k_end;
-    if constexpr (B_NCONTIG) {
-        bload.base = b + col0;
-        bload.k_stride = p.b_sk;
-        bload.vec_ok = (p.b_sk % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.b) & 15) == 0) && (b_off % 4 == 0) &&
-                       (col0 % 4 == 0);
-    } else {
-        bload.base = b + col0 * p.b_sn;
-        bload.row_stride = p.b_sn;
-        bload.vec_ok = (p.b_sn % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.b) & 15) == 0) && (b_off % 4 == 0);
-    }
-    bload.rows_left = p.n - col0;
-    bload.k_total = k_end;
-
     Accum<Shape> acc;
-    MainLoop<Shape>(aload, bload, k_begin, k_end, lds, acc);
+    acc.zero();
+    // Interior tiles with 16-byte aligned rows take unchecked float4 loads for
+    // every full K tile; edge tiles and the K remainder use the checked form.
+    const bool a_vec = (A_KCONTIG ? p.a_sm : p.a_sk) % 4 == 0 && ((reinterpret_cast<uintptr_t>(a) & 15) == 0);
+    const bool b_vec = (B_NCONTIG ? p.b_sk : p.b_sn) % 4 == 0 && ((reinterpret_cast<uintptr_t>(b) & 15) == 0);
+    const bool interior = a_vec && b_vec && row0 + Shape::kBM <= p.m && col0 + Shape::kBN <= p.n;
+    const int64_t k_full = interior ? k_begin + (k_end - k_begin) / Shape::kBK * Shape::kBK : k_begin;
+    if (k_full > k_begin) {
+        const auto aload = MakeOperand<Shape::kBM, Shape::kBK, Shape::kThreads, Shape::kPitchA, A_KCONTIG, false>(
+            a, row0, p.a_sm, p.a_sk, p.m, k_full);
+        const auto bload = MakeOperand<Shape::kBN, Shape::kBK, Shape::kThreads, Shape::kPitchB, !B_NCONTIG, false>(
+            b, col0, p.b_sn, p.b_sk, p.n, k_full);
+        MainLoop<Shape>(aload, bload, k_begin, k_full, lds, acc);
+    }
+    if (k_full < k_end) {
+        const auto aload = MakeOperand<Shape::kBM, Shape::kBK, Shape::kThreads, Shape::kPitchA, A_KCONTIG, true>(
+            a, row0, p.a_sm, p.a_sk, p.m, k_end);
+        const auto bload = MakeOperand<Shape::kBN, Shape::kBK, Shape::kThreads, Shape::kPitchB, !B_NCONTIG, true>(
+            b, col0, p.b_sn, p.b_sk, p.n, k_end);
+        MainLoop<Shape>(aload, bload, k_full, k_end, lds, acc);
+    }
 
     const int64_t plane = p.m * p.n;
     if (p.partial != nullptr) {
@@ -175,7 +168,9 @@ int64_t TileCount(const GemmArgs& p, int64_t batches) {
     return ((p.m + Shape::kBM - 1) / Shape::kBM) * ((p.n + Shape::kBN - 1) / Shape::kBN) * batches;
 }
 
-void Launch(GemmArgs p, int64_t batches, hipStream_t stream) {
+} // namespace
+
+void LaunchGemm(GemmArgs p, int64_t batches, hipStream_t stream) {
     if (p.m == 0 || p.n == 0 || batches == 0) {
         return;
     }
@@ -227,7 +222,6 @@ void Launch(GemmArgs p, int64_t batches, hipStream_t stream) {
     }
 }
 
-} // namespace
 } // namespace nert_hip
 
 extern "C" {
@@ -254,7 +248,7 @@ int nert_hip_gemm_f32(const float* a, const float* b, const float* c, float* y, 
         p.bias_sm = c_rank == 2 ? n : 0;
         p.bias_sn = 1;
         p.batch_rank = 0;
-        nert_hip::Launch(p, 1, nert_hip::StreamOr(stream));
+        nert_hip::LaunchGemm(p, 1, nert_hip::StreamOr(stream));
     });
 }
 
@@ -290,7 +284,7 @@ int nert_hip_matmul_f32(const float* a, const float* b, float* y, int64_t m, int
         if (batches > 65535) {
             throw nert_hip::Error("matmul: more than 65535 batches");
         }
-        nert_hip::Launch(p, batches, nert_hip::StreamOr(stream));
+        nert_hip::LaunchGemm(p, batches, nert_hip::StreamOr(stream));
     });
 }
 

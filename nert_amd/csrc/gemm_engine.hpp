@@ -1,0 +1,31 @@
+#pragma once
+// Internal launch interface of the MFMA GEMM engine (gemm.hip), shared by the
+// rows that reduce to a plain or batched GEMM (Gemm, MatMul, pointwise Conv).
+
+#include "common.hpp"
+
+namespace nert_hip {
+
+// Y[b](m, n) = alpha * sum_k A[b](m, k) * B[b](k, n) + beta * bias(m, n)
+struct GemmArgs {
+    const float* a;
+    const float* b;
+    float* y;
+    const float* bias;
+    int64_t m, n, k;
+    int64_t a_sm, a_sk; // A(m,k) = a[m*a_sm + k*a_sk]; one of the two is 1
+    int64_t b_sk, b_sn; // B(k,n) = b[k*b_sk + n*b_sn]; one of the two is 1
+    int64_t bias_sm, bias_sn; // bias(m,n) = bias[m*bias_sm + n*bias_sn]
+    float alpha, beta;
+    int has_bias;
+    int batch_rank; // up to 4 broadcast batch axes; Y batches are dense (m*n apart)
+    int64_t bdims[4];
+    int64_t a_bs[4];
+    int64_t b_bs[4];
+    int64_t k_per_split; // set by LaunchGemm
+    float* partial;      // set by LaunchGemm
+};
+
+void LaunchGemm(GemmArgs p, int64_t batches, hipStream_t stream);
+
+} // namespace nert_hip

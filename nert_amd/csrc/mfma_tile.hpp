@@ -94,23 +94,29 @@ __device__ __forceinline__ void MmaTile(const float* __restrict__ as, const floa
     }
 }
 
-// The K loop: ALoader/BLoader stage K tiles [k_begin, k_end) through LDS.
+// The K loop: ALoader/BLoader stage K tiles [k_begin, k_end) through LDS and
+// accumulate into `acc` (the caller zeroes it once, so a block may run an
+// unchecked interior loop and a checked tail loop into the same registers).
 // Loader interface:
 //   typename Stage;                       registers for one thread's share
 //   void load(int64_t k0, Stage&)         global -> registers (zero-padded)
 //   void store(const Stage&, float* lds)  registers -> k-major LDS tile
 template <class Shape, class ALoader, class BLoader>
-__device__ __forceinline__ void MainLoop(ALoader& aload, BLoader& bload, int64_t k_begin, int64_t k_end,
+__device__ __forceinline__ void MainLoop(const ALoader& aload, const BLoader& bload, int64_t k_begin, int64_t k_end,
                                          float* lds, Accum<Shape>& acc) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wave_m = wave % Shape::kWavesM;
     const int wave_n = wave / Shape::kWavesM;
-    float* as[2] = {lds, lds + Shape::kLdsA + Shape::kLdsB};
-    float* bs[2] = {lds + Shape::kLdsA, lds + 2 * Shape::kLdsA + Shape::kLdsB};
+    // Both LDS buffers sit at compile-time offsets from the shared array and
+    // the tile loop is unrolled by two, so every LDS access keeps the LDS
+    // address space (ds_read/ds_write) instead of decaying to flat accesses.
+    float* const a0 = lds;
+    float* const b0 = lds + Shape::kLdsA;
+    float* const a1 = lds + Shape::kLdsA + Shape::kLdsB;
+    float* const b1 = lds + 2 * Shape::kLdsA + Shape::kLdsB;
 
-    acc.zero();
     if (k_begin >= k_end) {
         return;
     }
@@ -118,23 +124,41 @@ __device__ __forceinline__ void MainLoop(ALoader& aload, BLoader& bload, int64_t
     typename BLoader::Stage sb;
     aload.load(k_begin, sa);
     bload.load(k_begin, sb);
-    aload.store(sa, as[0]);
-    bload.store(sb, bs[0]);
+    aload.store(sa, a0);
+    bload.store(sb, b0);
     __syncthreads();
-    int cur = 0;
-    for (int64_t k0 = k_begin; k0 < k_end; k0 += Shape::kBK) {
-        const bool more = k0 + Shape::kBK < k_end;
+    int64_t k0 = k_begin;
+    while (true) {
+        bool more = k0 + Shape::kBK < k_end;
         if (more) {
             aload.load(k0 + Shape::kBK, sa);
             bload.load(k0 + Shape::kBK, sb);
         }
-        MmaTile<Shape>(as[cur], bs[cur], acc, wave_m, wave_n, lane);
+        MmaTile<Shape>(a0, b0, acc, wave_m, wave_n, lane);
         if (more) {
-            aload.store(sa, as[cur ^ 1]);
-            bload.store(sb, bs[cur ^ 1]);
+            aload.store(sa, a1);
+            bload.store(sb, b1);
         }
         __syncthreads();
-        cur ^= 1;
+        if (!more) {
+            break;
+        }
+        k0 += Shape::kBK;
+        more = k0 + Shape::kBK < k_end;
+        if (more) {
+            aload.load(k0 + Shape::kBK, sa);
+            bload.load(k0 + Shape::kBK, sb);
+        }
+        MmaTile<Shape>(a1, b1, acc, wave_m, wave_n, lane);
+        if (more) {
+            aload.store(sa, a0);
+            bload.store(sb, b0);
+        }
+        __syncthreads();
+        if (!more) {
+            break;
+        }
+        k0 += Shape::kBK;
     }
 }
 
@@ -163,18 +187,22 @@ __device__ __forceinline__ void ForEachAccum(const Accum<Shape>& acc, F&& fn) {
 }
 
 // ---------------------------------------------------------------------------
-// Strided operand loaders (Gemm / MatMul).
+// Strided operand loaders (Gemm / MatMul / the weight side of Conv).
 //
-// A(m, k) = a[m * sm + k * sk]; exactly one of sm, sk is 1 in practice
-// (row-major A or transposed A). B(k, n) = b[k * sk + n * sn].
-// "Row" = the operand's non-K index (m for A, n for B).
+// A(m, k) = a[m * sm + k * sk]; exactly one of sm, sk is 1 (row-major or
+// transposed A). B(k, n) = b[k * sk + n * sn]. "Row" = the operand's non-K
+// index (m for A, n for B). CHECKED = false is the interior-tile form: every
+// element is in range and 16-byte aligned, so loads are unconditional float4
+// and the compiler can keep them all in flight. CHECKED = true guards rows and
+// k with a clamped address and a select instead of a branch, so edge tiles do
+// not serialise their loads either.
 // ---------------------------------------------------------------------------
 
-// Loader for an operand whose K index is contiguous in memory (A row-major,
-// or B transposed). Each thread loads runs of 4 consecutive k for one row.
-template <int ROWS, int BK, int THREADS, int PITCH>
+// Operand whose K index is contiguous in memory (A row-major, B transposed):
+// each thread loads runs of 4 consecutive k of one row.
+template <int ROWS, int BK, int THREADS, int PITCH, bool CHECKED>
 struct KContigLoader {
-    static constexpr int kQuads = ROWS * BK / 4;             // float4 groups per tile
+    static constexpr int kQuads = ROWS * BK / 4;
     static constexpr int kPer = (kQuads + THREADS - 1) / THREADS;
     struct Stage {
         float v[kPer][4];
@@ -183,9 +211,8 @@ struct KContigLoader {
     int64_t row_stride;
     int64_t rows_left; // valid rows in this tile (<= ROWS)
     int64_t k_total;
-    bool vec_ok; // row_stride % 4 == 0 and base 16-byte aligned
 
-    __device__ void load(int64_t k0, Stage& s) const {
+    __device__ __forceinline__ void load(int64_t k0, Stage& s) const {
         const int tid = threadIdx.x;
 #pragma unroll
         for (int p = 0; p < kPer; ++p) {
@@ -193,30 +220,33 @@ struct KContigLoader {
             const int row = q / (BK / 4);
             const int kq = (q % (BK / 4)) * 4;
             const int64_t k = k0 + kq;
-            float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (q < kQuads && row < rows_left) {
-                const float* src = base + row * row_stride + k;
-                if (vec_ok && k + 3 < k_total) {
-                    val = *reinterpret_cast<const float4*>(src);
-                } else {
-                    val.x = k + 0 < k_total ? src[0] : 0.f;
-                    val.y = k + 1 < k_total ? src[1] : 0.f;
-                    val.z = k + 2 < k_total ? src[2] : 0.f;
-                    val.w = k + 3 < k_total ? src[3] : 0.f;
+            if constexpr (!CHECKED) {
+                if (kQuads % THREADS != 0 && q >= kQuads) {
+                    continue; // this thread owns no quad in this pass
+                }
+                const nert_floatx4 val = *reinterpret_cast<const nert_floatx4*>(base + row * row_stride + k);
+                s.v[p][0] = val[0];
+                s.v[p][1] = val[1];
+                s.v[p][2] = val[2];
+                s.v[p][3] = val[3];
+            } else {
+                const bool row_ok = q < kQuads && row < rows_left;
+                const int64_t row_off = row_ok ? row * row_stride : 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bool ok = row_ok && k + e < k_total;
+                    const float v = base[ok ? row_off + k + e : 0];
+                    s.v[p][e] = ok ? v : 0.f;
                 }
             }
-            s.v[p][0] = val.x;
-            s.v[p][1] = val.y;
-            s.v[p][2] = val.z;
-            s.v[p][3] = val.w;
         }
     }
-    __device__ void store(const Stage& s, float* lds) const {
+    __device__ __forceinline__ void store(const Stage& s, float* lds) const {
         const int tid = threadIdx.x;
 #pragma unroll
         for (int p = 0; p < kPer; ++p) {
             const int q = tid + p * THREADS;
-            if (q < kQuads) {
+            if (kQuads % THREADS == 0 || q < kQuads) {
                 const int row = q / (BK / 4);
                 const int kq = (q % (BK / 4)) * 4;
 #pragma unroll
@@ -228,22 +258,21 @@ struct KContigLoader {
     }
 };
 
-// Loader for an operand whose row index is contiguous (A transposed, or B
-// row-major). Each thread loads runs of 4 consecutive rows at one k.
-template <int ROWS, int BK, int THREADS, int PITCH>
+// Operand whose row index is contiguous (A transposed, B row-major): each
+// thread loads runs of 4 consecutive rows at one k.
+template <int ROWS, int BK, int THREADS, int PITCH, bool CHECKED>
 struct RowContigLoader {
     static constexpr int kQuads = ROWS * BK / 4;
     static constexpr int kPer = (kQuads + THREADS - 1) / THREADS;
     struct Stage {
-        float4 v[kPer];
+        nert_floatx4 v[kPer]; // native vectors: HIP's float4 class defeats register promotion
     };
     const float* base; // &op(row0, 0)
     int64_t k_stride;
     int64_t rows_left;
     int64_t k_total;
-    bool vec_ok; // k_stride % 4 == 0 and base 16-byte aligned
 
-    __device__ void load(int64_t k0, Stage& s) const {
+    __device__ __forceinline__ void load(int64_t k0, Stage& s) const {
         const int tid = threadIdx.x;
 #pragma unroll
         for (int p = 0; p < kPer; ++p) {
@@ -251,30 +280,34 @@ struct RowContigLoader {
             const int kk = q / (ROWS / 4);
             const int row = (q % (ROWS / 4)) * 4;
             const int64_t k = k0 + kk;
-            float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (q < kQuads && k < k_total) {
-                const float* src = base + k * k_stride + row;
-                if (vec_ok && row + 3 < rows_left) {
-                    val = *reinterpret_cast<const float4*>(src);
-                } else {
-                    val.x = row + 0 < rows_left ? src[0] : 0.f;
-                    val.y = row + 1 < rows_left ? src[1] : 0.f;
-                    val.z = row + 2 < rows_left ? src[2] : 0.f;
-                    val.w = row + 3 < rows_left ? src[3] : 0.f;
+            if constexpr (!CHECKED) {
+                if (kQuads % THREADS != 0 && q >= kQuads) {
+                    continue; // this thread owns no quad in this pass
                 }
+                s.v[p] = *reinterpret_cast<const nert_floatx4*>(base + k * k_stride + row);
+            } else {
+                const bool k_ok = q < kQuads && k < k_total;
+                const int64_t k_off = k_ok ? k * k_stride : 0;
+                float e4[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bool ok = k_ok && row + e < rows_left;
+                    const float v = base[ok ? k_off + row + e : 0];
+                    e4[e] = ok ? v : 0.f;
+                }
+                s.v[p] = nert_floatx4{e4[0], e4[1], e4[2], e4[3]};
             }
-            s.v[p] = val;
         }
     }
-    __device__ void store(const Stage& s, float* lds) const {
+    __device__ __forceinline__ void store(const Stage& s, float* lds) const {
         const int tid = threadIdx.x;
 #pragma unroll
         for (int p = 0; p < kPer; ++p) {
             const int q = tid + p * THREADS;
-            if (q < kQuads) {
+            if (kQuads % THREADS == 0 || q < kQuads) {
                 const int kk = q / (ROWS / 4);
                 const int row = (q % (ROWS / 4)) * 4;
-                *reinterpret_cast<float4*>(lds + kk * PITCH + row) = s.v[p];
+                *reinterpret_cast<nert_floatx4*>(lds + kk * PITCH + row) = s.v[p];
             }
         }
     }
