@@ -61,6 +61,22 @@ inline unsigned GridFor(int64_t work, int per_block, int64_t cap = 1 << 20) {
     return static_cast<unsigned>(blocks);
 }
 
+// Number of K splits for a tiled GEMM-shaped launch. The grid should fill
+// the blocks the chip holds at once (`resident`, e.g. 256 CUs x 2) without
+// spilling into a second, partly empty round; each split keeps at least
+// `min_k_tiles` K tiles so the pipeline prologue stays amortised.
+inline int PlanSplits(int64_t tiles, int64_t k_tiles, int64_t resident, int64_t min_k_tiles, int max_splits = 16) {
+    int splits = 1;
+    while (splits < max_splits && tiles * splits * 2 <= resident && k_tiles >= min_k_tiles * splits * 2) {
+        splits *= 2;
+    }
+    return splits;
+}
+
+// Blocks of one 256-thread MFMA tile kernel the chip keeps resident
+// (256 CUs, two such blocks per CU at the engine's register use).
+constexpr int64_t kResidentBlocks = 512;
+
 // Runs `body` and converts exceptions into a C status code.
 template <typename F>
 int Guard(F&& body) {

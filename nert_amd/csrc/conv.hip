@@ -236,25 +236,40 @@ __global__ __launch_bounds__(Shape::kThreads) void ConvKernel(ConvArgs p) {
     });
 }
 
-__global__ void ConvSplitReduceKernel(ConvArgs p, int splits) {
+// Sums the split-K partials in split order (deterministic) and applies the
+// bias, four outputs per thread when an image plane holds whole quads.
+__global__ void ConvSplitReduceKernel(ConvArgs p, int splits, int vec) {
     const int64_t per_split = p.group * p.mg * p.n_total;
-    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < per_split;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        float sum = 0.f;
-        for (int s = 0; s < splits; ++s) {
-            sum += p.partial[s * per_split + i];
-        }
+    const int64_t quads = per_split / vec;
+    for (int64_t q = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; q < quads;
+         q += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t i = q * vec;
         const int64_t gc = i % p.n_total;
         const int64_t oc = i / p.n_total; // g * mg + m
         const int64_t b = gc / p.plane_out;
         const int64_t pix = gc - b * p.plane_out;
-        p.y[(b * p.m + oc) * p.plane_out + pix] = p.bias != nullptr ? sum + p.bias[oc] : sum;
+        const float bias = p.bias != nullptr ? p.bias[oc] : 0.f;
+        float* out = p.y + (b * p.m + oc) * p.plane_out + pix;
+        if (vec == 4) {
+            nert_floatx4 sum = *reinterpret_cast<const nert_floatx4*>(p.partial + i);
+            for (int s = 1; s < splits; ++s) {
+                sum += *reinterpret_cast<const nert_floatx4*>(p.partial + s * per_split + i);
+            }
+            sum += bias;
+            *reinterpret_cast<nert_floatx4*>(out) = sum;
+        } else {
+            float sum = p.partial[i];
+            for (int s = 1; s < splits; ++s) {
+                sum += p.partial[s * per_split + i];
+            }
+            *out = sum + bias;
+        }
     }
 }
 
-using ConvShapeL = TileShape<128, 128, 16, 2, 2>;
-using ConvShapeM = TileShape<64, 128, 16, 2, 2>;
-using ConvShapeS = TileShape<32, 128, 16, 1, 4>;
+using ConvShapeL = TileShape<128, 128, 16, 2, 2>; // 4 waves, 64x64 each
+using ConvShapeW = TileShape<64, 256, 16, 1, 4>;  // 4 waves, 64x64 each, for M_g <= 64
+using ConvShapeS = TileShape<32, 128, 16, 1, 4>;  // 4 waves, 32x32 each, for M_g <= 32
 
 template <class Shape>
 int64_t ConvTiles(const ConvArgs& p) {
@@ -265,12 +280,7 @@ template <class Shape>
 void LaunchConv(ConvArgs p, hipStream_t stream) {
     const int64_t k_tiles = (p.kg + Shape::kBK - 1) / Shape::kBK;
     const int64_t tiles = ConvTiles<Shape>(p);
-    // Split K until there are at least two blocks per CU, keeping each split
-    // at least 8 K tiles deep.
-    int splits = 1;
-    while (tiles * splits < 512 && k_tiles / (splits * 2) >= 8 && splits < 16) {
-        splits *= 2;
-    }
+    const int splits = PlanSplits(tiles, k_tiles, kResidentBlocks, 8);
     p.k_per_split = ((k_tiles + splits - 1) / splits) * Shape::kBK;
     p.partial = nullptr;
     if (splits > 1) {
@@ -290,8 +300,9 @@ void LaunchConv(ConvArgs p, hipStream_t stream) {
     }
     CheckLaunch("ConvKernel launch");
     if (splits > 1) {
-        const int64_t total = p.group * p.mg * p.n_total;
-        ConvSplitReduceKernel<<<GridFor(total, 256, 4096), 256, 0, stream>>>(p, splits);
+        const int vec = (p.plane_out % 4 == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0) ? 4 : 1;
+        const int64_t work = p.group * p.mg * p.n_total / vec;
+        ConvSplitReduceKernel<<<GridFor(work, 256, 8192), 256, 0, stream>>>(p, splits, vec);
         CheckLaunch("ConvSplitReduceKernel launch");
     }
 }
@@ -390,7 +401,7 @@ extern "C" int nert_hip_conv_f32(const float* x, const float* w, const float* bi
         if (p.mg <= 32) {
             nert_hip::LaunchConv<nert_hip::ConvShapeS>(p, s);
         } else if (p.mg <= 64) {
-            nert_hip::LaunchConv<nert_hip::ConvShapeM>(p, s);
+            nert_hip::LaunchConv<nert_hip::ConvShapeW>(p, s);
         } else {
             nert_hip::LaunchConv<nert_hip::ConvShapeL>(p, s);
         }

@@ -117,29 +117,34 @@ __global__ __launch_bounds__(Shape::kThreads) void GemmKernel(GemmArgs p) {
     });
 }
 
-// Sums the split-K partials in split order and applies the epilogue.
-__global__ void SplitReduceKernel(GemmArgs p, int splits, int64_t batches) {
+// Sums the split-K partials in split order (deterministic) and applies the
+// epilogue, four outputs per thread when rows hold whole quads.
+__global__ void SplitReduceKernel(GemmArgs p, int splits, int64_t batches, int vec) {
     const int64_t plane = p.m * p.n;
     const int64_t total = plane * batches;
-    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        float sum = 0.f;
-        for (int s = 0; s < splits; ++s) {
-            sum += p.partial[s * total + i];
-        }
+    const int64_t quads = total / vec;
+    for (int64_t q = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; q < quads;
+         q += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t i = q * vec;
         const int64_t e = i % plane;
         const int64_t r = e / p.n;
         const int64_t c = e % p.n;
-        float value = p.alpha * sum;
-        if (p.has_bias) {
-            value += p.beta * p.bias[r * p.bias_sm + c * p.bias_sn];
+        for (int v = 0; v < vec; ++v) {
+            float sum = p.partial[i + v];
+            for (int s = 1; s < splits; ++s) {
+                sum += p.partial[s * total + i + v];
+            }
+            float value = p.alpha * sum;
+            if (p.has_bias) {
+                value += p.beta * p.bias[r * p.bias_sm + (c + v) * p.bias_sn];
+            }
+            p.y[i + v] = value;
         }
-        p.y[i] = value;
     }
 }
 
 using ShapeL = TileShape<128, 128, 16, 2, 2>; // 4 waves, 64x64 per wave
-using ShapeM = TileShape<64, 64, 16, 2, 2>;   // 4 waves, 32x32 per wave
+using ShapeW = TileShape<64, 256, 16, 1, 4>;  // 4 waves, 64x64 per wave, for M <= 64
 using ShapeS = TileShape<32, 64, 32, 1, 2>;   // 2 waves, skinny M
 
 template <class Shape>
@@ -161,8 +166,6 @@ void LaunchShape(GemmArgs p, int64_t batches, int splits, hipStream_t stream) {
     CheckLaunch("GemmKernel launch");
 }
 
-constexpr int64_t kTargetBlocks = 512; // two blocks per CU on 256 CUs
-
 template <class Shape>
 int64_t TileCount(const GemmArgs& p, int64_t batches) {
     return ((p.m + Shape::kBM - 1) / Shape::kBM) * ((p.n + Shape::kBN - 1) / Shape::kBN) * batches;
@@ -178,23 +181,18 @@ void LaunchGemm(GemmArgs p, int64_t batches, hipStream_t stream) {
     if (!(p.a_sk == 1 || p.a_sm == 1) || !(p.b_sn == 1 || p.b_sk == 1)) {
         throw Error("gemm: operands must be contiguous in one index");
     }
-    int shape = 0; // 0 = L, 1 = M, 2 = S
+    int shape = 0; // 0 = L, 1 = W, 2 = S
     int64_t tiles = TileCount<ShapeL>(p, batches);
     if (p.m <= 32) {
         shape = 2;
         tiles = TileCount<ShapeS>(p, batches);
-    } else if (tiles < kTargetBlocks / 2) {
+    } else if (p.m <= 64) {
         shape = 1;
-        tiles = TileCount<ShapeM>(p, batches);
+        tiles = TileCount<ShapeW>(p, batches);
     }
     const int bk = shape == 2 ? ShapeS::kBK : ShapeL::kBK;
-    // Split K while the grid is under one block per CU and each split keeps
-    // at least 8 K tiles of work.
-    int splits = 1;
     const int64_t k_tiles = (p.k + bk - 1) / bk;
-    while (tiles * splits < 256 && k_tiles / (splits * 2) >= 8 && splits < 32) {
-        splits *= 2;
-    }
+    int splits = PlanSplits(tiles, k_tiles, kResidentBlocks, 8, 32);
     p.k_per_split = ((k_tiles + splits - 1) / splits) * bk;
     if (p.k == 0) {
         p.k_per_split = 0;
@@ -209,15 +207,16 @@ void LaunchGemm(GemmArgs p, int64_t batches, hipStream_t stream) {
         LaunchShape<ShapeL>(p, batches, splits, stream);
         break;
     case 1:
-        LaunchShape<ShapeM>(p, batches, splits, stream);
+        LaunchShape<ShapeW>(p, batches, splits, stream);
         break;
     default:
         LaunchShape<ShapeS>(p, batches, splits, stream);
         break;
     }
     if (splits > 1) {
-        const int64_t total = batches * p.m * p.n;
-        SplitReduceKernel<<<GridFor(total, 256, 4096), 256, 0, stream>>>(p, splits, batches);
+        const int vec = p.n % 4 == 0 ? 4 : 1;
+        const int64_t work = batches * p.m * p.n / vec;
+        SplitReduceKernel<<<GridFor(work, 256, 8192), 256, 0, stream>>>(p, splits, batches, vec);
         CheckLaunch("SplitReduceKernel launch");
     }
 }
