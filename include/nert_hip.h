@@ -200,6 +200,40 @@ int nert_hip_avgpool2d_f32(const float* x, float* y, const nert_pool_desc* d, vo
  * src/kernels/global_average_pool.cpp:32-69. */
 int nert_hip_global_avgpool_f32(const float* x, float* y, int64_t planes, int64_t spatial, void* stream);
 
+/* ----------------------------------------------------------- reductions --- */
+
+enum nert_reduce_op {
+    NERT_RED_SUM = 0, /* src/kernels/reduce_sum.cpp (f32 in double, i64 exact) */
+    NERT_RED_MEAN,    /* src/kernels/reduce_mean.cpp */
+    NERT_RED_MAX,     /* src/kernels/reduce_max.cpp (std::max from lowest()) */
+    NERT_RED_L2       /* src/kernels/reduce_l2.cpp */
+};
+
+/* Reduces the axes flagged in `reduced` (one byte per axis of `dims`); the
+ * output holds the kept axes in order (keepdims does not change the data). */
+int nert_hip_reduce(int op, int dtype, const void* x, void* y, int rank, const int64_t* dims, const uint8_t* reduced,
+                    void* stream);
+/* Softmax over `dim` with x viewed as [outer, dim, inner]
+ * (src/kernels/softmax.cpp:47-120). */
+int nert_hip_softmax_f32(const float* x, float* y, int64_t outer, int64_t dim, int64_t inner, void* stream);
+/* LayerNormalization over rows of `inner` elements; Scale/B per element or
+ * scalar; Mean/InvStdDev outputs optional (NULL)
+ * (src/kernels/layer_normalization.cpp:77-160). */
+int nert_hip_layernorm_f32(const float* x, const float* scale, int scale_scalar, const float* bias, int bias_scalar,
+                           float* y, float* mean_out, float* invstd_out, int64_t rows, int64_t inner, double epsilon,
+                           void* stream);
+/* InstanceNormalization over each (n, c) plane
+ * (src/kernels/instance_normalization.cpp:44-106). */
+int nert_hip_instancenorm_f32(const float* x, const float* scale, const float* bias, float* y, int64_t batch,
+                              int64_t channels, int64_t spatial, double epsilon, void* stream);
+/* ArgMax along `dim` of [outer, dim, inner] -> int64 [outer, inner]
+ * (src/kernels/arg_max.cpp:41-123). */
+int nert_hip_argmax(int dtype, const void* x, int64_t* y, int64_t outer, int64_t dim, int64_t inner, int select_last,
+                    void* stream);
+/* CumSum along `dim` (src/kernels/cum_sum.cpp:40-145). */
+int nert_hip_cumsum(int dtype, const void* x, void* y, int64_t outer, int64_t dim, int64_t inner, int exclusive,
+                    int reverse, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

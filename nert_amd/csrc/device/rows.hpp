@@ -67,6 +67,17 @@ NERT_HIP_ROW(MaxPool);
 NERT_HIP_ROW(AveragePool);
 NERT_HIP_ROW(GlobalAveragePool);
 
+// rows_reduce.cpp
+NERT_HIP_ROW(ReduceMean);
+NERT_HIP_ROW(ReduceMax);
+NERT_HIP_ROW(ReduceSum);
+NERT_HIP_ROW(ReduceL2);
+NERT_HIP_ROW(Softmax);
+NERT_HIP_ROW(LayerNormalization);
+NERT_HIP_ROW(InstanceNormalization);
+NERT_HIP_ROW(ArgMax);
+NERT_HIP_ROW(CumSum);
+
 // rows_shape.cpp
 NERT_HIP_ROW(Identity);
 NERT_HIP_ROW(Flatten);

@@ -54,6 +54,15 @@ nert::KernelFn FindRow(const std::string& op_type) {
         {"MaxPool", &MaxPool},
         {"AveragePool", &AveragePool},
         {"GlobalAveragePool", &GlobalAveragePool},
+        {"ReduceMean", &ReduceMean},
+        {"ReduceMax", &ReduceMax},
+        {"ReduceSum", &ReduceSum},
+        {"ReduceL2", &ReduceL2},
+        {"Softmax", &Softmax},
+        {"LayerNormalization", &LayerNormalization},
+        {"InstanceNormalization", &InstanceNormalization},
+        {"ArgMax", &ArgMax},
+        {"CumSum", &CumSum},
         {"Identity", &Identity},
         {"Flatten", &Flatten},
         {"Reshape", &Reshape},

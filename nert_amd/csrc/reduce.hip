@@ -1,0 +1,645 @@
+// Reductions: ReduceSum/Mean/Max/L2, Softmax, LayerNormalization,
+// InstanceNormalization, ArgMax and CumSum.
+//
+// Layout: a contiguous reduction (the reduced axes are the trailing ones, or
+// the normalised axis is last) gives each output row to one wave: lanes read
+// consecutive elements (coalesced), accumulate in double like the reference
+// rows do, and combine with a __shfl_xor butterfly. A reduction over a middle
+// block of axes, [A, R, B] with B > 1, gives each (a, b) pair to one lane and
+// walks R with stride B, so neighbouring lanes still read neighbouring
+// addresses. Anything else falls back to a per-output walk over the reduced
+// index space.
+//
+// Semantics follow the reference rows: sums of float32 in double rounded once
+// (src/kernels/reduce_sum.cpp:33-70, reduce_mean.cpp:180-197), ReduceMax
+// starting from the lowest float with std::max so NaN never wins
+// (reduce_max.cpp:152-165), ReduceL2 as sqrt of a double sum of squares
+// (reduce_l2.cpp:63-80), Softmax with a float peak and double exponentials
+// (softmax.cpp:98-119), LayerNorm/InstanceNorm two-pass double statistics
+// (layer_normalization.cpp:134-159, instance_normalization.cpp:80-103),
+// ArgMax's sequential first/last-maximum rule (arg_max.cpp:41-57) and
+// CumSum's sequential scan (cum_sum.cpp:40-70).
+
+#include "common.hpp"
+#include "../../include/nert_hip.h"
+
+#include <vector>
+
+namespace nert_hip {
+namespace {
+
+constexpr int kMaxRank = 8;
+
+template <typename T>
+__device__ __forceinline__ T WaveAllSum(T v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        v += __shfl_xor(v, off, 64);
+    }
+    return v;
+}
+
+__device__ __forceinline__ float RefMax(float a, float b) { return (a < b) ? b : a; } // std::max(a, b)
+
+struct ReduceShape {
+    int kept_rank;
+    int red_rank;
+    int64_t kept_dims[kMaxRank];
+    int64_t kept_strides[kMaxRank];
+    int64_t red_dims[kMaxRank];
+    int64_t red_strides[kMaxRank];
+    int64_t red_count;
+};
+
+template <typename Acc>
+struct OpState {
+    Acc v;
+};
+
+// ---- contiguous rows: one wave per output ----------------------------------
+template <int OP, typename T>
+__global__ __launch_bounds__(256) void ReduceRowsKernel(const T* __restrict__ x, T* __restrict__ y, int64_t rows,
+                                                        int64_t len) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) {
+        return;
+    }
+    const T* p = x + row * len;
+    if constexpr (OP == NERT_RED_MAX) {
+        float best = -3.402823466e+38f;
+        for (int64_t i = lane; i < len; i += 64) {
+            best = RefMax(best, p[i]);
+        }
+        // NaN never wins std::max against a number, so the order of the
+        // combination does not matter.
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            best = RefMax(best, __shfl_xor(best, off, 64));
+        }
+        if (lane == 0) {
+            y[row] = best;
+        }
+    } else if constexpr (sizeof(T) == 8) { // int64 ReduceSum: exact wrap-around sum
+        uint64_t sum = 0;
+        for (int64_t i = lane; i < len; i += 64) {
+            sum += static_cast<uint64_t>(p[i]);
+        }
+        sum = WaveAllSum(sum);
+        if (lane == 0) {
+            y[row] = static_cast<T>(sum);
+        }
+    } else {
+        double sum = 0.0;
+        for (int64_t i = lane; i < len; i += 64) {
+            const double v = static_cast<double>(p[i]);
+            sum += OP == NERT_RED_L2 ? v * v : v;
+        }
+        sum = WaveAllSum(sum);
+        if (lane == 0) {
+            double r = sum;
+            if (OP == NERT_RED_MEAN) {
+                r = sum / static_cast<double>(len);
+            } else if (OP == NERT_RED_L2) {
+                r = sqrt(sum);
+            }
+            y[row] = static_cast<T>(r);
+        }
+    }
+}
+
+// ---- [A, R, B]: one lane per (a, b) -----------------------------------------
+template <int OP, typename T>
+__global__ void ReduceColsKernel(const T* __restrict__ x, T* __restrict__ y, int64_t A, int64_t R, int64_t B) {
+    const int64_t total = A * B;
+    for (int64_t o = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; o < total;
+         o += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t a = o / B;
+        const int64_t b = o - a * B;
+        const T* p = x + a * R * B + b;
+        if constexpr (OP == NERT_RED_MAX) {
+            float best = -3.402823466e+38f;
+            for (int64_t r = 0; r < R; ++r) {
+                best = RefMax(best, p[r * B]);
+            }
+            y[o] = best;
+        } else if constexpr (sizeof(T) == 8) {
+            uint64_t sum = 0;
+            for (int64_t r = 0; r < R; ++r) {
+                sum += static_cast<uint64_t>(p[r * B]);
+            }
+            y[o] = static_cast<T>(sum);
+        } else {
+            double sum = 0.0;
+            for (int64_t r = 0; r < R; ++r) {
+                const double v = static_cast<double>(p[r * B]);
+                sum += OP == NERT_RED_L2 ? v * v : v;
+            }
+            if (OP == NERT_RED_MEAN) {
+                sum /= static_cast<double>(R);
+            } else if (OP == NERT_RED_L2) {
+                sum = sqrt(sum);
+            }
+            y[o] = static_cast<T>(sum);
+        }
+    }
+}
+
+// ---- general: one lane per output, decoded reduced index ----------------------
+template <int OP, typename T>
+__global__ void ReduceGeneralKernel(const T* __restrict__ x, T* __restrict__ y, ReduceShape s, int64_t outputs) {
+    for (int64_t o = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; o < outputs;
+         o += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        int64_t base = 0;
+        int64_t rem = o;
+        for (int d = s.kept_rank - 1; d >= 0; --d) {
+            const int64_t c = rem % s.kept_dims[d];
+            rem /= s.kept_dims[d];
+            base += c * s.kept_strides[d];
+        }
+        float best = -3.402823466e+38f;
+        double sum = 0.0;
+        uint64_t isum = 0;
+        for (int64_t r = 0; r < s.red_count; ++r) {
+            int64_t off = base;
+            int64_t rr = r;
+            for (int d = s.red_rank - 1; d >= 0; --d) {
+                const int64_t c = rr % s.red_dims[d];
+                rr /= s.red_dims[d];
+                off += c * s.red_strides[d];
+            }
+            if constexpr (OP == NERT_RED_MAX) {
+                best = RefMax(best, static_cast<float>(x[off]));
+            } else if constexpr (sizeof(T) == 8) {
+                isum += static_cast<uint64_t>(x[off]);
+            } else {
+                const double v = static_cast<double>(x[off]);
+                sum += OP == NERT_RED_L2 ? v * v : v;
+            }
+        }
+        if constexpr (OP == NERT_RED_MAX) {
+            y[o] = static_cast<T>(best);
+        } else if constexpr (sizeof(T) == 8) {
+            y[o] = static_cast<T>(isum);
+        } else {
+            if (OP == NERT_RED_MEAN) {
+                sum /= static_cast<double>(s.red_count);
+            } else if (OP == NERT_RED_L2) {
+                sum = sqrt(sum);
+            }
+            y[o] = static_cast<T>(sum);
+        }
+    }
+}
+
+template <int OP, typename T>
+void LaunchReduce(const T* x, T* y, int rank, const int64_t* dims, const uint8_t* reduced, hipStream_t s) {
+    // Collapse neighbouring axes with the same reduced flag.
+    std::vector<int64_t> cd;
+    std::vector<bool> cr;
+    for (int d = 0; d < rank; ++d) {
+        if (dims[d] == 1) {
+            continue;
+        }
+        const bool r = reduced[d] != 0;
+        if (!cd.empty() && cr.back() == r) {
+            cd.back() *= dims[d];
+        } else {
+            cd.push_back(dims[d]);
+            cr.push_back(r);
+        }
+    }
+    int64_t outputs = 1;
+    int64_t red = 1;
+    for (size_t i = 0; i < cd.size(); ++i) {
+        (cr[i] ? red : outputs) *= cd[i];
+    }
+    if (outputs == 0 || red == 0) {
+        return;
+    }
+    const size_t n = cd.size();
+    if (n == 0 || (n == 1 && cr[0]) || (n == 2 && !cr[0] && cr[1]) || (n == 1 && !cr[0])) {
+        // [outputs, red] with red contiguous (red may be 1: a copy).
+        const int64_t blocks = (outputs + 3) / 4;
+        ReduceRowsKernel<OP, T><<<static_cast<unsigned>(blocks), 256, 0, s>>>(x, y, outputs, red);
+    } else if ((n == 2 && cr[0] && !cr[1]) || (n == 3 && !cr[0] && cr[1] && !cr[2])) {
+        const int64_t A = n == 3 ? cd[0] : 1;
+        const int64_t R = n == 3 ? cd[1] : cd[0];
+        const int64_t B = n == 3 ? cd[2] : cd[1];
+        ReduceColsKernel<OP, T><<<GridFor(A * B, 256, 8192), 256, 0, s>>>(x, y, A, R, B);
+    } else {
+        ReduceShape sh{};
+        std::vector<int64_t> strides(n, 1);
+        for (size_t i = n; i-- > 1;) {
+            strides[i - 1] = strides[i] * cd[i];
+        }
+        for (size_t i = 0; i < n; ++i) {
+            if (cr[i]) {
+                if (sh.red_rank >= kMaxRank) {
+                    throw Error("reduce: too many reduced axis groups");
+                }
+                sh.red_dims[sh.red_rank] = cd[i];
+                sh.red_strides[sh.red_rank++] = strides[i];
+            } else {
+                if (sh.kept_rank >= kMaxRank) {
+                    throw Error("reduce: too many kept axis groups");
+                }
+                sh.kept_dims[sh.kept_rank] = cd[i];
+                sh.kept_strides[sh.kept_rank++] = strides[i];
+            }
+        }
+        sh.red_count = red;
+        ReduceGeneralKernel<OP, T><<<GridFor(outputs, 256, 8192), 256, 0, s>>>(x, y, sh, outputs);
+    }
+    CheckLaunch("reduce launch");
+}
+
+// ---- Softmax ---------------------------------------------------------------
+// Rows along the last axis: one wave per row.
+__global__ __launch_bounds__(256) void SoftmaxRowsKernel(const float* __restrict__ x, float* __restrict__ y,
+                                                         int64_t rows, int64_t dim) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) {
+        return;
+    }
+    const float* p = x + row * dim;
+    float* q = y + row * dim;
+    // Peak with the reference's rule (value > peak, starting at element 0):
+    // NaN elements after the first never raise it, so a parallel max over the
+    // non-NaN elements seeded with element 0 is the same value.
+    const float first = p[0];
+    float peak = first;
+    for (int64_t i = lane; i < dim; i += 64) {
+        const float v = p[i];
+        peak = v > peak ? v : peak;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float o = __shfl_xor(peak, off, 64);
+        peak = o > peak ? o : peak;
+    }
+    if (first != first) {
+        peak = first;
+    }
+    const double dp = static_cast<double>(peak);
+    double total = 0.0;
+    for (int64_t i = lane; i < dim; i += 64) {
+        total += exp(static_cast<double>(p[i]) - dp);
+    }
+    total = WaveAllSum(total);
+    for (int64_t i = lane; i < dim; i += 64) {
+        q[i] = static_cast<float>(exp(static_cast<double>(p[i]) - dp) / total);
+    }
+}
+
+// Normalised axis with inner > 1: one lane per (outer, inner) column.
+__global__ void SoftmaxColsKernel(const float* __restrict__ x, float* __restrict__ y, int64_t outer, int64_t dim,
+                                  int64_t inner) {
+    const int64_t total_cols = outer * inner;
+    for (int64_t c = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; c < total_cols;
+         c += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t o = c / inner;
+        const int64_t n = c - o * inner;
+        const float* p = x + o * dim * inner + n;
+        float* q = y + o * dim * inner + n;
+        float peak = p[0];
+        for (int64_t k = 1; k < dim; ++k) {
+            const float v = p[k * inner];
+            if (v > peak) {
+                peak = v;
+            }
+        }
+        const double dp = static_cast<double>(peak);
+        double total = 0.0;
+        for (int64_t k = 0; k < dim; ++k) {
+            total += exp(static_cast<double>(p[k * inner]) - dp);
+        }
+        for (int64_t k = 0; k < dim; ++k) {
+            q[k * inner] = static_cast<float>(exp(static_cast<double>(p[k * inner]) - dp) / total);
+        }
+    }
+}
+
+// ---- LayerNorm / InstanceNorm ------------------------------------------------
+// One wave per row: mean, then centred sum of squares, in double.
+__global__ __launch_bounds__(256) void LayerNormKernel(const float* __restrict__ x, const float* __restrict__ scale,
+                                                       int scale_scalar, const float* __restrict__ bias,
+                                                       int bias_scalar, float* __restrict__ y, float* mean_out,
+                                                       float* invstd_out, int64_t rows, int64_t inner, double eps) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) {
+        return;
+    }
+    const float* p = x + row * inner;
+    float* q = y + row * inner;
+    double sum = 0.0;
+    for (int64_t i = lane; i < inner; i += 64) {
+        sum += static_cast<double>(p[i]);
+    }
+    const double mean = WaveAllSum(sum) / static_cast<double>(inner);
+    double sq = 0.0;
+    for (int64_t i = lane; i < inner; i += 64) {
+        const double c = static_cast<double>(p[i]) - mean;
+        sq += c * c;
+    }
+    const double inv = 1.0 / sqrt(WaveAllSum(sq) / static_cast<double>(inner) + eps);
+    for (int64_t i = lane; i < inner; i += 64) {
+        const double scaled = (static_cast<double>(p[i]) - mean) * inv * static_cast<double>(scale[scale_scalar ? 0 : i]);
+        q[i] = static_cast<float>(bias != nullptr ? scaled + static_cast<double>(bias[bias_scalar ? 0 : i]) : scaled);
+    }
+    if (lane == 0) {
+        if (mean_out != nullptr) {
+            mean_out[row] = static_cast<float>(mean);
+        }
+        if (invstd_out != nullptr) {
+            invstd_out[row] = static_cast<float>(inv);
+        }
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ T BlockSum(T v, T* smem) {
+    v = WaveAllSum(v);
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    __syncthreads();
+    if (lane == 0) {
+        smem[wave] = v;
+    }
+    __syncthreads();
+    T total = 0;
+    for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) {
+        total += smem[w];
+    }
+    return total;
+}
+
+// One 256-thread block per (n, c) plane.
+__global__ __launch_bounds__(256) void InstanceNormKernel(const float* __restrict__ x, const float* __restrict__ scale,
+                                                          const float* __restrict__ bias, float* __restrict__ y,
+                                                          int64_t channels, int64_t spatial, double eps) {
+    __shared__ double smem[4];
+    const int64_t plane = blockIdx.x;
+    const int64_t c = plane % channels;
+    const float* p = x + plane * spatial;
+    float* q = y + plane * spatial;
+    double sum = 0.0;
+    for (int64_t i = threadIdx.x; i < spatial; i += blockDim.x) {
+        sum += static_cast<double>(p[i]);
+    }
+    const double mean = BlockSum(sum, smem) / static_cast<double>(spatial);
+    double sq = 0.0;
+    for (int64_t i = threadIdx.x; i < spatial; i += blockDim.x) {
+        const double d = static_cast<double>(p[i]) - mean;
+        sq += d * d;
+    }
+    const double inv = 1.0 / sqrt(BlockSum(sq, smem) / static_cast<double>(spatial) + eps);
+    const double s = static_cast<double>(scale[c]);
+    const double b = static_cast<double>(bias[c]);
+    for (int64_t i = threadIdx.x; i < spatial; i += blockDim.x) {
+        q[i] = static_cast<float>((static_cast<double>(p[i]) - mean) * inv * s + b);
+    }
+}
+
+// ---- ArgMax ----------------------------------------------------------------
+// Sequential rule: index i replaces the best when v > best, or (last) when
+// v == best; so NaN never wins after index 0 and a NaN at index 0 wins.
+template <typename T>
+__device__ __forceinline__ bool Beats(T v, int64_t i, T bv, int64_t bi, bool last) {
+    // Combination of two candidates where bi < i in scan order.
+    return v > bv || (last && v == bv);
+}
+
+template <typename T>
+__global__ void ArgMaxKernel(const T* __restrict__ x, int64_t* __restrict__ y, int64_t outer, int64_t dim,
+                             int64_t inner, int last) {
+    const int64_t total = outer * inner;
+    for (int64_t c = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; c < total;
+         c += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t o = c / inner;
+        const int64_t n = c - o * inner;
+        const T* p = x + o * dim * inner + n;
+        int64_t best = 0;
+        T bv = p[0];
+        for (int64_t i = 1; i < dim; ++i) {
+            const T v = p[i * inner];
+            if (v > bv || (last && v == bv)) {
+                bv = v;
+                best = i;
+            }
+        }
+        y[c] = best;
+    }
+}
+
+// inner == 1 and long rows: one wave per row. Each lane scans a strided
+// subsequence in order, then candidates are merged in index order with the
+// same rule; a NaN at index 0 short-circuits to 0.
+template <typename T>
+__global__ __launch_bounds__(256) void ArgMaxRowsKernel(const T* __restrict__ x, int64_t* __restrict__ y,
+                                                        int64_t rows, int64_t dim, int last) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) {
+        return;
+    }
+    const T* p = x + row * dim;
+    const T first = p[0];
+    int64_t bi = -1;
+    T bv = first;
+    for (int64_t i = lane; i < dim; i += 64) {
+        const T v = p[i];
+        if (v == v && (bi < 0 || v > bv || (last && v == bv))) {
+            bv = v;
+            bi = i;
+        }
+    }
+    // Merge: prefer the larger value; on ties the smaller index (first) or
+    // the larger index (last). Lanes without a non-NaN candidate lose.
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const T ov = __shfl_xor(bv, off, 64);
+        const int64_t oi = __shfl_xor(bi, off, 64);
+        bool take;
+        if (oi < 0) {
+            take = false;
+        } else if (bi < 0) {
+            take = true;
+        } else if (ov != bv) {
+            take = ov > bv;
+        } else {
+            take = last ? oi > bi : oi < bi;
+        }
+        if (take) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (lane == 0) {
+        y[row] = (first != first || bi < 0) ? 0 : bi;
+    }
+}
+
+// ---- CumSum ----------------------------------------------------------------
+template <typename T, typename Acc>
+__global__ void CumSumKernel(const T* __restrict__ x, T* __restrict__ y, int64_t outer, int64_t dim, int64_t inner,
+                             int exclusive, int reverse) {
+    const int64_t total = outer * inner;
+    for (int64_t c = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; c < total;
+         c += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t o = c / inner;
+        const int64_t n = c - o * inner;
+        Acc run = Acc{};
+        for (int64_t s = 0; s < dim; ++s) {
+            const int64_t i = reverse ? dim - 1 - s : s;
+            const int64_t idx = (o * dim + i) * inner + n;
+            if (exclusive) {
+                y[idx] = static_cast<T>(run);
+                run += static_cast<Acc>(x[idx]);
+            } else {
+                run += static_cast<Acc>(x[idx]);
+                y[idx] = static_cast<T>(run);
+            }
+        }
+    }
+}
+
+unsigned RowBlocks(int64_t rows) {
+    const int64_t b = (rows + 3) / 4;
+    if (b > 0x7FFFFFFF) {
+        throw Error("too many rows");
+    }
+    return static_cast<unsigned>(b < 1 ? 1 : b);
+}
+
+} // namespace
+} // namespace nert_hip
+
+using namespace nert_hip;
+
+extern "C" {
+
+int nert_hip_reduce(int op, int dtype, const void* x, void* y, int rank, const int64_t* dims, const uint8_t* reduced,
+                    void* stream) {
+    return Guard([&] {
+        hipStream_t s = StreamOr(stream);
+        if (dtype == NERT_I64) {
+            if (op != NERT_RED_SUM) {
+                throw Error("reduce: int64 supports sum only");
+            }
+            LaunchReduce<NERT_RED_SUM, int64_t>(static_cast<const int64_t*>(x), static_cast<int64_t*>(y), rank, dims,
+                                                reduced, s);
+            return;
+        }
+        const float* xf = static_cast<const float*>(x);
+        float* yf = static_cast<float*>(y);
+        switch (op) {
+        case NERT_RED_SUM:
+            LaunchReduce<NERT_RED_SUM, float>(xf, yf, rank, dims, reduced, s);
+            break;
+        case NERT_RED_MEAN:
+            LaunchReduce<NERT_RED_MEAN, float>(xf, yf, rank, dims, reduced, s);
+            break;
+        case NERT_RED_MAX:
+            LaunchReduce<NERT_RED_MAX, float>(xf, yf, rank, dims, reduced, s);
+            break;
+        case NERT_RED_L2:
+            LaunchReduce<NERT_RED_L2, float>(xf, yf, rank, dims, reduced, s);
+            break;
+        default:
+            throw Error("reduce: unknown op");
+        }
+    });
+}
+
+int nert_hip_softmax_f32(const float* x, float* y, int64_t outer, int64_t dim, int64_t inner, void* stream) {
+    return Guard([&] {
+        if (outer * dim * inner == 0) {
+            return;
+        }
+        hipStream_t s = StreamOr(stream);
+        if (inner == 1) {
+            SoftmaxRowsKernel<<<RowBlocks(outer), 256, 0, s>>>(x, y, outer, dim);
+        } else {
+            SoftmaxColsKernel<<<GridFor(outer * inner, 256, 8192), 256, 0, s>>>(x, y, outer, dim, inner);
+        }
+        CheckLaunch("softmax launch");
+    });
+}
+
+int nert_hip_layernorm_f32(const float* x, const float* scale, int scale_scalar, const float* bias, int bias_scalar,
+                           float* y, float* mean_out, float* invstd_out, int64_t rows, int64_t inner, double epsilon,
+                           void* stream) {
+    return Guard([&] {
+        if (rows * inner == 0) {
+            return;
+        }
+        LayerNormKernel<<<RowBlocks(rows), 256, 0, StreamOr(stream)>>>(x, scale, scale_scalar, bias, bias_scalar, y,
+                                                                        mean_out, invstd_out, rows, inner, epsilon);
+        CheckLaunch("layernorm launch");
+    });
+}
+
+int nert_hip_instancenorm_f32(const float* x, const float* scale, const float* bias, float* y, int64_t batch,
+                              int64_t channels, int64_t spatial, double epsilon, void* stream) {
+    return Guard([&] {
+        const int64_t planes = batch * channels;
+        if (planes * spatial == 0) {
+            return;
+        }
+        if (planes > 0x7FFFFFFF) {
+            throw Error("instancenorm: too many planes");
+        }
+        InstanceNormKernel<<<static_cast<unsigned>(planes), 256, 0, StreamOr(stream)>>>(x, scale, bias, y, channels,
+                                                                                        spatial, epsilon);
+        CheckLaunch("instancenorm launch");
+    });
+}
+
+int nert_hip_argmax(int dtype, const void* x, int64_t* y, int64_t outer, int64_t dim, int64_t inner, int select_last,
+                    void* stream) {
+    return Guard([&] {
+        if (outer * dim * inner == 0) {
+            return;
+        }
+        hipStream_t s = StreamOr(stream);
+        if (inner == 1 && dim >= 256) {
+            if (dtype == NERT_F32) {
+                ArgMaxRowsKernel<float><<<RowBlocks(outer), 256, 0, s>>>(static_cast<const float*>(x), y, outer, dim,
+                                                                          select_last);
+            } else {
+                ArgMaxRowsKernel<int64_t><<<RowBlocks(outer), 256, 0, s>>>(static_cast<const int64_t*>(x), y, outer,
+                                                                            dim, select_last);
+            }
+        } else if (dtype == NERT_F32) {
+            ArgMaxKernel<float><<<GridFor(outer * inner, 256, 8192), 256, 0, s>>>(static_cast<const float*>(x), y,
+                                                                                   outer, dim, inner, select_last);
+        } else {
+            ArgMaxKernel<int64_t><<<GridFor(outer * inner, 256, 8192), 256, 0, s>>>(static_cast<const int64_t*>(x), y,
+                                                                                     outer, dim, inner, select_last);
+        }
+        CheckLaunch("argmax launch");
+    });
+}
+
+int nert_hip_cumsum(int dtype, const void* x, void* y, int64_t outer, int64_t dim, int64_t inner, int exclusive,
+                    int reverse, void* stream) {
+    return Guard([&] {
+        if (outer * dim * inner == 0) {
+            return;
+        }
+        hipStream_t s = StreamOr(stream);
+        if (dtype == NERT_F32) {
+            CumSumKernel<float, double><<<GridFor(outer * inner, 256, 8192), 256, 0, s>>>(
+                static_cast<const float*>(x), static_cast<float*>(y), outer, dim, inner, exclusive, reverse);
+        } else {
+            CumSumKernel<int64_t, int64_t><<<GridFor(outer * inner, 256, 8192), 256, 0, s>>>(
+                static_cast<const int64_t*>(x), static_cast<int64_t*>(y), outer, dim, inner, exclusive, reverse);
+        }
+        CheckLaunch("cumsum launch");
+    });
+}
+
+} // extern "C"
