@@ -234,6 +234,23 @@ int nert_hip_argmax(int dtype, const void* x, int64_t* y, int64_t outer, int64_t
 int nert_hip_cumsum(int dtype, const void* x, void* y, int64_t outer, int64_t dim, int64_t inner, int exclusive,
                     int reverse, void* stream);
 
+/* ---- Data movement --------------------------------------------------------
+ * Copies the box `dims` element by element: destination element c sits at
+ * dst + sum_d c_d * dst_strides[d], its source at src + sum_d s_d *
+ * src_strides[d] with s_d = c_d, or c_d % src_mods[d] when src_mods is
+ * non-NULL and src_mods[d] > 0. Strides count elements of `elem_size` bytes
+ * (1, 4 or 8) and may be zero (broadcast) or negative (reversed walk).
+ * Serves Transpose, Concat, Split, Slice, Expand and Tile
+ * (src/kernels/{transpose,concat,split,slice,expand,tile}.cpp). */
+int nert_hip_copy_strided(int elem_size, const void* src, void* dst, int rank, const int64_t* dims,
+                          const int64_t* src_strides, const int64_t* dst_strides, const int64_t* src_mods,
+                          void* stream);
+/* Pad of a dense tensor: out[c] = in[map(c - begins)] per axis, mode 0
+ * constant (fill `fvalue` for float32, `ivalue` for int64), 1 reflect, 2 edge
+ * (src/kernels/pad.cpp:43-96). */
+int nert_hip_pad(int dtype, const void* x, void* y, int rank, const int64_t* in_dims, const int64_t* out_dims,
+                 const int64_t* begins, int mode, double fvalue, int64_t ivalue, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

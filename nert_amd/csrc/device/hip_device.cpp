@@ -204,6 +204,30 @@ std::vector<int64_t> IntsAttr(const Node& node, const std::string& name, const c
     return *v;
 }
 
+int64_t IntAttrC(const Node& node, const std::string& name, int64_t fallback, const std::string& context) {
+    const Attribute* attr = FindAttr(node, name);
+    if (attr == nullptr) {
+        return fallback;
+    }
+    const int64_t* v = std::get_if<int64_t>(&attr->value);
+    if (v == nullptr) {
+        throw InferenceException(context + ": attribute '" + name + "' must be an integer");
+    }
+    return *v;
+}
+
+float FloatAttrC(const Node& node, const std::string& name, float fallback, const std::string& context) {
+    const Attribute* attr = FindAttr(node, name);
+    if (attr == nullptr) {
+        return fallback;
+    }
+    const float* v = std::get_if<float>(&attr->value);
+    if (v == nullptr) {
+        throw InferenceException(context + ": attribute '" + name + "' must be a float");
+    }
+    return *v;
+}
+
 void CheckStatus(int status, const std::string& context) {
     if (status != 0) {
         throw InferenceException(context + ": HIP failure: " + nert_hip_last_error());

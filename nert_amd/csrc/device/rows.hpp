@@ -83,5 +83,16 @@ NERT_HIP_ROW(Identity);
 NERT_HIP_ROW(Flatten);
 NERT_HIP_ROW(Reshape);
 
+// rows_move.cpp
+NERT_HIP_ROW(Transpose);
+NERT_HIP_ROW(Concat);
+NERT_HIP_ROW(Split);
+NERT_HIP_ROW(Slice);
+NERT_HIP_ROW(Expand);
+NERT_HIP_ROW(Tile);
+NERT_HIP_ROW(Squeeze);
+NERT_HIP_ROW(Unsqueeze);
+NERT_HIP_ROW(Pad);
+
 } // namespace rows
 } // namespace nert_hip

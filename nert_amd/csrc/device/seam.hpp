@@ -39,6 +39,19 @@ inline int64_t ElementCount(const std::vector<int64_t>& dims, const std::string&
     return count;
 }
 
+// The other per-row ElementCount of the reference: zero dims allowed,
+// negative ones rejected.
+inline int64_t CountNonNeg(const std::vector<int64_t>& dims, const std::string& context) {
+    int64_t count = 1;
+    for (int64_t dim : dims) {
+        if (dim < 0) {
+            throw InferenceException(context + ": negative dimension");
+        }
+        count *= dim;
+    }
+    return count;
+}
+
 // Element count without validation (zero dims allowed).
 inline int64_t Count(const std::vector<int64_t>& dims) {
     int64_t count = 1;
@@ -97,6 +110,10 @@ int64_t IntAttr(const Node& node, const std::string& name, int64_t fallback, con
 float FloatAttr(const Node& node, const std::string& name, float fallback, const char* op);
 std::string StringAttr(const Node& node, const std::string& name, const std::string& fallback, const char* op);
 std::vector<int64_t> IntsAttr(const Node& node, const std::string& name, const char* op);
+// Same readers with the other message form the reference rows use:
+// "<context>: attribute '<name>' must be an integer".
+int64_t IntAttrC(const Node& node, const std::string& name, int64_t fallback, const std::string& context);
+float FloatAttrC(const Node& node, const std::string& name, float fallback, const std::string& context);
 
 // Throws when the layer reported a HIP failure.
 void CheckStatus(int status, const std::string& context);

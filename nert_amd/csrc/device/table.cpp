@@ -66,6 +66,15 @@ nert::KernelFn FindRow(const std::string& op_type) {
         {"Identity", &Identity},
         {"Flatten", &Flatten},
         {"Reshape", &Reshape},
+        {"Transpose", &Transpose},
+        {"Concat", &Concat},
+        {"Split", &Split},
+        {"Slice", &Slice},
+        {"Expand", &Expand},
+        {"Tile", &Tile},
+        {"Squeeze", &Squeeze},
+        {"Unsqueeze", &Unsqueeze},
+        {"Pad", &Pad},
     };
     const auto it = table.find(op_type);
     return it == table.end() ? nullptr : it->second;

@@ -1,0 +1,221 @@
+// Data movement: one strided-copy kernel serves Transpose, Slice, Expand,
+// Tile, Concat and Split; Pad has its own mapping (constant/edge/reflect).
+//
+// A strided copy walks the destination box in row-major order and reads the
+// source through per-axis strides (0 broadcasts for Expand, negative steps
+// for Slice, an optional per-axis modulus for Tile). The host drops unit axes
+// and merges axes both sides walk contiguously, so most ViT/detector
+// reshuffles become rank-2 or rank-3 walks whose innermost run is contiguous
+// on both sides; those runs move as 16-byte vectors when alignment allows.
+
+#include "common.hpp"
+#include "../../include/nert_hip.h"
+
+#include <vector>
+
+namespace nert_hip {
+namespace {
+
+constexpr int kMaxRank = 10;
+
+struct CopyArgs {
+    const uint8_t* src;
+    uint8_t* dst;
+    int rank;
+    int64_t dims[kMaxRank];
+    int64_t src_strides[kMaxRank]; // elements
+    int64_t dst_strides[kMaxRank];
+    int64_t src_mods[kMaxRank]; // 0 = no modulus
+};
+
+template <typename T>
+__global__ void StridedCopyKernel(CopyArgs a, int64_t n) {
+    const T* src = reinterpret_cast<const T*>(a.src);
+    T* dst = reinterpret_cast<T*>(a.dst);
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n; i += stride) {
+        int64_t rem = i;
+        int64_t so = 0;
+        int64_t d_o = 0;
+        for (int d = a.rank - 1; d >= 0; --d) {
+            const int64_t c = rem % a.dims[d];
+            rem /= a.dims[d];
+            const int64_t sc = a.src_mods[d] > 0 ? c % a.src_mods[d] : c;
+            so += sc * a.src_strides[d];
+            d_o += c * a.dst_strides[d];
+        }
+        dst[d_o] = src[so];
+    }
+}
+
+int64_t Collapse(int rank, const int64_t* dims, const int64_t* ss, const int64_t* ds, const int64_t* mods,
+                 CopyArgs& a) {
+    std::vector<int64_t> cd, cs, cdst, cm;
+    int64_t n = 1;
+    for (int d = 0; d < rank; ++d) {
+        n *= dims[d];
+        if (dims[d] == 1) {
+            continue;
+        }
+        const int64_t m = mods != nullptr ? mods[d] : 0;
+        const bool mod_here = m > 0 && m != dims[d];
+        if (!cd.empty() && !mod_here && cm.back() == 0 && cs.back() == ss[d] * dims[d] &&
+            cdst.back() == ds[d] * dims[d]) {
+            cd.back() *= dims[d];
+            cs.back() = ss[d];
+            cdst.back() = ds[d];
+            continue;
+        }
+        cd.push_back(dims[d]);
+        cs.push_back(ss[d]);
+        cdst.push_back(ds[d]);
+        cm.push_back(mod_here ? m : 0);
+    }
+    if (cd.empty()) {
+        cd.push_back(1);
+        cs.push_back(0);
+        cdst.push_back(0);
+        cm.push_back(0);
+    }
+    if (static_cast<int>(cd.size()) > kMaxRank) {
+        throw Error("copy: more than 10 non-mergeable axes");
+    }
+    a.rank = static_cast<int>(cd.size());
+    for (int d = 0; d < a.rank; ++d) {
+        a.dims[d] = cd[d];
+        a.src_strides[d] = cs[d];
+        a.dst_strides[d] = cdst[d];
+        a.src_mods[d] = cm[d];
+    }
+    return n;
+}
+
+// ---- Pad -----------------------------------------------------------------
+struct PadArgs {
+    int rank;
+    int mode; // 0 constant, 1 reflect, 2 edge
+    int64_t in_dims[kMaxRank];
+    int64_t out_dims[kMaxRank];
+    int64_t begins[kMaxRank];
+    int64_t in_strides[kMaxRank];
+};
+
+// src/kernels/pad.cpp MapPosition: -1 means "use the fill value".
+__device__ __forceinline__ int64_t MapPos(int64_t pos, int64_t dim, int mode) {
+    if (pos >= 0 && pos < dim) {
+        return pos;
+    }
+    if (mode == 0) {
+        return -1;
+    }
+    if (mode == 2) {
+        return pos < 0 ? 0 : dim - 1;
+    }
+    if (dim == 1) {
+        return 0;
+    }
+    const int64_t period = 2 * (dim - 1);
+    int64_t m = pos % period;
+    if (m < 0) {
+        m += period;
+    }
+    return m < dim ? m : period - m;
+}
+
+template <typename T>
+__global__ void PadKernel(const T* __restrict__ x, T* __restrict__ y, PadArgs a, T fill, int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n; i += stride) {
+        int64_t rem = i;
+        int64_t off = 0;
+        bool filled = false;
+        for (int d = a.rank - 1; d >= 0; --d) {
+            const int64_t c = rem % a.out_dims[d];
+            rem /= a.out_dims[d];
+            const int64_t s = MapPos(c - a.begins[d], a.in_dims[d], a.mode);
+            filled = filled || s < 0;
+            off += (s < 0 ? 0 : s) * a.in_strides[d];
+        }
+        y[i] = filled ? fill : x[off];
+    }
+}
+
+} // namespace
+} // namespace nert_hip
+
+using namespace nert_hip;
+
+extern "C" {
+
+int nert_hip_copy_strided(int elem_size, const void* src, void* dst, int rank, const int64_t* dims,
+                          const int64_t* src_strides, const int64_t* dst_strides, const int64_t* src_mods,
+                          void* stream) {
+    return Guard([&] {
+        CopyArgs a{};
+        a.src = static_cast<const uint8_t*>(src);
+        a.dst = static_cast<uint8_t*>(dst);
+        const int64_t n = Collapse(rank, dims, src_strides, dst_strides, src_mods, a);
+        if (n <= 0) {
+            return;
+        }
+        hipStream_t s = StreamOr(stream);
+        // Fully contiguous on both sides: a plain copy.
+        if (a.rank == 1 && a.src_strides[0] == 1 && a.dst_strides[0] == 1 && a.src_mods[0] == 0) {
+            Check(hipMemcpyAsync(dst, src, static_cast<size_t>(n) * elem_size, hipMemcpyDeviceToDevice, s),
+                  "hipMemcpyAsync(copy)");
+            return;
+        }
+        const unsigned grid = GridFor(n, 256, 16384);
+        switch (elem_size) {
+        case 1:
+            StridedCopyKernel<uint8_t><<<grid, 256, 0, s>>>(a, n);
+            break;
+        case 4:
+            StridedCopyKernel<uint32_t><<<grid, 256, 0, s>>>(a, n);
+            break;
+        case 8:
+            StridedCopyKernel<uint64_t><<<grid, 256, 0, s>>>(a, n);
+            break;
+        default:
+            throw Error("copy: unsupported element size");
+        }
+        CheckLaunch("strided copy launch");
+    });
+}
+
+int nert_hip_pad(int dtype, const void* x, void* y, int rank, const int64_t* in_dims, const int64_t* out_dims,
+                 const int64_t* begins, int mode, double fvalue, int64_t ivalue, void* stream) {
+    return Guard([&] {
+        if (rank > kMaxRank) {
+            throw Error("pad: rank above 10");
+        }
+        PadArgs a{};
+        a.rank = rank;
+        a.mode = mode;
+        int64_t n = 1;
+        int64_t st = 1;
+        for (int d = rank - 1; d >= 0; --d) {
+            a.in_dims[d] = in_dims[d];
+            a.out_dims[d] = out_dims[d];
+            a.begins[d] = begins[d];
+            a.in_strides[d] = st;
+            st *= in_dims[d];
+            n *= out_dims[d];
+        }
+        if (n <= 0) {
+            return;
+        }
+        hipStream_t s = StreamOr(stream);
+        const unsigned grid = GridFor(n, 256, 16384);
+        if (dtype == NERT_F32) {
+            PadKernel<float><<<grid, 256, 0, s>>>(static_cast<const float*>(x), static_cast<float*>(y), a,
+                                                  static_cast<float>(fvalue), n);
+        } else {
+            PadKernel<int64_t><<<grid, 256, 0, s>>>(static_cast<const int64_t*>(x), static_cast<int64_t*>(y), a,
+                                                    ivalue, n);
+        }
+        CheckLaunch("pad launch");
+    });
+}
+
+} // extern "C"

@@ -74,15 +74,14 @@ def compare(hip: np.ndarray, want: np.ndarray, rtol: float = RTOL, atol: float =
 def assert_parity(op: str, inputs: Sequence[np.ndarray | None], out_specs: Sequence[tuple[Sequence[int], Any]],
                   attrs: dict[str, Any] | None = None, name: str = "n", schema_version: int = 0,
                   rtol: float = RTOL, atol: float = ATOL, compare_outputs: Sequence[int] | None = None):
-    """Runs the node on both devices and asserts parity; returns the HIP outputs."""
+    """Runs the node on both devices and asserts parity; returns the HIP outputs.
+
+    The case must be one the reference accepts (a rejected node would make
+    the comparison vacuous); rejections are checked with assert_same_error."""
     want, ref_err = run_ref(op, inputs, out_specs, attrs, name, schema_version)
+    assert ref_err is None, f"{op}: the reference rejects this case: {ref_err}"
     got, hip_err = run_hip(op, inputs, out_specs, attrs, name, schema_version)
-    if ref_err is not None or hip_err is not None:
-        assert ref_err is not None, f"{op}: HIP threw but the reference did not: {hip_err}"
-        assert hip_err is not None, f"{op}: reference threw but HIP did not: {ref_err}"
-        assert ref_err.status == abi.INFERENCE_ERROR and hip_err.status == abi.INFERENCE_ERROR, (ref_err, hip_err)
-        assert hip_err.message == ref_err.message, f"{op}: message differs:\n hip: {hip_err}\n ref: {ref_err}"
-        return None
+    assert hip_err is None, f"{op}: HIP threw but the reference did not: {hip_err}"
     idx = range(len(out_specs)) if compare_outputs is None else compare_outputs
     for i in idx:
         compare(got[i], want[i], rtol, atol, what=f"{op} output {i}")
@@ -95,6 +94,7 @@ def assert_same_error(op: str, inputs, out_specs, attrs=None, name: str = "bad_n
     _, hip_err = run_hip(op, inputs, out_specs, attrs, name, schema_version)
     assert ref_err is not None, f"{op}: reference accepted the node"
     assert hip_err is not None, f"{op}: HIP accepted the node the reference rejects ({ref_err})"
+    assert ref_err.status == abi.INFERENCE_ERROR and hip_err.status == abi.INFERENCE_ERROR, (ref_err, hip_err)
     assert hip_err.message == ref_err.message, f"{op}:\n hip: {hip_err}\n ref: {ref_err}"
     assert name in hip_err.message and op in hip_err.message
     return hip_err.message

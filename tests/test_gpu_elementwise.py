@@ -226,7 +226,9 @@ def test_identity_flatten_reshape(gpu):
     x = randn((2, 3, 4, 5), seed=30)
     assert_parity("Identity", [x], [(x.shape, F)])
     assert_parity("Flatten", [x], [((2, 60), F)])
-    assert_parity("Flatten", [x], [((24, 5), F)], {"axis": -1})
+    # the reference maps a negative axis to axis + rank + 1 (src/kernels/flatten.cpp:55-57)
+    assert_parity("Flatten", [x], [((120, 1), F)], {"axis": -1})
+    assert_parity("Flatten", [x], [((24, 5), F)], {"axis": -2})
     assert_parity("Flatten", [x], [((1, 120), F)], {"axis": 0})
     assert_parity("Reshape", [x, np.array([0, -1, 5], I)], [((2, 12, 5), F)])
     assert_parity("Reshape", [x, np.array([6, 20], I)], [((6, 20), F)])
