@@ -60,9 +60,10 @@ int nert_hip_event_destroy(void* event);
 
 /* HIP-graph capture of the layer stream. Everything queued on the layer
  * stream between begin and end (kernel launches of any rows, device-to-device
- * copies) becomes one replayable graph; rows that must synchronise (control
- * reads without a host shadow, data-dependent error checks) cannot be
- * captured and fail the capture. Workspace growth must happen before capture
+ * copies) becomes one replayable graph; rows that must read device memory on
+ * the host (control operands without a host shadow) cannot be captured and
+ * fail the capture, while data-dependent error checks are deferred (see
+ * nert_hip_take_error_flags). Workspace growth must happen before capture
  * (run the sequence once eagerly first). No reference counterpart: the
  * reference executor launches rows one by one (src/executor.cpp:480-535). */
 int nert_hip_capture_begin(void);
@@ -72,7 +73,9 @@ int nert_hip_graph_destroy(void* graph_exec);
 
 /* Reads (and clears when set) the device error word that rows with
  * data-dependent failures raise: bit 0 = integer division by zero,
- * bit 1 = index out of range. Synchronises `stream`. */
+ * bit 1 = index out of range. Synchronises `stream`. While `stream` is being
+ * captured into a graph it reports 0 without reading: the flag stays raised
+ * and the first call after a replay reports it. */
 int nert_hip_take_error_flags(int32_t* flags_out, void* stream);
 
 /* ---------------------------------------------------------- node level --- */
@@ -250,6 +253,33 @@ int nert_hip_copy_strided(int elem_size, const void* src, void* dst, int rank, c
  * (src/kernels/pad.cpp:43-96). */
 int nert_hip_pad(int dtype, const void* x, void* y, int rank, const int64_t* in_dims, const int64_t* out_dims,
                  const int64_t* begins, int mode, double fvalue, int64_t ivalue, void* stream);
+
+/* ---- Index rows --------------------------------------------------------------
+ * Gather over x viewed as [outer, dim, inner] with `index_count` int64
+ * indices (negative wrap); y is [outer, index_count, inner]. An index still
+ * out of range raises error bit 1 (src/kernels/gather.cpp:29-46). */
+int nert_hip_gather(int elem_size, const void* x, const int64_t* indices, void* y, int64_t outer, int64_t dim,
+                    int64_t index_count, int64_t inner, void* stream);
+/* GatherElements: y has the indices' shape `idx_dims`; off-axis coordinates
+ * must already lie inside `in_dims` (the row checks the shapes); an index out
+ * of range along `axis` raises error bit 1 (src/kernels/gather_elements.cpp:28-71). */
+int nert_hip_gather_elements(int elem_size, const void* x, const int64_t* indices, void* y, int rank,
+                             const int64_t* in_dims, const int64_t* idx_dims, int axis, void* stream);
+/* ScatterND: out = data, then slice s of `updates` lands at the k-tuple
+ * indices[s]; duplicates resolve to the last slice, as in the reference's
+ * in-order loop. Out-of-range tuples raise error bit 1
+ * (src/kernels/scatter_nd.cpp:31-118). */
+int nert_hip_scatter_nd(int elem_size, const void* data, const int64_t* indices, const void* updates, void* out,
+                        int data_rank, const int64_t* data_dims, int64_t slice_count, int k, void* stream);
+/* Range: y[i] = start + i * delta, float32 rounded after the product and
+ * after the sum (src/kernels/range.cpp:62-64), or int64. */
+int nert_hip_range(int dtype, double fstart, double fdelta, int64_t istart, int64_t idelta, void* y, int64_t count,
+                   void* stream);
+/* Writes `count` (<= 16) int64 values passed by value, with no host buffer
+ * (capture-safe): the payload of Shape (src/kernels/shape.cpp:66-70). */
+int nert_hip_store_i64(int64_t* y, const int64_t* values, int count, void* stream);
+/* EyeLike: ones where col - row == k (src/kernels/eye_like.cpp:54-79). */
+int nert_hip_eye_like(int dtype, void* y, int64_t rows, int64_t cols, int64_t k, void* stream);
 
 #ifdef __cplusplus
 }

@@ -261,6 +261,24 @@ std::vector<float> ReadFloat(const TensorView& view, int64_t count, const std::s
     return ReadControl<float>(view, count, context);
 }
 
+bool HostShadowInt64(const TensorView& view, int64_t count, std::vector<int64_t>& out) {
+    if (count <= 0 || view.data == nullptr) {
+        return false;
+    }
+    out.resize(static_cast<size_t>(count));
+    if (ShadowGet(view.data, count * static_cast<int64_t>(sizeof(int64_t)), out.data())) {
+        return true;
+    }
+    out.clear();
+    return false;
+}
+
+void PutHostShadow(void* device_ptr, const void* host, int64_t bytes) {
+    if (device_ptr != nullptr && bytes > 0) {
+        ShadowPut(device_ptr, host, bytes);
+    }
+}
+
 void AfterRow(const Views& outputs, const std::string& context) {
     for (const TensorView& out : outputs) {
         if (out.data != nullptr) {

@@ -94,5 +94,14 @@ NERT_HIP_ROW(Squeeze);
 NERT_HIP_ROW(Unsqueeze);
 NERT_HIP_ROW(Pad);
 
+// rows_index.cpp
+NERT_HIP_ROW(Gather);
+NERT_HIP_ROW(GatherElements);
+NERT_HIP_ROW(ScatterND);
+NERT_HIP_ROW(Shape);
+NERT_HIP_ROW(ConstantOfShape);
+NERT_HIP_ROW(Range);
+NERT_HIP_ROW(EyeLike);
+
 } // namespace rows
 } // namespace nert_hip

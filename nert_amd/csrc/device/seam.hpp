@@ -122,6 +122,13 @@ void CheckStatus(int status, const std::string& context);
 std::vector<int64_t> ReadInt64(const TensorView& view, int64_t count, const std::string& context);
 std::vector<float> ReadFloat(const TensorView& view, int64_t count, const std::string& context);
 
+// Host shadow only (no device read): true and `out` filled when the
+// view's bytes are shadowed.
+bool HostShadowInt64(const TensorView& view, int64_t count, std::vector<int64_t>& out);
+// Records `bytes` at `device_ptr` as the host view of a value a queued kernel
+// writes there (rows whose outputs are known on the host, e.g. Shape).
+void PutHostShadow(void* device_ptr, const void* host, int64_t bytes);
+
 // Must be called by every row after queuing writes to `outputs`: drops host
 // shadows the writes made stale and, in the debug mode (NERT_HIP_SYNC=1),
 // synchronises so a device fault is attributed to this row.

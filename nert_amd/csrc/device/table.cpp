@@ -75,6 +75,13 @@ nert::KernelFn FindRow(const std::string& op_type) {
         {"Squeeze", &Squeeze},
         {"Unsqueeze", &Unsqueeze},
         {"Pad", &Pad},
+        {"Gather", &Gather},
+        {"GatherElements", &GatherElements},
+        {"ScatterND", &ScatterND},
+        {"Shape", &Shape},
+        {"ConstantOfShape", &ConstantOfShape},
+        {"Range", &Range},
+        {"EyeLike", &EyeLike},
     };
     const auto it = table.find(op_type);
     return it == table.end() ? nullptr : it->second;

@@ -546,6 +546,14 @@ int nert_hip_take_error_flags(int32_t* flags_out, void* stream) {
     return Guard([&] {
         hipStream_t s = StreamOr(stream);
         int32_t* flags = ErrorFlags();
+        // Under stream capture the check is deferred: the flag stays raised
+        // and the first call after the captured work ran reports it.
+        hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+        Check(hipStreamIsCapturing(s, &capture), "hipStreamIsCapturing");
+        if (capture != hipStreamCaptureStatusNone) {
+            *flags_out = 0;
+            return;
+        }
         Check(hipMemcpyAsync(flags_out, flags, sizeof(int32_t), hipMemcpyDeviceToHost, s), "hipMemcpyAsync(flags)");
         Check(hipStreamSynchronize(s), "hipStreamSynchronize");
         if (*flags_out != 0) {

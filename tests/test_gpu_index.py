@@ -1,0 +1,186 @@
+"""GPU parity: index and generator rows (Gather, GatherElements, ScatterND,
+Shape, ConstantOfShape, Range, EyeLike) against the reference CpuDevice rows.
+
+Out-of-range indices must throw the reference's message on both routes the
+HIP rows take: indices uploaded from the host (checked from the host shadow
+before launch; uploads up to 64 KiB) and larger index tensors (checked by the
+kernel's device flag)."""
+
+import numpy as np
+import pytest
+
+from rowcheck import assert_parity, assert_same_error, randn, rng
+
+pytestmark = pytest.mark.gpu
+
+F, I, B = np.float32, np.int64, np.bool_
+EXACT = {"rtol": 0.0, "atol": 0.0}
+BIG = 10000  # 80 KB of int64 indices: beyond the host-shadow limit
+
+
+def _data(shape, dtype, seed=0):
+    if dtype == F:
+        return randn(shape, seed=seed)
+    if dtype == I:
+        return rng(seed).integers(-1 << 40, 1 << 40, shape).astype(I)
+    return rng(seed).integers(0, 2, shape).astype(B)
+
+
+def _gather_shape(shape, idx_shape, axis):
+    axis %= len(shape)
+    return tuple(shape[:axis]) + tuple(idx_shape) + tuple(shape[axis + 1:])
+
+
+@pytest.mark.parametrize("dtype", [F, I, B])
+@pytest.mark.parametrize("shape,idx,axis", [
+    ((16, 197, 768), np.array(0, I), 1),                 # ViT class token
+    ((8, 8400, 4), rng(1).integers(-8400, 8400, (300,)).astype(I), 1),
+    ((5, 6, 7), np.array([[0, -1], [4, 2]], I), 0),
+    ((5, 6, 7), np.array([6, 0, -7], I), -1),
+    ((1000, 3), rng(2).integers(-1000, 1000, (BIG,)).astype(I), 0),
+    ((4, 5), np.zeros((0,), I), 1),
+])
+def test_gather(gpu, dtype, shape, idx, axis):
+    x = _data(shape, dtype, seed=3)
+    assert_parity("Gather", [x, idx], [(_gather_shape(shape, idx.shape, axis), dtype)], {"axis": axis}, **EXACT)
+
+
+def test_gather_out_of_range(gpu):
+    x = randn((6, 5))
+    assert_same_error("Gather", [x, np.array([0, 6], I)], [((2, 5), F)])
+    assert_same_error("Gather", [x, np.array([-6, 0], I)], [((6, 2), F)], {"axis": 1})
+    big = rng(4).integers(0, 6, (BIG,)).astype(I)
+    big[7777] = 6
+    assert_same_error("Gather", [x, big], [((BIG, 5), F)])
+    big[7777] = -7
+    assert_same_error("Gather", [x, big], [((BIG, 5), F)])
+    # the error flag is consumed: the next good call passes
+    big[7777] = 1
+    assert_parity("Gather", [x, big], [((BIG, 5), F)], **EXACT)
+    # nothing is checked when the outer extent is empty (src/kernels/gather.cpp:31)
+    assert_parity("Gather", [np.zeros((0, 5), F), np.array([9], I)], [((0, 1), F)], {"axis": 1})
+    assert_same_error("Gather", [x, np.array([0.0], F)], [((1, 5), F)])
+    assert_same_error("Gather", [x, np.array([0], I)], [((1, 6), F)])
+    assert_same_error("Gather", [x, np.array([0], I)], [((1, 5), F)], {"axis": 2})
+
+
+@pytest.mark.parametrize("dtype", [F, I])
+@pytest.mark.parametrize("shape,idx_shape,axis", [
+    ((4, 5, 6), (4, 3, 6), 1), ((4, 5, 6), (2, 5, 6), 0), ((4, 5, 6), (4, 5, 9), -1), ((7,), (12,), 0),
+    ((3, 4), (2, 3), 1), ((100, 100), (100, 100), 0),
+])
+def test_gather_elements(gpu, dtype, shape, idx_shape, axis):
+    x = _data(shape, dtype, seed=5)
+    dim = shape[axis]
+    idx = rng(6).integers(-dim, dim, idx_shape).astype(I)
+    assert_parity("GatherElements", [x, idx], [(idx_shape, dtype)], {"axis": axis}, **EXACT)
+
+
+def test_gather_elements_errors(gpu):
+    x = randn((4, 5))
+    assert_same_error("GatherElements", [x, np.array([[5]], I)], [((1, 1), F)])
+    assert_same_error("GatherElements", [x, np.zeros((5, 1), I)], [((5, 1), F)])
+    idx = rng(7).integers(0, 5, (4, 3000)).astype(I)  # 96 KB: device-checked
+    idx[3, 2999] = -6
+    assert_same_error("GatherElements", [randn((4, 5)), idx], [((4, 3000), F)])
+    idx[3, 2999] = -5
+    assert_parity("GatherElements", [randn((4, 5)), idx], [((4, 3000), F)], **EXACT)
+    assert_same_error("GatherElements", [x.astype(B), np.zeros((4, 1), I)], [((4, 1), B)])
+
+
+@pytest.mark.parametrize("dtype", [F, I, B])
+def test_scatter_nd(gpu, dtype):
+    data = _data((4, 5, 6), dtype, seed=8)
+    # k = 1: whole [5, 6] slices, with duplicates (last wins) and negatives
+    idx = np.array([[1], [-1], [1], [0]], I)
+    upd = _data((4, 5, 6), dtype, seed=9)
+    assert_parity("ScatterND", [data, idx, upd], [((4, 5, 6), dtype)], **EXACT)
+    # k = 2: rows
+    idx = np.array([[[0, 1], [3, -2]], [[0, 1], [2, 4]]], I)
+    upd = _data((2, 2, 6), dtype, seed=10)
+    assert_parity("ScatterND", [data, idx, upd], [((4, 5, 6), dtype)], **EXACT)
+    # k = rank: single elements, many duplicates
+    idx = rng(11).integers(-2, 2, (500, 3)).astype(I)
+    upd = _data((500,), dtype, seed=12)
+    assert_parity("ScatterND", [data, idx, upd], [((4, 5, 6), dtype)], **EXACT)
+
+
+def test_scatter_nd_large_and_errors(gpu):
+    data = randn((3000, 8))
+    idx = rng(13).integers(0, 3000, (6000, 1)).astype(I)  # 48 KB
+    upd = randn((6000, 8), seed=14)
+    assert_parity("ScatterND", [data, idx, upd], [((3000, 8), F)], **EXACT)
+    idx = rng(15).integers(-3000, 3000, (9000, 1)).astype(I)  # 72 KB: device-checked
+    upd = randn((9000, 8), seed=16)
+    assert_parity("ScatterND", [data, idx, upd], [((3000, 8), F)], **EXACT)
+    idx[8000, 0] = 3000
+    assert_same_error("ScatterND", [data, idx, upd], [((3000, 8), F)])
+    assert_same_error("ScatterND", [data, np.array([[3000]], I), randn((1, 8))], [((3000, 8), F)])
+    assert_same_error("ScatterND", [data, np.array([[0, 0, 0]], I), randn((1,))], [((3000, 8), F)])
+    assert_same_error("ScatterND", [data, np.array([[0]], I), randn((1, 7))], [((3000, 8), F)])
+
+
+def test_shape(gpu):
+    x = randn((2, 3, 4, 5))
+    assert_parity("Shape", [x], [((4,), I)], **EXACT)
+    assert_parity("Shape", [x], [((2,), I)], {"start": 1, "end": -1}, **EXACT)
+    assert_parity("Shape", [x], [((1,), I)], {"start": -1}, **EXACT)
+    assert_parity("Shape", [x], [((0,), I)], {"start": 3, "end": 1}, **EXACT)
+    assert_parity("Shape", [x.astype(B)], [((4,), I)], {"start": -10, "end": 10}, **EXACT)
+    assert_parity("Shape", [np.array(1.0, F)], [((0,), I)], **EXACT)
+    assert_same_error("Shape", [x], [((3,), I)])
+    assert_same_error("Shape", [x], [((4,), F)])
+
+
+def test_shape_feeds_control_reads(gpu):
+    """Shape's output is read back by a later row (Reshape) without a device
+    round trip; the values must be the ones the kernel writes."""
+    from nert_amd.device import DeviceArray, run_node
+
+    x = DeviceArray.from_host(randn((6, 4)))
+    shp = DeviceArray.from_host(np.zeros((2,), I))
+    run_node("Shape", [x], [shp], {}, "s")
+    y = DeviceArray.from_host(np.zeros((6, 4), F))
+    run_node("Reshape", [x, shp], [y], {}, "r")
+    np.testing.assert_array_equal(shp.to_host(), [6, 4])
+    np.testing.assert_array_equal(y.to_host(), x.to_host())
+
+
+def test_constant_of_shape(gpu):
+    assert_parity("ConstantOfShape", [np.array([2, 3], I)], [((2, 3), F)], **EXACT)
+    assert_parity("ConstantOfShape", [np.array([4], I)], [((4,), F)], {"value": 2.5}, **EXACT)
+    assert_parity("ConstantOfShape", [np.array([3, 1, 2], I)], [((3, 1, 2), I)], {"value": -7}, **EXACT)
+    assert_parity("ConstantOfShape", [np.array([5], I)], [((5,), B)], {"value": True}, **EXACT)
+    assert_parity("ConstantOfShape", [np.array([0, 3], I)], [((0, 3), F)], **EXACT)
+    assert_parity("ConstantOfShape", [np.array([1 << 20], I)], [((1 << 20,), F)], {"value": 1.0}, **EXACT)
+    assert_same_error("ConstantOfShape", [np.array([2], I)], [((2,), I)], {"value": 1.0})
+    assert_same_error("ConstantOfShape", [np.array([-1], I)], [((1,), F)])
+    assert_same_error("ConstantOfShape", [np.array([2], I)], [((3,), F)])
+
+
+def test_range(gpu):
+    def f(v):
+        return np.array(v, F)
+
+    def i(v):
+        return np.array(v, I)
+
+    def n(start, limit, delta):  # the length ONNX Range defines, from float32 operands
+        return max(int(np.ceil((np.float64(f(limit)) - np.float64(f(start))) / np.float64(f(delta)))), 0)
+
+    for start, limit, delta in [(0.5, 10.0, 0.3), (3.0, -4.0, -0.7), (1e6, 1e6 + 3e4, 0.37), (-2.0, 2.0, 0.1)]:
+        assert_parity("Range", [f(start), f(limit), f(delta)], [((n(start, limit, delta),), F)], **EXACT)
+    assert_parity("Range", [i(-5), i(100), i(7)], [((15,), I)], **EXACT)
+    assert_parity("Range", [i(10), i(-10), i(-3)], [((7,), I)], **EXACT)
+    assert_parity("Range", [i(10), i(1), i(1)], [((0,), I)], **EXACT)
+    assert_same_error("Range", [i(0), i(10), i(0)], [((0,), I)])
+    assert_same_error("Range", [i(0), i(10), i(3)], [((3,), I)])
+    assert_same_error("Range", [f(0), i(10), f(3)], [((4,), F)])
+    assert_same_error("Range", [f(0), f(10), np.array([1, 2], F)], [((4,), F)])
+
+
+@pytest.mark.parametrize("dtype", [F, I, B])
+def test_eye_like(gpu, dtype):
+    for shape, k in [((4, 4), 0), ((3, 7), 2), ((6, 2), -3), ((5, 5), 9), ((300, 200), -1)]:
+        assert_parity("EyeLike", [np.zeros(shape, F)], [(shape, dtype)], {"k": k}, **EXACT)
+    assert_same_error("EyeLike", [np.zeros((2, 3, 4), F)], [((2, 3, 4), dtype)])
