@@ -271,6 +271,12 @@ int nert_hip_gather_elements(int elem_size, const void* x, const int64_t* indice
  * (src/kernels/scatter_nd.cpp:31-118). */
 int nert_hip_scatter_nd(int elem_size, const void* data, const int64_t* indices, const void* updates, void* out,
                         int data_rank, const int64_t* data_dims, int64_t slice_count, int k, void* stream);
+/* TopK (largest, sorted) along `dim` of x viewed as [outer, dim, inner]:
+ * values [outer, k, inner] f32 and int64 indices, ordered by value
+ * descending and equal values by ascending index, -0.0 equal to +0.0
+ * (src/kernels/top_k.cpp:125-141). Requires 0 < k <= dim < 2^32. */
+int nert_hip_topk_f32(const float* x, float* values, int64_t* indices, int64_t outer, int64_t dim, int64_t inner,
+                      int64_t k, void* stream);
 /* Range: y[i] = start + i * delta, float32 rounded after the product and
  * after the sum (src/kernels/range.cpp:62-64), or int64. */
 int nert_hip_range(int dtype, double fstart, double fdelta, int64_t istart, int64_t idelta, void* y, int64_t count,

@@ -98,6 +98,7 @@ NERT_HIP_ROW(Pad);
 NERT_HIP_ROW(Gather);
 NERT_HIP_ROW(GatherElements);
 NERT_HIP_ROW(ScatterND);
+NERT_HIP_ROW(TopK);
 NERT_HIP_ROW(Shape);
 NERT_HIP_ROW(ConstantOfShape);
 NERT_HIP_ROW(Range);

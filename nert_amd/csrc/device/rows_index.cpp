@@ -1,7 +1,7 @@
-// Index and generator rows: Gather, GatherElements, ScatterND, Shape,
+// Index and generator rows: Gather, GatherElements, ScatterND, TopK, Shape,
 // ConstantOfShape, Range, EyeLike. Validation mirrors
-// src/kernels/{gather,gather_elements,scatter_nd,shape,constant_of_shape,
-// range,eye_like}.cpp.
+// src/kernels/{gather,gather_elements,scatter_nd,top_k,shape,
+// constant_of_shape,range,eye_like}.cpp.
 //
 // Out-of-range indices throw like the reference. When the indices are in the
 // host shadow (initializers, small uploads) they are checked on the host
@@ -244,6 +244,82 @@ NERT_HIP_ROW(ScatterND) {
     if (!on_host) {
         ThrowOnDeviceFlag(context, "index out of range");
     }
+}
+
+// src/kernels/top_k.cpp:38-142
+NERT_HIP_ROW(TopK) {
+    const std::string context = "TopK (node '" + node.name + "')";
+    if (inputs.size() != 2 || outputs.size() != 2) {
+        throw InferenceException(context + ": expected an input, a K input, and values/indices outputs");
+    }
+    const TensorView& in = inputs[0];
+    const TensorView& k_view = inputs[1];
+    const TensorView& values = outputs[0];
+    const TensorView& indices = outputs[1];
+    if (in.dtype != DataType::Float32) {
+        throw InferenceException(context + ": TopK input must be float32");
+    }
+    if (values.dtype != DataType::Float32) {
+        throw InferenceException(context + ": TopK values must be float32");
+    }
+    if (indices.dtype != DataType::Int64) {
+        throw InferenceException(context + ": TopK indices must be int64");
+    }
+    if (k_view.dtype != DataType::Int64) {
+        throw InferenceException(context + ": TopK requires a K input");
+    }
+    if (IntAttrC(node, "largest", 1, context) != 1) {
+        throw InferenceException(context + ": TopK 'largest' must be 1 here");
+    }
+    if (IntAttrC(node, "sorted", 1, context) != 1) {
+        throw InferenceException(context + ": TopK 'sorted' must be 1 here");
+    }
+    if (CountNonNeg(k_view.dims, context) != 1) {
+        throw InferenceException(context + ": TopK K input must be a scalar Int64 constant");
+    }
+    if (k_view.data == nullptr) {
+        throw InferenceException(context + ": null K buffer");
+    }
+    const int64_t k = ReadInt64(k_view, 1, context)[0];
+    if (k <= 0) {
+        throw InferenceException(context + ": TopK K must be positive");
+    }
+    const int64_t rank = static_cast<int64_t>(in.dims.size());
+    int64_t axis = IntAttrC(node, "axis", -1, context);
+    if (rank == 0 || axis < -rank || axis >= rank) {
+        throw InferenceException(context + ": TopK axis is out of range");
+    }
+    if (axis < 0) {
+        axis += rank;
+    }
+    const int64_t dim = in.dims[static_cast<size_t>(axis)];
+    if (k > dim) {
+        throw InferenceException(context + ": TopK K exceeds the axis dim");
+    }
+    std::vector<int64_t> expected = in.dims;
+    expected[static_cast<size_t>(axis)] = k;
+    if (values.dims != expected || indices.dims != expected) {
+        throw InferenceException(context + ": output shapes do not match the selected K");
+    }
+    const int64_t values_count = CountNonNeg(values.dims, context);
+    (void)CountNonNeg(in.dims, context);
+    if (values_count > 0 && (in.data == nullptr || values.data == nullptr || indices.data == nullptr)) {
+        throw InferenceException(context + ": null buffer");
+    }
+    int64_t outer = 1;
+    for (int64_t i = 0; i < axis; ++i) {
+        outer *= in.dims[static_cast<size_t>(i)];
+    }
+    int64_t inner = 1;
+    for (int64_t i = axis + 1; i < rank; ++i) {
+        inner *= in.dims[static_cast<size_t>(i)];
+    }
+    if (values_count > 0) {
+        CheckStatus(nert_hip_topk_f32(static_cast<const float*>(in.data), static_cast<float*>(values.data),
+                                      static_cast<int64_t*>(indices.data), outer, dim, inner, k, Stream()),
+                    context);
+    }
+    AfterRow(outputs, context);
 }
 
 // src/kernels/shape.cpp:40-72

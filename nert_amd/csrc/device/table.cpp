@@ -78,6 +78,7 @@ nert::KernelFn FindRow(const std::string& op_type) {
         {"Gather", &Gather},
         {"GatherElements", &GatherElements},
         {"ScatterND", &ScatterND},
+        {"TopK", &TopK},
         {"Shape", &Shape},
         {"ConstantOfShape", &ConstantOfShape},
         {"Range", &Range},

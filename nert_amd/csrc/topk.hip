@@ -1,0 +1,368 @@
+// TopK (largest = 1, sorted = 1) along an axis of a float32 tensor.
+//
+// Order (src/kernels/top_k.cpp:125-134): value descending, equal values by
+// ascending index (-0.0 and +0.0 compare equal). Every element gets a unique
+// 64-bit key
+//     key = orderable(value) << 32 | (0xFFFFFFFF - index)
+// where orderable() maps float bits to an unsigned integer with the float
+// order (-0.0 folded onto +0.0, NaN above +inf), so "descending key" is
+// exactly the reference's order and there are no ties left.
+//
+// Rows of up to kSmallRow elements sort in one workgroup's LDS. Longer rows
+// (the detector's [8, 672000], K = 300) run a radix select over the key,
+// 8 bits per pass from the top, with many workgroups per row: each pass builds
+// a 256-bin histogram of the keys that still match the chosen prefix, and a
+// one-block-per-row scan picks the bin holding the K-th largest key. When
+// that bin is needed whole the threshold is final and later passes return at
+// once. Keys >= threshold (exactly K per row) are collected, sorted in
+// 4096-key LDS runs, merged by per-key binary search, and written out.
+
+#include "common.hpp"
+#include "../../include/nert_hip.h"
+
+namespace nert_hip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kSmallRow = 4096;
+constexpr int kRun = 4096;
+
+struct RowGeom {
+    int64_t dim;
+    int64_t inner;
+    int64_t k;
+};
+
+__device__ __forceinline__ int64_t RowBase(int64_t row, const RowGeom& g) {
+    const int64_t o = row / g.inner;
+    const int64_t n = row - o * g.inner;
+    return o * g.dim * g.inner + n;
+}
+
+__device__ __forceinline__ uint64_t KeyOf(float v, int64_t index) {
+    uint32_t b = __float_as_uint(v);
+    if ((b & 0x7FFFFFFFu) == 0) {
+        b = 0; // -0.0 == +0.0
+    }
+    uint32_t ord;
+    if ((b & 0x7FFFFFFFu) > 0x7F800000u) {
+        ord = 0xFFFFFFFFu; // NaN: above +inf
+    } else {
+        ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    }
+    return (static_cast<uint64_t>(ord) << 32) | static_cast<uint64_t>(0xFFFFFFFFu - static_cast<uint32_t>(index));
+}
+
+__device__ __forceinline__ int64_t IndexOf(uint64_t key) {
+    return static_cast<int64_t>(0xFFFFFFFFu - static_cast<uint32_t>(key & 0xFFFFFFFFu));
+}
+
+// Descending bitonic sort of n (a power of two) keys in LDS.
+__device__ void BitonicDesc(uint64_t* s, int n) {
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < n / 2; i += blockDim.x) {
+                const int lo = 2 * stride * (i / stride) + (i % stride);
+                const int hi = lo + stride;
+                const bool up = (lo & size) == 0;
+                const uint64_t a = s[lo];
+                const uint64_t b = s[hi];
+                if ((a < b) == up) {
+                    s[lo] = b;
+                    s[hi] = a;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+__device__ __forceinline__ void WriteOut(const float* x, float* values, int64_t* indices, int64_t row, int64_t t,
+                                         uint64_t key, const RowGeom& g) {
+    const int64_t idx = IndexOf(key);
+    const int64_t o = row / g.inner;
+    const int64_t n = row - o * g.inner;
+    const int64_t dst = (o * g.k + t) * g.inner + n;
+    values[dst] = x[RowBase(row, g) + idx * g.inner];
+    indices[dst] = idx;
+}
+
+// One workgroup per row: the whole row sorts in LDS.
+__global__ void __launch_bounds__(kThreads) SmallRowKernel(const float* __restrict__ x, float* __restrict__ values,
+                                                           int64_t* __restrict__ indices, RowGeom g, int n_pow2) {
+    __shared__ uint64_t s[kSmallRow];
+    const int64_t row = blockIdx.x;
+    const int64_t base = RowBase(row, g);
+    for (int i = threadIdx.x; i < n_pow2; i += blockDim.x) {
+        s[i] = i < g.dim ? KeyOf(x[base + i * g.inner], i) : 0;
+    }
+    __syncthreads();
+    BitonicDesc(s, n_pow2);
+    for (int t = threadIdx.x; t < g.k; t += blockDim.x) {
+        WriteOut(x, values, indices, row, t, s[t], g);
+    }
+}
+
+// ---- long rows: radix select ----------------------------------------------
+
+struct SelectState {
+    uint64_t prefix; // chosen high bits of the threshold key
+    int64_t remaining; // keys still to take from inside the prefix
+    int32_t done;
+    int32_t count; // collected keys
+};
+
+__global__ void InitSelectKernel(SelectState* st, uint32_t* hist, int64_t rows, int64_t k) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < rows * 256; i += stride) {
+        hist[i] = 0;
+        if (i < rows) {
+            st[i].prefix = 0;
+            st[i].remaining = k;
+            st[i].done = 0;
+            st[i].count = 0;
+        }
+    }
+}
+
+__global__ void __launch_bounds__(kThreads) HistKernel(const float* __restrict__ x, RowGeom g, int64_t chunk,
+                                                       int chunks, const SelectState* __restrict__ st,
+                                                       uint32_t* __restrict__ hist, int pass) {
+    const int64_t row = blockIdx.x / chunks;
+    const int c = blockIdx.x - static_cast<int>(row * chunks);
+    const SelectState s = st[row];
+    if (s.done) {
+        return;
+    }
+    __shared__ uint32_t h[256];
+    h[threadIdx.x] = 0;
+    __syncthreads();
+    const int shift = 56 - 8 * pass;
+    const int64_t begin = c * chunk;
+    int64_t end = begin + chunk;
+    if (end > g.dim) {
+        end = g.dim;
+    }
+    const int64_t base = RowBase(row, g);
+    for (int64_t i = begin + threadIdx.x; i < end; i += blockDim.x) {
+        const uint64_t key = KeyOf(x[base + i * g.inner], i);
+        // pass 0 has no prefix to match (a 64-bit shift would be undefined)
+        const bool match = pass == 0 || (key >> (shift + 8)) == (s.prefix >> (shift + 8));
+        if (match) {
+            atomicAdd(&h[(key >> shift) & 0xFF], 1u);
+        }
+    }
+    __syncthreads();
+    const uint32_t v = h[threadIdx.x];
+    if (v != 0) {
+        atomicAdd(&hist[row * 256 + threadIdx.x], v);
+    }
+}
+
+// One wave per row: finds the bin holding the remaining-th largest key.
+__global__ void ScanKernel(SelectState* st, uint32_t* hist, int pass) {
+    const int64_t row = blockIdx.x;
+    SelectState s = st[row];
+    uint32_t* h = hist + row * 256;
+    if (s.done) {
+        return;
+    }
+    __shared__ uint32_t bins[256];
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) {
+        bins[i] = h[i];
+        h[i] = 0; // ready for the next pass
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int shift = 56 - 8 * pass;
+        int64_t before = 0;
+        for (int d = 255; d >= 0; --d) {
+            const int64_t n = bins[d];
+            if (before + n >= s.remaining) {
+                s.prefix |= static_cast<uint64_t>(d) << shift;
+                s.remaining -= before;
+                if (n == s.remaining) {
+                    s.done = 1;
+                }
+                break;
+            }
+            before += n;
+        }
+        st[row] = s;
+    }
+}
+
+__global__ void __launch_bounds__(kThreads) CollectKernel(const float* __restrict__ x, RowGeom g, int64_t chunk,
+                                                          int chunks, SelectState* st, uint64_t* __restrict__ cand) {
+    const int64_t row = blockIdx.x / chunks;
+    const int c = blockIdx.x - static_cast<int>(row * chunks);
+    const uint64_t threshold = st[row].prefix;
+    const int64_t begin = c * chunk;
+    int64_t end = begin + chunk;
+    if (end > g.dim) {
+        end = g.dim;
+    }
+    const int64_t base = RowBase(row, g);
+    for (int64_t i = begin + threadIdx.x; i < end; i += blockDim.x) {
+        const uint64_t key = KeyOf(x[base + i * g.inner], i);
+        if (key >= threshold) {
+            const int pos = atomicAdd(&st[row].count, 1);
+            if (pos < g.k) {
+                cand[row * g.k + pos] = key;
+            }
+        }
+    }
+}
+
+// Sorts runs of kRun candidates (descending) in LDS, in place.
+__global__ void __launch_bounds__(kThreads) SortRunsKernel(uint64_t* cand, int64_t k, int runs_per_row, int n_pow2) {
+    __shared__ uint64_t s[kRun];
+    const int64_t row = blockIdx.x / runs_per_row;
+    const int r = blockIdx.x - static_cast<int>(row * runs_per_row);
+    uint64_t* p = cand + row * k + static_cast<int64_t>(r) * kRun;
+    int64_t len = k - static_cast<int64_t>(r) * kRun;
+    if (len > kRun) {
+        len = kRun;
+    }
+    for (int i = threadIdx.x; i < n_pow2; i += blockDim.x) {
+        s[i] = i < len ? p[i] : 0;
+    }
+    __syncthreads();
+    BitonicDesc(s, n_pow2);
+    for (int i = threadIdx.x; i < len; i += blockDim.x) {
+        p[i] = s[i];
+    }
+}
+
+// Merges pairs of sorted runs of `width`: a key's new place is its place in
+// its run plus the number of keys of the partner run greater than it.
+__global__ void MergeKernel(const uint64_t* __restrict__ src, uint64_t* __restrict__ dst, int64_t rows, int64_t k,
+                            int64_t width) {
+    const int64_t total = rows * k;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < total; e += stride) {
+        const int64_t row = e / k;
+        const int64_t i = e - row * k;
+        const int64_t run = i / width;
+        const int64_t pair_base = (run & ~int64_t{1}) * width;
+        const int64_t pos = i - run * width;
+        const int64_t partner = run ^ 1;
+        int64_t p_begin = partner * width;
+        int64_t p_end = p_begin + width;
+        if (p_end > k) {
+            p_end = k;
+        }
+        const uint64_t key = src[e];
+        int64_t greater = 0;
+        if (p_begin < k) {
+            // partner is descending: count of keys > key
+            int64_t lo = p_begin;
+            int64_t hi = p_end;
+            const uint64_t* q = src + row * k;
+            while (lo < hi) {
+                const int64_t mid = (lo + hi) >> 1;
+                if (q[mid] > key) {
+                    lo = mid + 1;
+                } else {
+                    hi = mid;
+                }
+            }
+            greater = lo - p_begin;
+        }
+        dst[row * k + pair_base + pos + greater] = key;
+    }
+}
+
+__global__ void EmitKernel(const float* __restrict__ x, const uint64_t* __restrict__ sorted, float* values,
+                           int64_t* indices, int64_t rows, RowGeom g) {
+    const int64_t total = rows * g.k;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < total; e += stride) {
+        const int64_t row = e / g.k;
+        WriteOut(x, values, indices, row, e - row * g.k, sorted[e], g);
+    }
+}
+
+int PowTwoAtLeast(int64_t n) {
+    int p = 1;
+    while (p < n) {
+        p <<= 1;
+    }
+    return p;
+}
+
+} // namespace
+} // namespace nert_hip
+
+using namespace nert_hip;
+
+extern "C" {
+
+int nert_hip_topk_f32(const float* x, float* values, int64_t* indices, int64_t outer, int64_t dim, int64_t inner,
+                      int64_t k, void* stream) {
+    return Guard([&] {
+        if (k <= 0 || k > dim || dim > 0xFFFFFFFFll) {
+            throw Error("topk: need 0 < k <= dim < 2^32");
+        }
+        const int64_t rows = outer * inner;
+        if (rows <= 0) {
+            return;
+        }
+        hipStream_t s = StreamOr(stream);
+        const RowGeom g{dim, inner, k};
+        if (dim <= kSmallRow) {
+            if (rows > 0x7FFFFFFF) {
+                throw Error("topk: too many rows");
+            }
+            SmallRowKernel<<<static_cast<unsigned>(rows), kThreads, 0, s>>>(x, values, indices, g, PowTwoAtLeast(dim));
+            CheckLaunch("topk small-row launch");
+            return;
+        }
+        // Long rows: about 2048 workgroups over all rows, >= 4096 keys each.
+        int64_t chunks = (2048 + rows - 1) / rows;
+        const int64_t max_chunks = (dim + 4095) / 4096;
+        if (chunks > max_chunks) {
+            chunks = max_chunks;
+        }
+        if (chunks < 1) {
+            chunks = 1;
+        }
+        const int64_t chunk = (dim + chunks - 1) / chunks;
+        if (rows * chunks > 0x7FFFFFFF) {
+            throw Error("topk: too many rows");
+        }
+        // Workspace: state | histograms | two candidate buffers.
+        const int64_t st_bytes = (rows * static_cast<int64_t>(sizeof(SelectState)) + 255) / 256 * 256;
+        const int64_t hist_bytes = (rows * 256 * 4 + 255) / 256 * 256;
+        const int64_t cand_bytes = (rows * k * 8 + 255) / 256 * 256;
+        auto* ws = static_cast<uint8_t*>(Workspace(st_bytes + hist_bytes + 2 * cand_bytes, s));
+        auto* st = reinterpret_cast<SelectState*>(ws);
+        auto* hist = reinterpret_cast<uint32_t*>(ws + st_bytes);
+        auto* cand = reinterpret_cast<uint64_t*>(ws + st_bytes + hist_bytes);
+        auto* cand2 = reinterpret_cast<uint64_t*>(ws + st_bytes + hist_bytes + cand_bytes);
+
+        InitSelectKernel<<<GridFor(rows * 256, 256, 4096), 256, 0, s>>>(st, hist, rows, k);
+        const unsigned blocks = static_cast<unsigned>(rows * chunks);
+        for (int pass = 0; pass < 8; ++pass) {
+            HistKernel<<<blocks, kThreads, 0, s>>>(x, g, chunk, static_cast<int>(chunks), st, hist, pass);
+            ScanKernel<<<static_cast<unsigned>(rows), 64, 0, s>>>(st, hist, pass);
+        }
+        CollectKernel<<<blocks, kThreads, 0, s>>>(x, g, chunk, static_cast<int>(chunks), st, cand);
+        const int64_t runs = (k + kRun - 1) / kRun;
+        const int run_pow2 = PowTwoAtLeast(k < kRun ? k : kRun);
+        SortRunsKernel<<<static_cast<unsigned>(rows * runs), kThreads, 0, s>>>(cand, k, static_cast<int>(runs),
+                                                                             run_pow2);
+        uint64_t* src = cand;
+        uint64_t* dst = cand2;
+        for (int64_t width = kRun; width < k; width *= 2) {
+            MergeKernel<<<GridFor(rows * k, 256, 16384), 256, 0, s>>>(src, dst, rows, k, width);
+            uint64_t* t = src;
+            src = dst;
+            dst = t;
+        }
+        EmitKernel<<<GridFor(rows * k, 256, 16384), 256, 0, s>>>(x, src, values, indices, rows, g);
+        CheckLaunch("topk launch");
+    });
+}
+
+} // extern "C"

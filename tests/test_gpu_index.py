@@ -184,3 +184,46 @@ def test_eye_like(gpu, dtype):
     for shape, k in [((4, 4), 0), ((3, 7), 2), ((6, 2), -3), ((5, 5), 9), ((300, 200), -1)]:
         assert_parity("EyeLike", [np.zeros(shape, F)], [(shape, dtype)], {"k": k}, **EXACT)
     assert_same_error("EyeLike", [np.zeros((2, 3, 4), F)], [((2, 3, 4), dtype)])
+
+
+def _topk_case(x, k, axis=-1):
+    out = list(x.shape)
+    out[axis] = k
+    out = tuple(out)
+    assert_parity("TopK", [x, np.array(k, I)], [(out, F), (out, I)], {"axis": axis}, **EXACT)
+
+
+@pytest.mark.parametrize("shape,k,axis", [
+    ((2, 4), 2, -1), ((1000, 80), 5, 1), ((50, 7, 3), 4, 1), ((4096,), 4096, 0), ((3, 4097), 17, -1),
+])
+def test_topk_rows(gpu, shape, k, axis):
+    _topk_case(randn(shape, seed=21), k, axis)
+    ties = rng(22).integers(-3, 4, shape).astype(F)  # many equal values: index order decides
+    _topk_case(ties, k, axis)
+
+
+def test_topk_detector_shape(gpu):
+    """The detector's score selection: [8, 672000] with K = 300 (radix select)."""
+    x = randn((8, 672000), seed=23)
+    _topk_case(x, 300)
+    _topk_case(rng(24).integers(0, 50, (8, 672000)).astype(F), 300)  # ~13k-way ties per value
+
+
+def test_topk_long_rows(gpu):
+    _topk_case(randn((2, 20000), seed=25), 5000)       # sorted runs + merge passes
+    _topk_case(randn((1, 9000), seed=26), 9000)        # K = dim on a long row
+    _topk_case(randn((3, 6000, 2), seed=27), 100, 1)   # strided rows
+    z = np.zeros((2, 10000), F)
+    z[:, 1::2] = -0.0
+    z[1, 7777] = 1e-30
+    _topk_case(z, 64)                                   # -0.0 ties with +0.0
+
+
+def test_topk_errors(gpu):
+    x = randn((3, 5))
+    assert_same_error("TopK", [x, np.array(6, I)], [((3, 6), F), ((3, 6), I)])
+    assert_same_error("TopK", [x, np.array(0, I)], [((3, 0), F), ((3, 0), I)])
+    assert_same_error("TopK", [x, np.array(2, I)], [((3, 2), F), ((3, 2), I)], {"largest": 0})
+    assert_same_error("TopK", [x, np.array(2, I)], [((3, 2), F), ((3, 2), I)], {"sorted": 0})
+    assert_same_error("TopK", [x, np.array(2, I)], [((2, 5), F), ((2, 5), I)], {"axis": 2})
+    assert_same_error("TopK", [x, np.array([2, 2], I)], [((3, 2), F), ((3, 2), I)])
