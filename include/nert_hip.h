@@ -287,6 +287,49 @@ int nert_hip_store_i64(int64_t* y, const int64_t* values, int count, void* strea
 /* EyeLike: ones where col - row == k (src/kernels/eye_like.cpp:54-79). */
 int nert_hip_eye_like(int dtype, void* y, int64_t rows, int64_t cols, int64_t k, void* stream);
 
+/* ---- Resampling ------------------------------------------------------------ */
+
+enum nert_resize_code {
+    /* coordinate_transformation_mode */
+    NERT_RESIZE_HALF_PIXEL = 0,
+    NERT_RESIZE_PYTORCH_HALF_PIXEL = 1,
+    NERT_RESIZE_ALIGN_CORNERS = 2,
+    NERT_RESIZE_ASYMMETRIC = 3,
+    /* nearest_mode */
+    NERT_RESIZE_ROUND_PREFER_FLOOR = 0,
+    NERT_RESIZE_ROUND_PREFER_CEIL = 1,
+    NERT_RESIZE_FLOOR = 2,
+    NERT_RESIZE_CEIL = 3
+};
+/* Resize of a dense rank <= 8 tensor; scales[d] is the per-axis scale the
+ * coordinate transform divides by (src/kernels/resize.cpp:48-123,230-255).
+ * linear = 0: nearest (float32 or int64); 1: linear (float32). */
+int nert_hip_resize(int dtype, const void* x, void* y, int rank, const int64_t* in_dims, const int64_t* out_dims,
+                    const double* scales, int linear, int transform, int nearest, void* stream);
+
+enum nert_grid_padding { NERT_GRID_ZEROS = 0, NERT_GRID_BORDER = 1, NERT_GRID_REFLECTION = 2 };
+/* GridSample: X [n,c,h,w], grid [n,ho,wo,2] (x, y in [-1, 1]) -> [n,c,ho,wo]
+ * (src/kernels/grid_sample.cpp:41-71,132-157). nearest = 0: bilinear. */
+int nert_hip_grid_sample_f32(const float* x, const float* grid, float* y, int64_t n, int64_t c, int64_t h, int64_t w,
+                             int64_t ho, int64_t wo, int nearest, int padding, int align_corners, void* stream);
+
+/* ---- Contractions ------------------------------------------------------------
+ * Einsum over one (b = NULL) or two float32 operands, resolved by the caller
+ * into labels: y is dense over the output labels (out_size, row-major); each
+ * element sums, in double, the product of the operands over the summed labels
+ * (sum_size, odometer order, last fastest). Strides are per label and operand,
+ * in elements; a repeated label (diagonal) carries the sum of its strides
+ * (src/kernels/einsum.cpp:205-258). At most 16 labels of each kind. */
+int nert_hip_einsum_f32(const float* a, const float* b, float* y, int n_out, const int64_t* out_size,
+                        const int64_t* out_stride_a, const int64_t* out_stride_b, int n_sum, const int64_t* sum_size,
+                        const int64_t* sum_stride_a, const int64_t* sum_stride_b, void* stream);
+/* 2-D ConvTranspose, NCHW, weight [C, M/group, kh, kw], optional bias [M].
+ * geom = {batch, C, M, group, in_h, in_w, out_h, out_w, kh, kw, stride_h,
+ * stride_w, pad_top, pad_left, dilation_h, dilation_w}; strides > 0
+ * (src/kernels/conv_transpose.cpp:76-188). */
+int nert_hip_conv_transpose_f32(const float* x, const float* w, const float* bias, float* y, const int64_t* geom,
+                                void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -104,5 +104,11 @@ NERT_HIP_ROW(ConstantOfShape);
 NERT_HIP_ROW(Range);
 NERT_HIP_ROW(EyeLike);
 
+// rows_contract.cpp
+NERT_HIP_ROW(Resize);
+NERT_HIP_ROW(GridSample);
+NERT_HIP_ROW(Einsum);
+NERT_HIP_ROW(ConvTranspose);
+
 } // namespace rows
 } // namespace nert_hip

@@ -83,6 +83,10 @@ nert::KernelFn FindRow(const std::string& op_type) {
         {"ConstantOfShape", &ConstantOfShape},
         {"Range", &Range},
         {"EyeLike", &EyeLike},
+        {"Resize", &Resize},
+        {"GridSample", &GridSample},
+        {"Einsum", &Einsum},
+        {"ConvTranspose", &ConvTranspose},
     };
     const auto it = table.find(op_type);
     return it == table.end() ? nullptr : it->second;

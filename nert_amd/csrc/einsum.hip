@@ -1,0 +1,188 @@
+// Einsum over one or two float32 operands, and ConvTranspose.
+//
+// Einsum: the host resolves the equation into per-label extents and strides
+// (output labels, then summed labels in alphabetical order); one thread per
+// output element walks the summed labels as an odometer, last label
+// fastest, multiplying the operands in double and accumulating in double, so
+// each output sums its terms in the same order as the reference's odometer
+// over all labels (src/kernels/einsum.cpp:205-258) and rounds once.
+//
+// ConvTranspose: the reference scatters every input pixel into the output
+// (src/kernels/conv_transpose.cpp:160-188). Here each output element gathers
+// the (channel, tap) pairs that land on it: tap kh contributes when
+// oh + pad - kh * dilation is a non-negative multiple of the stride inside
+// the input. No atomics, one write per output; sums run in double.
+
+#include "common.hpp"
+#include "../../include/nert_hip.h"
+
+namespace nert_hip {
+namespace {
+
+constexpr int kMaxLabels = 16;
+
+struct EinsumArgs {
+    int n_out;
+    int n_sum;
+    int two;
+    int64_t out_size[kMaxLabels];
+    int64_t out_sa[kMaxLabels];
+    int64_t out_sb[kMaxLabels];
+    int64_t sum_size[kMaxLabels];
+    int64_t sum_sa[kMaxLabels];
+    int64_t sum_sb[kMaxLabels];
+    int64_t sum_total;
+};
+
+__global__ void EinsumKernel(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ y,
+                             EinsumArgs e, int64_t n) {
+#pragma clang fp contract(off)
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n; i += stride) {
+        int64_t rem = i;
+        int64_t oa = 0;
+        int64_t ob = 0;
+        for (int d = e.n_out - 1; d >= 0; --d) {
+            const int64_t c = rem % e.out_size[d];
+            rem /= e.out_size[d];
+            oa += c * e.out_sa[d];
+            ob += c * e.out_sb[d];
+        }
+        int64_t coord[kMaxLabels];
+        for (int d = 0; d < e.n_sum; ++d) {
+            coord[d] = 0;
+        }
+        double acc = 0.0;
+        for (int64_t step = 0; step < e.sum_total; ++step) {
+            double prod = 1.0;
+            prod = prod * static_cast<double>(a[oa]);
+            if (e.two) {
+                prod = prod * static_cast<double>(b[ob]);
+            }
+            acc += prod;
+            for (int d = e.n_sum - 1; d >= 0; --d) {
+                ++coord[d];
+                oa += e.sum_sa[d];
+                ob += e.sum_sb[d];
+                if (coord[d] < e.sum_size[d]) {
+                    break;
+                }
+                oa -= e.sum_sa[d] * e.sum_size[d];
+                ob -= e.sum_sb[d] * e.sum_size[d];
+                coord[d] = 0;
+            }
+        }
+        y[i] = static_cast<float>(acc);
+    }
+}
+
+struct ConvTArgs {
+    int64_t batch, in_c, out_c, group, in_h, in_w, out_h, out_w, k_h, k_w;
+    int64_t stride_h, stride_w, pad_h, pad_w, dil_h, dil_w;
+};
+
+__global__ void ConvTransposeKernel(const float* __restrict__ x, const float* __restrict__ w,
+                                    const float* __restrict__ bias, float* __restrict__ y, ConvTArgs p, int64_t n) {
+    const int64_t in_per_group = p.in_c / p.group;
+    const int64_t out_per_group = p.out_c / p.group;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n; i += stride) {
+        const int64_t ow = i % p.out_w;
+        const int64_t oh = (i / p.out_w) % p.out_h;
+        const int64_t m = (i / (p.out_w * p.out_h)) % p.out_c;
+        const int64_t b = i / (p.out_w * p.out_h * p.out_c);
+        const int64_t g = m / out_per_group;
+        const int64_t oc = m - g * out_per_group;
+        double acc = 0.0;
+        for (int64_t kh = 0; kh < p.k_h; ++kh) {
+            const int64_t th = oh + p.pad_h - kh * p.dil_h;
+            if (th < 0 || th % p.stride_h != 0) {
+                continue;
+            }
+            const int64_t ih = th / p.stride_h;
+            if (ih >= p.in_h) {
+                continue;
+            }
+            for (int64_t kw = 0; kw < p.k_w; ++kw) {
+                const int64_t tw = ow + p.pad_w - kw * p.dil_w;
+                if (tw < 0 || tw % p.stride_w != 0) {
+                    continue;
+                }
+                const int64_t iw = tw / p.stride_w;
+                if (iw >= p.in_w) {
+                    continue;
+                }
+                for (int64_t ic = 0; ic < in_per_group; ++ic) {
+                    const int64_t c = g * in_per_group + ic;
+                    const float xv = x[((b * p.in_c + c) * p.in_h + ih) * p.in_w + iw];
+                    const float wv = w[((c * out_per_group + oc) * p.k_h + kh) * p.k_w + kw];
+                    acc += static_cast<double>(xv) * static_cast<double>(wv);
+                }
+            }
+        }
+        const float init = bias != nullptr ? bias[m] : 0.0f;
+        y[i] = static_cast<float>(static_cast<double>(init) + acc);
+    }
+}
+
+} // namespace
+} // namespace nert_hip
+
+using namespace nert_hip;
+
+extern "C" {
+
+int nert_hip_einsum_f32(const float* a, const float* b, float* y, int n_out, const int64_t* out_size,
+                        const int64_t* out_stride_a, const int64_t* out_stride_b, int n_sum, const int64_t* sum_size,
+                        const int64_t* sum_stride_a, const int64_t* sum_stride_b, void* stream) {
+    return Guard([&] {
+        if (n_out < 0 || n_out > kMaxLabels || n_sum < 0 || n_sum > kMaxLabels) {
+            throw Error("einsum: at most 16 output and 16 summed labels");
+        }
+        EinsumArgs e{};
+        e.n_out = n_out;
+        e.n_sum = n_sum;
+        e.two = b != nullptr ? 1 : 0;
+        int64_t n = 1;
+        for (int d = 0; d < n_out; ++d) {
+            e.out_size[d] = out_size[d];
+            e.out_sa[d] = out_stride_a[d];
+            e.out_sb[d] = b != nullptr ? out_stride_b[d] : 0;
+            n *= out_size[d];
+        }
+        e.sum_total = 1;
+        for (int d = 0; d < n_sum; ++d) {
+            e.sum_size[d] = sum_size[d];
+            e.sum_sa[d] = sum_stride_a[d];
+            e.sum_sb[d] = b != nullptr ? sum_stride_b[d] : 0;
+            e.sum_total *= sum_size[d];
+        }
+        if (n <= 0) {
+            return;
+        }
+        EinsumKernel<<<GridFor(n, 256, 16384), 256, 0, StreamOr(stream)>>>(a, b != nullptr ? b : a, y, e, n);
+        CheckLaunch("einsum launch");
+    });
+}
+
+int nert_hip_conv_transpose_f32(const float* x, const float* w, const float* bias, float* y, const int64_t* geom,
+                                void* stream) {
+    return Guard([&] {
+        ConvTArgs p{};
+        int64_t* f = &p.batch;
+        for (int i = 0; i < 16; ++i) {
+            f[i] = geom[i];
+        }
+        if (p.group <= 0 || p.in_c % p.group != 0 || p.out_c % p.group != 0 || p.stride_h <= 0 || p.stride_w <= 0) {
+            throw Error("conv_transpose: bad geometry");
+        }
+        const int64_t n = p.batch * p.out_c * p.out_h * p.out_w;
+        if (n <= 0) {
+            return;
+        }
+        ConvTransposeKernel<<<GridFor(n, 256, 16384), 256, 0, StreamOr(stream)>>>(x, w, bias, y, p, n);
+        CheckLaunch("conv_transpose launch");
+    });
+}
+
+} // extern "C"

@@ -1,0 +1,266 @@
+// Resampling: Resize (nearest / linear with the ONNX coordinate transforms)
+// and GridSample (bilinear / nearest, zeros / border / reflection padding).
+//
+// Both follow the reference's double-precision coordinate math step for step
+// (src/kernels/resize.cpp:48-123, src/kernels/grid_sample.cpp:41-71,132-157),
+// evaluated per output element on the device instead of through host tables,
+// so nothing is uploaded per call and the rows stay capturable. Contraction
+// of a*b+c into fma is off in these kernels: every product and sum rounds
+// where the reference's does.
+
+#include "common.hpp"
+#include "../../include/nert_hip.h"
+
+#pragma clang fp contract(off)
+
+namespace nert_hip {
+namespace {
+
+constexpr int kMaxRank = 8;
+
+struct ResizeArgs {
+    int rank;
+    int linear;
+    int transform; // NERT_RESIZE_* transform codes
+    int nearest;   // NERT_RESIZE_* nearest codes
+    int64_t in_dims[kMaxRank];
+    int64_t out_dims[kMaxRank];
+    int64_t in_strides[kMaxRank];
+    double scales[kMaxRank];
+};
+
+// src/kernels/resize.cpp:48-63
+__device__ double SourceCoord(int transform, int64_t o, int64_t in_len, int64_t out_len, double scale) {
+    const double x = static_cast<double>(o);
+    switch (transform) {
+    case NERT_RESIZE_HALF_PIXEL:
+        return (x + 0.5) / scale - 0.5;
+    case NERT_RESIZE_PYTORCH_HALF_PIXEL:
+        return out_len > 1 ? (x + 0.5) / scale - 0.5 : 0.0;
+    case NERT_RESIZE_ALIGN_CORNERS:
+        return out_len == 1 ? 0.0 : x * static_cast<double>(in_len - 1) / static_cast<double>(out_len - 1);
+    default: // NERT_RESIZE_ASYMMETRIC
+        return x / scale;
+    }
+}
+
+// static_cast<int64_t>(double) as x86-64 does it: NaN and out-of-range give
+// INT64_MIN.
+__device__ __forceinline__ int64_t ToI64(double v) {
+    if (!(v >= -9223372036854775808.0 && v < 9223372036854775808.0)) {
+        return static_cast<int64_t>(0x8000000000000000ULL);
+    }
+    return static_cast<int64_t>(v);
+}
+
+// std::min(std::max(x, lo), hi), NaN passing through as x.
+__device__ __forceinline__ double ClampRef(double x, double lo, double hi) {
+    const double a = x < lo ? lo : x;
+    return hi < a ? hi : a;
+}
+
+// src/kernels/resize.cpp:65-82
+__device__ int64_t NearestIndex(int mode, double x, int64_t in_len) {
+    int64_t index;
+    if (mode == NERT_RESIZE_ROUND_PREFER_FLOOR) {
+        const double f = floor(x);
+        index = ToI64(x - f == 0.5 ? f : round(x));
+    } else if (mode == NERT_RESIZE_ROUND_PREFER_CEIL) {
+        index = ToI64(round(x));
+    } else if (mode == NERT_RESIZE_FLOOR) {
+        index = ToI64(floor(x));
+    } else {
+        index = ToI64(ceil(x));
+    }
+    return index < 0 ? 0 : (index > in_len - 1 ? in_len - 1 : index);
+}
+
+template <typename T>
+__global__ void ResizeKernel(const T* __restrict__ x, T* __restrict__ y, ResizeArgs a, int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n; i += stride) {
+        // Per axis: lower/upper source index and the upper weight.
+        int64_t lower[kMaxRank];
+        int64_t upper[kMaxRank];
+        double weight[kMaxRank];
+        int64_t rem = i;
+        for (int d = a.rank - 1; d >= 0; --d) {
+            const int64_t o = rem % a.out_dims[d];
+            rem /= a.out_dims[d];
+            const double src = SourceCoord(a.transform, o, a.in_dims[d], a.out_dims[d], a.scales[d]);
+            if (!a.linear) {
+                lower[d] = upper[d] = NearestIndex(a.nearest, src, a.in_dims[d]);
+                weight[d] = 0.0;
+                continue;
+            }
+            const double clamped = ClampRef(src, 0.0, static_cast<double>(a.in_dims[d] - 1));
+            lower[d] = ToI64(floor(clamped));
+            upper[d] = lower[d] + 1 < a.in_dims[d] - 1 ? lower[d] + 1 : a.in_dims[d] - 1;
+            weight[d] = upper[d] == lower[d] ? 0.0 : clamped - static_cast<double>(lower[d]);
+        }
+        // Taps in the reference's order: each interpolating axis doubles
+        // the list, lower before upper (src/kernels/resize.cpp:102-122).
+        int interp[kMaxRank];
+        int m = 0;
+        int64_t base = 0;
+        for (int d = 0; d < a.rank; ++d) {
+            if (weight[d] == 0.0) {
+                base += lower[d] * a.in_strides[d];
+            } else {
+                interp[m++] = d;
+            }
+        }
+        if (m == 0) {
+            y[i] = x[base];
+            continue;
+        }
+        double value = 0.0;
+        for (int t = 0; t < (1 << m); ++t) {
+            int64_t off = base;
+            double w = 1.0;
+            for (int q = 0; q < m; ++q) {
+                const int d = interp[q];
+                const bool up = (t >> (m - 1 - q)) & 1;
+                off += (up ? upper[d] : lower[d]) * a.in_strides[d];
+                w = w * (up ? weight[d] : 1.0 - weight[d]);
+            }
+            value += w * static_cast<double>(x[off]);
+        }
+        y[i] = static_cast<T>(value);
+    }
+}
+
+// ---- GridSample -------------------------------------------------------------
+
+// src/kernels/grid_sample.cpp:41-51
+__device__ double Reflect(double x, double lo, double hi) {
+    if (hi == lo) {
+        return lo;
+    }
+    const double range = hi - lo;
+    const double d = fabs(x - lo);
+    const double flips = floor(d / range);
+    const double extra = d - flips * range;
+    return fmod(flips, 2.0) == 0.0 ? lo + extra : hi - extra;
+}
+
+// src/kernels/grid_sample.cpp:54-65
+__device__ double GridCoord(double g, int64_t len, bool align, int padding) {
+    const double size = static_cast<double>(len);
+    double x = align ? (g + 1.0) / 2.0 * (size - 1.0) : ((g + 1.0) * size - 1.0) / 2.0;
+    if (padding == NERT_GRID_REFLECTION) {
+        x = align ? Reflect(x, 0.0, size - 1.0) : Reflect(x, -0.5, size - 0.5);
+        x = ClampRef(x, 0.0, size - 1.0);
+    } else if (padding == NERT_GRID_BORDER) {
+        x = ClampRef(x, 0.0, size - 1.0);
+    }
+    return x;
+}
+
+// One thread per output pixel (b, i, j); the channel loop reuses the
+// coordinates, as the reference does.
+__global__ void GridSampleKernel(const float* __restrict__ x, const float* __restrict__ grid, float* __restrict__ y,
+                                 int64_t n, int64_t c, int64_t h, int64_t w, int64_t ho, int64_t wo, int nearest,
+                                 int padding, int align) {
+    const int64_t pixels = n * ho * wo;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t p = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; p < pixels; p += stride) {
+        const int64_t j = p % wo;
+        const int64_t i = (p / wo) % ho;
+        const int64_t b = p / (wo * ho);
+        const float* g = grid + p * 2;
+        const double px = GridCoord(static_cast<double>(g[0]), w, align != 0, padding);
+        const double py = GridCoord(static_cast<double>(g[1]), h, align != 0, padding);
+        int64_t x0, y0;
+        double wx = 0.0, wy = 0.0;
+        if (nearest) {
+            x0 = ToI64(rint(px));
+            y0 = ToI64(rint(py));
+        } else {
+            const double fx = floor(px);
+            const double fy = floor(py);
+            x0 = ToI64(fx);
+            y0 = ToI64(fy);
+            wx = px - fx;
+            wy = py - fy;
+        }
+        const bool in00 = y0 >= 0 && y0 < h && x0 >= 0 && x0 < w;
+        const bool in01 = y0 >= 0 && y0 < h && x0 + 1 >= 0 && x0 + 1 < w;
+        const bool in10 = y0 + 1 >= 0 && y0 + 1 < h && x0 >= 0 && x0 < w;
+        const bool in11 = y0 + 1 >= 0 && y0 + 1 < h && x0 + 1 >= 0 && x0 + 1 < w;
+        for (int64_t ch = 0; ch < c; ++ch) {
+            const float* plane = x + (b * c + ch) * h * w;
+            double value;
+            const double v00 = in00 ? static_cast<double>(plane[y0 * w + x0]) : 0.0;
+            if (nearest) {
+                value = v00;
+            } else {
+                const double v01 = in01 ? static_cast<double>(plane[y0 * w + x0 + 1]) : 0.0;
+                const double v10 = in10 ? static_cast<double>(plane[(y0 + 1) * w + x0]) : 0.0;
+                const double v11 = in11 ? static_cast<double>(plane[(y0 + 1) * w + x0 + 1]) : 0.0;
+                value = v00 * (1.0 - wx) * (1.0 - wy) + v01 * wx * (1.0 - wy) + v10 * (1.0 - wx) * wy + v11 * wx * wy;
+            }
+            y[((b * c + ch) * ho + i) * wo + j] = static_cast<float>(value);
+        }
+    }
+}
+
+} // namespace
+} // namespace nert_hip
+
+using namespace nert_hip;
+
+extern "C" {
+
+int nert_hip_resize(int dtype, const void* x, void* y, int rank, const int64_t* in_dims, const int64_t* out_dims,
+                    const double* scales, int linear, int transform, int nearest, void* stream) {
+    return Guard([&] {
+        if (rank < 1 || rank > kMaxRank) {
+            throw Error("resize: rank must be 1..8");
+        }
+        ResizeArgs a{};
+        a.rank = rank;
+        a.linear = linear;
+        a.transform = transform;
+        a.nearest = nearest;
+        int64_t n = 1;
+        int64_t st = 1;
+        for (int d = rank - 1; d >= 0; --d) {
+            a.in_dims[d] = in_dims[d];
+            a.out_dims[d] = out_dims[d];
+            a.scales[d] = scales[d];
+            a.in_strides[d] = st;
+            st *= in_dims[d];
+            n *= out_dims[d];
+        }
+        if (n <= 0) {
+            return;
+        }
+        hipStream_t s = StreamOr(stream);
+        const unsigned grid = GridFor(n, 256, 16384);
+        if (dtype == NERT_F32) {
+            ResizeKernel<float><<<grid, 256, 0, s>>>(static_cast<const float*>(x), static_cast<float*>(y), a, n);
+        } else if (dtype == NERT_I64 && !linear) {
+            ResizeKernel<int64_t><<<grid, 256, 0, s>>>(static_cast<const int64_t*>(x), static_cast<int64_t*>(y), a,
+                                                       n);
+        } else {
+            throw Error("resize: float32, or int64 for nearest");
+        }
+        CheckLaunch("resize launch");
+    });
+}
+
+int nert_hip_grid_sample_f32(const float* x, const float* grid, float* y, int64_t n, int64_t c, int64_t h, int64_t w,
+                             int64_t ho, int64_t wo, int nearest, int padding, int align_corners, void* stream) {
+    return Guard([&] {
+        const int64_t pixels = n * ho * wo;
+        if (pixels <= 0 || c <= 0) {
+            return;
+        }
+        GridSampleKernel<<<GridFor(pixels, 256, 16384), 256, 0, StreamOr(stream)>>>(x, grid, y, n, c, h, w, ho, wo,
+                                                                                    nearest, padding, align_corners);
+        CheckLaunch("grid_sample launch");
+    });
+}
+
+} // extern "C"

@@ -1,0 +1,172 @@
+"""GPU parity: Resize, GridSample, Einsum and ConvTranspose against the
+reference CpuDevice rows.
+
+Resize nearest is a copy and must be bit-exact; linear Resize and
+GridSample follow the reference's double-precision coordinate and weight
+arithmetic step for step, so they are held to the same float32 bar as the
+other float rows (|d| <= 1e-4 + 1e-4 |ref|). ConvTranspose accumulates in
+double where the reference scatters in float32 (same bar)."""
+
+import numpy as np
+import pytest
+
+from rowcheck import assert_parity, assert_same_error, randn, rng
+
+pytestmark = pytest.mark.gpu
+
+F, I = np.float32, np.int64
+EXACT = {"rtol": 0.0, "atol": 0.0}
+NONE = None
+
+
+def _resize_scales(shape, scales):
+    return tuple(int(np.floor(np.float64(d) * np.float64(np.float32(s)))) for d, s in zip(shape, scales))
+
+
+TRANSFORMS = ["half_pixel", "pytorch_half_pixel", "align_corners", "asymmetric"]
+
+
+@pytest.mark.parametrize("transform", TRANSFORMS)
+@pytest.mark.parametrize("nearest", ["round_prefer_floor", "round_prefer_ceil", "floor", "ceil"])
+def test_resize_nearest(gpu, transform, nearest):
+    x = randn((2, 3, 7, 9), seed=1)
+    attrs = {"mode": "nearest", "coordinate_transformation_mode": transform, "nearest_mode": nearest}
+    for scales in ([1, 1, 2, 2], [1, 1, 0.6, 1.7], [1, 1, 3.3, 0.5]):
+        out = _resize_scales(x.shape, scales)
+        assert_parity("Resize", [x, NONE, np.array(scales, F)], [(out, F)], attrs, **EXACT)
+    sizes = np.array([2, 3, 5, 13], I)
+    assert_parity("Resize", [x, NONE, NONE, sizes], [(tuple(sizes), F)], attrs, **EXACT)
+    xi = rng(2).integers(-100, 100, (2, 3, 4, 5)).astype(I)
+    assert_parity("Resize", [xi, NONE, np.array([1, 1, 2.5, 1.5], F)], [((2, 3, 10, 7), I)], attrs, **EXACT)
+
+
+def test_resize_detector_upsample(gpu):
+    """The detector's x2 nearest upsampling of a [8, 256, 20, 20] map (bit-exact)."""
+    x = randn((8, 256, 20, 20), seed=3)
+    assert_parity("Resize", [x, np.zeros((0,), F), np.array([1, 1, 2, 2], F)], [((8, 256, 40, 40), F)],
+                  {"mode": "nearest", "coordinate_transformation_mode": "asymmetric", "nearest_mode": "floor"},
+                  **EXACT)
+
+
+@pytest.mark.parametrize("transform", TRANSFORMS)
+def test_resize_linear(gpu, transform):
+    x = randn((2, 3, 6, 8), seed=4)
+    attrs = {"mode": "linear", "coordinate_transformation_mode": transform}
+    for scales in ([1, 1, 2, 2], [1, 1, 0.5, 1.3], [1.5, 1, 1.7, 0.9]):
+        out = _resize_scales(x.shape, scales)
+        assert_parity("Resize", [x, NONE, np.array(scales, F)], [(out, F)], attrs)
+    assert_parity("Resize", [x, NONE, NONE, np.array([2, 3, 11, 5], I)], [((2, 3, 11, 5), F)], attrs)
+    x3 = randn((5, 6, 7), seed=5)  # three interpolating axes: eight taps
+    assert_parity("Resize", [x3, NONE, np.array([1.5, 1.5, 1.5], F)], [((7, 9, 10), F)], attrs)
+
+
+def test_resize_errors(gpu):
+    x = randn((1, 1, 4, 4))
+    s = np.array([1, 1, 2, 2], F)
+    assert_same_error("Resize", [x, NONE, s], [((1, 1, 8, 8), F)], {"mode": "cubic"})
+    assert_same_error("Resize", [x, NONE, s], [((1, 1, 8, 8), F)], {"coordinate_transformation_mode": "tf"})
+    assert_same_error("Resize", [x, NONE, s], [((1, 1, 8, 8), F)], {"nearest_mode": "up"})
+    assert_same_error("Resize", [x, NONE, s], [((1, 1, 8, 9), F)])
+    assert_same_error("Resize", [x, NONE, s, np.array([1, 1, 8, 8], I)], [((1, 1, 8, 8), F)])
+    assert_same_error("Resize", [x.astype(I), NONE, s], [((1, 1, 8, 8), I)], {"mode": "linear"})
+    assert_same_error("Resize", [x, NONE, np.array([1, 1, 0.1, 2], F)], [((1, 1, 0, 8), F)])
+
+
+@pytest.mark.parametrize("mode", ["bilinear", "nearest"])
+@pytest.mark.parametrize("padding", ["zeros", "border", "reflection"])
+@pytest.mark.parametrize("align", [0, 1])
+def test_grid_sample(gpu, mode, padding, align):
+    x = randn((2, 3, 9, 11), seed=6)
+    grid = (randn((2, 5, 7, 2), seed=7) * 0.8).astype(F)  # includes samples outside [-1, 1]
+    grid[0, 0, 0] = [1.0, -1.0]
+    grid[1, 4, 6] = [0.0, 0.0]
+    grid[1, 3, 2] = [2.7, -3.9]
+    attrs = {"mode": mode, "padding_mode": padding, "align_corners": align}
+    assert_parity("GridSample", [x, grid], [((2, 3, 5, 7), F)], attrs)
+
+
+def test_grid_sample_errors(gpu):
+    x = randn((1, 2, 4, 4))
+    g = np.zeros((1, 3, 3, 2), F)
+    assert_same_error("GridSample", [x, g], [((1, 2, 3, 3), F)], {"mode": "bicubic"})
+    assert_same_error("GridSample", [x, g], [((1, 2, 3, 3), F)], {"padding_mode": "wrap"})
+    assert_same_error("GridSample", [x, g], [((1, 2, 3, 3), F)], {"align_corners": 2})
+    assert_same_error("GridSample", [x, g], [((1, 2, 3, 4), F)])
+    assert_same_error("GridSample", [x, np.zeros((2, 3, 3, 2), F)], [((1, 2, 3, 3), F)])
+
+
+EINSUM_CASES = [
+    ("ij,jk->ik", [(5, 7), (7, 3)]),
+    ("bij,bjk->bik", [(4, 5, 6), (4, 6, 3)]),
+    ("bhqd,bhkd->bhqk", [(2, 3, 5, 8), (2, 3, 6, 8)]),
+    ("ij,ij->", [(4, 5), (4, 5)]),
+    ("i,j->ij", [(4,), (6,)]),
+    ("ii->i", [(5, 5)]),
+    ("ii", [(6, 6)]),
+    ("ij->ji", [(3, 4)]),
+    ("ijk->", [(3, 4, 5)]),
+    ("ij,jk", [(3, 4), (4, 5)]),            # implicit output: ik
+    ("Ab,bC->CA", [(3, 4), (4, 2)]),        # upper-case labels sort first
+    ("...ij,...jk->...ik", [(2, 3, 4, 5), (3, 5, 6)]),
+    ("...ij,jk->...ik", [(7, 3, 4), (4, 2)]),
+    ("b...i,b...i->b...", [(2, 3, 4, 5), (2, 1, 4, 5)]),
+    (" i j , j k -> i k ", [(2, 3), (3, 4)]),
+]
+
+
+@pytest.mark.parametrize("equation,shapes", EINSUM_CASES)
+def test_einsum(gpu, equation, shapes):
+    xs = [randn(s, seed=10 + i) for i, s in enumerate(shapes)]
+    eq = equation.replace(" ", "")
+    if "->" not in eq:
+        counts = {}
+        for c in eq.replace(",", ""):
+            counts[c] = counts.get(c, 0) + 1
+        eq = eq + "->" + "".join(sorted(c for c, n in counts.items() if n == 1))
+    want = np.einsum(eq, *[x.astype(np.float64) for x in xs])
+    assert_parity("Einsum", xs, [(want.shape, F)], {"equation": equation})
+
+
+def test_einsum_errors(gpu):
+    a, b = randn((3, 4)), randn((4, 5))
+    assert_same_error("Einsum", [a, b], [((3, 5), F)], {"equation": "ij,jk->iq"})
+    assert_same_error("Einsum", [a, b], [((3, 5), F)], {"equation": "ij,jk->ii"})
+    assert_same_error("Einsum", [a, b], [((3, 5), F)], {"equation": "ij,kk->ik"})
+    assert_same_error("Einsum", [a, b], [((3, 5), F)], {"equation": "ij,jk,kl->il"})
+    assert_same_error("Einsum", [a, b], [((3, 5), F)], {"equation": "i1,jk->ik"})
+    assert_same_error("Einsum", [a, b], [((3, 5), F)], {"equation": "...ij,jk"})
+    assert_same_error("Einsum", [a, b], [((3, 5), F)], {"equation": "ij..,jk->ik"})
+    assert_same_error("Einsum", [a, b], [((3, 5), F)], {"equation": "ijk,jk->ik"})
+    assert_same_error("Einsum", [a, b], [((3, 6), F)], {"equation": "ij,jk->ik"})
+    assert_same_error("Einsum", [a, b], [((3, 5), F)], {})
+
+
+@pytest.mark.parametrize("geom", [
+    dict(x=(2, 4, 5, 6), w=(4, 3, 3, 3), attrs={}),
+    dict(x=(2, 4, 5, 6), w=(4, 3, 3, 3), attrs={"strides": [2, 2]}),
+    dict(x=(1, 6, 7, 5), w=(6, 2, 4, 3), attrs={"strides": [3, 2], "pads": [1, 0, 2, 1], "group": 3}),
+    dict(x=(1, 4, 5, 5), w=(4, 4, 3, 3), attrs={"strides": [2, 2], "dilations": [2, 1], "output_padding": [1, 1]}),
+    dict(x=(2, 8, 16, 16), w=(8, 4, 2, 2), attrs={"strides": [2, 2]}),          # 2x learned upsampling
+    dict(x=(1, 3, 4, 4), w=(3, 2, 3, 3), attrs={"pads": [1, 1, 1, 1], "auto_pad": "VALID"}),
+])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_conv_transpose(gpu, geom, with_bias):
+    a = geom["attrs"]
+    x, w = randn(geom["x"], seed=20), randn(geom["w"], seed=21)
+    s, d = a.get("strides", [1, 1]), a.get("dilations", [1, 1])
+    op, p = a.get("output_padding", [0, 0]), a.get("pads", [0, 0, 0, 0])
+    if a.get("auto_pad") == "VALID":
+        p = [0, 0, 0, 0]
+    m = w.shape[1] * a.get("group", 1)
+    oh = s[0] * (x.shape[2] - 1) + op[0] + d[0] * (w.shape[2] - 1) + 1 - p[0] - p[2]
+    ow = s[1] * (x.shape[3] - 1) + op[1] + d[1] * (w.shape[3] - 1) + 1 - p[1] - p[3]
+    inputs = [x, w] + ([randn((m,), seed=22)] if with_bias else [])
+    assert_parity("ConvTranspose", inputs, [((x.shape[0], m, oh, ow), F)], a)
+
+
+def test_conv_transpose_errors(gpu):
+    x, w = randn((1, 4, 3, 3)), randn((4, 2, 3, 3))
+    assert_same_error("ConvTranspose", [x, w], [((1, 2, 5, 6), F)])
+    assert_same_error("ConvTranspose", [x, randn((3, 2, 3, 3))], [((1, 2, 5, 5), F)])
+    assert_same_error("ConvTranspose", [x, w, randn((3,))], [((1, 2, 5, 5), F)])
+    assert_same_error("ConvTranspose", [x, w], [((1, 2, 5, 5), F)], {"strides": [1, 1, 1]})
