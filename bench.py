@@ -78,6 +78,9 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline leg")
     ap.add_argument("--eager", action="store_true", help="time per-row launches instead of graph replay")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="end with one elementwise pass over 256 MiB (read 256 MiB, write 256 MiB): the "
+                         "known-size kernel that scales the FETCH_SIZE/WRITE_SIZE counters of a --pmc run")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -163,7 +166,10 @@ def main() -> int:
             "peak": PEAK_FP32_MFMA_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
-            "traffic": None,
+            "traffic": (measured_traffic() or {}).get("bytes_per_conv_row"),
+            "traffic_unit": "HBM bytes per Conv row",
+            "traffic_source": "profiles/conv_resnet18_bs32_traffic.json (rocprofv3 --pmc FETCH_SIZE and "
+                              "WRITE_SIZE passes, scaled by the copy probe)",
             "conv_ms_per_step": round(float(conv_ms.sum()), 4),
             "conv_launch_avg_us": round(float(conv_ms.mean()) * 1e3, 2),
             "conv_gflop_per_step": round(float(conv_flops.sum()) / 1e9, 3),
@@ -177,7 +183,32 @@ def main() -> int:
             f"logit parity max rel {result['cpu_baseline']['logits_max_rel_err_vs_gpu']:.2e}")
     print(json.dumps(result), flush=True)
     prog.close()
+    if args.copy_probe:
+        copy_probe()
     return 0
+
+
+COPY_PROBE_FLOATS = 64 << 20
+
+
+def copy_probe() -> None:
+    """One Relu over 64 Mi non-negative floats: 256 MiB read, 256 MiB written."""
+    from nert_amd import device
+
+    buf = device.DeviceArray.from_host(np.ones(COPY_PROBE_FLOATS, np.float32))
+    out = device.DeviceArray((COPY_PROBE_FLOATS,), np.float32)
+    device.check(device.lib().nert_hip_unary(0, 0, buf.ptr, out.ptr, COPY_PROBE_FLOATS, 0.0, 0.0, None), "relu")
+    device.synchronize()
+    buf.close()
+    out.close()
+
+
+def measured_traffic() -> dict | None:
+    """HBM bytes per Conv row from the committed --pmc passes, if present."""
+    path = ROOT / "profiles" / "conv_resnet18_bs32_traffic.json"
+    if not path.exists():
+        return None
+    return json.loads(path.read_text())
 
 
 def Graph_flops(g, idx: int) -> int:
