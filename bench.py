@@ -4,9 +4,12 @@
 
 A step is one forward pass of the seeded ResNet-18 (configs[2] of
 BN folded, [32,3,224,224] -> [32,1000]) through the gfx950
-HipDevice rows, with weights and the input already resident in HBM. The 49
-row calls are captured once into a HIP graph and replayed; K replays are
-timed with HIP events on the layer stream, bracketed by stream syncs.
+HipDevice rows, with weights and the input already resident in HBM. The
+runner first fuses each Conv -> [Add] -> [Relu] chain into one FusedConv row
+(bias, residual and Relu in the conv epilogue, bit-identical outputs), which
+leaves 24 rows out of 49; they are captured once into a HIP graph and
+replayed. K replays are timed with HIP events on the layer stream, bracketed
+by stream syncs.
 
 Extra keys on the one JSON line:
   roofline      the Conv rows (implicit GEMM on fp32 MFMA), the dominant
@@ -121,20 +124,23 @@ def main() -> int:
     logits = prog.output(g.outputs[0])
     log(f"{'eager' if args.eager else 'graph'}: {ms_per_step:.3f} ms/step, {img_s:.1f} img/s")
 
-    # Roofline of the dominant kernel family (Conv rows), events per row.
-    conv_idx = [i for i, n in enumerate(g.nodes) if n.op == "Conv"]
+    # Roofline of the dominant kernel family (Conv rows, fused or not),
+    # events per row.
+    pg = prog.graph
+    conv_ops = {"Conv", "FusedConv"}
+    conv_idx = [i for i, n in enumerate(pg.nodes) if n.op in conv_ops]
     reps = 5
     conv_ms = np.zeros(len(conv_idx))
     for _ in range(reps):
-        t = prog.run_timed({"Conv"})
+        t = prog.run_timed(conv_ops)
         conv_ms += np.array([t[i] for i in conv_idx])
     conv_ms /= reps
     device.synchronize()
-    conv_flops = np.array([Graph_flops(g, i) for i in conv_idx], dtype=np.float64)
+    conv_flops = np.array([Graph_flops(pg, i) for i in conv_idx], dtype=np.float64)
     achieved = conv_flops.sum() / (conv_ms.sum() / 1e3) / 1e12
     for i, ms, fl in zip(conv_idx, conv_ms, conv_flops):
-        n = g.nodes[i]
-        log(f"  {n.name:10s} W{g.tensors[n.inputs[1]][1]} -> {g.tensors[n.outputs[0]][1]}: "
+        n = pg.nodes[i]
+        log(f"  {n.op:9s} {n.name:10s} W{pg.tensors[n.inputs[1]][1]} -> {pg.tensors[n.outputs[0]][1]}: "
             f"{ms * 1e3:8.1f} us {fl / (ms / 1e3) / 1e12:6.1f} TFLOP/s")
     log(f"Conv total {conv_ms.sum():.3f} ms/step ({conv_ms.sum() / ms_per_step * 100:.0f}% of step), "
         f"{achieved:.1f} TFLOP/s")
@@ -156,12 +162,15 @@ def main() -> int:
             "workload": "configs[2] ResNet-18 forward, batch 32, [32,3,224,224] -> [32,1000], opset-17 rows",
             "batch": args.batch,
             "nodes": len(g.nodes),
+            "rows_after_fusion": len(pg.nodes),
             "gflop_per_step": round(g.flops() / 1e9, 3),
-            "launch": "eager rows" if args.eager else "HIP graph replay of the 49 rows",
+            "launch": ("eager rows" if args.eager else "HIP graph replay") +
+                      " after Conv->Add->Relu fusion (bit-identical outputs)",
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "Conv rows (implicit-GEMM ConvKernel + split-K reduce), 20 per step",
+            "kernel": "Conv rows (implicit-GEMM conv kernels + split-K reduce; 17 of 20 carry the fused "
+                      "Add/Relu epilogue), 20 per step",
             "achieved": round(achieved, 3),
             "peak": PEAK_FP32_MFMA_TFLOPS,
             "unit": "TFLOP/s",

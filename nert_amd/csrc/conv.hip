@@ -71,7 +71,22 @@ struct ConvArgs {
     FastDiv div_kvol, div_khw, div_kw;
     int64_t k_per_split;
     float* partial; // [splits][group][M_g][N] when split
+    // Optional epilogue (fused rows): y = act(acc + bias + residual), in that
+    // order, so the result equals Conv, then Add, then Relu bit for bit.
+    const float* residual; // same layout as y, or null
+    int32_t relu;
 };
+
+// std::max(0.0f, v): NaN maps to 0 like the reference Relu.
+__device__ __forceinline__ float Finish(const ConvArgs& p, float v, int64_t y_index) {
+    if (p.residual != nullptr) {
+        v = v + p.residual[y_index];
+    }
+    if (p.relu) {
+        v = (0.0f < v) ? v : 0.0f;
+    }
+    return v;
+}
 
 // Gathers B(k, n) = X_col for one K tile. Thread t owns column nn = t % BN for
 // every pass (the column decode happens once per block); rows are assigned
@@ -330,7 +345,8 @@ __device__ __forceinline__ void ConvEpilogue(const ConvArgs& p, const Accum<Shap
             const int64_t b = gc / p.plane_out;
             const int64_t pix = gc - b * p.plane_out;
             const float value = p.bias != nullptr ? v + p.bias[oc] : v;
-            p.y[(b * p.m + oc) * p.plane_out + pix] = value;
+            const int64_t yi = (b * p.m + oc) * p.plane_out + pix;
+            p.y[yi] = Finish(p, value, yi);
         }
     });
 }
@@ -427,7 +443,8 @@ __global__ __launch_bounds__(Shape::kThreads) void ConvKernel(ConvArgs p) {
             const int64_t b = gc / p.plane_out;
             const int64_t pix = gc - b * p.plane_out;
             const float value = p.bias != nullptr ? v + p.bias[oc] : v;
-            p.y[(b * p.m + oc) * p.plane_out + pix] = value;
+            const int64_t yi = (b * p.m + oc) * p.plane_out + pix;
+            p.y[yi] = Finish(p, value, yi);
         }
     });
 }
@@ -445,20 +462,26 @@ __global__ void ConvSplitReduceKernel(ConvArgs p, int splits, int vec) {
         const int64_t b = gc / p.plane_out;
         const int64_t pix = gc - b * p.plane_out;
         const float bias = p.bias != nullptr ? p.bias[oc] : 0.f;
-        float* out = p.y + (b * p.m + oc) * p.plane_out + pix;
+        const int64_t yi = (b * p.m + oc) * p.plane_out + pix;
+        float* out = p.y + yi;
         if (vec == 4) {
             nert_floatx4 sum = *reinterpret_cast<const nert_floatx4*>(p.partial + i);
             for (int s = 1; s < splits; ++s) {
                 sum += *reinterpret_cast<const nert_floatx4*>(p.partial + s * per_split + i);
             }
             sum += bias;
+            if (p.residual != nullptr || p.relu) {
+                for (int e = 0; e < 4; ++e) {
+                    sum[e] = Finish(p, sum[e], yi + e);
+                }
+            }
             *reinterpret_cast<nert_floatx4*>(out) = sum;
         } else {
             float sum = p.partial[i];
             for (int s = 1; s < splits; ++s) {
                 sum += p.partial[s * per_split + i];
             }
-            *out = sum + bias;
+            *out = Finish(p, sum + bias, yi);
         }
     }
 }
@@ -553,14 +576,16 @@ bool TryPointwise(const ConvArgs& p, hipStream_t stream) {
 } // namespace
 } // namespace nert_hip
 
-extern "C" int nert_hip_conv_f32(const float* x, const float* w, const float* bias, float* y, const nert_conv_desc* d,
-                                 void* stream) {
+extern "C" int nert_hip_conv_fused_f32(const float* x, const float* w, const float* bias, const float* residual,
+                                       float* y, const nert_conv_desc* d, int relu, void* stream) {
     return nert_hip::Guard([&] {
         nert_hip::ConvArgs p{};
         p.x = x;
         p.w = w;
         p.bias = bias;
         p.y = y;
+        p.residual = residual;
+        p.relu = relu != 0 ? 1 : 0;
         p.batch = d->batch;
         p.c = d->in_channels;
         p.m = d->out_channels;
@@ -605,7 +630,7 @@ extern "C" int nert_hip_conv_f32(const float* x, const float* w, const float* bi
             return;
         }
         hipStream_t s = nert_hip::StreamOr(stream);
-        if (nert_hip::TryPointwise(p, s)) {
+        if (p.residual == nullptr && !p.relu && nert_hip::TryPointwise(p, s)) {
             return;
         }
         if (p.mg <= 32) {
@@ -616,4 +641,9 @@ extern "C" int nert_hip_conv_f32(const float* x, const float* w, const float* bi
             nert_hip::LaunchConv<nert_hip::ConvShapeL>(p, s);
         }
     });
+}
+
+extern "C" int nert_hip_conv_f32(const float* x, const float* w, const float* bias, float* y, const nert_conv_desc* d,
+                                 void* stream) {
+    return nert_hip_conv_fused_f32(x, w, bias, nullptr, y, d, 0, stream);
 }

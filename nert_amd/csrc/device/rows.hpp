@@ -16,6 +16,7 @@ using nert::Node;
 NERT_HIP_ROW(Gemm);
 NERT_HIP_ROW(MatMul);
 NERT_HIP_ROW(Conv);
+NERT_HIP_ROW(FusedConv); // not a reference row: the runner's Conv+Add+Relu fusion
 
 // Window helpers shared by Conv, ConvTranspose and the pools
 // (src/kernels/conv.cpp:78-134, src/kernels/max_pool.cpp).

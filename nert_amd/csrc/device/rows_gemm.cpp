@@ -292,16 +292,15 @@ int64_t WindowOutput(const std::string& context, int64_t in, int64_t kernel, int
     return out;
 }
 
-// Validation follows src/kernels/conv.cpp:138-231.
-void Conv(const Node& node, const Views& inputs, const Views& outputs) {
-    const std::string context = "Conv (node '" + node.name + "')";
-    if (inputs.size() < 2 || inputs.size() > 3 || outputs.size() != 1) {
-        throw InferenceException(context + ": expected two or three inputs and one output");
-    }
+namespace {
+
+// The Conv row's work, shared with FusedConv: `residual` (or null) is added
+// and Relu applied in the kernel epilogue when the fused row asks for it.
+void ConvCore(const Node& node, const std::string& context, const Views& inputs, bool has_bias,
+              const TensorView* residual, bool relu, const Views& outputs) {
     const TensorView& x = inputs[0];
     const TensorView& w = inputs[1];
     const TensorView& out = outputs[0];
-    const bool has_bias = inputs.size() == 3;
     if (x.dtype != DataType::Float32 || w.dtype != DataType::Float32 || out.dtype != DataType::Float32) {
         throw InferenceException(context + ": tensors must be float32");
     }
@@ -395,10 +394,51 @@ void Conv(const Node& node, const Views& inputs, const Views& outputs) {
         d.dilation[i] = real ? dilations[s] : 1;
         d.pad[i] = real ? pad_begin[s] : 0;
     }
-    CheckStatus(nert_hip_conv_f32(static_cast<const float*>(x.data), static_cast<const float*>(w.data), bias,
-                                  static_cast<float*>(out.data), &d, Stream()),
+    const float* res = nullptr;
+    if (residual != nullptr) {
+        if (residual->dtype != DataType::Float32 || residual->dims != out.dims) {
+            throw InferenceException(context + ": the summed input must be float32 with the output's shape");
+        }
+        if (residual->data == nullptr) {
+            throw InferenceException(context + ": null buffer");
+        }
+        res = static_cast<const float*>(residual->data);
+    }
+    CheckStatus(nert_hip_conv_fused_f32(static_cast<const float*>(x.data), static_cast<const float*>(w.data), bias, res,
+                                        static_cast<float*>(out.data), &d, relu ? 1 : 0, Stream()),
                 context);
     AfterRow(outputs, context);
+}
+
+} // namespace
+
+// Validation follows src/kernels/conv.cpp:138-231.
+void Conv(const Node& node, const Views& inputs, const Views& outputs) {
+    const std::string context = "Conv (node '" + node.name + "')";
+    if (inputs.size() < 2 || inputs.size() > 3 || outputs.size() != 1) {
+        throw InferenceException(context + ": expected two or three inputs and one output");
+    }
+    ConvCore(node, context, inputs, inputs.size() == 3, nullptr, false, outputs);
+}
+
+// Not a reference row: Y = activation(Conv(X, W, B) + Z), the contract of
+// the com.microsoft FusedConv contrib op (inputs X, W, optional B, optional
+// Z; attribute `activation`, here "Relu" or absent). The nert_amd runner
+// rewrites Conv -> [Add] -> [Relu] chains into it; every step rounds as the
+// separate rows do, so results are bit-identical to the unfused graph.
+void FusedConv(const Node& node, const Views& inputs, const Views& outputs) {
+    const std::string context = "FusedConv (node '" + node.name + "')";
+    if (inputs.size() < 2 || inputs.size() > 4 || outputs.size() != 1) {
+        throw InferenceException(context + ": expected two to four inputs and one output");
+    }
+    const std::string activation = StringAttr(node, "activation", "", "FusedConv");
+    if (!activation.empty() && activation != "Relu") {
+        throw InferenceException(context + ": unsupported activation '" + activation + "'");
+    }
+    const bool has_bias = inputs.size() >= 3 && inputs[2].dtype != DataType::Unknown;
+    const TensorView* z = inputs.size() == 4 && inputs[3].dtype != DataType::Unknown ? &inputs[3] : nullptr;
+    Views conv_inputs(inputs.begin(), inputs.begin() + (has_bias ? 3 : 2));
+    ConvCore(node, context, conv_inputs, has_bias, z, activation == "Relu", outputs);
 }
 
 } // namespace rows

@@ -17,6 +17,7 @@ nert::KernelFn FindRow(const std::string& op_type) {
         {"Gemm", &Gemm},
         {"MatMul", &MatMul},
         {"Conv", &Conv},
+        {"FusedConv", &FusedConv},
         {"Relu", &Relu},
         {"Sigmoid", &Sigmoid},
         {"Tanh", &Tanh},

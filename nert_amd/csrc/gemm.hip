@@ -143,8 +143,12 @@ __global__ void SplitReduceKernel(GemmArgs p, int splits, int64_t batches, int v
     }
 }
 
-using ShapeL = TileShape<128, 128, 16, 2, 2>; // 4 waves, 64x64 per wave
-using ShapeW = TileShape<64, 256, 16, 1, 4>;  // 4 waves, 64x64 per wave, for M <= 64
+// Tile shapes, chosen from a sweep over the BASELINE GEMM/MatMul shapes and
+// the ViT projections on MI355X: 8 waves of 64x32 for problems with at least
+// 1024 such tiles (4096^3: 135 TFLOP/s), 4 waves of 32x64 below that (more
+// workgroups in flight hide the load latency), 2 waves for M <= 32.
+using ShapeL = TileShape<128, 128, 16, 2, 4>; // 8 waves, 64x32 per wave
+using ShapeM = TileShape<64, 128, 16, 2, 2>;  // 4 waves, 32x64 per wave
 using ShapeS = TileShape<32, 64, 32, 1, 2>;   // 2 waves, skinny M
 
 template <class Shape>
@@ -181,18 +185,21 @@ void LaunchGemm(GemmArgs p, int64_t batches, hipStream_t stream) {
     if (!(p.a_sk == 1 || p.a_sm == 1) || !(p.b_sn == 1 || p.b_sk == 1)) {
         throw Error("gemm: operands must be contiguous in one index");
     }
-    int shape = 0; // 0 = L, 1 = W, 2 = S
+    int shape = 0; // 0 = L, 1 = M, 2 = S
     int64_t tiles = TileCount<ShapeL>(p, batches);
+    int64_t min_k_tiles = 8;
     if (p.m <= 32) {
         shape = 2;
         tiles = TileCount<ShapeS>(p, batches);
-    } else if (p.m <= 64) {
+        min_k_tiles = 2;
+    } else if (tiles < 1024) {
         shape = 1;
-        tiles = TileCount<ShapeW>(p, batches);
+        tiles = TileCount<ShapeM>(p, batches);
     }
     const int bk = shape == 2 ? ShapeS::kBK : ShapeL::kBK;
     const int64_t k_tiles = (p.k + bk - 1) / bk;
-    int splits = PlanSplits(tiles, k_tiles, kResidentBlocks, 8, 32);
+    // The 2- and 4-wave shapes keep about 1024 workgroups resident.
+    int splits = PlanSplits(tiles, k_tiles, shape == 0 ? kResidentBlocks : 2 * kResidentBlocks, min_k_tiles, 32);
     p.k_per_split = ((k_tiles + splits - 1) / splits) * bk;
     if (p.k == 0) {
         p.k_per_split = 0;
@@ -207,7 +214,7 @@ void LaunchGemm(GemmArgs p, int64_t batches, hipStream_t stream) {
         LaunchShape<ShapeL>(p, batches, splits, stream);
         break;
     case 1:
-        LaunchShape<ShapeW>(p, batches, splits, stream);
+        LaunchShape<ShapeM>(p, batches, splits, stream);
         break;
     default:
         LaunchShape<ShapeS>(p, batches, splits, stream);

@@ -23,7 +23,7 @@ import numpy as np
 
 from . import abi
 from .device import DeviceArray, Event, NertError, check, lib
-from .graph import Graph
+from .graph import Graph, Node
 
 ALIGN = 256
 
@@ -63,6 +63,72 @@ def plan_arena(g: Graph) -> tuple[dict[str, int], int]:
     return offsets, arena
 
 
+def fuse_conv_chains(g: Graph) -> Graph:
+    """Rewrites Conv -> [Add] -> [Relu] chains into single FusedConv nodes.
+
+    A chain fuses when each intermediate tensor has exactly one consumer and is
+    not a graph output, and the Add sums the conv output with a tensor of the
+    same shape (no broadcasting). The fused node takes the place of the chain's
+    last node, where every operand (including the Add's other input) already
+    exists. The FusedConv row applies bias, summand and Relu in the kernel
+    epilogue in the unfused order, so the outputs are bit-identical; the
+    chain's intermediates are never written to memory.
+    """
+    consumers: dict[str, list[int]] = {}
+    for idx, n in enumerate(g.nodes):
+        for t in n.inputs:
+            if t:
+                consumers.setdefault(t, []).append(idx)
+    outputs = set(g.outputs)
+
+    def sole(t: str, op: str) -> int | None:
+        if t in outputs:
+            return None
+        c = consumers.get(t, [])
+        if len(c) == 1 and g.nodes[c[0]].op == op:
+            return c[0]
+        return None
+
+    replace: dict[int, Node] = {}
+    dropped: set[int] = set()
+    for idx, n in enumerate(g.nodes):
+        if n.op != "Conv" or idx in dropped:
+            continue
+        out = n.outputs[0]
+        z = ""
+        last = idx
+        a = sole(out, "Add")
+        if a is not None and a not in dropped:
+            add = g.nodes[a]
+            others = [t for t in add.inputs if t != out]
+            if len(add.inputs) == 2 and len(others) == 1 and others[0] and \
+                    tuple(g.tensors[others[0]][1]) == tuple(g.tensors[out][1]):
+                z = others[0]
+                dropped.add(a)
+                out = add.outputs[0]
+                last = a
+        activation = None
+        r = sole(out, "Relu")
+        if r is not None and r not in dropped:
+            activation = "Relu"
+            dropped.add(r)
+            out = g.nodes[r].outputs[0]
+            last = r
+        if last == idx:
+            continue
+        inputs = [n.inputs[0], n.inputs[1], n.inputs[2] if len(n.inputs) > 2 else "", z]
+        while inputs and not inputs[-1]:
+            inputs.pop()
+        attrs = dict(n.attrs)
+        if activation:
+            attrs["activation"] = activation
+        dropped.add(idx)
+        dropped.discard(last)
+        replace[last] = Node("FusedConv", inputs, [out], attrs, n.name)
+    nodes = [replace.get(i, nd) for i, nd in enumerate(g.nodes) if i not in dropped or i in replace]
+    return Graph(nodes=nodes, initializers=g.initializers, inputs=g.inputs, outputs=g.outputs, tensors=g.tensors)
+
+
 class _PackedNode:
     __slots__ = ("op", "name", "attrs", "ins", "outs", "err")
 
@@ -76,7 +142,9 @@ class _PackedNode:
 
 
 class Program:
-    def __init__(self, g: Graph):
+    def __init__(self, g: Graph, fuse: bool = True):
+        if fuse:
+            g = fuse_conv_chains(g)
         self.graph = g
         self.offsets, self.arena_bytes = plan_arena(g)
         self.arena = DeviceArray((max(self.arena_bytes, 1),), np.uint8)

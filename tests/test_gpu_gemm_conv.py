@@ -181,3 +181,61 @@ def test_config1c_skinny_gemm(gpu):
     b = uniform((1000, 512), seed=16)
     c = uniform((1000,), seed=17)
     assert_parity("Gemm", [a, b, c], [((32, 1000), F)], {"transB": 1})
+
+
+# --- FusedConv: the runner's Conv -> Add -> Relu fusion ------------------------
+
+FUSED_CASES = [
+    ((2, 64, 14, 14), (64, 64, 3, 3), {"pads": [1, 1, 1, 1]}),                      # tap-major, split-K
+    ((1, 256, 7, 7), (512, 256, 3, 3), {"pads": [1, 1, 1, 1]}),                     # deep split-K
+    ((2, 3, 32, 32), (16, 3, 7, 7), {"pads": [3, 3, 3, 3], "strides": [2, 2]}),     # gather path (C=3)
+    ((2, 32, 9, 9), (48, 32, 1, 1), {}),                                            # pointwise shape
+    ((1, 64, 20, 20), (64, 16, 3, 3), {"pads": [1, 1, 1, 1], "group": 4}),          # groups
+]
+
+
+@pytest.mark.parametrize("xs,ws,attrs", FUSED_CASES)
+@pytest.mark.parametrize("with_z", [False, True])
+def test_fused_conv_bit_identical(gpu, xs, ws, attrs, with_z):
+    """FusedConv == Conv row, then float32 Add, then Relu, bit for bit; and
+    within the Conv tolerance of the reference rows."""
+    x, w, b = randn(xs, seed=40), randn(ws, seed=41, scale=0.1), randn((ws[0],), seed=42)
+    conv = _hip("Conv", [x, w, b], _conv_out(xs, ws, attrs), attrs)
+    z = randn(conv.shape, seed=43) if with_z else None
+    want = conv + z if with_z else conv
+    want = np.where(want > 0, want, np.float32(0)).astype(F)
+    fattrs = dict(attrs, activation="Relu")
+    got = _hip("FusedConv", [x, w, b] + ([z] if with_z else []), conv.shape, fattrs)
+    assert np.array_equal(got, want)
+    # without an activation and without a bias
+    got = _hip("FusedConv", [x, w, None] + ([z] if with_z else []), conv.shape, attrs)
+    plain = _hip("Conv", [x, w], conv.shape, attrs)
+    assert np.array_equal(got, plain + z if with_z else plain)
+    ref_conv = restate.conv(x, w, b, **_restate_args(attrs))
+    ref = ref_conv + z if with_z else ref_conv
+    compare(_hip("FusedConv", [x, w, b] + ([z] if with_z else []), conv.shape, fattrs),
+            np.maximum(ref, 0).astype(F), what="FusedConv vs reference")
+
+
+def test_fused_conv_errors(gpu):
+    from nert_amd.device import NertError
+
+    x, w = randn((1, 4, 5, 5)), randn((4, 4, 3, 3))
+    with pytest.raises(NertError, match=r"FusedConv \(node 'n'\): unsupported activation 'Tanh'"):
+        _hip("FusedConv", [x, w], (1, 4, 3, 3), {"activation": "Tanh"})
+    with pytest.raises(NertError, match=r"FusedConv \(node 'n'\): the summed input must be float32"):
+        _hip("FusedConv", [x, w, None, randn((1, 4, 3, 2))], (1, 4, 3, 3))
+    with pytest.raises(NertError, match=r"FusedConv \(node 'n'\): output shape does not match the convolution"):
+        _hip("FusedConv", [x, w], (1, 4, 5, 5))
+
+
+def _conv_out(xs, ws, attrs):
+    pads = attrs.get("pads", [0, 0, 0, 0])
+    s = attrs.get("strides", [1, 1])
+    oh = (xs[2] + pads[0] + pads[2] - ws[2]) // s[0] + 1
+    ow = (xs[3] + pads[1] + pads[3] - ws[3]) // s[1] + 1
+    return (xs[0], ws[0], oh, ow)
+
+
+def _restate_args(attrs):
+    return {"strides": attrs.get("strides"), "pads": attrs.get("pads"), "group": attrs.get("group", 1)}

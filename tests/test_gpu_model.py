@@ -94,3 +94,16 @@ def test_reference_executor_on_hipdevice(resnet):
     got, secs, arena = _dropin_run(lg, np.ascontiguousarray(x[:2]))
     assert arena > 0
     compare(got, want, rtol=RTOL, atol=RTOL, what="drop-in logits")
+
+
+def test_fused_program_is_bit_identical(gpu):
+    """The runner's Conv+Add+Relu fusion changes no output bit (batch 2)."""
+    g, inputs = workloads.resnet18(batch=2)
+    outs = []
+    for fuse in (False, True):
+        prog = Program(g, fuse=fuse)
+        prog.set_input("input", inputs["input"])
+        prog.run()
+        outs.append(prog.output(g.outputs[0]))
+        prog.close()
+    assert np.array_equal(outs[0], outs[1])

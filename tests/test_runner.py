@@ -1,0 +1,72 @@
+"""CPU: the runner's graph rewrite (Conv -> Add -> Relu fusion) and arena plan."""
+
+import numpy as np
+
+from nert_amd import workloads
+from nert_amd.graph import Graph
+from nert_amd.runner import fuse_conv_chains, plan_arena
+
+F = np.float32
+
+
+def _valid_order(g):
+    avail = set(g.initializers) | set(g.inputs)
+    for n in g.nodes:
+        for t in n.inputs:
+            assert not t or t in avail, (n.op, t)
+        avail.update(n.outputs)
+    assert all(o in avail for o in g.outputs)
+
+
+def test_resnet18_fusion():
+    g, _ = workloads.resnet18(batch=2)
+    f = fuse_conv_chains(g)
+    ops = [n.op for n in f.nodes]
+    # 20 convs: 17 end in Relu (9 plain, 8 with the residual Add); the three
+    # 1x1 downsample convs feed an Add and stay plain.
+    assert ops.count("FusedConv") == 17 and ops.count("Conv") == 3
+    assert "Relu" not in ops and "Add" not in ops
+    assert sum(1 for n in f.nodes if n.op == "FusedConv" and len(n.inputs) == 4) == 8
+    assert all(n.attrs.get("activation") == "Relu" for n in f.nodes if n.op == "FusedConv")
+    _valid_order(f)
+    assert f.outputs == g.outputs
+
+
+def _chain(extra_consumer=False, output_mid=False, broadcast=False):
+    g = Graph()
+    x = g.add_input("x", F, (1, 4, 6, 6))
+    w = g.add_initializer("w", np.ones((4, 4, 3, 3), F))
+    zshape = (1, 4, 1, 1) if broadcast else (1, 4, 6, 6)
+    z = g.add_input("z", F, zshape)
+    (c,) = g.add_node("Conv", [x, w], [("c", F, (1, 4, 6, 6))], {"pads": [1, 1, 1, 1]})
+    (a,) = g.add_node("Add", [c, z], [("a", F, (1, 4, 6, 6))])
+    (r,) = g.add_node("Relu", [a], [("r", F, (1, 4, 6, 6))])
+    g.outputs = [r]
+    if extra_consumer:
+        (e,) = g.add_node("Relu", [c], [("e", F, (1, 4, 6, 6))])
+        g.outputs.append(e)
+    if output_mid:
+        g.outputs.append(a)
+    return g
+
+
+def test_fusion_rules():
+    f = fuse_conv_chains(_chain())
+    assert [n.op for n in f.nodes] == ["FusedConv"]
+    assert f.nodes[0].inputs == ["x", "w", "", "z"] and f.nodes[0].outputs == ["r"]
+    # the conv output has a second consumer: nothing fuses into the conv
+    assert [n.op for n in fuse_conv_chains(_chain(extra_consumer=True)).nodes] == ["Conv", "Add", "Relu", "Relu"]
+    # the Add output is a graph output: Conv+Add fuse, the Relu stays
+    assert [n.op for n in fuse_conv_chains(_chain(output_mid=True)).nodes] == ["FusedConv", "Relu"]
+    # a broadcasting Add is left alone; the Relu cannot reach the conv
+    assert [n.op for n in fuse_conv_chains(_chain(broadcast=True)).nodes] == ["Conv", "Add", "Relu"]
+
+
+def test_arena_plan_reuses_memory():
+    g, _ = workloads.resnet18(batch=2)
+    offsets, size = plan_arena(fuse_conv_chains(g))
+    total = sum(int(np.prod(g.tensors[t][1])) * 4 for t in offsets)
+    assert size < total / 2
+    assert all(o % 256 == 0 for o in offsets.values())
+    # fusion removes the chain intermediates from the plan altogether
+    assert size < plan_arena(g)[1]
