@@ -180,8 +180,9 @@ struct ConvBLoader {
 
 // ---- Tap-major implicit GEMM (C_g a multiple of BK) ---------------------------
 //
-// K is walked tap-major, k' = tap * C_g + c, so one K tile is BK channels at a
-// single filter tap (kh, kw). For a given column the padding test and the
+// K is walked in tiles of BK channels at a single filter tap (kh, kw): the
+// weight view is A[m][k'] with k' = tap * C_g + c, and the tiles are visited
+// channel block by channel block, all taps of a block in a row. For a given column the padding test and the
 // input address then hold for the whole tile: each thread computes its
 // pixel's byte offset once per tile and reads the tile's channels at
 // wave-uniform plane strides. Operands are read with buffer loads: the
@@ -232,8 +233,12 @@ struct TapALoader {
         }
     }
     __device__ __forceinline__ void load(int64_t k0, Stage& s) const {
-        const int32_t tap = static_cast<int32_t>(k0) / cg;
-        const int32_t c0 = static_cast<int32_t>(k0) - tap * cg;
+        // K tiles run channel-block-major, taps inside: tile kt covers
+        // channels (kt / taps) * BK .. + BK at tap kt % taps, so the KH*KW
+        // taps of one channel block reuse the same X rows from L2.
+        const int32_t kt = static_cast<int32_t>(k0) / BK;
+        const int32_t tap = kt % taps;
+        const int32_t c0 = (kt / taps) * BK;
         const uint32_t soff = static_cast<uint32_t>((c0 * taps + tap) * 4);
 #pragma unroll
         for (int j = 0; j < kPer; ++j) {
@@ -263,7 +268,7 @@ struct TapBLoader {
     uint32_t pix;  // byte offset of (b, g*C_g, 0, 0) + window origin, or kOutOfRange
     int32_t ih0, iw0;
     int32_t in_h, in_w, d_h, d_w, k_w;
-    int32_t cg;
+    int32_t cg, taps;
     uint32_t plane_bytes;
     int32_t kk0;
 
@@ -277,6 +282,7 @@ struct TapBLoader {
         d_w = p.d_w;
         k_w = p.k_w;
         cg = static_cast<int32_t>(p.cg);
+        taps = KH > 0 ? KH * KW : p.k_h * p.k_w;
         plane_bytes = static_cast<uint32_t>(p.plane_in * 4);
         if (n < p.n_total) {
             const int64_t b = n / p.plane_out;
@@ -293,8 +299,9 @@ struct TapBLoader {
         }
     }
     __device__ __forceinline__ void load(int64_t k0, Stage& s) const {
-        const int32_t tap = static_cast<int32_t>(k0) / cg;
-        const int32_t c0 = static_cast<int32_t>(k0) - tap * cg;
+        const int32_t kt = static_cast<int32_t>(k0) / BK; // same tile order as TapALoader
+        const int32_t tap = kt % taps;
+        const int32_t c0 = (kt / taps) * BK;
         int32_t kh, kw;
         if constexpr (KH > 0) {
             kh = tap / KW;
