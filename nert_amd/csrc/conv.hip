@@ -344,18 +344,58 @@ __device__ __forceinline__ void ConvEpilogue(const ConvArgs& p, const Accum<Shap
         });
         return;
     }
-    ForEachAccum<Shape>(acc, [&](int r, int c, float v) {
-        const int64_t gr = row0 + r;
-        const int64_t gc = col0 + c;
-        if (gr < p.mg && gc < p.n_total) {
-            const int64_t oc = static_cast<int64_t>(g) * p.mg + gr;
-            const int64_t b = gc / p.plane_out;
-            const int64_t pix = gc - b * p.plane_out;
-            const float value = p.bias != nullptr ? v + p.bias[oc] : v;
-            const int64_t yi = (b * p.m + oc) * p.plane_out + pix;
-            p.y[yi] = Finish(p, value, yi);
+    // Column (pixel) decode once per 32-column block; bias and residual
+    // operands are loaded from clamped, always-valid addresses before any
+    // store, so the loads of a lane are all in flight together instead of
+    // one per guarded branch.
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wave_m = wave % Shape::kWavesM;
+    const int wave_n = wave / Shape::kWavesM;
+    const int half = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < Shape::kSubN; ++j) {
+        const int64_t gc = col0 + wave_n * Shape::kWaveN + 32 * j + (lane & 31);
+        const bool col_ok = gc < p.n_total;
+        const int64_t gcc = col_ok ? gc : 0;
+        const int64_t b = gcc / p.plane_out;
+        const int64_t ybase = b * p.m * p.plane_out + (gcc - b * p.plane_out);
+#pragma unroll
+        for (int i = 0; i < Shape::kSubM; ++i) {
+            float value[16];
+            int64_t yi[16];
+            bool ok[16];
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int64_t gr = row0 + wave_m * Shape::kWaveM + 32 * i + 8 * (v >> 2) + 4 * half + (v & 3);
+                ok[v] = col_ok && gr < p.mg;
+                const int64_t oc = static_cast<int64_t>(g) * p.mg + (ok[v] ? gr : 0);
+                yi[v] = ybase + oc * p.plane_out;
+                value[v] = p.bias != nullptr ? acc.c[i][j][v] + p.bias[oc] : acc.c[i][j][v];
+            }
+            if (p.residual != nullptr) {
+                float res[16];
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    res[v] = p.residual[ok[v] ? yi[v] : 0];
+                }
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    value[v] = value[v] + res[v];
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                float out = value[v];
+                if (p.relu) {
+                    out = (0.0f < out) ? out : 0.0f; // std::max(0.0f, v)
+                }
+                if (ok[v]) {
+                    p.y[yi[v]] = out;
+                }
+            }
         }
-    });
+    }
 }
 
 template <class Shape, int KH, int KW>
@@ -547,6 +587,210 @@ void LaunchConv(ConvArgs p, hipStream_t stream) {
     }
 }
 
+// ---- Small-channel convolution from an LDS input patch -------------------------
+//
+// For C_g <= 4 (image stems: 3 input channels) the K dimension is only C*KH*KW
+// and a K tile would hold a few channels of many taps, so the gather loaders
+// spend their time on index arithmetic. Instead each workgroup owns a 16x16
+// block of output pixels for 64 output channels: it copies the input patch
+// that block reads (C x PH x PW, zero outside the image) and the weights of
+// its 64 channels ([m][c][kh][kw] rows, as stored) into LDS once, then runs
+// every MFMA out of LDS. An MFMA step covers two neighbouring taps of one
+// filter row (kw = 2q and 2q + 1); for an odd KW the last step's second tap
+// does not exist, and its lanes read a zero from the patch's zero slot.
+constexpr int kPatchTile = 16;    // output tile is kPatchTile x kPatchTile pixels
+constexpr int kPatchM = 64;       // output channels per workgroup
+constexpr int kPatchMaxIn = 8192; // patch floats
+
+struct PatchGeom {
+    int32_t knat;      // C_g * KH * KW, the weight row length
+    int32_t wpitch;    // LDS weight row pitch (odd: conflict-free column reads)
+    int32_t ph, pw;    // patch rows / row pitch
+    int32_t tiles_w, tiles_h;
+};
+
+template <int PAIRS>
+__global__ __launch_bounds__(512) void PatchConvKernel(ConvArgs p, PatchGeom pg) {
+    // Dynamic LDS: weights [kPatchM][wpitch], then the patch and one zero float.
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    float* const ws = smem;
+    float* const patch = smem + kPatchM * pg.wpitch;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int64_t blk = blockIdx.x;
+    const int tx0 = static_cast<int>(blk % pg.tiles_w) * kPatchTile;
+    const int ty0 = static_cast<int>((blk / pg.tiles_w) % pg.tiles_h) * kPatchTile;
+    const int64_t b = blk / (static_cast<int64_t>(pg.tiles_w) * pg.tiles_h);
+    const int g = blockIdx.z;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kPatchM;
+    const int cg = static_cast<int>(p.cg);
+    const int kh_n = p.k_h, kw_n = p.k_w;
+
+    // Weights: one wave per row, lanes along the row (zero rows past M_g).
+    const float* wg = p.w + (static_cast<int64_t>(g) * p.mg + m0) * pg.knat;
+    for (int m = wave; m < kPatchM; m += 8) {
+        const bool ok = m0 + m < p.mg;
+        for (int k = lane; k < pg.knat; k += 64) {
+            ws[m * pg.wpitch + k] = ok ? wg[static_cast<int64_t>(m) * pg.knat + k] : 0.0f;
+        }
+    }
+    // Input patch, zero outside the image (the padding taps): one wave per
+    // patch row, lanes along the row.
+    const int ih0 = ty0 * p.s_h - p.p_h;
+    const int iw0 = tx0 * p.s_w - p.p_w;
+    const float* xb = p.x + (b * p.c + static_cast<int64_t>(g) * cg) * p.plane_in;
+    const int plane_patch = pg.ph * pg.pw;
+    for (int r = wave; r < cg * pg.ph; r += 8) {
+        const int c = r / pg.ph;
+        const int ih = ih0 + (r - c * pg.ph);
+        const bool row_in = static_cast<unsigned>(ih) < static_cast<unsigned>(p.in_h);
+        const float* src = xb + static_cast<int64_t>(c) * p.plane_in + static_cast<int64_t>(ih) * p.in_w;
+        for (int px = lane; px < pg.pw; px += 64) {
+            const int iw = iw0 + px;
+            const bool in = row_in && static_cast<unsigned>(iw) < static_cast<unsigned>(p.in_w);
+            patch[r * pg.pw + px] = in ? src[iw] : 0.0f;
+        }
+    }
+    const int zero_slot = cg * plane_patch;
+    float* const bias_s = patch + zero_slot + 1; // kPatchM floats
+    if (tid == 0) {
+        patch[zero_slot] = 0.0f;
+    }
+    if (tid < kPatchM) {
+        const int64_t m = m0 + tid;
+        bias_s[tid] = p.bias != nullptr && m < p.mg ? p.bias[static_cast<int64_t>(g) * p.mg + m] : 0.0f;
+    }
+    __syncthreads();
+
+    // 8 waves: 2 along M (32 rows each) x 4 along N (64 pixels = 4 tile rows).
+    const int wave_m = wave & 1;
+    const int wave_n = wave >> 1;
+    const int half = lane >> 5;
+    const int col = lane & 31;
+    int poff[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = wave_n * 64 + j * 32 + col;
+        poff[j] = (n / kPatchTile) * p.s_h * pg.pw + (n % kPatchTile) * p.s_w + half * p.d_w;
+    }
+    nert_floatx16 acc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            acc[j][v] = 0.0f;
+        }
+    }
+    const bool odd = kw_n != 2 * PAIRS;
+    const float* wrow = ws + (wave_m * 32 + col) * pg.wpitch + half;
+    for (int row = 0; row < cg * kh_n; ++row) {
+        const int c = row / kh_n;
+        const int kh = row - c * kh_n;
+        const int rbase = c * plane_patch + kh * p.d_h * pg.pw;
+        const float* wr = wrow + row * kw_n;
+#pragma unroll
+        for (int q = 0; q < PAIRS; ++q) {
+            // Lanes of the missing tap read a real (finite) weight and a zero input.
+            const bool zero = odd && half == 1 && q == PAIRS - 1;
+            const float a = wr[zero ? -1 : 2 * q];
+            const int off = rbase + 2 * q * p.d_w;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const float bv = patch[zero ? zero_slot : off + poff[j]];
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bv, acc[j], 0, 0, 0);
+            }
+        }
+    }
+
+    // Epilogue: D row = output channel, column = pixel of the 16x16 block.
+    // Operand loads come from clamped addresses ahead of the guarded stores.
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = wave_n * 64 + j * 32 + col;
+        const int oy = ty0 + n / kPatchTile;
+        const int ox = tx0 + n % kPatchTile;
+        const bool pix_ok = oy < p.out_h && ox < p.out_w;
+        const int64_t pix = pix_ok ? static_cast<int64_t>(oy) * p.out_w + ox : 0;
+        float value[16];
+        int64_t yi[16];
+        bool ok[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int ml = wave_m * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+            ok[v] = pix_ok && m0 + ml < p.mg;
+            const int64_t oc = static_cast<int64_t>(g) * p.mg + (ok[v] ? m0 + ml : 0);
+            yi[v] = (b * p.m + oc) * p.plane_out + pix;
+            value[v] = p.bias != nullptr ? acc[j][v] + bias_s[ml] : acc[j][v];
+        }
+        if (p.residual != nullptr) {
+            float res[16];
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                res[v] = p.residual[ok[v] ? yi[v] : 0];
+            }
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                value[v] = value[v] + res[v];
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            float out = value[v];
+            if (p.relu) {
+                out = (0.0f < out) ? out : 0.0f; // std::max(0.0f, v)
+            }
+            if (ok[v]) {
+                p.y[yi[v]] = out;
+            }
+        }
+    }
+}
+
+// True when the patch kernel applies: 2-D, few channels per group, filter
+// rows of up to 8 taps, and one block's weights and input patch fit in 64 KiB
+// of LDS.
+bool TryPatchConv(const ConvArgs& p, hipStream_t stream) {
+    if (p.k_d != 1 || p.in_d != 1 || p.out_d != 1 || p.cg > 4 || p.k_w > 8) {
+        return false;
+    }
+    PatchGeom pg{};
+    const int pairs = (p.k_w + 1) / 2;
+    pg.knat = static_cast<int32_t>(p.cg) * p.k_h * p.k_w;
+    pg.wpitch = pg.knat | 1;
+    pg.ph = (kPatchTile - 1) * p.s_h + (p.k_h - 1) * p.d_h + 1;
+    pg.pw = (kPatchTile - 1) * p.s_w + (2 * pairs - 1) * p.d_w + 1;
+    const int64_t patch_floats = p.cg * pg.ph * pg.pw + 1 + kPatchM; // + zero slot + bias
+    const size_t lds_bytes = (static_cast<size_t>(kPatchM) * pg.wpitch + patch_floats) * sizeof(float);
+    if (patch_floats > kPatchMaxIn || lds_bytes > 64 * 1024) {
+        return false;
+    }
+    pg.tiles_w = (p.out_w + kPatchTile - 1) / kPatchTile;
+    pg.tiles_h = (p.out_h + kPatchTile - 1) / kPatchTile;
+    const int64_t blocks = p.batch * pg.tiles_w * pg.tiles_h;
+    const int64_t m_blocks = (p.mg + kPatchM - 1) / kPatchM;
+    if (blocks > 0x7FFFFFFF || m_blocks > 65535 || p.group > 65535) {
+        return false;
+    }
+    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(m_blocks), static_cast<unsigned>(p.group));
+    switch (pairs) {
+    case 1:
+        PatchConvKernel<1><<<grid, 512, lds_bytes, stream>>>(p, pg);
+        break;
+    case 2:
+        PatchConvKernel<2><<<grid, 512, lds_bytes, stream>>>(p, pg);
+        break;
+    case 3:
+        PatchConvKernel<3><<<grid, 512, lds_bytes, stream>>>(p, pg);
+        break;
+    default:
+        PatchConvKernel<4><<<grid, 512, lds_bytes, stream>>>(p, pg);
+        break;
+    }
+    CheckLaunch("PatchConvKernel launch");
+    return true;
+}
+
 // A 1x1, stride-1, unpadded, ungrouped convolution is Y[b] = W[M,C] * X[b][C,P]
 // with P = D*H*W: a batched GEMM whose B batches are the images.
 bool TryPointwise(const ConvArgs& p, hipStream_t stream) {
@@ -638,6 +882,9 @@ extern "C" int nert_hip_conv_fused_f32(const float* x, const float* w, const flo
         }
         hipStream_t s = nert_hip::StreamOr(stream);
         if (p.residual == nullptr && !p.relu && nert_hip::TryPointwise(p, s)) {
+            return;
+        }
+        if (nert_hip::TryPatchConv(p, s)) {
             return;
         }
         if (p.mg <= 32) {

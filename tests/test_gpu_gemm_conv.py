@@ -232,10 +232,34 @@ def test_fused_conv_errors(gpu):
 def _conv_out(xs, ws, attrs):
     pads = attrs.get("pads", [0, 0, 0, 0])
     s = attrs.get("strides", [1, 1])
-    oh = (xs[2] + pads[0] + pads[2] - ws[2]) // s[0] + 1
-    ow = (xs[3] + pads[1] + pads[3] - ws[3]) // s[1] + 1
+    d = attrs.get("dilations", [1, 1])
+    oh = (xs[2] + pads[0] + pads[2] - (d[0] * (ws[2] - 1) + 1)) // s[0] + 1
+    ow = (xs[3] + pads[1] + pads[3] - (d[1] * (ws[3] - 1) + 1)) // s[1] + 1
     return (xs[0], ws[0], oh, ow)
 
 
 def _restate_args(attrs):
     return {"strides": attrs.get("strides"), "pads": attrs.get("pads"), "group": attrs.get("group", 1)}
+
+
+# --- small-channel convolutions (image stems) --------------------------------
+
+@pytest.mark.parametrize("xs,ws,attrs", [
+    ((4, 3, 64, 64), (64, 3, 7, 7), {"pads": [3, 3, 3, 3], "strides": [2, 2]}),     # ResNet stem
+    ((2, 3, 70, 50), (16, 3, 3, 3), {"pads": [1, 1, 1, 1], "strides": [2, 2]}),     # detector stem, ragged
+    ((2, 1, 33, 31), (100, 1, 5, 4), {"pads": [2, 1, 2, 2], "dilations": [2, 1]}),  # M > 64, even KW
+    ((2, 4, 20, 20), (8, 2, 3, 3), {"pads": [1, 1, 1, 1], "group": 2}),             # groups
+])
+def test_small_channel_conv(gpu, xs, ws, attrs):
+    x, w, b = randn(xs, seed=50), randn(ws, seed=51), randn((ws[0],), seed=52)
+    assert_parity("Conv", [x, w, b], [(_conv_out(xs, ws, attrs), F)], attrs)
+
+
+def test_small_channel_conv_nonfinite_inputs(gpu):
+    """A padded (zero-weight) tap must not turn an inf input into NaN."""
+    x = randn((1, 3, 40, 40), seed=53)
+    x[0, 1, 10, 13] = np.inf
+    x[0, 2, 30, 7] = -np.inf
+    w, b = randn((64, 3, 7, 7), seed=54), randn((64,), seed=55)
+    attrs = {"pads": [3, 3, 3, 3], "strides": [2, 2]}
+    assert_parity("Conv", [x, w, b], [(_conv_out(x.shape, w.shape, attrs), F)], attrs)
