@@ -50,6 +50,39 @@ void ShadowPut(const void* dst, const void* src, int64_t bytes);
 void ShadowDrop(const void* dst, int64_t bytes);
 bool ShadowGet(const void* src, int64_t bytes, void* out);
 
+// Unsigned division by a runtime divisor via multiply-high and shift
+// (Granlund & Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994): q = (umulhi(n, m) + n) >> s, exact for all
+// 32-bit n when evaluated in 64 bits. Kernels whose index space fits 32 bits
+// decode multi-dimensional indices with it instead of 64-bit division.
+struct FastDiv {
+    uint32_t d;
+    uint32_t m;
+    uint32_t s;
+    static FastDiv Make(uint32_t d) {
+        FastDiv f{d, 0, 0};
+        if (d > 1) {
+            uint32_t l = 0;
+            while ((uint64_t{1} << l) < d) {
+                ++l;
+            }
+            f.s = l;
+            f.m = static_cast<uint32_t>(((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1);
+        }
+        return f;
+    }
+    __device__ __forceinline__ uint32_t Div(uint32_t n) const {
+        return static_cast<uint32_t>((static_cast<uint64_t>(__umulhi(n, m)) + n) >> s);
+    }
+};
+
+// Quotient and remainder of a 32-bit index by FastDiv `f`.
+__device__ __forceinline__ uint32_t DivMod(const FastDiv& f, uint32_t n, uint32_t& rem) {
+    const uint32_t q = f.Div(n);
+    rem = n - q * f.d;
+    return q;
+}
+
 inline unsigned GridFor(int64_t work, int per_block, int64_t cap = 1 << 20) {
     int64_t blocks = (work + per_block - 1) / per_block;
     if (blocks < 1) {

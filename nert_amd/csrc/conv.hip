@@ -27,31 +27,6 @@
 namespace nert_hip {
 namespace {
 
-// Unsigned division by a runtime divisor via multiply-high and shift
-// (Granlund & Montgomery, "Division by invariant integers using
-// multiplication", PLDI 1994): q = (umulhi(n, m) + n) >> s, exact for all
-// 32-bit n when evaluated in 64 bits.
-struct FastDiv {
-    uint32_t d;
-    uint32_t m;
-    uint32_t s;
-    static FastDiv Make(uint32_t d) {
-        FastDiv f{d, 0, 0};
-        if (d > 1) {
-            uint32_t l = 0;
-            while ((uint64_t{1} << l) < d) {
-                ++l;
-            }
-            f.s = l;
-            f.m = static_cast<uint32_t>(((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1);
-        }
-        return f;
-    }
-    __device__ __forceinline__ uint32_t Div(uint32_t n) const {
-        return static_cast<uint32_t>((static_cast<uint64_t>(__umulhi(n, m)) + n) >> s);
-    }
-};
-
 struct ConvArgs {
     const float* x;
     const float* w;

@@ -20,18 +20,39 @@ constexpr int kMaxRank = 10;
 
 __device__ __forceinline__ void RaiseFlag(int32_t* flags, int32_t bit) { atomicOr(flags, bit); }
 
+// Divisors of the [outer, index_count, inner] decomposition; the 32-bit
+// path is taken when the output has < 2^31 elements.
+struct GatherDivs {
+    FastDiv inner, count;
+    int32_t small;
+};
+
+__device__ __forceinline__ void GatherDecode(int64_t i, int64_t inner, int64_t index_count, const GatherDivs& g,
+                                             int64_t& o, int64_t& j, int64_t& e) {
+    if (g.small) {
+        uint32_t r;
+        const uint32_t q = DivMod(g.inner, static_cast<uint32_t>(i), r);
+        e = r;
+        o = DivMod(g.count, q, r);
+        j = r;
+    } else {
+        e = i % inner;
+        const int64_t q = i / inner;
+        j = q % index_count;
+        o = q / index_count;
+    }
+}
+
 // y[o, j, n] = x[o, wrap(idx[j]), n] over [outer, index_count, inner]
 // (src/kernels/gather.cpp:29-46).
 template <typename T>
 __global__ void GatherKernel(const T* __restrict__ x, const int64_t* __restrict__ idx, T* __restrict__ y, int64_t outer,
-                             int64_t dim, int64_t index_count, int64_t inner, int32_t* flags) {
+                             int64_t dim, int64_t index_count, int64_t inner, GatherDivs g, int32_t* flags) {
     const int64_t n = outer * index_count * inner;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n; i += stride) {
-        const int64_t e = i % inner;
-        const int64_t r = i / inner;
-        const int64_t j = r % index_count;
-        const int64_t o = r / index_count;
+        int64_t o, j, e;
+        GatherDecode(i, inner, index_count, g, o, j, e);
         int64_t k = idx[j];
         if (k < 0) {
             k += dim;
@@ -47,14 +68,13 @@ __global__ void GatherKernel(const T* __restrict__ x, const int64_t* __restrict_
 // Rows of 16-byte vectors when inner is a multiple of the vector width.
 template <typename V>
 __global__ void GatherRowsKernel(const V* __restrict__ x, const int64_t* __restrict__ idx, V* __restrict__ y,
-                                 int64_t outer, int64_t dim, int64_t index_count, int64_t inner_v, int32_t* flags) {
+                                 int64_t outer, int64_t dim, int64_t index_count, int64_t inner_v, GatherDivs g,
+                                 int32_t* flags) {
     const int64_t n = outer * index_count * inner_v;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n; i += stride) {
-        const int64_t e = i % inner_v;
-        const int64_t r = i / inner_v;
-        const int64_t j = r % index_count;
-        const int64_t o = r / index_count;
+        int64_t o, j, e;
+        GatherDecode(i, inner_v, index_count, g, o, j, e);
         int64_t k = idx[j];
         if (k < 0) {
             k += dim;
@@ -205,15 +225,20 @@ void LaunchGather(const void* x, const int64_t* idx, void* y, int64_t outer, int
     const int64_t bytes_inner = inner * static_cast<int64_t>(sizeof(T));
     const bool vec = bytes_inner % 16 == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0 &&
                      (reinterpret_cast<uintptr_t>(y) % 16) == 0;
+    const int64_t unit = vec ? bytes_inner / 16 : inner;
+    const int64_t n = outer * index_count * unit;
+    GatherDivs g{};
+    g.small = n < (int64_t{1} << 31) ? 1 : 0;
+    if (g.small) {
+        g.inner = FastDiv::Make(static_cast<uint32_t>(unit));
+        g.count = FastDiv::Make(static_cast<uint32_t>(index_count));
+    }
     if (vec) {
-        const int64_t inner_v = bytes_inner / 16;
-        const int64_t n = outer * index_count * inner_v;
         GatherRowsKernel<uint4><<<GridFor(n, 256, 16384), 256, 0, s>>>(
-            static_cast<const uint4*>(x), idx, static_cast<uint4*>(y), outer, dim, index_count, inner_v, ErrorFlags());
+            static_cast<const uint4*>(x), idx, static_cast<uint4*>(y), outer, dim, index_count, unit, g, ErrorFlags());
     } else {
-        const int64_t n = outer * index_count * inner;
         GatherKernel<T><<<GridFor(n, 256, 16384), 256, 0, s>>>(static_cast<const T*>(x), idx, static_cast<T*>(y),
-                                                               outer, dim, index_count, inner, ErrorFlags());
+                                                               outer, dim, index_count, unit, g, ErrorFlags());
     }
 }
 

@@ -26,7 +26,34 @@ struct CopyArgs {
     int64_t src_strides[kMaxRank]; // elements
     int64_t dst_strides[kMaxRank];
     int64_t src_mods[kMaxRank]; // 0 = no modulus
+    FastDiv div[kMaxRank];      // by dims (32-bit index path)
+    FastDiv mod_div[kMaxRank];  // by src_mods
 };
+
+// Index spaces below 2^31 elements (all but giant tensors): the same walk
+// with 32-bit multiply-shift division instead of 64-bit division.
+template <typename T>
+__global__ void StridedCopy32Kernel(CopyArgs a, uint32_t n) {
+    const T* src = reinterpret_cast<const T*>(a.src);
+    T* dst = reinterpret_cast<T*>(a.dst);
+    const uint32_t stride = gridDim.x * blockDim.x;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        uint32_t rem = i;
+        int64_t so = 0;
+        int64_t d_o = 0;
+        for (int d = a.rank - 1; d >= 0; --d) {
+            uint32_t c;
+            rem = DivMod(a.div[d], rem, c);
+            uint32_t sc = c;
+            if (a.src_mods[d] > 0) {
+                DivMod(a.mod_div[d], c, sc);
+            }
+            so += static_cast<int64_t>(sc) * a.src_strides[d];
+            d_o += static_cast<int64_t>(c) * a.dst_strides[d];
+        }
+        dst[d_o] = src[so];
+    }
+}
 
 template <typename T>
 __global__ void StridedCopyKernel(CopyArgs a, int64_t n) {
@@ -86,6 +113,10 @@ int64_t Collapse(int rank, const int64_t* dims, const int64_t* ss, const int64_t
         a.src_strides[d] = cs[d];
         a.dst_strides[d] = cdst[d];
         a.src_mods[d] = cm[d];
+        if (n < (int64_t{1} << 31)) {
+            a.div[d] = FastDiv::Make(static_cast<uint32_t>(cd[d]));
+            a.mod_div[d] = FastDiv::Make(static_cast<uint32_t>(cm[d] > 0 ? cm[d] : 1));
+        }
     }
     return n;
 }
@@ -98,6 +129,8 @@ struct PadArgs {
     int64_t out_dims[kMaxRank];
     int64_t begins[kMaxRank];
     int64_t in_strides[kMaxRank];
+    FastDiv div[kMaxRank]; // by out_dims (32-bit index path)
+    int32_t small;         // output has < 2^31 elements
 };
 
 // src/kernels/pad.cpp MapPosition: -1 means "use the fill value".
@@ -127,11 +160,19 @@ __global__ void PadKernel(const T* __restrict__ x, T* __restrict__ y, PadArgs a,
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n; i += stride) {
         int64_t rem = i;
+        uint32_t rem32 = static_cast<uint32_t>(i);
         int64_t off = 0;
         bool filled = false;
         for (int d = a.rank - 1; d >= 0; --d) {
-            const int64_t c = rem % a.out_dims[d];
-            rem /= a.out_dims[d];
+            int64_t c;
+            if (a.small) {
+                uint32_t c32;
+                rem32 = DivMod(a.div[d], rem32, c32);
+                c = c32;
+            } else {
+                c = rem % a.out_dims[d];
+                rem /= a.out_dims[d];
+            }
             const int64_t s = MapPos(c - a.begins[d], a.in_dims[d], a.mode);
             filled = filled || s < 0;
             off += (s < 0 ? 0 : s) * a.in_strides[d];
@@ -166,15 +207,20 @@ int nert_hip_copy_strided(int elem_size, const void* src, void* dst, int rank, c
             return;
         }
         const unsigned grid = GridFor(n, 256, 16384);
+        const bool small = n < (int64_t{1} << 31);
+        const uint32_t n32 = static_cast<uint32_t>(small ? n : 0);
         switch (elem_size) {
         case 1:
-            StridedCopyKernel<uint8_t><<<grid, 256, 0, s>>>(a, n);
+            small ? StridedCopy32Kernel<uint8_t><<<grid, 256, 0, s>>>(a, n32)
+                  : StridedCopyKernel<uint8_t><<<grid, 256, 0, s>>>(a, n);
             break;
         case 4:
-            StridedCopyKernel<uint32_t><<<grid, 256, 0, s>>>(a, n);
+            small ? StridedCopy32Kernel<uint32_t><<<grid, 256, 0, s>>>(a, n32)
+                  : StridedCopyKernel<uint32_t><<<grid, 256, 0, s>>>(a, n);
             break;
         case 8:
-            StridedCopyKernel<uint64_t><<<grid, 256, 0, s>>>(a, n);
+            small ? StridedCopy32Kernel<uint64_t><<<grid, 256, 0, s>>>(a, n32)
+                  : StridedCopyKernel<uint64_t><<<grid, 256, 0, s>>>(a, n);
             break;
         default:
             throw Error("copy: unsupported element size");
@@ -198,6 +244,8 @@ int nert_hip_pad(int dtype, const void* x, void* y, int rank, const int64_t* in_
             a.in_dims[d] = in_dims[d];
             a.out_dims[d] = out_dims[d];
             a.begins[d] = begins[d];
+            a.div[d] = FastDiv::Make(static_cast<uint32_t>(out_dims[d] > 0 && out_dims[d] < (int64_t{1} << 32)
+                                                                ? out_dims[d] : 1));
             a.in_strides[d] = st;
             st *= in_dims[d];
             n *= out_dims[d];
@@ -205,6 +253,7 @@ int nert_hip_pad(int dtype, const void* x, void* y, int rank, const int64_t* in_
         if (n <= 0) {
             return;
         }
+        a.small = n < (int64_t{1} << 31) ? 1 : 0;
         hipStream_t s = StreamOr(stream);
         const unsigned grid = GridFor(n, 256, 16384);
         if (dtype == NERT_F32) {

@@ -21,16 +21,34 @@ struct PoolArgs {
     int32_t k_h, k_w, s_h, s_w, d_h, d_w, p_h, p_w;
     int32_t pad_end_h, pad_end_w;
     int32_t count_include_pad;
+    FastDiv div_w, div_h; // by out_w, out_h (32-bit index path)
 };
 
+// Output index -> (plane, oh, ow); SMALL when the output has < 2^31 elements.
+template <bool SMALL>
+__device__ __forceinline__ void PoolDecode(const PoolArgs& p, int64_t i, int64_t& plane, int32_t& oh, int32_t& ow) {
+    if constexpr (SMALL) {
+        uint32_t r;
+        const uint32_t t = DivMod(p.div_w, static_cast<uint32_t>(i), r);
+        ow = static_cast<int32_t>(r);
+        plane = DivMod(p.div_h, t, r);
+        oh = static_cast<int32_t>(r);
+    } else {
+        ow = static_cast<int32_t>(i % p.out_w);
+        const int64_t t = i / p.out_w;
+        oh = static_cast<int32_t>(t % p.out_h);
+        plane = t / p.out_h;
+    }
+}
+
+template <bool SMALL>
 __global__ void MaxPool2dKernel(PoolArgs p) {
     const int64_t total = p.planes * p.out_h * p.out_w;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total; i += stride) {
-        const int32_t ow = static_cast<int32_t>(i % p.out_w);
-        const int64_t t = i / p.out_w;
-        const int32_t oh = static_cast<int32_t>(t % p.out_h);
-        const int64_t plane = t / p.out_h;
+        int64_t plane;
+        int32_t oh, ow;
+        PoolDecode<SMALL>(p, i, plane, oh, ow);
         const float* xp = p.x + plane * p.in_h * p.in_w;
         const int32_t h0 = oh * p.s_h - p.p_h;
         const int32_t w0 = ow * p.s_w - p.p_w;
@@ -61,14 +79,14 @@ __global__ void MaxPool2dKernel(PoolArgs p) {
 // by either the clipped tap count or (count_include_pad) the window clipped to
 // the padded extent. Same operations in the same order, so the result is
 // bit-identical to the reference.
+template <bool SMALL>
 __global__ void AvgPool2dKernel(PoolArgs p) {
     const int64_t total = p.planes * p.out_h * p.out_w;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total; i += stride) {
-        const int32_t ow = static_cast<int32_t>(i % p.out_w);
-        const int64_t t = i / p.out_w;
-        const int32_t oh = static_cast<int32_t>(t % p.out_h);
-        const int64_t plane = t / p.out_h;
+        int64_t plane;
+        int32_t oh, ow;
+        PoolDecode<SMALL>(p, i, plane, oh, ow);
         const float* xp = p.x + plane * p.in_h * p.in_w;
         const int32_t h_start = oh * p.s_h - p.p_h;
         const int32_t h_end = min(h_start + p.k_h, p.in_h + p.pad_end_h);
@@ -138,6 +156,8 @@ PoolArgs MakeArgs(const float* x, float* y, const nert_pool_desc* d) {
     p.pad_end_h = static_cast<int32_t>(d->pad_end[0]);
     p.pad_end_w = static_cast<int32_t>(d->pad_end[1]);
     p.count_include_pad = static_cast<int32_t>(d->count_include_pad);
+    p.div_w = FastDiv::Make(static_cast<uint32_t>(p.out_w > 0 ? p.out_w : 1));
+    p.div_h = FastDiv::Make(static_cast<uint32_t>(p.out_h > 0 ? p.out_h : 1));
     return p;
 }
 
@@ -155,7 +175,11 @@ int nert_hip_maxpool2d_f32(const float* x, float* y, const nert_pool_desc* d, vo
         if (total <= 0) {
             return;
         }
-        MaxPool2dKernel<<<GridFor(total, 256, 16384), 256, 0, StreamOr(stream)>>>(p);
+        if (total < (int64_t{1} << 31)) {
+            MaxPool2dKernel<true><<<GridFor(total, 256, 16384), 256, 0, StreamOr(stream)>>>(p);
+        } else {
+            MaxPool2dKernel<false><<<GridFor(total, 256, 16384), 256, 0, StreamOr(stream)>>>(p);
+        }
         CheckLaunch("MaxPool2dKernel launch");
     });
 }
@@ -167,7 +191,11 @@ int nert_hip_avgpool2d_f32(const float* x, float* y, const nert_pool_desc* d, vo
         if (total <= 0) {
             return;
         }
-        AvgPool2dKernel<<<GridFor(total, 256, 16384), 256, 0, StreamOr(stream)>>>(p);
+        if (total < (int64_t{1} << 31)) {
+            AvgPool2dKernel<true><<<GridFor(total, 256, 16384), 256, 0, StreamOr(stream)>>>(p);
+        } else {
+            AvgPool2dKernel<false><<<GridFor(total, 256, 16384), 256, 0, StreamOr(stream)>>>(p);
+        }
         CheckLaunch("AvgPool2dKernel launch");
     });
 }

@@ -27,6 +27,8 @@ struct ResizeArgs {
     int64_t out_dims[kMaxRank];
     int64_t in_strides[kMaxRank];
     double scales[kMaxRank];
+    FastDiv div[kMaxRank]; // by out_dims (32-bit index path)
+    int32_t small;         // output has < 2^31 elements
 };
 
 // src/kernels/resize.cpp:48-63
@@ -84,9 +86,17 @@ __global__ void ResizeKernel(const T* __restrict__ x, T* __restrict__ y, ResizeA
         int64_t upper[kMaxRank];
         double weight[kMaxRank];
         int64_t rem = i;
+        uint32_t rem32 = static_cast<uint32_t>(i);
         for (int d = a.rank - 1; d >= 0; --d) {
-            const int64_t o = rem % a.out_dims[d];
-            rem /= a.out_dims[d];
+            int64_t o;
+            if (a.small) {
+                uint32_t c;
+                rem32 = DivMod(a.div[d], rem32, c);
+                o = c;
+            } else {
+                o = rem % a.out_dims[d];
+                rem /= a.out_dims[d];
+            }
             const double src = SourceCoord(a.transform, o, a.in_dims[d], a.out_dims[d], a.scales[d]);
             if (!a.linear) {
                 lower[d] = upper[d] = NearestIndex(a.nearest, src, a.in_dims[d]);
@@ -229,6 +239,8 @@ int nert_hip_resize(int dtype, const void* x, void* y, int rank, const int64_t* 
             a.in_dims[d] = in_dims[d];
             a.out_dims[d] = out_dims[d];
             a.scales[d] = scales[d];
+            a.div[d] = FastDiv::Make(static_cast<uint32_t>(out_dims[d] > 0 && out_dims[d] < (int64_t{1} << 32)
+                                                                ? out_dims[d] : 1));
             a.in_strides[d] = st;
             st *= in_dims[d];
             n *= out_dims[d];
@@ -236,6 +248,7 @@ int nert_hip_resize(int dtype, const void* x, void* y, int rank, const int64_t* 
         if (n <= 0) {
             return;
         }
+        a.small = n < (int64_t{1} << 31) ? 1 : 0;
         hipStream_t s = StreamOr(stream);
         const unsigned grid = GridFor(n, 256, 16384);
         if (dtype == NERT_F32) {
