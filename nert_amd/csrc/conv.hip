@@ -562,6 +562,349 @@ void LaunchConv(ConvArgs p, hipStream_t stream) {
     }
 }
 
+// ---- 3x3 convolution from an LDS input patch shared by all taps -------------
+//
+// The tap-major kernel above stages a fresh B tile for every (channel block,
+// tap) pair, although the nine taps of a 3x3 filter read shifted windows of
+// the same input rows. Here a workgroup owns BM output channels x BN
+// consecutive output pixels (flattened over batch, rows and columns) and
+// walks the channels in blocks of kHaloBK. Per block it copies into LDS
+//   - the input patch those pixels read: every input row any of them touches,
+//     full padded width, zero outside the image, all kHaloBK channels of a
+//     position side by side (kHaloCS floats per position), and
+//   - the weights of its BM channels for the block, [m][tap][c],
+// then runs all nine taps out of LDS: the B fragment of tap (kh, kw) for a
+// pixel is the patch position of its window origin shifted by
+// kh * d_h * PW + kw * d_w, a wave-uniform offset. Pixels of one tile may
+// belong to several images: the patch then holds one run of rows per image
+// (the first and last run partial) and a pixel's origin row counts from the
+// start of its image's run.
+//
+// Each lane's half of an MFMA's K = 2 pair is a channel: lanes 0-31 take
+// channel kk and lanes 32-63 channel 4 + kk of the block (kk = 0..3), so one
+// 16-byte LDS read returns a lane's operand for four consecutive MFMAs; A and
+// B use the same pairing, so the sum over the block's eight channels is the
+// same convolution. Two barriers per block; the next block's global loads are
+// in flight during the current block's 9 x 4 MFMA steps.
+constexpr int kHaloBK = 8;               // channels per K step
+constexpr int kHaloCS = kHaloBK + 4;     // LDS floats per patch position (16-byte aligned rows)
+constexpr int kHaloMaxLds = 64 * 1024;   // dynamic LDS budget per workgroup
+
+struct HaloGeom {
+    int32_t pw;            // patch row length: (OW - 1) * s_w + (KW - 1) * d_w + 1
+    int32_t positions;     // patch positions (rows * pw) the LDS holds
+    int32_t blocks;        // channel blocks per group: C_g / kHaloBK
+    int32_t blocks_per_split;
+    FastDiv div_plane_out; // by OH * OW
+    FastDiv div_out_w;     // by OW
+    FastDiv div_pw;        // by pw
+    FastDiv div_rows_full; // by the patch rows of a whole image
+    int32_t rows_full;
+};
+
+// Register budget: 128 VGPRs (four waves per SIMD, two workgroups per CU),
+// except with four patch positions per thread, where that would spill.
+template <class Shape, int KH, int KW, int NPOS>
+__global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKernel(ConvArgs p, HaloGeom h) {
+    constexpr int BM = Shape::kBM;
+    constexpr int BN = Shape::kBN;
+    constexpr int BK = kHaloBK;
+    constexpr int THREADS = Shape::kThreads;
+    constexpr int kTaps = KH * KW;
+    constexpr int kAPitch = kTaps * BK + 4;                        // [m][tap][c] rows, 16-byte aligned
+    constexpr int kQuadsRow = kTaps * BK / 4;                      // 16-byte weight loads per row and block
+    constexpr int kAQuads = (BM * kQuadsRow + THREADS - 1) / THREADS; // weight loads per thread
+    static_assert(BK == 8 && (kTaps * BK) % 4 == 0, "weight rows must split into 16-byte loads");
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    float* const as = smem;
+    float* const bs = smem + BM * kAPitch;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wave_m = wave % Shape::kWavesM;
+    const int wave_n = wave / Shape::kWavesM;
+    const int half = lane >> 5;
+    const int64_t tiles_m = (p.mg + BM - 1) / BM;
+    const int64_t row0 = (blockIdx.x % tiles_m) * BM;
+    const int64_t col0 = (blockIdx.x / tiles_m) * BN;
+    const int g = blockIdx.y;
+    const int split = blockIdx.z;
+    const int cb_begin = split * h.blocks_per_split;
+    const int cb_end = min(cb_begin + h.blocks_per_split, h.blocks);
+
+    // The tile's first and last pixels: image and output row of each.
+    uint32_t rem;
+    const uint32_t n_first = static_cast<uint32_t>(col0);
+    const uint32_t n_last = static_cast<uint32_t>(min(col0 + BN, p.n_total) - 1);
+    const int32_t b_first = static_cast<int32_t>(DivMod(h.div_plane_out, n_first, rem));
+    const int32_t oh_first = static_cast<int32_t>(h.div_out_w.Div(rem));
+    const int32_t b_last = static_cast<int32_t>(DivMod(h.div_plane_out, n_last, rem));
+    const int32_t oh_last = static_cast<int32_t>(h.div_out_w.Div(rem));
+    const int32_t halo = (KH - 1) * p.d_h + 1;
+    const int32_t run0_end = b_last == b_first ? oh_last : p.out_h - 1;
+    const int32_t rows0 = (run0_end - oh_first) * p.s_h + halo; // patch rows of the first image
+
+    // Patch positions this thread copies: q = tid + i * THREADS. Their byte
+    // offsets at channel 0 of the group are fixed for the whole K walk.
+    const __amdgpu_buffer_rsrc_t xr = MakeRsrc(p.x, static_cast<uint32_t>(p.batch * p.c * p.plane_in * 4));
+    uint32_t bvoff[NPOS];
+#pragma unroll
+    for (int i = 0; i < NPOS; ++i) {
+        const uint32_t q = static_cast<uint32_t>(tid + i * THREADS);
+        uint32_t off = kOutOfRange;
+        if (q < static_cast<uint32_t>(h.positions)) {
+            uint32_t x;
+            const int32_t r = static_cast<int32_t>(DivMod(h.div_pw, q, x));
+            int32_t seg = 0;
+            int32_t local = r;
+            if (r >= rows0) {
+                uint32_t lr;
+                seg = 1 + static_cast<int32_t>(DivMod(h.div_rows_full, static_cast<uint32_t>(r - rows0), lr));
+                local = static_cast<int32_t>(lr);
+            }
+            const int32_t b = b_first + seg;
+            const int32_t ih = (seg == 0 ? oh_first : 0) * p.s_h - p.p_h + local;
+            const int32_t iw = static_cast<int32_t>(x) - p.p_w;
+            if (b <= b_last && ih >= 0 && ih < p.in_h && iw >= 0 && iw < p.in_w) {
+                off = static_cast<uint32_t>(((static_cast<int64_t>(b) * p.c + static_cast<int64_t>(g) * p.cg) *
+                                                 p.plane_in +
+                                             ih * p.in_w + iw) *
+                                            4);
+            }
+        }
+        bvoff[i] = off;
+    }
+    const uint32_t plane_bytes = static_cast<uint32_t>(p.plane_in * 4);
+
+    // Weights: a block's slice of a row is kTaps * BK consecutive floats
+    // (channel-major, taps inside), copied as 16-byte loads; quad
+    // e = tid + j * THREADS is row e / kQuadsRow, floats 4 * (e % kQuadsRow)...
+    // The host guarantees 16-byte alignment (C_g a multiple of 4).
+    const __amdgpu_buffer_rsrc_t wr = MakeRsrc(p.w, static_cast<uint32_t>(p.m * p.kg * 4));
+    uint32_t avoff[kAQuads];
+#pragma unroll
+    for (int j = 0; j < kAQuads; ++j) {
+        const int e = tid + j * THREADS;
+        const int64_t m = row0 + e / kQuadsRow;
+        const int k0 = (e % kQuadsRow) * 4;
+        avoff[j] = e < BM * kQuadsRow && m < p.mg ? static_cast<uint32_t>(((g * p.mg + m) * p.kg + k0) * 4)
+                                                  : kOutOfRange;
+    }
+
+    // MFMA operand bases: A row of this lane, B patch position of the window
+    // origin of each of the wave's pixel columns.
+    const int a_lane = (wave_m * Shape::kWaveM + (lane & 31)) * kAPitch + half * 4;
+    int b_lane[Shape::kSubN];
+#pragma unroll
+    for (int j = 0; j < Shape::kSubN; ++j) {
+        const int64_t n = col0 + wave_n * Shape::kWaveN + 32 * j + (lane & 31);
+        int32_t pos = 0; // columns past the end read position 0; their results are never stored
+        if (n < p.n_total) {
+            const int32_t b = static_cast<int32_t>(DivMod(h.div_plane_out, static_cast<uint32_t>(n), rem));
+            uint32_t ow;
+            const int32_t oh = static_cast<int32_t>(DivMod(h.div_out_w, rem, ow));
+            const int32_t seg = b - b_first;
+            const int32_t start = seg == 0 ? 0 : rows0 + (seg - 1) * h.rows_full;
+            const int32_t first = seg == 0 ? oh_first : 0;
+            pos = (start + (oh - first) * p.s_h) * h.pw + static_cast<int32_t>(ow) * p.s_w;
+        }
+        b_lane[j] = pos * kHaloCS + half * 4;
+    }
+    const int row_step = p.d_h * h.pw * kHaloCS;
+    const int col_step = p.d_w * kHaloCS;
+
+    float bv[NPOS][BK];
+    nert_floatx4 av[kAQuads];
+    auto load = [&](int cb) {
+        const uint32_t c_off = static_cast<uint32_t>(cb * BK) * plane_bytes;
+#pragma unroll
+        for (int i = 0; i < NPOS; ++i) {
+#pragma unroll
+            for (int c = 0; c < BK; ++c) {
+                bv[i][c] = BufferLoad(xr, bvoff[i], c_off + static_cast<uint32_t>(c) * plane_bytes);
+            }
+        }
+        const uint32_t w_off = static_cast<uint32_t>(cb * BK * kTaps * 4);
+#pragma unroll
+        for (int j = 0; j < kAQuads; ++j) {
+            av[j] = __builtin_bit_cast(nert_floatx4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         wr, static_cast<int>(avoff[j]), static_cast<int>(w_off), 0));
+        }
+    };
+    auto store = [&]() {
+#pragma unroll
+        for (int i = 0; i < NPOS; ++i) {
+            const int q = tid + i * THREADS;
+            if (q < h.positions) {
+                float* dst = bs + q * kHaloCS;
+                *reinterpret_cast<nert_floatx4*>(dst) = nert_floatx4{bv[i][0], bv[i][1], bv[i][2], bv[i][3]};
+                *reinterpret_cast<nert_floatx4*>(dst + 4) = nert_floatx4{bv[i][4], bv[i][5], bv[i][6], bv[i][7]};
+            }
+        }
+        // Weight float k of a row slice is channel k / kTaps, tap k % kTaps.
+#pragma unroll
+        for (int j = 0; j < kAQuads; ++j) {
+            const int e = tid + j * THREADS;
+            if (e < BM * kQuadsRow) {
+                float* row = as + (e / kQuadsRow) * kAPitch;
+                const int k0 = (e % kQuadsRow) * 4;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int k = k0 + q;
+                    row[(k % kTaps) * BK + k / kTaps] = av[j][q];
+                }
+            }
+        }
+    };
+
+    Accum<Shape> acc;
+    acc.zero();
+    if (cb_begin < cb_end) {
+        load(cb_begin);
+    }
+    for (int cb = cb_begin; cb < cb_end; ++cb) {
+        store();
+        __syncthreads();
+        if (cb + 1 < cb_end) {
+            load(cb + 1);
+        }
+        // Operands of tap t + 1 are read while the MFMAs of tap t run; the
+        // scheduling barriers keep the compiler from sinking the reads back
+        // behind the MFMAs.
+        nert_floatx4 a_next[Shape::kSubM];
+        nert_floatx4 b_next[Shape::kSubN];
+#pragma unroll
+        for (int i = 0; i < Shape::kSubM; ++i) {
+            a_next[i] = *reinterpret_cast<const nert_floatx4*>(as + a_lane + i * 32 * kAPitch);
+        }
+#pragma unroll
+        for (int j = 0; j < Shape::kSubN; ++j) {
+            b_next[j] = *reinterpret_cast<const nert_floatx4*>(bs + b_lane[j]);
+        }
+#pragma unroll
+        for (int t = 0; t < kTaps; ++t) {
+            nert_floatx4 a[Shape::kSubM];
+            nert_floatx4 b[Shape::kSubN];
+#pragma unroll
+            for (int i = 0; i < Shape::kSubM; ++i) {
+                a[i] = a_next[i];
+            }
+#pragma unroll
+            for (int j = 0; j < Shape::kSubN; ++j) {
+                b[j] = b_next[j];
+            }
+            if (t + 1 < kTaps) {
+                const int toff = ((t + 1) / KW) * row_step + ((t + 1) % KW) * col_step;
+#pragma unroll
+                for (int i = 0; i < Shape::kSubM; ++i) {
+                    a_next[i] = *reinterpret_cast<const nert_floatx4*>(as + a_lane + i * 32 * kAPitch + (t + 1) * BK);
+                }
+#pragma unroll
+                for (int j = 0; j < Shape::kSubN; ++j) {
+                    b_next[j] = *reinterpret_cast<const nert_floatx4*>(bs + b_lane[j] + toff);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+                for (int i = 0; i < Shape::kSubM; ++i) {
+#pragma unroll
+                    for (int j = 0; j < Shape::kSubN; ++j) {
+                        acc.c[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][kk], b[j][kk], acc.c[i][j], 0, 0, 0);
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        __syncthreads();
+    }
+    ConvEpilogue<Shape>(p, acc, row0, col0, g, split);
+}
+
+// Measured on the ResNet-18 bs32 3x3 layers: 64x256 tiles for 64 output
+// channels, 64x128 tiles (8 waves of 32x32) otherwise; 128x128 tiles and
+// four-wave workgroups were 1-10% slower.
+using HaloShapeW = TileShape<64, 256, kHaloBK, 2, 4>; // 8 waves, 32x64 each, for M_g <= 64
+using HaloShapeM = TileShape<64, 128, kHaloBK, 2, 4>; // 8 waves, 32x32 each
+
+template <class Shape, int NPOS>
+void LaunchHalo(const ConvArgs& p, const HaloGeom& h, dim3 grid, size_t lds, hipStream_t stream) {
+    HaloConvKernel<Shape, 3, 3, NPOS><<<grid, Shape::kThreads, lds, stream>>>(p, h);
+}
+
+// 3x3, 2-D, C_g a multiple of kHaloBK, stride no larger than the filter's
+// extent, everything addressable with 32-bit offsets, and one workgroup's
+// patch and weights within kHaloMaxLds.
+template <class Shape>
+bool TryHaloShape(ConvArgs p, hipStream_t stream) {
+    constexpr int kTaps = 9;
+    HaloGeom h{};
+    h.pw = (p.out_w - 1) * p.s_w + 2 * p.d_w + 1;
+    h.rows_full = (p.out_h - 1) * p.s_h + 2 * p.d_h + 1;
+    // A tile's pixels touch at most r_max output rows in at most s_max
+    // images; its patch has rows * s_h + images * (2 * d_h + 1 - s_h) rows.
+    const int64_t r_max = (Shape::kBN - 1 + p.out_w - 1) / p.out_w + 1;
+    const int64_t s_max = std::min<int64_t>((r_max - 1 + p.out_h - 1) / p.out_h + 1, p.batch);
+    const int64_t rows = r_max * p.s_h + s_max * (2 * p.d_h + 1 - p.s_h);
+    const int64_t positions = rows * h.pw;
+    const int64_t lds = (static_cast<int64_t>(Shape::kBM) * (kTaps * kHaloBK + 4) + positions * kHaloCS) * 4;
+    if (lds > kHaloMaxLds) {
+        return false;
+    }
+    const int64_t per_thread = (positions + Shape::kThreads - 1) / Shape::kThreads;
+    if (per_thread > 4) {
+        return false;
+    }
+    h.positions = static_cast<int32_t>(positions);
+    h.blocks = static_cast<int32_t>(p.cg / kHaloBK);
+    h.div_plane_out = FastDiv::Make(static_cast<uint32_t>(p.plane_out));
+    h.div_out_w = FastDiv::Make(static_cast<uint32_t>(p.out_w));
+    h.div_pw = FastDiv::Make(static_cast<uint32_t>(h.pw));
+    h.div_rows_full = FastDiv::Make(static_cast<uint32_t>(h.rows_full));
+    const int64_t tiles = ((p.mg + Shape::kBM - 1) / Shape::kBM) * ((p.n_total + Shape::kBN - 1) / Shape::kBN);
+    const int splits = PlanSplits(tiles * p.group, h.blocks, kResidentBlocks, 4);
+    h.blocks_per_split = (h.blocks + splits - 1) / splits;
+    p.k_per_split = 0;
+    p.partial = nullptr;
+    if (splits > 1) {
+        p.partial =
+            static_cast<float*>(Workspace(static_cast<int64_t>(splits) * p.group * p.mg * p.n_total * 4, stream));
+    }
+    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(p.group), static_cast<unsigned>(splits));
+    if (per_thread == 1) {
+        LaunchHalo<Shape, 1>(p, h, grid, static_cast<size_t>(lds), stream);
+    } else if (per_thread == 2) {
+        LaunchHalo<Shape, 2>(p, h, grid, static_cast<size_t>(lds), stream);
+    } else {
+        LaunchHalo<Shape, 4>(p, h, grid, static_cast<size_t>(lds), stream);
+    }
+    CheckLaunch("HaloConvKernel launch");
+    if (splits > 1) {
+        const int vec = (p.plane_out % 4 == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0) ? 4 : 1;
+        const int64_t work = p.group * p.mg * p.n_total / vec;
+        ConvSplitReduceKernel<<<GridFor(work, 256, 8192), 256, 0, stream>>>(p, splits, vec);
+        CheckLaunch("ConvSplitReduceKernel launch");
+    }
+    return true;
+}
+
+bool TryHaloConv(const ConvArgs& p, hipStream_t stream) {
+    const bool fits = p.k_d == 1 && p.in_d == 1 && p.out_d == 1 && p.k_h == 3 && p.k_w == 3 &&
+                      p.cg % kHaloBK == 0 && reinterpret_cast<uintptr_t>(p.w) % 16 == 0 && p.s_h >= 1 && p.s_w >= 1 && p.d_h >= 1 && p.d_w >= 1 &&
+                      p.s_h <= 2 * p.d_h + 1 && p.n_total < (int64_t{1} << 31) &&
+                      p.batch * p.c * p.plane_in * 4 < (int64_t{1} << 31) && p.m * p.kg * 4 < (int64_t{1} << 31) &&
+                      p.out_w < (1 << 16) && p.out_h < (1 << 16);
+    if (!fits) {
+        return false;
+    }
+    if (p.mg <= 64 && TryHaloShape<HaloShapeW>(p, stream)) {
+        return true;
+    }
+    return TryHaloShape<HaloShapeM>(p, stream);
+}
+
 // ---- Small-channel convolution from an LDS input patch -------------------------
 //
 // For C_g <= 4 (image stems: 3 input channels) the K dimension is only C*KH*KW
@@ -860,6 +1203,9 @@ extern "C" int nert_hip_conv_fused_f32(const float* x, const float* w, const flo
             return;
         }
         if (nert_hip::TryPatchConv(p, s)) {
+            return;
+        }
+        if (nert_hip::TryHaloConv(p, s)) {
             return;
         }
         if (p.mg <= 32) {

@@ -148,6 +148,36 @@ def test_conv_random(gpu, xs, ws, attrs):
     compare(got[0], ref, what="conv vs restatement")
 
 
+# 3x3 convolutions with C_g a multiple of 8 take the LDS-patch kernel; these
+# cover tiles that straddle images, several images per tile, strides 2 and 3,
+# dilation, asymmetric pads, groups, deep split-K and a too-wide patch that
+# falls back to the tap-major kernel.
+HALO_CASES = [
+    ((2, 64, 56, 56), (64, 64, 3, 3), {"pads": [1, 1, 1, 1]}),
+    ((5, 64, 7, 7), (128, 64, 3, 3), {"pads": [1, 1, 1, 1]}),
+    ((3, 32, 29, 31), (48, 32, 3, 3), {"pads": [1, 1, 1, 1], "strides": [2, 2]}),
+    ((2, 16, 20, 18), (40, 16, 3, 3), {"pads": [2, 2, 2, 2], "dilations": [2, 2]}),
+    ((2, 8, 15, 13), (24, 8, 3, 3), {"pads": [0, 1, 2, 0]}),
+    ((2, 8, 11, 12), (8, 8, 3, 3), {}),
+    ((2, 32, 12, 12), (48, 16, 3, 3), {"pads": [1, 1, 1, 1], "group": 2}),
+    ((2, 256, 9, 9), (96, 256, 3, 3), {"pads": [1, 1, 1, 1]}),
+    ((1, 8, 20, 20), (8, 8, 3, 3), {"strides": [3, 3], "pads": [1, 1, 1, 1]}),
+    ((2, 16, 10, 9), (16, 16, 3, 3), {"strides": [1, 2], "dilations": [2, 1], "pads": [2, 0, 1, 1]}),
+    ((1, 8, 6, 700), (16, 8, 3, 3), {"pads": [1, 1, 1, 1]}),
+]
+
+
+@pytest.mark.parametrize("xs,ws,attrs", HALO_CASES)
+def test_conv_lds_patch(gpu, xs, ws, attrs):
+    x = randn(xs, seed=sum(xs) + 1)
+    w = randn(ws, seed=sum(ws) + 1, scale=float(np.sqrt(2.0 / (ws[1] * 9))))
+    b = randn((ws[0],), seed=5, scale=0.1)
+    ref = restate.conv(x, w, b, attrs.get("strides"), attrs.get("dilations"), attrs.get("pads"),
+                       attrs.get("group", 1), "NOTSET")
+    got = assert_parity("Conv", [x, w, b], [(ref.shape, F)], attrs)
+    compare(got[0], ref, what="conv vs restatement")
+
+
 # --- BASELINE.json configs at full size -----------------------------------
 
 def test_config0_conv_3x3(gpu):
