@@ -909,14 +909,18 @@ bool TryHaloConv(const ConvArgs& p, hipStream_t stream) {
 //
 // For C_g <= 4 (image stems: 3 input channels) the K dimension is only C*KH*KW
 // and a K tile would hold a few channels of many taps, so the gather loaders
-// spend their time on index arithmetic. Instead each workgroup owns a 16x16
-// block of output pixels for 64 output channels: it copies the input patch
-// that block reads (C x PH x PW, zero outside the image) and the weights of
-// its 64 channels ([m][c][kh][kw] rows, as stored) into LDS once, then runs
-// every MFMA out of LDS. An MFMA step covers two neighbouring taps of one
-// filter row (kw = 2q and 2q + 1); for an odd KW the last step's second tap
-// does not exist, and its lanes read a zero from the patch's zero slot.
-constexpr int kPatchTile = 16;    // output tile is kPatchTile x kPatchTile pixels
+// spend their time on index arithmetic. Instead a workgroup keeps the weights
+// of its 64 output channels in LDS ([m][c][kh][kw] rows, as stored) and walks
+// 16x16 blocks of output pixels: for each it copies the input patch the block
+// reads (C x PH x PW, zero outside the image) into LDS and runs every MFMA out
+// of LDS. The workgroups are persistent (about two per CU, each taking every
+// gridDim.x-th block), so the weights are read once per workgroup, and the
+// patch is double buffered: the next block's patch is loaded into registers
+// while the current block's MFMAs run, one barrier per block. An MFMA step
+// covers two neighbouring taps of one filter row (kw = 2q and 2q + 1); for an
+// odd KW the last step's second tap does not exist, and its lanes read the
+// zero slot.
+constexpr int kPatchTile = 16;    // output block is kPatchTile x kPatchTile pixels
 constexpr int kPatchM = 64;       // output channels per workgroup
 constexpr int kPatchMaxIn = 8192; // patch floats
 
@@ -925,21 +929,25 @@ struct PatchGeom {
     int32_t wpitch;    // LDS weight row pitch (odd: conflict-free column reads)
     int32_t ph, pw;    // patch rows / row pitch
     int32_t tiles_w, tiles_h;
+    int32_t patch_floats;  // C_g * ph * pw
+    int32_t patch_stride;  // LDS floats between the two patch buffers
+    int32_t blocks;        // batch * tiles_h * tiles_w
+    FastDiv div_plane;     // by ph * pw
+    FastDiv div_pw;        // by pw
 };
 
 template <int PAIRS>
-__global__ __launch_bounds__(512) void PatchConvKernel(ConvArgs p, PatchGeom pg) {
-    // Dynamic LDS: weights [kPatchM][wpitch], then the patch and one zero float.
+__global__ __launch_bounds__(512, 4) void PatchConvKernel(ConvArgs p, PatchGeom pg) {
+    // Dynamic LDS: weights [kPatchM][wpitch], bias [kPatchM], the zero slot
+    // (4 floats), then two patch buffers.
     extern __shared__ __attribute__((aligned(16))) float smem[];
     float* const ws = smem;
-    float* const patch = smem + kPatchM * pg.wpitch;
+    float* const bias_s = ws + kPatchM * pg.wpitch;
+    float* const zero_s = bias_s + kPatchM;
+    float* const patches = zero_s + 4;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int64_t blk = blockIdx.x;
-    const int tx0 = static_cast<int>(blk % pg.tiles_w) * kPatchTile;
-    const int ty0 = static_cast<int>((blk / pg.tiles_w) % pg.tiles_h) * kPatchTile;
-    const int64_t b = blk / (static_cast<int64_t>(pg.tiles_w) * pg.tiles_h);
     const int g = blockIdx.z;
     const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kPatchM;
     const int cg = static_cast<int>(p.cg);
@@ -953,35 +961,47 @@ __global__ __launch_bounds__(512) void PatchConvKernel(ConvArgs p, PatchGeom pg)
             ws[m * pg.wpitch + k] = ok ? wg[static_cast<int64_t>(m) * pg.knat + k] : 0.0f;
         }
     }
-    // Input patch, zero outside the image (the padding taps): one wave per
-    // patch row, lanes along the row.
-    const int ih0 = ty0 * p.s_h - p.p_h;
-    const int iw0 = tx0 * p.s_w - p.p_w;
-    const float* xb = p.x + (b * p.c + static_cast<int64_t>(g) * cg) * p.plane_in;
-    const int plane_patch = pg.ph * pg.pw;
-    for (int r = wave; r < cg * pg.ph; r += 8) {
-        const int c = r / pg.ph;
-        const int ih = ih0 + (r - c * pg.ph);
-        const bool row_in = static_cast<unsigned>(ih) < static_cast<unsigned>(p.in_h);
-        const float* src = xb + static_cast<int64_t>(c) * p.plane_in + static_cast<int64_t>(ih) * p.in_w;
-        for (int px = lane; px < pg.pw; px += 64) {
-            const int iw = iw0 + px;
-            const bool in = row_in && static_cast<unsigned>(iw) < static_cast<unsigned>(p.in_w);
-            patch[r * pg.pw + px] = in ? src[iw] : 0.0f;
-        }
-    }
-    const int zero_slot = cg * plane_patch;
-    float* const bias_s = patch + zero_slot + 1; // kPatchM floats
-    if (tid == 0) {
-        patch[zero_slot] = 0.0f;
-    }
     if (tid < kPatchM) {
         const int64_t m = m0 + tid;
         bias_s[tid] = p.bias != nullptr && m < p.mg ? p.bias[static_cast<int64_t>(g) * p.mg + m] : 0.0f;
     }
-    __syncthreads();
+    if (tid == 0) {
+        zero_s[0] = 0.0f;
+    }
 
-    // 8 waves: 2 along M (32 rows each) x 4 along N (64 pixels = 4 tile rows).
+    // Patch element e = tid + i * 512 is channel e / (ph * pw), row, column.
+    // The copy goes straight from memory into LDS (buffer loads with the LDS
+    // flag: no registers, zero for the padding taps via the range check); a
+    // wave's 64 lanes fill 64 consecutive floats.
+    auto load_patch = [&](int blk, float* dst) {
+        const int tx0 = (blk % pg.tiles_w) * kPatchTile;
+        const int rest = blk / pg.tiles_w;
+        const int ty0 = (rest % pg.tiles_h) * kPatchTile;
+        const int64_t b = rest / pg.tiles_h;
+        const int ih0 = ty0 * p.s_h - p.p_h;
+        const int iw0 = tx0 * p.s_w - p.p_w;
+        // One image's channels of group g: under 2 GiB (host check).
+        const __amdgpu_buffer_rsrc_t xr = MakeRsrc(p.x + (b * p.c + static_cast<int64_t>(g) * cg) * p.plane_in,
+                                                   static_cast<uint32_t>(cg * p.plane_in * 4));
+        const int plane_in = static_cast<int>(p.plane_in);
+        for (int w0 = wave * 64; w0 < pg.patch_floats; w0 += 512) {
+            const int e = w0 + lane;
+            if (e < pg.patch_floats) {
+                uint32_t rem, x;
+                const uint32_t c = DivMod(pg.div_plane, static_cast<uint32_t>(e), rem);
+                const int ih = ih0 + static_cast<int>(DivMod(pg.div_pw, rem, x));
+                const int iw = iw0 + static_cast<int>(x);
+                const bool in = static_cast<unsigned>(ih) < static_cast<unsigned>(p.in_h) &&
+                                static_cast<unsigned>(iw) < static_cast<unsigned>(p.in_w);
+                const uint32_t off =
+                    in ? static_cast<uint32_t>((static_cast<int>(c) * plane_in + ih * p.in_w + iw) * 4) : kOutOfRange;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*)(dst + w0), 4,
+                                                         static_cast<int>(off), 0, 0, 0);
+            }
+        }
+    };
+
+    // 8 waves: 2 along M (32 rows each) x 4 along N (64 pixels = 4 block rows).
     const int wave_m = wave & 1;
     const int wave_n = wave >> 1;
     const int half = lane >> 5;
@@ -992,82 +1012,133 @@ __global__ __launch_bounds__(512) void PatchConvKernel(ConvArgs p, PatchGeom pg)
         const int n = wave_n * 64 + j * 32 + col;
         poff[j] = (n / kPatchTile) * p.s_h * pg.pw + (n % kPatchTile) * p.s_w + half * p.d_w;
     }
-    nert_floatx16 acc[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            acc[j][v] = 0.0f;
-        }
-    }
     const bool odd = kw_n != 2 * PAIRS;
     const float* wrow = ws + (wave_m * 32 + col) * pg.wpitch + half;
-    for (int row = 0; row < cg * kh_n; ++row) {
-        const int c = row / kh_n;
-        const int kh = row - c * kh_n;
-        const int rbase = c * plane_patch + kh * p.d_h * pg.pw;
-        const float* wr = wrow + row * kw_n;
-#pragma unroll
-        for (int q = 0; q < PAIRS; ++q) {
-            // Lanes of the missing tap read a real (finite) weight and a zero input.
-            const bool zero = odd && half == 1 && q == PAIRS - 1;
-            const float a = wr[zero ? -1 : 2 * q];
-            const int off = rbase + 2 * q * p.d_w;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const float bv = patch[zero ? zero_slot : off + poff[j]];
-                acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bv, acc[j], 0, 0, 0);
-            }
-        }
-    }
+    const int plane_patch = pg.ph * pg.pw;
 
-    // Epilogue: D row = output channel, column = pixel of the 16x16 block.
-    // Operand loads come from clamped addresses ahead of the guarded stores.
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int n = wave_n * 64 + j * 32 + col;
-        const int oy = ty0 + n / kPatchTile;
-        const int ox = tx0 + n % kPatchTile;
-        const bool pix_ok = oy < p.out_h && ox < p.out_w;
-        const int64_t pix = pix_ok ? static_cast<int64_t>(oy) * p.out_w + ox : 0;
-        float value[16];
-        int64_t yi[16];
-        bool ok[16];
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int ml = wave_m * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-            ok[v] = pix_ok && m0 + ml < p.mg;
-            const int64_t oc = static_cast<int64_t>(g) * p.mg + (ok[v] ? m0 + ml : 0);
-            yi[v] = (b * p.m + oc) * p.plane_out + pix;
-            value[v] = p.bias != nullptr ? acc[j][v] + bias_s[ml] : acc[j][v];
+    int blk = blockIdx.x;
+    if (blk < pg.blocks) {
+        load_patch(blk, patches);
+    }
+    for (int buf = 0; blk < pg.blocks; blk += gridDim.x, buf ^= 1) {
+        float* const patch = patches + buf * pg.patch_stride;
+        // This wave's copies of the current patch are complete; after the
+        // barrier everyone's are, and nobody still reads the other buffer.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        const int next = blk + static_cast<int>(gridDim.x);
+        if (next < pg.blocks) {
+            load_patch(next, patches + (buf ^ 1) * pg.patch_stride);
         }
-        if (p.residual != nullptr) {
-            float res[16];
+        nert_floatx16 acc[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                res[v] = p.residual[ok[v] ? yi[v] : 0];
-            }
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                value[v] = value[v] + res[v];
+                acc[j][v] = 0.0f;
             }
         }
+        for (int row = 0; row < cg * kh_n; ++row) {
+            const int c = row / kh_n;
+            const int kh = row - c * kh_n;
+            const int rbase = c * plane_patch + kh * p.d_h * pg.pw;
+            const float* wr = wrow + row * kw_n;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            float out = value[v];
-            if (p.relu) {
-                out = (0.0f < out) ? out : 0.0f; // std::max(0.0f, v)
+            for (int q = 0; q < PAIRS; ++q) {
+                // Lanes of the missing tap read a real (finite) weight and a zero input.
+                const bool zero = odd && half == 1 && q == PAIRS - 1;
+                const float a = wr[zero ? -1 : 2 * q];
+                const int off = rbase + 2 * q * p.d_w;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const float bv = *(zero ? zero_s : patch + off + poff[j]);
+                    acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bv, acc[j], 0, 0, 0);
+                }
             }
-            if (ok[v]) {
-                p.y[yi[v]] = out;
+        }
+
+        // Epilogue: D row = output channel, column = pixel of the 16x16 block;
+        // four channels (one accumulator row group) at a time, with 32-bit
+        // offsets into this image's output (under 2^31 elements, host check).
+        const int tx0 = (blk % pg.tiles_w) * kPatchTile;
+        const int rest = blk / pg.tiles_w;
+        const int ty0 = (rest % pg.tiles_h) * kPatchTile;
+        const int64_t b = rest / pg.tiles_h;
+        float* const yb = p.y + b * p.m * p.plane_out;
+        const float* const zb = p.residual != nullptr ? p.residual + b * p.m * p.plane_out : nullptr;
+        const int plane_out = static_cast<int>(p.plane_out);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int n = wave_n * 64 + j * 32 + col;
+            const int oy = ty0 + n / kPatchTile;
+            const int ox = tx0 + n % kPatchTile;
+            const bool pix_ok = oy < p.out_h && ox < p.out_w;
+            const int pix = pix_ok ? oy * p.out_w + ox : 0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int ml0 = wave_m * 32 + 8 * r + 4 * half;
+                float value[4];
+                int yi[4];
+                bool ok[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int ml = ml0 + v;
+                    ok[v] = pix_ok && m0 + ml < p.mg;
+                    const int oc = g * static_cast<int>(p.mg) + (ok[v] ? static_cast<int>(m0) + ml : 0);
+                    yi[v] = oc * plane_out + pix;
+                    value[v] = p.bias != nullptr ? acc[j][4 * r + v] + bias_s[ml] : acc[j][4 * r + v];
+                }
+                if (zb != nullptr) {
+                    float res[4];
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        res[v] = zb[ok[v] ? yi[v] : 0];
+                    }
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        value[v] = value[v] + res[v];
+                    }
+                }
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    float out = value[v];
+                    if (p.relu) {
+                        out = (0.0f < out) ? out : 0.0f; // std::max(0.0f, v)
+                    }
+                    if (ok[v]) {
+                        yb[yi[v]] = out;
+                    }
+                }
             }
         }
     }
 }
 
+// Raises PatchConvKernel<PAIRS>'s dynamic LDS limit above the 64 KiB default
+// once per process; false when the runtime refuses.
+template <int PAIRS>
+bool AllowPatchLds(size_t bytes) {
+    static const bool allowed =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&PatchConvKernel<PAIRS>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+    if (!allowed) {
+        (void)hipGetLastError();
+    }
+    return bytes <= 64 * 1024 || allowed;
+}
+
+template <int PAIRS>
+bool LaunchPatch(const ConvArgs& p, const PatchGeom& pg, dim3 grid, size_t lds, hipStream_t stream) {
+    if (!AllowPatchLds<PAIRS>(lds)) {
+        return false;
+    }
+    PatchConvKernel<PAIRS><<<grid, 512, lds, stream>>>(p, pg);
+    return true;
+}
+
 // True when the patch kernel applies: 2-D, few channels per group, filter
-// rows of up to 8 taps, and one block's weights and input patch fit in 64 KiB
-// of LDS.
+// rows of up to 8 taps, and a workgroup's weights and two input patches fit
+// in 160 KiB of LDS.
 bool TryPatchConv(const ConvArgs& p, hipStream_t stream) {
     if (p.k_d != 1 || p.in_d != 1 || p.out_d != 1 || p.cg > 4 || p.k_w > 8) {
         return false;
@@ -1078,35 +1149,52 @@ bool TryPatchConv(const ConvArgs& p, hipStream_t stream) {
     pg.wpitch = pg.knat | 1;
     pg.ph = (kPatchTile - 1) * p.s_h + (p.k_h - 1) * p.d_h + 1;
     pg.pw = (kPatchTile - 1) * p.s_w + (2 * pairs - 1) * p.d_w + 1;
-    const int64_t patch_floats = p.cg * pg.ph * pg.pw + 1 + kPatchM; // + zero slot + bias
-    const size_t lds_bytes = (static_cast<size_t>(kPatchM) * pg.wpitch + patch_floats) * sizeof(float);
-    if (patch_floats > kPatchMaxIn || lds_bytes > 64 * 1024) {
+    const int64_t patch_floats = p.cg * pg.ph * pg.pw;
+    if (patch_floats > kPatchMaxIn) {
+        return false;
+    }
+    pg.patch_floats = static_cast<int32_t>(patch_floats);
+    pg.patch_stride = static_cast<int32_t>((patch_floats + 3) / 4 * 4);
+    const size_t lds_bytes =
+        (static_cast<size_t>(kPatchM) * pg.wpitch + kPatchM + 4 + 2 * static_cast<size_t>(pg.patch_stride)) *
+        sizeof(float);
+    if (lds_bytes > 160 * 1024) {
         return false;
     }
     pg.tiles_w = (p.out_w + kPatchTile - 1) / kPatchTile;
     pg.tiles_h = (p.out_h + kPatchTile - 1) / kPatchTile;
     const int64_t blocks = p.batch * pg.tiles_w * pg.tiles_h;
     const int64_t m_blocks = (p.mg + kPatchM - 1) / kPatchM;
-    if (blocks > 0x7FFFFFFF || m_blocks > 65535 || p.group > 65535) {
+    if (blocks > 0x7FFFFFFF || m_blocks > 65535 || p.group > 65535 || p.cg * p.plane_in * 4 >= (int64_t{1} << 31) ||
+        p.m * p.plane_out >= (int64_t{1} << 31)) {
         return false;
     }
-    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(m_blocks), static_cast<unsigned>(p.group));
+    pg.blocks = static_cast<int32_t>(blocks);
+    pg.div_plane = FastDiv::Make(static_cast<uint32_t>(pg.ph * pg.pw));
+    pg.div_pw = FastDiv::Make(static_cast<uint32_t>(pg.pw));
+    // About two resident workgroups per CU in total, each walking blocks.
+    const int64_t per_slot = std::max<int64_t>(1, kResidentBlocks / (m_blocks * p.group));
+    const dim3 grid(static_cast<unsigned>(std::min(blocks, per_slot)), static_cast<unsigned>(m_blocks),
+                    static_cast<unsigned>(p.group));
+    bool launched;
     switch (pairs) {
     case 1:
-        PatchConvKernel<1><<<grid, 512, lds_bytes, stream>>>(p, pg);
+        launched = LaunchPatch<1>(p, pg, grid, lds_bytes, stream);
         break;
     case 2:
-        PatchConvKernel<2><<<grid, 512, lds_bytes, stream>>>(p, pg);
+        launched = LaunchPatch<2>(p, pg, grid, lds_bytes, stream);
         break;
     case 3:
-        PatchConvKernel<3><<<grid, 512, lds_bytes, stream>>>(p, pg);
+        launched = LaunchPatch<3>(p, pg, grid, lds_bytes, stream);
         break;
     default:
-        PatchConvKernel<4><<<grid, 512, lds_bytes, stream>>>(p, pg);
+        launched = LaunchPatch<4>(p, pg, grid, lds_bytes, stream);
         break;
     }
-    CheckLaunch("PatchConvKernel launch");
-    return true;
+    if (launched) {
+        CheckLaunch("PatchConvKernel launch");
+    }
+    return launched;
 }
 
 // A 1x1, stride-1, unpadded, ungrouped convolution is Y[b] = W[M,C] * X[b][C,P]
