@@ -20,6 +20,11 @@
 // adds, a bounds test and one load. Pointwise stride-1 unpadded convolutions
 // skip the gather and run as a batched GEMM on the same engine.
 
+#include <array>
+#include <cstdlib>
+#include <map>
+#include <mutex>
+
 #include "gemm_engine.hpp"
 #include "mfma_tile.hpp"
 #include "../../include/nert_hip.h"
@@ -823,11 +828,14 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
     ConvEpilogue<Shape>(p, acc, row0, col0, g, split);
 }
 
-// Measured on the ResNet-18 bs32 3x3 layers: 64x256 tiles for 64 output
-// channels, 64x128 tiles (8 waves of 32x32) otherwise; 128x128 tiles and
-// four-wave workgroups were 1-10% slower.
-using HaloShapeW = TileShape<64, 256, kHaloBK, 2, 4>; // 8 waves, 32x64 each, for M_g <= 64
+// Tile shapes. Which one (and which split-K count) is fastest depends on how
+// the tile count falls against the CUs: measured on the ResNet-18 bs32 3x3
+// layers the best of these is 3-6% ahead of a fixed choice, so the first call
+// of each geometry times them (below).
+using HaloShapeW = TileShape<64, 256, kHaloBK, 2, 4>; // 8 waves, 32x64 each (M_g <= 64)
 using HaloShapeM = TileShape<64, 128, kHaloBK, 2, 4>; // 8 waves, 32x32 each
+using HaloShapeQ = TileShape<64, 64, kHaloBK, 2, 2>;  // 4 waves, 32x32 each
+using HaloShapeN = TileShape<32, 128, kHaloBK, 1, 4>; // 4 waves, 32x32 each
 
 template <class Shape, int NPOS>
 void LaunchHalo(const ConvArgs& p, const HaloGeom& h, dim3 grid, size_t lds, hipStream_t stream) {
@@ -838,7 +846,7 @@ void LaunchHalo(const ConvArgs& p, const HaloGeom& h, dim3 grid, size_t lds, hip
 // extent, everything addressable with 32-bit offsets, and one workgroup's
 // patch and weights within kHaloMaxLds.
 template <class Shape>
-bool TryHaloShape(ConvArgs p, hipStream_t stream) {
+bool TryHaloShape(ConvArgs p, hipStream_t stream, int force_splits) {
     constexpr int kTaps = 9;
     HaloGeom h{};
     h.pw = (p.out_w - 1) * p.s_w + 2 * p.d_w + 1;
@@ -864,7 +872,8 @@ bool TryHaloShape(ConvArgs p, hipStream_t stream) {
     h.div_pw = FastDiv::Make(static_cast<uint32_t>(h.pw));
     h.div_rows_full = FastDiv::Make(static_cast<uint32_t>(h.rows_full));
     const int64_t tiles = ((p.mg + Shape::kBM - 1) / Shape::kBM) * ((p.n_total + Shape::kBN - 1) / Shape::kBN);
-    const int splits = PlanSplits(tiles * p.group, h.blocks, kResidentBlocks, 4);
+    const int splits = force_splits > 0 ? std::min(force_splits, static_cast<int>(h.blocks))
+                                        : PlanSplits(tiles * p.group, h.blocks, kResidentBlocks, 4);
     h.blocks_per_split = (h.blocks + splits - 1) / splits;
     p.k_per_split = 0;
     p.partial = nullptr;
@@ -890,19 +899,121 @@ bool TryHaloShape(ConvArgs p, hipStream_t stream) {
     return true;
 }
 
+bool HaloApplies(const ConvArgs& p) {
+    return p.k_d == 1 && p.in_d == 1 && p.out_d == 1 && p.k_h == 3 && p.k_w == 3 && p.cg % kHaloBK == 0 &&
+           reinterpret_cast<uintptr_t>(p.w) % 16 == 0 && p.s_h >= 1 && p.s_w >= 1 && p.d_h >= 1 && p.d_w >= 1 &&
+           p.s_h <= 2 * p.d_h + 1 && p.n_total < (int64_t{1} << 31) &&
+           p.batch * p.c * p.plane_in * 4 < (int64_t{1} << 31) && p.m * p.kg * 4 < (int64_t{1} << 31) &&
+           p.out_w < (1 << 16) && p.out_h < (1 << 16);
+}
+
+// A configuration: tile shape (0 W, 1 M, 2 Q, 3 N) and split-K count (0:
+// PlanSplits' choice).
+struct HaloChoice {
+    int shape;
+    int splits;
+};
+
+bool LaunchHaloChoice(const ConvArgs& p, HaloChoice c, hipStream_t stream) {
+    switch (c.shape) {
+    case 0:
+        return p.mg <= 64 && TryHaloShape<HaloShapeW>(p, stream, c.splits);
+    case 1:
+        return TryHaloShape<HaloShapeM>(p, stream, c.splits);
+    case 2:
+        return TryHaloShape<HaloShapeQ>(p, stream, c.splits);
+    default:
+        return TryHaloShape<HaloShapeN>(p, stream, c.splits);
+    }
+}
+
+// Per-geometry choice, made once per process: the first eager call of a
+// geometry runs every configuration that fits on a scratch output (one warm-up
+// and three timed launches each, HIP events on the caller's stream) and keeps
+// the fastest; later calls of the geometry, fused or not, reuse it, so one
+// process always computes a geometry the same way. A first call under stream
+// capture cannot time anything and fixes the default instead (64x256 tiles
+// for M_g <= 64, else 64x128, PlanSplits). NERT_HIP_CONV_TUNE=0 in the
+// environment makes every geometry take the default.
+using HaloKey = std::array<int64_t, 14>;
+
+HaloChoice DefaultHaloChoice(const ConvArgs& p) { return HaloChoice{p.mg <= 64 ? 0 : 1, 0}; }
+
+HaloChoice TuneHalo(const ConvArgs& p, hipStream_t stream) {
+    static const bool enabled = [] {
+        const char* e = std::getenv("NERT_HIP_CONV_TUNE");
+        return e == nullptr || std::string(e) != "0";
+    }();
+    HaloChoice best = DefaultHaloChoice(p);
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    Check(hipStreamIsCapturing(stream, &capture), "hipStreamIsCapturing");
+    if (!enabled || capture != hipStreamCaptureStatusNone) {
+        return best;
+    }
+    ConvArgs q = p;
+    const size_t y_bytes = static_cast<size_t>(p.batch * p.m * p.plane_out) * sizeof(float);
+    float* scratch = nullptr;
+    Check(hipMalloc(&scratch, y_bytes), "hipMalloc(conv tuning output)");
+    q.y = scratch;
+    hipEvent_t start, stop;
+    Check(hipEventCreate(&start), "hipEventCreate");
+    Check(hipEventCreate(&stop), "hipEventCreate");
+    float best_ms = -1.0f;
+    try {
+        for (int shape = 0; shape < 4; ++shape) {
+            for (int splits : {0, 1, 2, 4}) {
+                const HaloChoice c{shape, splits};
+                if (!LaunchHaloChoice(q, c, stream)) {
+                    break; // this shape does not fit the geometry
+                }
+                Check(hipEventRecord(start, stream), "hipEventRecord");
+                for (int r = 0; r < 3; ++r) {
+                    LaunchHaloChoice(q, c, stream);
+                }
+                Check(hipEventRecord(stop, stream), "hipEventRecord");
+                Check(hipEventSynchronize(stop), "hipEventSynchronize");
+                float ms = 0.0f;
+                Check(hipEventElapsedTime(&ms, start, stop), "hipEventElapsedTime");
+                if (best_ms < 0.0f || ms < best_ms) {
+                    best_ms = ms;
+                    best = c;
+                }
+            }
+        }
+    } catch (...) {
+        (void)hipStreamSynchronize(stream);
+        (void)hipEventDestroy(start);
+        (void)hipEventDestroy(stop);
+        (void)hipFree(scratch);
+        throw;
+    }
+    Check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    Check(hipEventDestroy(start), "hipEventDestroy");
+    Check(hipEventDestroy(stop), "hipEventDestroy");
+    Check(hipFree(scratch), "hipFree(conv tuning output)");
+    return best;
+}
+
 bool TryHaloConv(const ConvArgs& p, hipStream_t stream) {
-    const bool fits = p.k_d == 1 && p.in_d == 1 && p.out_d == 1 && p.k_h == 3 && p.k_w == 3 &&
-                      p.cg % kHaloBK == 0 && reinterpret_cast<uintptr_t>(p.w) % 16 == 0 && p.s_h >= 1 && p.s_w >= 1 && p.d_h >= 1 && p.d_w >= 1 &&
-                      p.s_h <= 2 * p.d_h + 1 && p.n_total < (int64_t{1} << 31) &&
-                      p.batch * p.c * p.plane_in * 4 < (int64_t{1} << 31) && p.m * p.kg * 4 < (int64_t{1} << 31) &&
-                      p.out_w < (1 << 16) && p.out_h < (1 << 16);
-    if (!fits) {
+    if (!HaloApplies(p)) {
         return false;
     }
-    if (p.mg <= 64 && TryHaloShape<HaloShapeW>(p, stream)) {
-        return true;
+    static std::mutex mu;
+    static std::map<HaloKey, HaloChoice> chosen;
+    const HaloKey key{p.batch, p.c, p.m, p.group, p.in_h, p.in_w, p.out_h, p.out_w,
+                      p.s_h, p.s_w, p.d_h, p.d_w, p.p_h, p.p_w};
+    HaloChoice c;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        auto it = chosen.find(key);
+        if (it == chosen.end()) {
+            it = chosen.emplace(key, TuneHalo(p, stream)).first;
+        }
+        c = it->second;
     }
-    return TryHaloShape<HaloShapeM>(p, stream);
+    // Whether a shape fits depends on the geometry alone, so a cached choice
+    // fits; the default is tried next only as a safeguard.
+    return LaunchHaloChoice(p, c, stream) || LaunchHaloChoice(p, DefaultHaloChoice(p), stream);
 }
 
 // ---- Small-channel convolution from an LDS input patch -------------------------
