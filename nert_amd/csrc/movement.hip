@@ -5,12 +5,17 @@
 // source through per-axis strides (0 broadcasts for Expand, negative steps
 // for Slice, an optional per-axis modulus for Tile). The host drops unit axes
 // and merges axes both sides walk contiguously, so most ViT/detector
-// reshuffles become rank-2 or rank-3 walks whose innermost run is contiguous
-// on both sides; those runs move as 16-byte vectors when alignment allows.
+// reshuffles become rank-2 or rank-3 walks. When the innermost run is
+// contiguous on both sides, it moves as 16-, 8- or 4-byte units (whatever
+// the run length, the other strides and both base addresses allow). When the
+// destination's contiguous axis is not the source's, the copy is a batched
+// 2-D transpose between those two axes and goes through 32x32 LDS tiles, so
+// reads and writes are both coalesced.
 
 #include "common.hpp"
 #include "../../include/nert_hip.h"
 
+#include <algorithm>
 #include <vector>
 
 namespace nert_hip {
@@ -72,6 +77,65 @@ __global__ void StridedCopyKernel(CopyArgs a, int64_t n) {
             d_o += c * a.dst_strides[d];
         }
         dst[d_o] = src[so];
+    }
+}
+
+// Batched transpose: axis `ai` is contiguous in the destination, axis `aj`
+// in the source; the remaining axes (batch) are decoded from the tile index.
+struct TransposeArgs {
+    const uint8_t* src;
+    uint8_t* dst;
+    int64_t di, dj;               // extents of the two axes
+    int64_t si, dj_stride;        // source stride of axis i, destination stride of axis j
+    int nb;                       // batch axes
+    int64_t bdims[kMaxRank];
+    int64_t bsrc[kMaxRank];
+    int64_t bdst[kMaxRank];
+    FastDiv bdiv[kMaxRank];
+    FastDiv tiles_i_div;          // by ceil(di / 32)
+    FastDiv tiles_ij_div;         // by tiles along i x tiles along j
+    uint32_t tiles;               // total tiles, under 2^31
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void TransposeTileKernel(TransposeArgs a) {
+    __shared__ T tile[32][33];
+    const T* src = reinterpret_cast<const T*>(a.src);
+    T* dst = reinterpret_cast<T*>(a.dst);
+    const int tx = threadIdx.x & 31;
+    const int ty = threadIdx.x >> 5;
+    for (uint32_t t = blockIdx.x; t < a.tiles; t += gridDim.x) {
+        uint32_t ij;
+        uint32_t b = DivMod(a.tiles_ij_div, t, ij);
+        uint32_t ti;
+        const uint32_t tj = DivMod(a.tiles_i_div, ij, ti);
+        int64_t so = 0, d_o = 0;
+        for (int d = a.nb - 1; d >= 0; --d) {
+            uint32_t c;
+            b = DivMod(a.bdiv[d], b, c);
+            so += static_cast<int64_t>(c) * a.bsrc[d];
+            d_o += static_cast<int64_t>(c) * a.bdst[d];
+        }
+        const int64_t i0 = static_cast<int64_t>(ti) * 32;
+        const int64_t j0 = static_cast<int64_t>(tj) * 32;
+        // Read along j (source-contiguous): row r = i offset.
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int r = ty + 8 * k;
+            if (i0 + r < a.di && j0 + tx < a.dj) {
+                tile[r][tx] = src[so + (i0 + r) * a.si + j0 + tx];
+            }
+        }
+        __syncthreads();
+        // Write along i (destination-contiguous): row r = j offset.
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int r = ty + 8 * k;
+            if (j0 + r < a.dj && i0 + tx < a.di) {
+                dst[d_o + (j0 + r) * a.dj_stride + i0 + tx] = tile[tx][r];
+            }
+        }
+        __syncthreads();
     }
 }
 
@@ -181,6 +245,71 @@ __global__ void PadKernel(const T* __restrict__ x, T* __restrict__ y, PadArgs a,
     }
 }
 
+// The destination's contiguous axis (the last) is not contiguous in the
+// source but another axis is: a batched 2-D transpose. Needs non-negative
+// strides, no modulus, and fewer than 2^31 tiles.
+bool TryTranspose(const CopyArgs& a, int elem_size, int64_t n, hipStream_t s) {
+    const int last = a.rank - 1;
+    if (a.rank < 2 || a.dst_strides[last] != 1 || a.src_strides[last] == 1 || n < 1024 ||
+        (elem_size != 1 && elem_size != 4 && elem_size != 8)) {
+        return false;
+    }
+    int j = -1;
+    for (int d = 0; d < a.rank; ++d) {
+        if (a.src_mods[d] != 0 || a.src_strides[d] < 0) {
+            return false;
+        }
+        if (d != last && a.src_strides[d] == 1) {
+            j = d;
+        }
+    }
+    if (j < 0 || a.dims[last] < 8 || a.dims[j] < 8) {
+        return false;
+    }
+    TransposeArgs t{};
+    t.src = a.src;
+    t.dst = a.dst;
+    t.di = a.dims[last];
+    t.dj = a.dims[j];
+    t.si = a.src_strides[last];
+    t.dj_stride = a.dst_strides[j];
+    int64_t batch = 1;
+    for (int d = 0; d < a.rank; ++d) {
+        if (d == last || d == j) {
+            continue;
+        }
+        t.bdims[t.nb] = a.dims[d];
+        t.bsrc[t.nb] = a.src_strides[d];
+        t.bdst[t.nb] = a.dst_strides[d];
+        t.bdiv[t.nb] = FastDiv::Make(static_cast<uint32_t>(a.dims[d]));
+        ++t.nb;
+        batch *= a.dims[d];
+    }
+    const int64_t ti = (t.di + 31) / 32;
+    const int64_t tj = (t.dj + 31) / 32;
+    const int64_t tiles = ti * tj * batch;
+    if (tiles >= (int64_t{1} << 31) || ti * tj >= (int64_t{1} << 31)) {
+        return false;
+    }
+    t.tiles = static_cast<uint32_t>(tiles);
+    t.tiles_i_div = FastDiv::Make(static_cast<uint32_t>(ti));
+    t.tiles_ij_div = FastDiv::Make(static_cast<uint32_t>(ti * tj));
+    const unsigned grid = static_cast<unsigned>(std::min<int64_t>(tiles, 16384));
+    switch (elem_size) {
+    case 1:
+        TransposeTileKernel<uint8_t><<<grid, 256, 0, s>>>(t);
+        break;
+    case 4:
+        TransposeTileKernel<uint32_t><<<grid, 256, 0, s>>>(t);
+        break;
+    default:
+        TransposeTileKernel<uint64_t><<<grid, 256, 0, s>>>(t);
+        break;
+    }
+    CheckLaunch("transpose launch");
+    return true;
+}
+
 } // namespace
 } // namespace nert_hip
 
@@ -205,6 +334,51 @@ int nert_hip_copy_strided(int elem_size, const void* src, void* dst, int rank, c
             Check(hipMemcpyAsync(dst, src, static_cast<size_t>(n) * elem_size, hipMemcpyDeviceToDevice, s),
                   "hipMemcpyAsync(copy)");
             return;
+        }
+        if (TryTranspose(a, elem_size, n, s)) {
+            return;
+        }
+        // Innermost run contiguous on both sides: move it in wider units.
+        const int last = a.rank - 1;
+        if (a.src_strides[last] == 1 && a.dst_strides[last] == 1 && a.src_mods[last] == 0) {
+            for (int unit : {16, 8}) {
+                if (unit <= elem_size || unit % elem_size != 0) {
+                    continue;
+                }
+                const int64_t per = unit / elem_size;
+                bool ok = a.dims[last] % per == 0 && reinterpret_cast<uintptr_t>(src) % unit == 0 &&
+                          reinterpret_cast<uintptr_t>(dst) % unit == 0;
+                for (int d = 0; d < last && ok; ++d) {
+                    ok = a.src_strides[d] % per == 0 && a.dst_strides[d] % per == 0 && a.src_mods[d] == 0;
+                }
+                if (!ok) {
+                    continue;
+                }
+                int64_t dims[kMaxRank], ss[kMaxRank], ds[kMaxRank];
+                for (int d = 0; d < a.rank; ++d) {
+                    dims[d] = d == last ? a.dims[d] / per : a.dims[d];
+                    ss[d] = d == last ? 1 : a.src_strides[d] / per;
+                    ds[d] = d == last ? 1 : a.dst_strides[d] / per;
+                }
+                CopyArgs v{};
+                v.src = a.src;
+                v.dst = a.dst;
+                const int64_t nv = Collapse(a.rank, dims, ss, ds, nullptr, v);
+                const unsigned vgrid = GridFor(nv, 256, 16384);
+                if (nv >= (int64_t{1} << 31)) {
+                    if (unit == 16) {
+                        StridedCopyKernel<uint4><<<vgrid, 256, 0, s>>>(v, nv);
+                    } else {
+                        StridedCopyKernel<uint2><<<vgrid, 256, 0, s>>>(v, nv);
+                    }
+                } else if (unit == 16) {
+                    StridedCopy32Kernel<uint4><<<vgrid, 256, 0, s>>>(v, static_cast<uint32_t>(nv));
+                } else {
+                    StridedCopy32Kernel<uint2><<<vgrid, 256, 0, s>>>(v, static_cast<uint32_t>(nv));
+                }
+                CheckLaunch("strided copy launch");
+                return;
+            }
         }
         const unsigned grid = GridFor(n, 256, 16384);
         const bool small = n < (int64_t{1} << 31);

@@ -24,6 +24,11 @@ def _data(shape, dtype, seed=0):
 @pytest.mark.parametrize("shape,perm", [
     ((16, 197, 12, 64), [0, 2, 1, 3]),   # ViT head split
     ((16, 12, 197, 64), [0, 2, 1, 3]),   # ViT head merge
+    ((16, 12, 197, 64), [0, 1, 3, 2]),   # K^T: batched LDS-tile transpose
+    ((8, 84, 8400), [0, 2, 1]),          # detector head, ragged tiles
+    ((3, 37, 45), [0, 2, 1]),
+    ((5, 33, 7, 40), [3, 1, 0, 2]),
+    ((9, 40, 3), [1, 0, 2]),             # 3-element runs: scalar path
     ((2048, 1024), [1, 0]),
     ((2, 3, 4, 5, 6), [4, 2, 0, 3, 1]),
     ((3, 1, 5), [1, 2, 0]),
