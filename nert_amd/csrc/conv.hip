@@ -21,11 +21,11 @@
 // skip the gather and run as a batched GEMM on the same engine.
 
 #include <array>
-#include <cstdlib>
 #include <map>
 #include <mutex>
 
 #include "gemm_engine.hpp"
+#include "tune.hpp"
 #include "mfma_tile.hpp"
 #include "../../include/nert_hip.h"
 
@@ -908,17 +908,10 @@ bool HaloApplies(const ConvArgs& p) {
 }
 
 // ---- Per-geometry choice of a kernel configuration ----------------------------
-//
-// Which tile shape and split-K count is fastest depends on how the tile count
-// of a geometry falls against the CUs (ResNet-18 bs32: the best of the
-// candidates is 3-6% ahead of any fixed rule on the 3x3 layers, and the
-// 1x1 stride-2 layers want small tiles). So the first eager call of each
-// geometry runs every candidate configuration that fits on a scratch output
-// (one warm-up and three timed launches each, HIP events on the caller's
-// stream) and keeps the fastest; later calls of the geometry, fused or not,
-// reuse it, so within a process a geometry is always computed the same way.
-// A first call under stream capture cannot time anything and fixes the
-// default instead, as does NERT_HIP_CONV_TUNE=0 in the environment.
+// (tune.hpp). Measured on ResNet-18 bs32: the best candidate is 3-6% ahead of
+// any fixed rule on the 3x3 layers, and the 1x1 stride-2 layers want small
+// tiles. The cache key is the geometry alone, so a Conv row and a FusedConv
+// row of the same geometry compute their sums the same way.
 using ConvKey = std::array<int64_t, 22>;
 
 ConvKey KeyOf(const ConvArgs& p) {
@@ -926,66 +919,16 @@ ConvKey KeyOf(const ConvArgs& p) {
                    p.out_h, p.out_w, p.s_d,   p.s_h,   p.s_w,  p.d_d,  p.d_h,  p.d_w, p.p_d, p.p_h, p.p_w};
 }
 
-// launch(i, args, stream) -> false when candidate i does not fit.
 template <class Launch>
-int ChooseConfig(std::map<ConvKey, int>& cache, const ConvArgs& p, hipStream_t stream, int count, int fallback,
-                 Launch launch) {
+int ChooseConvConfig(std::map<ConvKey, int>& cache, const ConvArgs& p, hipStream_t stream, int count, int fallback,
+                     Launch launch) {
     static std::mutex mu;
-    static const bool enabled = [] {
-        const char* e = std::getenv("NERT_HIP_CONV_TUNE");
-        return e == nullptr || std::string(e) != "0";
-    }();
-    std::lock_guard<std::mutex> lock(mu);
-    const ConvKey key = KeyOf(p);
-    auto it = cache.find(key);
-    if (it != cache.end()) {
-        return it->second;
-    }
-    int best = fallback;
-    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-    Check(hipStreamIsCapturing(stream, &capture), "hipStreamIsCapturing");
-    if (enabled && capture == hipStreamCaptureStatusNone && count > 1) {
+    const size_t y_bytes = static_cast<size_t>(p.batch * p.m * p.plane_out) * sizeof(float);
+    return ChooseConfig(cache, mu, KeyOf(p), y_bytes, stream, count, fallback, [&](int i, float* scratch) {
         ConvArgs q = p;
-        float* scratch = nullptr;
-        Check(hipMalloc(&scratch, static_cast<size_t>(p.batch * p.m * p.plane_out) * sizeof(float)),
-              "hipMalloc(conv tuning output)");
         q.y = scratch;
-        hipEvent_t start = nullptr, stop = nullptr;
-        float best_ms = -1.0f;
-        try {
-            Check(hipEventCreate(&start), "hipEventCreate");
-            Check(hipEventCreate(&stop), "hipEventCreate");
-            for (int i = 0; i < count; ++i) {
-                if (!launch(i, q, stream)) {
-                    continue;
-                }
-                Check(hipEventRecord(start, stream), "hipEventRecord");
-                for (int r = 0; r < 3; ++r) {
-                    launch(i, q, stream);
-                }
-                Check(hipEventRecord(stop, stream), "hipEventRecord");
-                Check(hipEventSynchronize(stop), "hipEventSynchronize");
-                float ms = 0.0f;
-                Check(hipEventElapsedTime(&ms, start, stop), "hipEventElapsedTime");
-                if (best_ms < 0.0f || ms < best_ms) {
-                    best_ms = ms;
-                    best = i;
-                }
-            }
-        } catch (...) {
-            (void)hipStreamSynchronize(stream);
-            (void)hipEventDestroy(start);
-            (void)hipEventDestroy(stop);
-            (void)hipFree(scratch);
-            throw;
-        }
-        Check(hipStreamSynchronize(stream), "hipStreamSynchronize");
-        Check(hipEventDestroy(start), "hipEventDestroy");
-        Check(hipEventDestroy(stop), "hipEventDestroy");
-        Check(hipFree(scratch), "hipFree(conv tuning output)");
-    }
-    cache.emplace(key, best);
-    return best;
+        return launch(i, q, stream);
+    });
 }
 
 // 3x3 candidates: tile shape i / 4 (0 W, 1 M, 2 Q, 3 N) with split-K count
@@ -1013,7 +956,7 @@ bool TryHaloConv(const ConvArgs& p, hipStream_t stream) {
     }
     static std::map<ConvKey, int> chosen;
     const int fallback = p.mg <= 64 ? 0 : 4; // 64x256 tiles for M_g <= 64, else 64x128
-    const int c = ChooseConfig(chosen, p, stream, kHaloCandidates, fallback, LaunchHaloCandidate);
+    const int c = ChooseConvConfig(chosen, p, stream, kHaloCandidates, fallback, LaunchHaloCandidate);
     // Whether a candidate fits depends on the geometry alone, so a cached
     // choice fits; the default is tried next only as a safeguard.
     return LaunchHaloCandidate(c, p, stream) || LaunchHaloCandidate(fallback, p, stream);
@@ -1037,7 +980,7 @@ bool LaunchGatherCandidate(int i, const ConvArgs& p, hipStream_t stream) {
 void LaunchGatherConv(const ConvArgs& p, hipStream_t stream) {
     static std::map<ConvKey, int> chosen;
     const int fallback = p.mg <= 32 ? 2 : (p.mg <= 64 ? 1 : 0);
-    LaunchGatherCandidate(ChooseConfig(chosen, p, stream, 3, fallback, LaunchGatherCandidate), p, stream);
+    LaunchGatherCandidate(ChooseConvConfig(chosen, p, stream, 3, fallback, LaunchGatherCandidate), p, stream);
 }
 
 // ---- Small-channel convolution from an LDS input patch -------------------------

@@ -5,6 +5,8 @@
 
 #include "rows.hpp"
 
+#include <vector>
+
 #include <algorithm>
 #include <limits>
 
@@ -152,11 +154,25 @@ void Binary(const char* op, int code, BinaryKind kind, const Node& node, const V
     if (a.data == nullptr || b.data == nullptr || out.data == nullptr) {
         throw InferenceException(context + ": null buffer");
     }
-    Launch(code, DtypeCode(a.dtype), {&a, &b}, out, context);
     const bool int_division = (code == NERT_BIN_DIV || code == NERT_BIN_MOD) && a.dtype == DataType::Int64;
-    if (int_division) {
-        // A zero divisor must throw like the reference (src/kernels/div.cpp:110):
-        // wait for the flag the kernel raises.
+    // A zero divisor must throw like the reference (src/kernels/div.cpp:110).
+    // A divisor with a host shadow (an initializer, a shape) is checked here;
+    // otherwise the row waits for the flag the kernel raises. With an empty
+    // output no division happens and nothing throws.
+    bool checked_on_host = false;
+    if (int_division && Count(out.dims) > 0) {
+        std::vector<int64_t> divisor;
+        if (HostShadowInt64(b, Count(b.dims), divisor)) {
+            for (int64_t d : divisor) {
+                if (d == 0) {
+                    throw InferenceException(context + ": division by zero");
+                }
+            }
+            checked_on_host = true;
+        }
+    }
+    Launch(code, DtypeCode(a.dtype), {&a, &b}, out, context);
+    if (int_division && !checked_on_host) {
         ThrowOnDeviceFlag(context, "division by zero");
     }
     AfterRow(outputs, context);

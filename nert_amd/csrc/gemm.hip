@@ -10,7 +10,13 @@
 
 #include "gemm_engine.hpp"
 #include "mfma_tile.hpp"
+#include "tune.hpp"
 #include "../../include/nert_hip.h"
+
+#include <algorithm>
+#include <array>
+#include <map>
+#include <mutex>
 
 namespace nert_hip {
 namespace {
@@ -177,29 +183,28 @@ int64_t TileCount(const GemmArgs& p, int64_t batches) {
 
 } // namespace
 
-void LaunchGemm(GemmArgs p, int64_t batches, hipStream_t stream) {
-    if (p.m == 0 || p.n == 0 || batches == 0) {
-        return;
-    }
-    // Operand strides must make one of each pair unit (contiguous tensors).
-    if (!(p.a_sk == 1 || p.a_sm == 1) || !(p.b_sn == 1 || p.b_sk == 1)) {
-        throw Error("gemm: operands must be contiguous in one index");
-    }
-    int shape = 0; // 0 = L, 1 = M, 2 = S
-    int64_t tiles = TileCount<ShapeL>(p, batches);
+namespace {
+
+// One configuration: tile shape (0 L, 1 M, 2 S) and split-K count (0: the
+// PlanSplits choice for that shape).
+void LaunchConfig(GemmArgs p, int64_t batches, int shape, int force_splits, hipStream_t stream) {
+    int64_t tiles;
     int64_t min_k_tiles = 8;
-    if (p.m <= 32) {
-        shape = 2;
+    int bk = ShapeL::kBK;
+    if (shape == 0) {
+        tiles = TileCount<ShapeL>(p, batches);
+    } else if (shape == 1) {
+        tiles = TileCount<ShapeM>(p, batches);
+    } else {
         tiles = TileCount<ShapeS>(p, batches);
         min_k_tiles = 2;
-    } else if (tiles < 1024) {
-        shape = 1;
-        tiles = TileCount<ShapeM>(p, batches);
+        bk = ShapeS::kBK;
     }
-    const int bk = shape == 2 ? ShapeS::kBK : ShapeL::kBK;
     const int64_t k_tiles = (p.k + bk - 1) / bk;
     // The 2- and 4-wave shapes keep about 1024 workgroups resident.
-    int splits = PlanSplits(tiles, k_tiles, shape == 0 ? kResidentBlocks : 2 * kResidentBlocks, min_k_tiles, 32);
+    int splits = force_splits > 0
+                     ? static_cast<int>(std::min<int64_t>(force_splits, std::max<int64_t>(k_tiles, 1)))
+                     : PlanSplits(tiles, k_tiles, shape == 0 ? kResidentBlocks : 2 * kResidentBlocks, min_k_tiles, 32);
     p.k_per_split = ((k_tiles + splits - 1) / splits) * bk;
     if (p.k == 0) {
         p.k_per_split = 0;
@@ -226,6 +231,37 @@ void LaunchGemm(GemmArgs p, int64_t batches, hipStream_t stream) {
         SplitReduceKernel<<<GridFor(work, 256, 8192), 256, 0, stream>>>(p, splits, batches, vec);
         CheckLaunch("SplitReduceKernel launch");
     }
+}
+
+// Candidates: shape i / 4 with split count {PlanSplits, 1, 2, 4}[i % 4].
+// Fallback (capture, tuning off): 8-wave 128x128 tiles for problems with at
+// least 1024 of them, 4-wave 64x128 below, 2-wave 32x64 for M <= 32.
+using GemmKey = std::array<int64_t, 10>;
+constexpr int kGemmSplits[4] = {0, 1, 2, 4};
+
+} // namespace
+
+void LaunchGemm(GemmArgs p, int64_t batches, hipStream_t stream) {
+    if (p.m == 0 || p.n == 0 || batches == 0) {
+        return;
+    }
+    // Operand strides must make one of each pair unit (contiguous tensors).
+    if (!(p.a_sk == 1 || p.a_sm == 1) || !(p.b_sn == 1 || p.b_sk == 1)) {
+        throw Error("gemm: operands must be contiguous in one index");
+    }
+    const int fallback_shape = p.m <= 32 ? 2 : (TileCount<ShapeL>(p, batches) < 1024 ? 1 : 0);
+    static std::mutex mu;
+    static std::map<GemmKey, int> chosen;
+    const GemmKey key{p.m, p.n, p.k, batches, p.a_sk == 1, p.b_sn == 1, p.batch_rank, p.has_bias,
+                      p.bias_sm, p.bias_sn};
+    const size_t y_bytes = static_cast<size_t>(batches * p.m * p.n) * sizeof(float);
+    const int c = ChooseConfig(chosen, mu, key, y_bytes, stream, 12, 4 * fallback_shape, [&](int i, float* scratch) {
+        GemmArgs q = p;
+        q.y = scratch;
+        LaunchConfig(q, batches, i / 4, kGemmSplits[i % 4], stream);
+        return true;
+    });
+    LaunchConfig(p, batches, c / 4, kGemmSplits[c % 4], stream);
 }
 
 } // namespace nert_hip

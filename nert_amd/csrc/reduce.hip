@@ -293,6 +293,59 @@ __global__ __launch_bounds__(256) void SoftmaxRowsKernel(const float* __restrict
     }
 }
 
+// Rows of at most 64 * PER elements: the row is read once into registers and
+// each exponential is computed once (the reference evaluates the same exp
+// twice, so reusing it gives the same values).
+template <int PER>
+__global__ __launch_bounds__(256) void SoftmaxRowsRegKernel(const float* __restrict__ x, float* __restrict__ y,
+                                                            int64_t rows, int dim) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) {
+        return;
+    }
+    const float* p = x + row * dim;
+    float* q = y + row * dim;
+    float v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = lane + 64 * k;
+        v[k] = i < dim ? p[i] : -__builtin_huge_valf();
+    }
+    // Peak rule of the reference (value > peak from element 0): see
+    // SoftmaxRowsKernel.
+    const float first = __shfl(v[0], 0, 64);
+    float peak = first;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        peak = v[k] > peak ? v[k] : peak;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float o = __shfl_xor(peak, off, 64);
+        peak = o > peak ? o : peak;
+    }
+    if (first != first) {
+        peak = first;
+    }
+    const double dp = static_cast<double>(peak);
+    double e[PER];
+    double total = 0.0;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        e[k] = lane + 64 * k < dim ? exp(static_cast<double>(v[k]) - dp) : 0.0;
+        total += e[k];
+    }
+    total = WaveAllSum(total);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = lane + 64 * k;
+        if (i < dim) {
+            q[i] = static_cast<float>(e[k] / total);
+        }
+    }
+}
+
 // Normalised axis with inner > 1: one lane per (outer, inner) column.
 __global__ void SoftmaxColsKernel(const float* __restrict__ x, float* __restrict__ y, int64_t outer, int64_t dim,
                                   int64_t inner) {
@@ -348,6 +401,57 @@ __global__ __launch_bounds__(256) void LayerNormKernel(const float* __restrict__
     for (int64_t i = lane; i < inner; i += 64) {
         const double scaled = (static_cast<double>(p[i]) - mean) * inv * static_cast<double>(scale[scale_scalar ? 0 : i]);
         q[i] = static_cast<float>(bias != nullptr ? scaled + static_cast<double>(bias[bias_scalar ? 0 : i]) : scaled);
+    }
+    if (lane == 0) {
+        if (mean_out != nullptr) {
+            mean_out[row] = static_cast<float>(mean);
+        }
+        if (invstd_out != nullptr) {
+            invstd_out[row] = static_cast<float>(inv);
+        }
+    }
+}
+
+// Rows of at most 64 * PER elements held in registers: one read of the row.
+template <int PER>
+__global__ __launch_bounds__(256) void LayerNormRegKernel(const float* __restrict__ x, const float* __restrict__ scale,
+                                                          int scale_scalar, const float* __restrict__ bias,
+                                                          int bias_scalar, float* __restrict__ y, float* mean_out,
+                                                          float* invstd_out, int64_t rows, int inner, double eps) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) {
+        return;
+    }
+    const float* p = x + row * inner;
+    float* q = y + row * inner;
+    float v[PER];
+    double sum = 0.0;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = lane + 64 * k;
+        v[k] = i < inner ? p[i] : 0.0f;
+        sum += static_cast<double>(v[k]);
+    }
+    const double mean = WaveAllSum(sum) / static_cast<double>(inner);
+    double sq = 0.0;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        if (lane + 64 * k < inner) {
+            const double c = static_cast<double>(v[k]) - mean;
+            sq += c * c;
+        }
+    }
+    const double inv = 1.0 / sqrt(WaveAllSum(sq) / static_cast<double>(inner) + eps);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = lane + 64 * k;
+        if (i < inner) {
+            const double scaled =
+                (static_cast<double>(v[k]) - mean) * inv * static_cast<double>(scale[scale_scalar ? 0 : i]);
+            q[i] = static_cast<float>(bias != nullptr ? scaled + static_cast<double>(bias[bias_scalar ? 0 : i])
+                                                      : scaled);
+        }
     }
     if (lane == 0) {
         if (mean_out != nullptr) {
@@ -560,7 +664,11 @@ int nert_hip_softmax_f32(const float* x, float* y, int64_t outer, int64_t dim, i
             return;
         }
         hipStream_t s = StreamOr(stream);
-        if (inner == 1) {
+        if (inner == 1 && dim <= 256) {
+            SoftmaxRowsRegKernel<4><<<RowBlocks(outer), 256, 0, s>>>(x, y, outer, static_cast<int>(dim));
+        } else if (inner == 1 && dim <= 1024) {
+            SoftmaxRowsRegKernel<16><<<RowBlocks(outer), 256, 0, s>>>(x, y, outer, static_cast<int>(dim));
+        } else if (inner == 1) {
             SoftmaxRowsKernel<<<RowBlocks(outer), 256, 0, s>>>(x, y, outer, dim);
         } else {
             SoftmaxColsKernel<<<GridFor(outer * inner, 256, 8192), 256, 0, s>>>(x, y, outer, dim, inner);
@@ -576,8 +684,19 @@ int nert_hip_layernorm_f32(const float* x, const float* scale, int scale_scalar,
         if (rows * inner == 0) {
             return;
         }
-        LayerNormKernel<<<RowBlocks(rows), 256, 0, StreamOr(stream)>>>(x, scale, scale_scalar, bias, bias_scalar, y,
-                                                                        mean_out, invstd_out, rows, inner, epsilon);
+        hipStream_t s = StreamOr(stream);
+        if (inner <= 256) {
+            LayerNormRegKernel<4><<<RowBlocks(rows), 256, 0, s>>>(x, scale, scale_scalar, bias, bias_scalar, y,
+                                                                  mean_out, invstd_out, rows, static_cast<int>(inner),
+                                                                  epsilon);
+        } else if (inner <= 1024) {
+            LayerNormRegKernel<16><<<RowBlocks(rows), 256, 0, s>>>(x, scale, scale_scalar, bias, bias_scalar, y,
+                                                                   mean_out, invstd_out, rows, static_cast<int>(inner),
+                                                                   epsilon);
+        } else {
+            LayerNormKernel<<<RowBlocks(rows), 256, 0, s>>>(x, scale, scale_scalar, bias, bias_scalar, y, mean_out,
+                                                            invstd_out, rows, inner, epsilon);
+        }
         CheckLaunch("layernorm launch");
     });
 }

@@ -1,0 +1,84 @@
+#pragma once
+// Per-geometry choice among kernel configurations, made by timing.
+//
+// Which tile shape and split-K count is fastest depends on how a problem's
+// tile count falls against the 256 CUs, which no simple rule captures across
+// shapes. So the first eager call of each geometry runs every candidate that
+// fits on a scratch output (one warm-up and three timed launches each, HIP
+// events on the caller's stream) and keeps the fastest; later calls of the
+// geometry reuse it, so within a process a geometry is always computed the
+// same way. A first call under stream capture cannot time anything and fixes
+// the fallback instead, as does NERT_HIP_CONV_TUNE=0 in the environment.
+
+#include "common.hpp"
+
+#include <cstdlib>
+#include <map>
+#include <mutex>
+#include <string>
+
+namespace nert_hip {
+
+inline bool TuningEnabled() {
+    static const bool enabled = [] {
+        const char* e = std::getenv("NERT_HIP_CONV_TUNE");
+        return e == nullptr || std::string(e) != "0";
+    }();
+    return enabled;
+}
+
+// launch(i, scratch_y) -> false when candidate i does not fit; it must write
+// its output to scratch_y (scratch_bytes long) instead of the caller's.
+template <class Key, class Launch>
+int ChooseConfig(std::map<Key, int>& cache, std::mutex& mu, const Key& key, size_t scratch_bytes,
+                 hipStream_t stream, int count, int fallback, Launch launch) {
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) {
+        return it->second;
+    }
+    int best = fallback;
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    Check(hipStreamIsCapturing(stream, &capture), "hipStreamIsCapturing");
+    if (TuningEnabled() && capture == hipStreamCaptureStatusNone && count > 1 && scratch_bytes > 0) {
+        float* scratch = nullptr;
+        Check(hipMalloc(&scratch, scratch_bytes), "hipMalloc(tuning output)");
+        hipEvent_t start = nullptr, stop = nullptr;
+        float best_ms = -1.0f;
+        try {
+            Check(hipEventCreate(&start), "hipEventCreate");
+            Check(hipEventCreate(&stop), "hipEventCreate");
+            for (int i = 0; i < count; ++i) {
+                if (!launch(i, scratch)) {
+                    continue;
+                }
+                Check(hipEventRecord(start, stream), "hipEventRecord");
+                for (int r = 0; r < 3; ++r) {
+                    launch(i, scratch);
+                }
+                Check(hipEventRecord(stop, stream), "hipEventRecord");
+                Check(hipEventSynchronize(stop), "hipEventSynchronize");
+                float ms = 0.0f;
+                Check(hipEventElapsedTime(&ms, start, stop), "hipEventElapsedTime");
+                if (best_ms < 0.0f || ms < best_ms) {
+                    best_ms = ms;
+                    best = i;
+                }
+            }
+        } catch (...) {
+            (void)hipStreamSynchronize(stream);
+            (void)hipEventDestroy(start);
+            (void)hipEventDestroy(stop);
+            (void)hipFree(scratch);
+            throw;
+        }
+        Check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+        Check(hipEventDestroy(start), "hipEventDestroy");
+        Check(hipEventDestroy(stop), "hipEventDestroy");
+        Check(hipFree(scratch), "hipFree(tuning output)");
+    }
+    cache.emplace(key, best);
+    return best;
+}
+
+} // namespace nert_hip

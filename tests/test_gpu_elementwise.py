@@ -108,6 +108,19 @@ def test_int64_division_by_zero_throws(gpu, op):
     assert "division by zero" in msg
 
 
+@pytest.mark.parametrize("op", ["Div", "Mod"])
+def test_int64_division_by_zero_device_checked(gpu, op):
+    """A divisor above the 64 KiB host-shadow limit is checked by the kernel's
+    error flag instead of on the host: same exception."""
+    a = rng(13).integers(-1000, 1000, (9000,)).astype(I)
+    b = rng(14).integers(1, 50, (9000,)).astype(I)
+    b[8765] = 0
+    msg = assert_same_error(op, [a, b], [((9000,), I)])
+    assert "division by zero" in msg
+    b[8765] = 3
+    assert_parity(op, [a, b], [((9000,), I)])
+
+
 def test_float_division_by_zero_is_ieee(gpu):
     a = np.array([1, -1, 0], F)
     b = np.zeros(3, F)

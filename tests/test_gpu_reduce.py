@@ -67,7 +67,8 @@ def test_reduce_noop_and_special(gpu):
     assert_same_error("ReduceMax", [x, np.array([2], I)], [((3, 1), F)])
 
 
-SOFTMAX_CASES = [((16, 12, 197, 197), -1), ((4, 4096), -1), ((3, 5, 7), 1), ((2, 3, 4), 0), ((1000,), 0)]
+SOFTMAX_CASES = [((16, 12, 197, 197), -1), ((4, 4096), -1), ((3, 5, 7), 1), ((2, 3, 4), 0), ((1000,), 0),
+                 ((7, 300), -1), ((5, 64), -1)]
 
 
 @pytest.mark.parametrize("shape,axis", SOFTMAX_CASES)
@@ -85,7 +86,8 @@ def test_softmax_legacy_and_specials(gpu):
     assert_same_error("Softmax", [x], [((2, 3, 4), F)], {"axis": 3})
 
 
-@pytest.mark.parametrize("shape,axis", [((16, 197, 768), -1), ((4, 6, 10), 1), ((8, 33), 0), ((5, 1024), -1)])
+@pytest.mark.parametrize("shape,axis", [((16, 197, 768), -1), ((4, 6, 10), 1), ((8, 33), 0), ((5, 1024), -1),
+                                        ((3, 2000), -1), ((6, 256), -1)])
 def test_layernorm(gpu, shape, axis):
     x = randn(shape, seed=8, scale=2.0) + 0.5
     ax = axis % len(shape)
