@@ -275,7 +275,9 @@ __global__ void ArithF32FlatKernel(const float* __restrict__ x, const float* __r
 
 // Rank-2 float broadcast y[r, c] = x[r*xs0 + c*xs1] (op) z[r*zs0 + c*zs1]
 // with the inner axis walked four at a time when every operand allows it.
-__global__ void ArithF32Rank2Kernel(BcastArgs a, int op, int64_t rows, int64_t cols) {
+// SMALL: fewer than 2^31 quads, row index by 32-bit multiply-shift.
+template <bool SMALL>
+__global__ void ArithF32Rank2Kernel(BcastArgs a, int op, int64_t rows, int64_t cols, FastDiv div_cols4) {
     const float* x = static_cast<const float*>(a.in[0]);
     const float* z = static_cast<const float*>(a.in[1]);
     float* y = static_cast<float*>(a.out);
@@ -285,8 +287,15 @@ __global__ void ArithF32Rank2Kernel(BcastArgs a, int op, int64_t rows, int64_t c
     const int64_t total = rows * cols4;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total; i += stride) {
-        const int64_t r = i / cols4;
-        const int64_t c = (i - r * cols4) * 4;
+        int64_t r, c;
+        if constexpr (SMALL) {
+            uint32_t rem;
+            r = DivMod(div_cols4, static_cast<uint32_t>(i), rem);
+            c = static_cast<int64_t>(rem) * 4;
+        } else {
+            r = i / cols4;
+            c = (i - r * cols4) * 4;
+        }
         const float* xp = x + r * xs0 + c * xs1;
         const float* zp = z + r * zs0 + c * zs1;
         float4 u, v;
@@ -434,6 +443,16 @@ bool Rank2Vectorizable(const BcastArgs& a, int k) {
     return s1 == 0 || (s1 == 1 && s0 % 4 == 0 && Aligned16(a.in[k]));
 }
 
+void LaunchRank2(const BcastArgs& a, int op, hipStream_t s) {
+    const int64_t quads = a.dims[0] * (a.dims[1] / 4);
+    if (quads < (int64_t{1} << 31)) {
+        ArithF32Rank2Kernel<true><<<ElementGrid(quads), kBlock, 0, s>>>(
+            a, op, a.dims[0], a.dims[1], FastDiv::Make(static_cast<uint32_t>(a.dims[1] / 4)));
+    } else {
+        ArithF32Rank2Kernel<false><<<ElementGrid(quads), kBlock, 0, s>>>(a, op, a.dims[0], a.dims[1], FastDiv{});
+    }
+}
+
 } // namespace
 } // namespace nert_hip
 
@@ -528,7 +547,22 @@ int nert_hip_broadcast(int op, int dtype, int n_inputs, const void* const* input
                     static_cast<float*>(out), op, n, vec);
             } else if (a.rank == 2 && a.dims[1] % 4 == 0 && Aligned16(out) && Rank2Vectorizable(a, 0) &&
                        Rank2Vectorizable(a, 1)) {
-                ArithF32Rank2Kernel<<<ElementGrid(n / 4), kBlock, 0, s>>>(a, op, a.dims[0], a.dims[1]);
+                LaunchRank2(a, op, s);
+            } else if (a.rank == 1 && a.dims[0] % 4 == 0 && Aligned16(out)) {
+                // One operand a scalar: the rank-2 walk over a single row.
+                BcastArgs r = a;
+                r.rank = 2;
+                r.dims[1] = a.dims[0];
+                r.dims[0] = 1;
+                for (int k = 0; k < 2; ++k) {
+                    r.strides[k][1] = a.strides[k][0];
+                    r.strides[k][0] = 0;
+                }
+                if (Rank2Vectorizable(r, 0) && Rank2Vectorizable(r, 1)) {
+                    LaunchRank2(r, op, s);
+                } else {
+                    ArithKernel<float><<<grid, kBlock, 0, s>>>(a, op, n);
+                }
             } else {
                 ArithKernel<float><<<grid, kBlock, 0, s>>>(a, op, n);
             }

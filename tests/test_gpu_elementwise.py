@@ -69,6 +69,9 @@ BROADCASTS = [
     ((2, 3, 1, 5), (1, 1, 4, 1)),
     ((5,), ()),
     ((), (3, 4)),
+    ((16, 197, 64), ()),       # scalar operand: one-row rank-2 walk
+    ((), (2, 3, 8)),
+    ((1, 1, 4096), (1,)),
     ((3, 1), (1, 4)),
     ((2, 1, 3, 1, 4, 1, 2), (1, 5, 1, 6, 1, 7, 1)),
 ]
