@@ -6,9 +6,9 @@ A step is one forward pass of the seeded ResNet-18 (configs[2] of
 BN folded, [32,3,224,224] -> [32,1000]) through the gfx950
 HipDevice rows, with weights and the input already resident in HBM. The
 runner first fuses each Conv -> [Add] -> [Relu] chain into one FusedConv row
-(bias, residual and Relu in the conv epilogue, bit-identical outputs), which
-leaves 24 rows out of 49; they are captured once into a HIP graph and
-replayed. K replays are timed with HIP events on the layer stream, bracketed
+(bias, residual and Relu in the conv epilogue, bit-identical outputs) and
+turns the Flatten into a view of its input, which leaves 23 rows out of 49;
+they are captured once into a HIP graph and replayed. K replays are timed with HIP events on the layer stream, bracketed
 by stream syncs.
 
 Extra keys on the one JSON line:
@@ -165,7 +165,7 @@ def main() -> int:
             "rows_after_fusion": len(pg.nodes),
             "gflop_per_step": round(g.flops() / 1e9, 3),
             "launch": ("eager rows" if args.eager else "HIP graph replay") +
-                      " after Conv->Add->Relu fusion (bit-identical outputs)",
+                      " after Conv->Add->Relu fusion (bit-identical outputs) and view aliasing",
         },
         "roofline": {
             "bound": "mfma",

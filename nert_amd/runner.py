@@ -11,7 +11,9 @@ into one HIP graph and replayed, which removes per-row host overhead.
 The arena plan is a first-fit over definition/last-use intervals with 256-byte
 alignment, so intermediates whose lifetimes do not overlap share memory and
 the working set stays small enough to live in the 256 MB Infinity Cache where
-possible.
+possible. Rows that only reinterpret a dense buffer's shape (Reshape, Flatten,
+Squeeze, Unsqueeze, Identity) become views: their output shares the input's
+arena block for the union of both lifetimes, and no copy is queued.
 """
 
 from __future__ import annotations
@@ -28,20 +30,54 @@ from .graph import Graph, Node
 ALIGN = 256
 
 
-def plan_arena(g: Graph) -> tuple[dict[str, int], int]:
-    """Offsets for every node output that is not a graph input/initializer."""
+VIEW_OPS = {"Reshape", "Flatten", "Squeeze", "Unsqueeze", "Identity"}
+
+
+def alias_views(g: Graph) -> tuple[Graph, dict[str, str]]:
+    """Drops view rows whose output can share the input's buffer.
+
+    A row qualifies when its first input is an intermediate (produced by a
+    node, not a graph input or initializer), neither tensor is a graph output,
+    and dtype and element count agree (a dense row-major buffer reads the same
+    under either shape). Returns the graph without those rows and a map from
+    each aliased output to the tensor that owns the storage.
+    """
+    produced = {t for n in g.nodes for t in n.outputs}
+    outputs = set(g.outputs)
+    alias: dict[str, str] = {}
+    kept: list[Node] = []
+    for n in g.nodes:
+        if n.op in VIEW_OPS and n.inputs and n.inputs[0] and len(n.outputs) == 1:
+            x, y = n.inputs[0], n.outputs[0]
+            root = alias.get(x, x)
+            (xd, xs), (yd, ys) = g.tensors[x], g.tensors[y]
+            if (x in produced and x not in g.initializers and x not in g.inputs and x not in outputs
+                    and y not in outputs and np.dtype(xd) == np.dtype(yd)
+                    and int(np.prod(xs)) == int(np.prod(ys))):
+                alias[y] = root
+                continue
+        kept.append(n)
+    return (Graph(nodes=kept, initializers=g.initializers, inputs=g.inputs, outputs=g.outputs, tensors=g.tensors),
+            alias)
+
+
+def plan_arena(g: Graph, alias: dict[str, str] | None = None) -> tuple[dict[str, int], int]:
+    """Offsets for every node output that is not a graph input/initializer;
+    aliased tensors get their owner's offset, and the owner stays live until
+    the last use of any of its views."""
+    alias = alias or {}
     produced: dict[str, int] = {}
     last_use: dict[str, int] = {}
     for idx, n in enumerate(g.nodes):
         for t in n.inputs:
             if t:
-                last_use[t] = idx
+                last_use[alias.get(t, t)] = idx
         for t in n.outputs:
             produced.setdefault(t, idx)
             last_use.setdefault(t, idx)
     end = len(g.nodes)
     for t in g.outputs:
-        last_use[t] = end
+        last_use[alias.get(t, t)] = end
     live: list[tuple[int, int, int]] = []  # (offset, size, last_use)
     offsets: dict[str, int] = {}
     arena = 0
@@ -60,6 +96,9 @@ def plan_arena(g: Graph) -> tuple[dict[str, int], int]:
         offsets[t] = cursor
         live.append((cursor, size, last_use[t]))
         arena = max(arena, cursor + size)
+    for view, owner in alias.items():
+        if owner in offsets:
+            offsets[view] = offsets[owner]
     return offsets, arena
 
 
@@ -142,11 +181,14 @@ class _PackedNode:
 
 
 class Program:
-    def __init__(self, g: Graph, fuse: bool = True):
+    def __init__(self, g: Graph, fuse: bool = True, views: bool = True):
         if fuse:
             g = fuse_conv_chains(g)
+        self.alias: dict[str, str] = {}
+        if views:
+            g, self.alias = alias_views(g)
         self.graph = g
-        self.offsets, self.arena_bytes = plan_arena(g)
+        self.offsets, self.arena_bytes = plan_arena(g, self.alias)
         self.arena = DeviceArray((max(self.arena_bytes, 1),), np.uint8)
         self.resident: dict[str, DeviceArray] = {}
         for name, value in g.initializers.items():

@@ -70,3 +70,52 @@ def test_arena_plan_reuses_memory():
     assert all(o % 256 == 0 for o in offsets.values())
     # fusion removes the chain intermediates from the plan altogether
     assert size < plan_arena(g)[1]
+
+
+def _intervals(g, offsets, alias):
+    """(offset, size, first, last) per owned buffer, with views folded in."""
+    first, last = {}, {}
+    for idx, n in enumerate(g.nodes):
+        for t in n.outputs:
+            first.setdefault(t, idx)
+            last.setdefault(t, idx)
+        for t in n.inputs:
+            if t:
+                last[alias.get(t, t)] = idx
+    for t in g.outputs:
+        last[alias.get(t, t)] = len(g.nodes)
+    out = []
+    for t, start in first.items():
+        size = int(np.prod(g.tensors[t][1])) * np.dtype(g.tensors[t][0]).itemsize
+        out.append((offsets[t], max(size, 1), start, last[t], t))
+    return out
+
+
+def test_view_rows_alias_their_input():
+    from nert_amd.runner import alias_views
+
+    g, _ = workloads.vit_b16(batch=2, layers=2)
+    f, alias = alias_views(fuse_conv_chains(g))
+    dropped = [n for n in g.nodes if n.op in ("Reshape", "Squeeze", "Flatten", "Unsqueeze", "Identity")]
+    assert dropped and len(f.nodes) < len(g.nodes)
+    assert not any(n.op in ("Squeeze", "Reshape") and n.outputs[0] in alias for n in f.nodes)
+    _valid_order_with(f, alias)
+    offsets, size = plan_arena(f, alias)
+    for view, owner in alias.items():
+        assert offsets[view] == offsets[owner]
+        assert int(np.prod(g.tensors[view][1])) == int(np.prod(g.tensors[owner][1]))
+    # no two buffers that are live at the same time overlap
+    iv = _intervals(f, offsets, alias)
+    for i, (o1, s1, a1, b1, t1) in enumerate(iv):
+        for o2, s2, a2, b2, t2 in iv[i + 1:]:
+            if a1 <= b2 and a2 <= b1:
+                assert o1 + s1 <= o2 or o2 + s2 <= o1, (t1, t2)
+
+
+def _valid_order_with(g, alias):
+    avail = set(g.initializers) | set(g.inputs)
+    for n in g.nodes:
+        for t in n.inputs:
+            assert not t or alias.get(t, t) in avail or t in avail, (n.op, t)
+        avail.update(n.outputs)
+        avail.update(v for v, o in alias.items() if o in avail)
