@@ -10,6 +10,8 @@
 #include "common.hpp"
 #include "../../include/nert_hip.h"
 
+#include <algorithm>
+
 namespace nert_hip {
 namespace {
 
@@ -72,6 +74,115 @@ __global__ void MaxPool2dKernel(PoolArgs p) {
         }
         p.y[i] = best;
     }
+}
+
+// MaxPool through LDS: a workgroup owns `rows` output rows of one plane. It
+// copies the input rows they read (full width; rows outside the image as
+// -inf, which never wins the `x > best` test, so they act as skipped taps)
+// into LDS with 16-byte loads where the row length allows, then takes every
+// window max from LDS: each input element leaves HBM once instead of once
+// per window that covers it. Columns outside the image are skipped by the
+// bounds test, as the reference skips padded taps.
+struct PoolTile {
+    int32_t rows;      // output rows per workgroup
+    int32_t rows_in;   // input rows they read
+    int32_t row_blocks;
+    int32_t vec;       // 16-byte loads (in_w % 4 == 0, aligned input)
+    FastDiv div_blocks; // by row_blocks
+    FastDiv div_in_w;   // by in_w (or in_w / 4 with vec)
+    FastDiv div_out_w;  // by out_w
+};
+
+__global__ __launch_bounds__(256) void MaxPoolTileKernel(PoolArgs p, PoolTile t) {
+    extern __shared__ float tile[]; // [rows_in][in_w]
+    uint32_t rb;
+    const int64_t plane = DivMod(t.div_blocks, blockIdx.x, rb);
+    const int oh0 = static_cast<int>(rb) * t.rows;
+    const int ih0 = oh0 * p.s_h - p.p_h;
+    const float* xp = p.x + plane * p.in_h * p.in_w;
+    const float ninf = -__builtin_huge_valf();
+    if (t.vec) {
+        const int quads_row = p.in_w / 4;
+        const int quads = t.rows_in * quads_row;
+        for (int e = threadIdx.x; e < quads; e += blockDim.x) {
+            uint32_t c4;
+            const int r = static_cast<int>(DivMod(t.div_in_w, static_cast<uint32_t>(e), c4));
+            const int ih = ih0 + r;
+            nert_floatx4 v = {ninf, ninf, ninf, ninf};
+            if (static_cast<unsigned>(ih) < static_cast<unsigned>(p.in_h)) {
+                v = *reinterpret_cast<const nert_floatx4*>(xp + static_cast<int64_t>(ih) * p.in_w + 4 * c4);
+            }
+            *reinterpret_cast<nert_floatx4*>(tile + r * p.in_w + 4 * c4) = v;
+        }
+    } else {
+        const int elems = t.rows_in * p.in_w;
+        for (int e = threadIdx.x; e < elems; e += blockDim.x) {
+            uint32_t c;
+            const int r = static_cast<int>(DivMod(t.div_in_w, static_cast<uint32_t>(e), c));
+            const int ih = ih0 + r;
+            tile[e] = static_cast<unsigned>(ih) < static_cast<unsigned>(p.in_h)
+                          ? xp[static_cast<int64_t>(ih) * p.in_w + c]
+                          : ninf;
+        }
+    }
+    __syncthreads();
+    const int outs = t.rows * p.out_w;
+    float* yp = p.y + plane * p.out_h * p.out_w;
+    for (int o = threadIdx.x; o < outs; o += blockDim.x) {
+        uint32_t ow;
+        const int r = static_cast<int>(DivMod(t.div_out_w, static_cast<uint32_t>(o), ow));
+        const int oh = oh0 + r;
+        if (oh >= p.out_h) {
+            break; // o only grows
+        }
+        const int w0 = static_cast<int>(ow) * p.s_w - p.p_w;
+        float best = ninf;
+        for (int kh = 0; kh < p.k_h; ++kh) {
+            const float* row = tile + (r * p.s_h + kh * p.d_h) * p.in_w;
+            for (int kw = 0; kw < p.k_w; ++kw) {
+                const int iw = w0 + kw * p.d_w;
+                if (static_cast<unsigned>(iw) >= static_cast<unsigned>(p.in_w)) {
+                    continue;
+                }
+                const float v = row[iw];
+                if (v > best) {
+                    best = v;
+                }
+            }
+        }
+        yp[static_cast<int64_t>(oh) * p.out_w + ow] = best;
+    }
+}
+
+// True when a useful tile fits in 48 KiB of LDS: at least 4 output rows, or
+// the whole output height.
+bool TryMaxPoolTile(const PoolArgs& p, hipStream_t s) {
+    constexpr int64_t kLdsFloats = 48 * 1024 / 4;
+    const int64_t halo = static_cast<int64_t>(p.k_h - 1) * p.d_h + 1;
+    int64_t rows = 16;
+    while (rows > 1 && ((rows - 1) * p.s_h + halo) * p.in_w > kLdsFloats) {
+        rows /= 2;
+    }
+    rows = std::min<int64_t>(rows, p.out_h);
+    const int64_t rows_in = (rows - 1) * p.s_h + halo;
+    if (rows_in * p.in_w > kLdsFloats || (rows < 4 && rows < p.out_h) || rows * p.out_w > (int64_t{1} << 30)) {
+        return false;
+    }
+    PoolTile t{};
+    t.rows = static_cast<int32_t>(rows);
+    t.rows_in = static_cast<int32_t>(rows_in);
+    t.row_blocks = static_cast<int32_t>((p.out_h + rows - 1) / rows);
+    const int64_t blocks = p.planes * t.row_blocks;
+    if (blocks >= (int64_t{1} << 31)) {
+        return false;
+    }
+    t.vec = p.in_w % 4 == 0 && (reinterpret_cast<uintptr_t>(p.x) & 15) == 0 ? 1 : 0;
+    t.div_blocks = FastDiv::Make(static_cast<uint32_t>(t.row_blocks));
+    t.div_in_w = FastDiv::Make(static_cast<uint32_t>(t.vec ? p.in_w / 4 : p.in_w));
+    t.div_out_w = FastDiv::Make(static_cast<uint32_t>(p.out_w));
+    const size_t lds = static_cast<size_t>(rows_in * p.in_w) * sizeof(float);
+    MaxPoolTileKernel<<<static_cast<unsigned>(blocks), 256, lds, s>>>(p, t);
+    return true;
 }
 
 // AveragePool, exactly as src/kernels/average_pool.cpp:196-223: a float sum
@@ -175,7 +286,9 @@ int nert_hip_maxpool2d_f32(const float* x, float* y, const nert_pool_desc* d, vo
         if (total <= 0) {
             return;
         }
-        if (total < (int64_t{1} << 31)) {
+        if (TryMaxPoolTile(p, StreamOr(stream))) {
+            // done
+        } else if (total < (int64_t{1} << 31)) {
             MaxPool2dKernel<true><<<GridFor(total, 256, 16384), 256, 0, StreamOr(stream)>>>(p);
         } else {
             MaxPool2dKernel<false><<<GridFor(total, 256, 16384), 256, 0, StreamOr(stream)>>>(p);

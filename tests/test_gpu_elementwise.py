@@ -193,6 +193,8 @@ POOL_CASES = [
     ((1, 2, 9, 9), {"kernel_shape": [3, 3], "strides": [2, 2], "ceil_mode": 1}),
     ((1, 2, 9, 9), {"kernel_shape": [2, 2], "auto_pad": "SAME_UPPER", "strides": [2, 2]}),
     ((1, 2, 9, 9), {"kernel_shape": [3, 3], "dilations": [2, 2], "pads": [2, 2, 2, 2]}),
+    ((2, 3, 30, 2000), {"kernel_shape": [3, 3], "pads": [1, 1, 1, 1]}),  # wide rows: 4-row LDS tiles
+    ((1, 1, 5, 5000), {"kernel_shape": [3, 3]}),                          # too wide for LDS: direct kernel
 ]
 
 
