@@ -149,6 +149,89 @@ __global__ void SplitReduceKernel(GemmArgs p, int splits, int64_t batches, int v
     }
 }
 
+// Skinny GEMM (M <= 32, K contiguous in both operands: the ResNet classifier
+// and Gemm with transB): one workgroup per 32 output columns; each of its 4
+// waves takes a quarter of K and runs MFMAs straight from 16-byte global loads
+// -- lane half h holds k = 8j + 4h .. 8j + 4h + 3 of its A row and B column,
+// so one load pair feeds four MFMA steps -- then the four partial 32x32
+// blocks are summed through LDS in wave order (deterministic) and the
+// epilogue is the engine's alpha * acc + beta * bias. One launch, no split-K
+// partials in memory.
+__global__ __launch_bounds__(256) void SkinnyGemmKernel(GemmArgs p, int64_t k_slice) {
+    __shared__ float part[3][64][17];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int half = lane >> 5;
+    const int64_t m = lane & 31;
+    const int64_t n = static_cast<int64_t>(blockIdx.x) * 32 + (lane & 31);
+    const int64_t k_begin = wave * k_slice;
+    const int64_t k_end = std::min<int64_t>(k_begin + k_slice, p.k);
+    const bool m_ok = m < p.m;
+    const bool n_ok = n < p.n;
+    const float* ap = p.a + (m_ok ? m : 0) * p.a_sm + 4 * half;
+    const float* bp = p.b + (n_ok ? n : 0) * p.b_sn + 4 * half;
+    nert_floatx16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        acc[v] = 0.0f;
+    }
+#pragma unroll 4
+    for (int64_t k = k_begin; k < k_end; k += 8) {
+        nert_floatx4 a = *reinterpret_cast<const nert_floatx4*>(ap + k);
+        nert_floatx4 b = *reinterpret_cast<const nert_floatx4*>(bp + k);
+        if (!m_ok) {
+            a = nert_floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        if (!n_ok) {
+            b = nert_floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk], b[kk], acc, 0, 0, 0);
+        }
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            part[wave - 1][lane][v] = acc[v];
+        }
+    }
+    __syncthreads();
+    if (wave != 0) {
+        return;
+    }
+#pragma unroll
+    for (int w = 0; w < 3; ++w) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            acc[v] += part[w][lane][v];
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int64_t r = 8 * (v >> 2) + 4 * half + (v & 3);
+        if (r < p.m && n_ok) {
+            float value = p.alpha * acc[v];
+            if (p.has_bias) {
+                value += p.beta * p.bias[r * p.bias_sm + n * p.bias_sn];
+            }
+            p.y[r * p.n + n] = value;
+        }
+    }
+}
+
+bool SkinnyApplies(const GemmArgs& p, int64_t batches) {
+    return batches == 1 && p.m <= 32 && p.a_sk == 1 && p.b_sk == 1 && p.k % 8 == 0 && p.a_sm % 4 == 0 &&
+           p.b_sn % 4 == 0 && (reinterpret_cast<uintptr_t>(p.a) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(p.b) & 15) == 0 && p.k > 0 && (p.n + 31) / 32 < (int64_t{1} << 31);
+}
+
+void LaunchSkinny(const GemmArgs& p, hipStream_t stream) {
+    const int64_t k_slice = ((p.k + 31) / 32) * 8; // a multiple of 8, four slices cover K
+    SkinnyGemmKernel<<<static_cast<unsigned>((p.n + 31) / 32), 256, 0, stream>>>(p, k_slice);
+    CheckLaunch("SkinnyGemmKernel launch");
+}
+
 // Tile shapes, chosen from a sweep over the BASELINE GEMM/MatMul shapes and
 // the ViT projections on MI355X: 8 waves of 64x32 for problems with at least
 // 1024 such tiles (4096^3: 135 TFLOP/s), 4 waves of 32x64 below that (more
@@ -255,13 +338,29 @@ void LaunchGemm(GemmArgs p, int64_t batches, hipStream_t stream) {
     const GemmKey key{p.m, p.n, p.k, batches, p.a_sk == 1, p.b_sn == 1, p.batch_rank, p.has_bias,
                       p.bias_sm, p.bias_sn};
     const size_t y_bytes = static_cast<size_t>(batches * p.m * p.n) * sizeof(float);
-    const int c = ChooseConfig(chosen, mu, key, y_bytes, stream, 12, 4 * fallback_shape, [&](int i, float* scratch) {
+    // Candidates 0-11: tile shape x split count; 12: the skinny kernel.
+    const bool skinny = SkinnyApplies(p, batches);
+    const int c = ChooseConfig(chosen, mu, key, y_bytes, stream, 13, 4 * fallback_shape, [&](int i, float* scratch) {
         GemmArgs q = p;
         q.y = scratch;
+        if (i == 12) {
+            if (!skinny) {
+                return false;
+            }
+            LaunchSkinny(q, stream);
+            return true;
+        }
         LaunchConfig(q, batches, i / 4, kGemmSplits[i % 4], stream);
         return true;
     });
-    LaunchConfig(p, batches, c / 4, kGemmSplits[c % 4], stream);
+    if (c == 12 && skinny) {
+        LaunchSkinny(p, stream);
+        return;
+    }
+    // (A cached skinny choice with operands that lost its alignment takes
+    // the fallback tiles.)
+    const int tiled = c == 12 ? 4 * fallback_shape : c;
+    LaunchConfig(p, batches, tiled / 4, kGemmSplits[tiled % 4], stream);
 }
 
 } // namespace nert_hip

@@ -216,6 +216,17 @@ def test_config1b_gemm_transb(gpu):
     compare(got, restate.gemm(a, b, c, trans_b=1), what="cfg1b")
 
 
+@pytest.mark.parametrize("m,n,k", [(7, 45, 72), (32, 33, 8), (1, 1000, 512), (20, 300, 4096)])
+def test_skinny_gemm_shapes(gpu, m, n, k):
+    """Few rows with K contiguous in both operands (transB): the skinny kernel's
+    territory, with ragged M and N, short and long K, a 2-D C and alpha/beta."""
+    a = uniform((m, k), seed=m + 1)
+    b = uniform((n, k), seed=n + 2)
+    assert_parity("Gemm", [a, b, uniform((n,), seed=3)], [((m, n), F)], {"transB": 1})
+    assert_parity("Gemm", [a, b, uniform((m, n), seed=4)], [((m, n), F)],
+                  {"transB": 1, "alpha": 0.5, "beta": -2.0})
+
+
 def test_config1c_skinny_gemm(gpu):
     """configs[1](c): A[32,512] x B[1000,512]^T + bias, against the reference row."""
     a = uniform((32, 512), seed=15)
