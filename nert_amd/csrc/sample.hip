@@ -2,9 +2,11 @@
 // and GridSample (bilinear / nearest, zeros / border / reflection padding).
 //
 // Both follow the reference's double-precision coordinate math step for step
-// (src/kernels/resize.cpp:48-123, src/kernels/grid_sample.cpp:41-71,132-157),
-// evaluated per output element on the device instead of through host tables,
-// so nothing is uploaded per call and the rows stay capturable. Contraction
+// (src/kernels/resize.cpp:48-123, src/kernels/grid_sample.cpp:41-71,132-157).
+// Resize evaluates it once per output coordinate of each axis, in a small
+// kernel that writes per-axis tables (lower and upper source index, weight)
+// to the workspace; the main kernel then only gathers. Nothing is uploaded
+// per call, so the row stays capturable. Contraction
 // of a*b+c into fma is off in these kernels: every product and sum rounds
 // where the reference's does.
 
@@ -77,11 +79,72 @@ __device__ int64_t NearestIndex(int mode, double x, int64_t in_len) {
     return index < 0 ? 0 : (index > in_len - 1 ? in_len - 1 : index);
 }
 
+// Per-axis tables: entry base[d] + o holds the source taps of output
+// coordinate o along axis d.
+struct ResizeTables {
+    int64_t* lower;
+    int64_t* upper;
+    double* weight;
+    int64_t base[kMaxRank];
+    int64_t total;
+};
+
+__global__ void ResizeTableKernel(ResizeArgs a, ResizeTables t) {
+    for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < t.total;
+         e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        int d = 0;
+        while (d + 1 < a.rank && e >= t.base[d + 1]) {
+            ++d;
+        }
+        const int64_t o = e - t.base[d];
+        const double src = SourceCoord(a.transform, o, a.in_dims[d], a.out_dims[d], a.scales[d]);
+        if (!a.linear) {
+            t.lower[e] = t.upper[e] = NearestIndex(a.nearest, src, a.in_dims[d]);
+            t.weight[e] = 0.0;
+            continue;
+        }
+        const double clamped = ClampRef(src, 0.0, static_cast<double>(a.in_dims[d] - 1));
+        const int64_t lo = ToI64(floor(clamped));
+        const int64_t up = lo + 1 < a.in_dims[d] - 1 ? lo + 1 : a.in_dims[d] - 1;
+        t.lower[e] = lo;
+        t.upper[e] = up;
+        t.weight[e] = up == lo ? 0.0 : clamped - static_cast<double>(lo);
+    }
+}
+
+// Nearest: one gather per output element through the tables.
 template <typename T>
-__global__ void ResizeKernel(const T* __restrict__ x, T* __restrict__ y, ResizeArgs a, int64_t n) {
+__global__ void ResizeNearestKernel(const T* __restrict__ x, T* __restrict__ y, ResizeArgs a, ResizeTables t,
+                                    int64_t n) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n; i += stride) {
-        // Per axis: lower/upper source index and the upper weight.
+        int64_t rem = i;
+        uint32_t rem32 = static_cast<uint32_t>(i);
+        int64_t off = 0;
+        for (int d = a.rank - 1; d >= 0; --d) {
+            int64_t o;
+            if (a.small) {
+                uint32_t c;
+                rem32 = DivMod(a.div[d], rem32, c);
+                o = c;
+            } else {
+                o = rem % a.out_dims[d];
+                rem /= a.out_dims[d];
+            }
+            off += t.lower[t.base[d] + o] * a.in_strides[d];
+        }
+        y[i] = x[off];
+    }
+}
+
+// Linear: the taps of every interpolating axis, in the reference's order
+// (each interpolating axis doubles the list, lower before upper,
+// src/kernels/resize.cpp:102-122), weights from the tables.
+template <typename T>
+__global__ void ResizeLinearKernel(const T* __restrict__ x, T* __restrict__ y, ResizeArgs a, ResizeTables t,
+                                   int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n; i += stride) {
         int64_t lower[kMaxRank];
         int64_t upper[kMaxRank];
         double weight[kMaxRank];
@@ -97,19 +160,10 @@ __global__ void ResizeKernel(const T* __restrict__ x, T* __restrict__ y, ResizeA
                 o = rem % a.out_dims[d];
                 rem /= a.out_dims[d];
             }
-            const double src = SourceCoord(a.transform, o, a.in_dims[d], a.out_dims[d], a.scales[d]);
-            if (!a.linear) {
-                lower[d] = upper[d] = NearestIndex(a.nearest, src, a.in_dims[d]);
-                weight[d] = 0.0;
-                continue;
-            }
-            const double clamped = ClampRef(src, 0.0, static_cast<double>(a.in_dims[d] - 1));
-            lower[d] = ToI64(floor(clamped));
-            upper[d] = lower[d] + 1 < a.in_dims[d] - 1 ? lower[d] + 1 : a.in_dims[d] - 1;
-            weight[d] = upper[d] == lower[d] ? 0.0 : clamped - static_cast<double>(lower[d]);
+            lower[d] = t.lower[t.base[d] + o];
+            upper[d] = t.upper[t.base[d] + o];
+            weight[d] = t.weight[t.base[d] + o];
         }
-        // Taps in the reference's order: each interpolating axis doubles
-        // the list, lower before upper (src/kernels/resize.cpp:102-122).
         int interp[kMaxRank];
         int m = 0;
         int64_t base = 0;
@@ -125,12 +179,12 @@ __global__ void ResizeKernel(const T* __restrict__ x, T* __restrict__ y, ResizeA
             continue;
         }
         double value = 0.0;
-        for (int t = 0; t < (1 << m); ++t) {
+        for (int q = 0; q < (1 << m); ++q) {
             int64_t off = base;
             double w = 1.0;
-            for (int q = 0; q < m; ++q) {
-                const int d = interp[q];
-                const bool up = (t >> (m - 1 - q)) & 1;
+            for (int j = 0; j < m; ++j) {
+                const int d = interp[j];
+                const bool up = (q >> (m - 1 - j)) & 1;
                 off += (up ? upper[d] : lower[d]) * a.in_strides[d];
                 w = w * (up ? weight[d] : 1.0 - weight[d]);
             }
@@ -249,15 +303,31 @@ int nert_hip_resize(int dtype, const void* x, void* y, int rank, const int64_t* 
             return;
         }
         a.small = n < (int64_t{1} << 31) ? 1 : 0;
-        hipStream_t s = StreamOr(stream);
-        const unsigned grid = GridFor(n, 256, 16384);
-        if (dtype == NERT_F32) {
-            ResizeKernel<float><<<grid, 256, 0, s>>>(static_cast<const float*>(x), static_cast<float*>(y), a, n);
-        } else if (dtype == NERT_I64 && !linear) {
-            ResizeKernel<int64_t><<<grid, 256, 0, s>>>(static_cast<const int64_t*>(x), static_cast<int64_t*>(y), a,
-                                                       n);
-        } else {
+        if (!(dtype == NERT_F32 || (dtype == NERT_I64 && !linear))) {
             throw Error("resize: float32, or int64 for nearest");
+        }
+        hipStream_t s = StreamOr(stream);
+        ResizeTables t{};
+        for (int d = 0; d < rank; ++d) {
+            t.base[d] = t.total;
+            t.total += out_dims[d];
+        }
+        char* ws = static_cast<char*>(Workspace(t.total * 24, s));
+        t.lower = reinterpret_cast<int64_t*>(ws);
+        t.upper = t.lower + t.total;
+        t.weight = reinterpret_cast<double*>(t.upper + t.total);
+        ResizeTableKernel<<<GridFor(t.total, 256, 1024), 256, 0, s>>>(a, t);
+        CheckLaunch("resize table launch");
+        const unsigned grid = GridFor(n, 256, 16384);
+        if (dtype == NERT_F32 && linear) {
+            ResizeLinearKernel<float><<<grid, 256, 0, s>>>(static_cast<const float*>(x), static_cast<float*>(y), a,
+                                                           t, n);
+        } else if (dtype == NERT_F32) {
+            ResizeNearestKernel<float><<<grid, 256, 0, s>>>(static_cast<const float*>(x), static_cast<float*>(y), a,
+                                                            t, n);
+        } else {
+            ResizeNearestKernel<int64_t><<<grid, 256, 0, s>>>(static_cast<const int64_t*>(x),
+                                                              static_cast<int64_t*>(y), a, t, n);
         }
         CheckLaunch("resize launch");
     });

@@ -11,11 +11,14 @@
 // Rows of up to kSmallRow elements sort in one workgroup's LDS. Longer rows
 // (the detector's [8, 672000], K = 300) run a radix select over the key,
 // 8 bits per pass from the top, with many workgroups per row: each pass builds
-// a 256-bin histogram of the keys that still match the chosen prefix, and a
-// one-block-per-row scan picks the bin holding the K-th largest key. When
-// that bin is needed whole the threshold is final and later passes return at
-// once. Keys >= threshold (exactly K per row) are collected, sorted in
-// 4096-key LDS runs, merged by per-key binary search, and written out.
+// a 256-bin histogram of the keys that still match the chosen prefix (one LDS
+// histogram per wave, so the waves do not contend for the same bins), and a
+// one-block-per-row kernel scans it in parallel and picks the bin holding the
+// K-th largest key. When that bin is needed whole the threshold is final and
+// later passes return at once. Keys >= threshold (exactly K per row) are
+// collected and ordered -- by rank (the count of larger keys, spread over
+// several workgroups per row) when K <= 1024, else in 4096-key LDS runs
+// merged by per-key binary search -- and written out.
 
 #include "common.hpp"
 #include "../../include/nert_hip.h"
@@ -134,8 +137,11 @@ __global__ void __launch_bounds__(kThreads) HistKernel(const float* __restrict__
     if (s.done) {
         return;
     }
-    __shared__ uint32_t h[256];
-    h[threadIdx.x] = 0;
+    __shared__ uint32_t h[kThreads / 64][256];
+    const int wave = threadIdx.x >> 6;
+    for (int w = 0; w < kThreads / 64; ++w) {
+        h[w][threadIdx.x] = 0;
+    }
     __syncthreads();
     const int shift = 56 - 8 * pass;
     const int64_t begin = c * chunk;
@@ -149,46 +155,51 @@ __global__ void __launch_bounds__(kThreads) HistKernel(const float* __restrict__
         // pass 0 has no prefix to match (a 64-bit shift would be undefined)
         const bool match = pass == 0 || (key >> (shift + 8)) == (s.prefix >> (shift + 8));
         if (match) {
-            atomicAdd(&h[(key >> shift) & 0xFF], 1u);
+            atomicAdd(&h[wave][(key >> shift) & 0xFF], 1u);
         }
     }
     __syncthreads();
-    const uint32_t v = h[threadIdx.x];
+    uint32_t v = 0;
+    for (int w = 0; w < kThreads / 64; ++w) {
+        v += h[w][threadIdx.x];
+    }
     if (v != 0) {
         atomicAdd(&hist[row * 256 + threadIdx.x], v);
     }
 }
 
-// One wave per row: finds the bin holding the remaining-th largest key.
-__global__ void ScanKernel(SelectState* st, uint32_t* hist, int pass) {
+// One 256-thread block per row: scan[j] = count of digit 255 - j, an
+// inclusive prefix sum, and the chosen digit is the one whose sum first
+// reaches `remaining`. Clears the row's histogram for the next pass.
+__global__ void __launch_bounds__(256) ScanKernel(SelectState* st, uint32_t* hist, int pass) {
     const int64_t row = blockIdx.x;
-    SelectState s = st[row];
-    uint32_t* h = hist + row * 256;
+    const SelectState s = st[row];
     if (s.done) {
         return;
     }
-    __shared__ uint32_t bins[256];
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) {
-        bins[i] = h[i];
-        h[i] = 0; // ready for the next pass
-    }
+    __shared__ uint32_t scan[256];
+    const int t = threadIdx.x;
+    uint32_t* rh = hist + row * 256;
+    const uint32_t count = rh[255 - t];
+    rh[255 - t] = 0;
+    scan[t] = count;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const int shift = 56 - 8 * pass;
-        int64_t before = 0;
-        for (int d = 255; d >= 0; --d) {
-            const int64_t n = bins[d];
-            if (before + n >= s.remaining) {
-                s.prefix |= static_cast<uint64_t>(d) << shift;
-                s.remaining -= before;
-                if (n == s.remaining) {
-                    s.done = 1;
-                }
-                break;
-            }
-            before += n;
+    for (int off = 1; off < 256; off <<= 1) {
+        const uint32_t add = t >= off ? scan[t - off] : 0u;
+        __syncthreads();
+        scan[t] += add;
+        __syncthreads();
+    }
+    const int64_t incl = scan[t];
+    const int64_t excl = incl - count;
+    if (excl < s.remaining && incl >= s.remaining) {
+        SelectState ns = s;
+        ns.prefix |= static_cast<uint64_t>(255 - t) << (56 - 8 * pass);
+        ns.remaining = s.remaining - excl;
+        if (static_cast<int64_t>(count) == ns.remaining) {
+            ns.done = 1;
         }
-        st[row] = s;
+        st[row] = ns;
     }
 }
 
@@ -273,6 +284,36 @@ __global__ void MergeKernel(const uint64_t* __restrict__ src, uint64_t* __restri
     }
 }
 
+// K <= kRankMax: a key's place is the number of larger keys (all keys are
+// unique). Workgroup (row, part) places keys part * 64 .. part * 64 + 63 of
+// the row, four threads per key each counting a quarter of the row's keys
+// out of an LDS copy.
+constexpr int kRankMax = 1024;
+
+__global__ void __launch_bounds__(256) RankSortKernel(const uint64_t* __restrict__ cand,
+                                                      uint64_t* __restrict__ sorted, int64_t k, int parts) {
+    __shared__ uint64_t s[kRankMax];
+    const int64_t row = blockIdx.x / parts;
+    const int part = blockIdx.x - static_cast<int>(row * parts);
+    const uint64_t* p = cand + row * k;
+    for (int i = threadIdx.x; i < k; i += blockDim.x) {
+        s[i] = p[i];
+    }
+    __syncthreads();
+    const int i = part * 64 + (threadIdx.x >> 2);
+    const int q = threadIdx.x & 3;
+    const uint64_t key = i < k ? s[i] : 0;
+    int larger = 0;
+    for (int j = q; j < k; j += 4) {
+        larger += s[j] > key ? 1 : 0;
+    }
+    larger += __shfl_xor(larger, 1, 64);
+    larger += __shfl_xor(larger, 2, 64);
+    if (q == 0 && i < k) {
+        sorted[row * k + larger] = key;
+    }
+}
+
 __global__ void EmitKernel(const float* __restrict__ x, const uint64_t* __restrict__ sorted, float* values,
                            int64_t* indices, int64_t rows, RowGeom g) {
     const int64_t total = rows * g.k;
@@ -345,9 +386,16 @@ int nert_hip_topk_f32(const float* x, float* values, int64_t* indices, int64_t o
         const unsigned blocks = static_cast<unsigned>(rows * chunks);
         for (int pass = 0; pass < 8; ++pass) {
             HistKernel<<<blocks, kThreads, 0, s>>>(x, g, chunk, static_cast<int>(chunks), st, hist, pass);
-            ScanKernel<<<static_cast<unsigned>(rows), 64, 0, s>>>(st, hist, pass);
+            ScanKernel<<<static_cast<unsigned>(rows), 256, 0, s>>>(st, hist, pass);
         }
         CollectKernel<<<blocks, kThreads, 0, s>>>(x, g, chunk, static_cast<int>(chunks), st, cand);
+        if (k <= kRankMax) {
+            const int parts = static_cast<int>((k + 63) / 64);
+            RankSortKernel<<<static_cast<unsigned>(rows * parts), 256, 0, s>>>(cand, cand2, k, parts);
+            EmitKernel<<<GridFor(rows * k, 256, 16384), 256, 0, s>>>(x, cand2, values, indices, rows, g);
+            CheckLaunch("topk launch");
+            return;
+        }
         const int64_t runs = (k + kRun - 1) / kRun;
         const int run_pow2 = PowTwoAtLeast(k < kRun ? k : kRun);
         SortRunsKernel<<<static_cast<unsigned>(rows * runs), kThreads, 0, s>>>(cand, k, static_cast<int>(runs),
