@@ -109,6 +109,18 @@ int nert_hip_matmul_f32(const float* a, const float* b, float* y, int64_t m, int
                         const int64_t* batch_dims, const int64_t* a_batch_strides, const int64_t* b_batch_strides,
                         void* stream);
 
+/* MatMul with its elementwise followers in the epilogue: Y = scale * (A B),
+ * then + bias[n] (bias may be NULL), then for act == 1 the erf Gelu chain
+ * Y = Y * (erf(Y / p[0]) + p[1]) * p[2] (act_params = p). Each operation
+ * rounds like the separate Mul / Add / Div / Erf / Add / Mul rows, so the
+ * result equals running them after nert_hip_matmul_f32 bit for bit.
+ * No counterpart in the reference: it backs the runner's FusedMatMul row
+ * (an internal row the runner creates from those chains). */
+int nert_hip_matmul_fused_f32(const float* a, const float* b, const float* bias, float* y, int64_t m, int64_t n,
+                              int64_t k, int batch_rank, const int64_t* batch_dims, const int64_t* a_batch_strides,
+                              const int64_t* b_batch_strides, float scale, int act, const float* act_params,
+                              void* stream);
+
 /* Convolution geometry, lifted to three spatial axes (depth, height, width)
  * with unit leading extents for 1-D/2-D, as src/kernels/conv.cpp:233-249. */
 typedef struct nert_conv_desc {

@@ -105,15 +105,13 @@ std::vector<int64_t> BatchStrides(const std::vector<int64_t>& in, const std::vec
 
 } // namespace
 
-// Validation follows src/kernels/mat_mul.cpp:79-139.
-void MatMul(const Node& node, const Views& inputs, const Views& outputs) {
-    const std::string context = "MatMul (node '" + node.name + "')";
-    if (inputs.size() != 2 || outputs.size() != 1) {
-        throw InferenceException(context + ": expected two inputs and one output");
-    }
-    const TensorView& a = inputs[0];
-    const TensorView& b = inputs[1];
-    const TensorView& out = outputs[0];
+namespace {
+
+// The MatMul row's work, shared with FusedMatMul: `scale`, `bias` (or null)
+// and the activation go to the GEMM epilogue. Validation follows
+// src/kernels/mat_mul.cpp:79-139.
+void MatMulCore(const std::string& context, const TensorView& a, const TensorView& b, const TensorView& out,
+                const Views& outputs, const float* bias, float scale, int act, const float* act_params) {
     if (a.dtype != DataType::Float32 || b.dtype != DataType::Float32 || out.dtype != DataType::Float32) {
         throw InferenceException(context + ": tensors must be float32");
     }
@@ -189,7 +187,8 @@ void MatMul(const Node& node, const Views& inputs, const Views& outputs) {
     }
     int64_t batches = Count(dims);
     if (b_shared && a_dense && batches > 1) {
-        CheckStatus(nert_hip_matmul_f32(ap, bp, yp, m * batches, n, k, 0, nullptr, nullptr, nullptr, Stream()),
+        CheckStatus(nert_hip_matmul_fused_f32(ap, bp, bias, yp, m * batches, n, k, 0, nullptr, nullptr, nullptr, scale,
+                                              act, act_params, Stream()),
                     context);
         AfterRow(outputs, context);
         return;
@@ -223,10 +222,55 @@ void MatMul(const Node& node, const Views& inputs, const Views& outputs) {
     if (cd.size() > 4) {
         throw InferenceException(context + ": more than four non-mergeable batch axes");
     }
-    CheckStatus(nert_hip_matmul_f32(ap, bp, yp, m, n, k, static_cast<int>(cd.size()), cd.data(), ca.data(), cb.data(),
-                                    Stream()),
+    CheckStatus(nert_hip_matmul_fused_f32(ap, bp, bias, yp, m, n, k, static_cast<int>(cd.size()), cd.data(), ca.data(),
+                                          cb.data(), scale, act, act_params, Stream()),
                 context);
     AfterRow(outputs, context);
+}
+
+} // namespace
+
+void MatMul(const Node& node, const Views& inputs, const Views& outputs) {
+    const std::string context = "MatMul (node '" + node.name + "')";
+    if (inputs.size() != 2 || outputs.size() != 1) {
+        throw InferenceException(context + ": expected two inputs and one output");
+    }
+    MatMulCore(context, inputs[0], inputs[1], outputs[0], outputs, nullptr, 1.0f, 0, nullptr);
+}
+
+// Not a reference row: the runner's fusion of MatMul -> [Mul by a scalar]
+// -> [Add of a [N] bias] -> [Div, Erf, Add, Mul, Mul: the erf Gelu chain].
+// Inputs A, B, optional bias [N]; attributes alpha (the scalar, default 1),
+// activation "" or "Gelu" with gelu_div, gelu_add, gelu_mul (the chain's
+// constants). The epilogue rounds each step like the separate rows, so the
+// output is bit-identical to the unfused chain.
+void FusedMatMul(const Node& node, const Views& inputs, const Views& outputs) {
+    const std::string context = "FusedMatMul (node '" + node.name + "')";
+    if (inputs.size() < 2 || inputs.size() > 3 || outputs.size() != 1) {
+        throw InferenceException(context + ": expected two or three inputs and one output");
+    }
+    const TensorView& out = outputs[0];
+    const float* bias = nullptr;
+    if (inputs.size() == 3 && inputs[2].data != nullptr) {
+        const TensorView& c = inputs[2];
+        if (c.dtype != DataType::Float32 || c.dims.size() != 1 || out.dims.empty() || c.dims[0] != out.dims.back()) {
+            throw InferenceException(context + ": bias must be float32 [N]");
+        }
+        bias = static_cast<const float*>(c.data);
+    }
+    const float alpha = FloatAttrC(node, "alpha", 1.0f, context);
+    const std::string activation = StringAttr(node, "activation", "", "FusedMatMul");
+    float params[3] = {0.0f, 0.0f, 0.0f};
+    int act = 0;
+    if (activation == "Gelu") {
+        act = 1;
+        params[0] = FloatAttrC(node, "gelu_div", 0.0f, context);
+        params[1] = FloatAttrC(node, "gelu_add", 0.0f, context);
+        params[2] = FloatAttrC(node, "gelu_mul", 0.0f, context);
+    } else if (!activation.empty()) {
+        throw InferenceException(context + ": unsupported activation '" + activation + "'");
+    }
+    MatMulCore(context, inputs[0], inputs[1], out, outputs, bias, alpha, act, params);
 }
 
 namespace {

@@ -18,6 +18,7 @@ nert::KernelFn FindRow(const std::string& op_type) {
         {"MatMul", &MatMul},
         {"Conv", &Conv},
         {"FusedConv", &FusedConv},
+        {"FusedMatMul", &FusedMatMul},
         {"Relu", &Relu},
         {"Sigmoid", &Sigmoid},
         {"Tanh", &Tanh},

@@ -43,6 +43,24 @@ __device__ __forceinline__ auto MakeOperand(const float* base, int64_t row0, int
     }
 }
 
+// The epilogue of every GEMM kernel: alpha * acc, plus beta * bias, then the
+// optional Gelu chain, each operation rounded on its own (no contraction),
+// so a fused MatMul -> Mul -> Add -> Div/Erf/Add/Mul/Mul row reproduces the
+// separate rows' float results bit for bit. The division is IEEE (HIP's
+// default correctly rounded fp32 divide), as in the Div row, and erff is the
+// Erf row's function.
+__device__ __forceinline__ float FinishGemm(const GemmArgs& p, float acc, int64_t r, int64_t c) {
+    float value = __fmul_rn(p.alpha, acc);
+    if (p.has_bias) {
+        value = __fadd_rn(value, __fmul_rn(p.beta, p.bias[r * p.bias_sm + c * p.bias_sn]));
+    }
+    if (p.act == 1) {
+        const float e = __fadd_rn(erff(value / p.act_div), p.act_add);
+        value = __fmul_rn(__fmul_rn(value, e), p.act_mul);
+    }
+    return value;
+}
+
 template <class Shape, bool A_KCONTIG, bool B_NCONTIG>
 __global__ __launch_bounds__(Shape::kThreads) void GemmKernel(GemmArgs p) {
     __shared__ __attribute__((aligned(16))) float lds[2 * (Shape::kLdsA + Shape::kLdsB)];
@@ -114,11 +132,7 @@ __global__ __launch_bounds__(Shape::kThreads) void GemmKernel(GemmArgs p) {
         const int64_t gr = row0 + r;
         const int64_t gc = col0 + c;
         if (gr < p.m && gc < p.n) {
-            float value = p.alpha * v;
-            if (p.has_bias) {
-                value += p.beta * p.bias[gr * p.bias_sm + gc * p.bias_sn];
-            }
-            out[gr * p.n + gc] = value;
+            out[gr * p.n + gc] = FinishGemm(p, v, gr, gc);
         }
     });
 }
@@ -140,11 +154,7 @@ __global__ void SplitReduceKernel(GemmArgs p, int splits, int64_t batches, int v
             for (int s = 1; s < splits; ++s) {
                 sum += p.partial[s * total + i + v];
             }
-            float value = p.alpha * sum;
-            if (p.has_bias) {
-                value += p.beta * p.bias[r * p.bias_sm + (c + v) * p.bias_sn];
-            }
-            p.y[i + v] = value;
+            p.y[i + v] = FinishGemm(p, sum, r, c + v);
         }
     }
 }
@@ -211,11 +221,7 @@ __global__ __launch_bounds__(256) void SkinnyGemmKernel(GemmArgs p, int64_t k_sl
     for (int v = 0; v < 16; ++v) {
         const int64_t r = 8 * (v >> 2) + 4 * half + (v & 3);
         if (r < p.m && n_ok) {
-            float value = p.alpha * acc[v];
-            if (p.has_bias) {
-                value += p.beta * p.bias[r * p.bias_sm + n * p.bias_sn];
-            }
-            p.y[r * p.n + n] = value;
+            p.y[r * p.n + n] = FinishGemm(p, acc[v], r, n);
         }
     }
 }
@@ -335,8 +341,9 @@ void LaunchGemm(GemmArgs p, int64_t batches, hipStream_t stream) {
     const int fallback_shape = p.m <= 32 ? 2 : (TileCount<ShapeL>(p, batches) < 1024 ? 1 : 0);
     static std::mutex mu;
     static std::map<GemmKey, int> chosen;
-    const GemmKey key{p.m, p.n, p.k, batches, p.a_sk == 1, p.b_sn == 1, p.batch_rank, p.has_bias,
-                      p.bias_sm, p.bias_sn};
+    // The key leaves the epilogue out: a fused and an unfused call of the
+    // same product sum in the same order.
+    const GemmKey key{p.m, p.n, p.k, batches, p.a_sk == 1, p.b_sn == 1, p.batch_rank, 0, 0, 0};
     const size_t y_bytes = static_cast<size_t>(batches * p.m * p.n) * sizeof(float);
     // Candidates 0-11: tile shape x split count; 12: the skinny kernel.
     const bool skinny = SkinnyApplies(p, batches);
@@ -396,7 +403,18 @@ int nert_hip_gemm_f32(const float* a, const float* b, const float* c, float* y, 
 int nert_hip_matmul_f32(const float* a, const float* b, float* y, int64_t m, int64_t n, int64_t k, int batch_rank,
                         const int64_t* batch_dims, const int64_t* a_batch_strides, const int64_t* b_batch_strides,
                         void* stream) {
+    return nert_hip_matmul_fused_f32(a, b, nullptr, y, m, n, k, batch_rank, batch_dims, a_batch_strides,
+                                     b_batch_strides, 1.0f, 0, nullptr, stream);
+}
+
+int nert_hip_matmul_fused_f32(const float* a, const float* b, const float* bias, float* y, int64_t m, int64_t n,
+                              int64_t k, int batch_rank, const int64_t* batch_dims, const int64_t* a_batch_strides,
+                              const int64_t* b_batch_strides, float scale, int act, const float* act_params,
+                              void* stream) {
     return nert_hip::Guard([&] {
+        if (act != 0 && (act != 1 || act_params == nullptr)) {
+            throw nert_hip::Error("matmul: unknown activation");
+        }
         if (batch_rank < 0 || batch_rank > 4) {
             throw nert_hip::Error("matmul: at most four batch axes are supported");
         }
@@ -411,9 +429,18 @@ int nert_hip_matmul_f32(const float* a, const float* b, float* y, int64_t m, int
         p.a_sk = 1;
         p.b_sk = n;
         p.b_sn = 1;
-        p.alpha = 1.0f;
-        p.beta = 0.0f;
-        p.has_bias = 0;
+        p.alpha = scale;
+        p.beta = 1.0f;
+        p.has_bias = bias != nullptr ? 1 : 0;
+        p.bias = bias;
+        p.bias_sm = 0;
+        p.bias_sn = 1;
+        p.act = act;
+        if (act == 1) {
+            p.act_div = act_params[0];
+            p.act_add = act_params[1];
+            p.act_mul = act_params[2];
+        }
         p.batch_rank = batch_rank;
         int64_t batches = 1;
         for (int d = 0; d < batch_rank; ++d) {

@@ -24,6 +24,10 @@ struct GemmArgs {
     int64_t b_bs[4];
     int64_t k_per_split; // set by LaunchGemm
     float* partial;      // set by LaunchGemm
+    // Optional activation after the bias (fused MatMul rows): act 1 is the
+    // erf Gelu chain y -> y * (erf(y / act_div) + act_add) * act_mul.
+    int act;
+    float act_div, act_add, act_mul;
 };
 
 void LaunchGemm(GemmArgs p, int64_t batches, hipStream_t stream);

@@ -168,6 +168,126 @@ def fuse_conv_chains(g: Graph) -> Graph:
     return Graph(nodes=nodes, initializers=g.initializers, inputs=g.inputs, outputs=g.outputs, tensors=g.tensors)
 
 
+def _scalar(g: Graph, name: str) -> float | None:
+    """The value of a float32 scalar initializer (shape () or (1,)), else None."""
+    v = g.initializers.get(name)
+    if v is None or v.dtype != np.float32 or v.size != 1 or v.ndim > 1:
+        return None
+    return float(v.reshape(()))
+
+
+def fuse_matmul_chains(g: Graph) -> Graph:
+    """Rewrites MatMul -> [Mul by a scalar] -> [Add of a [N] bias] -> [erf
+    Gelu: Div by c1, Erf, Add c2, Mul by the pre-Gelu value, Mul by c3] into
+    one FusedMatMul node (alpha, bias and the Gelu constants in its epilogue).
+
+    Every intermediate must have exactly the consumers the pattern names and
+    not be a graph output; scalars and the bias must be float32 initializers.
+    The fused node sits where the chain's last node was. Its epilogue rounds
+    each step like the separate rows, so the outputs are bit-identical.
+    """
+    consumers: dict[str, list[int]] = {}
+    for idx, n in enumerate(g.nodes):
+        for t in n.inputs:
+            if t:
+                consumers.setdefault(t, []).append(idx)
+    outputs = set(g.outputs)
+
+    def sole(t: str) -> int | None:
+        c = consumers.get(t, [])
+        return c[0] if len(c) == 1 and t not in outputs else None
+
+    def other(n: Node, t: str) -> str | None:
+        if len(n.inputs) != 2:
+            return None
+        if n.inputs[0] == t:
+            return n.inputs[1]
+        return n.inputs[0] if n.inputs[1] == t else None
+
+    dropped: set[int] = set()
+    replace: dict[int, Node] = {}
+    for idx, n in enumerate(g.nodes):
+        if n.op != "MatMul" or idx in dropped or len(n.inputs) != 2:
+            continue
+        chain = [idx]
+        cur = n.outputs[0]
+        shape = g.tensors[cur][1]
+        attrs: dict[str, Any] = {}
+        bias = ""
+        nxt = sole(cur)
+        if nxt is not None and g.nodes[nxt].op == "Mul":
+            c = other(g.nodes[nxt], cur)
+            v = _scalar(g, c) if c else None
+            if v is not None and g.tensors[g.nodes[nxt].outputs[0]][1] == shape:
+                attrs["alpha"] = v
+                chain.append(nxt)
+                cur = g.nodes[nxt].outputs[0]
+                nxt = sole(cur)
+        if nxt is not None and g.nodes[nxt].op == "Add":
+            c = other(g.nodes[nxt], cur)
+            init = g.initializers.get(c) if c else None
+            if (init is not None and init.dtype == np.float32 and init.shape == (shape[-1],)
+                    and g.tensors[g.nodes[nxt].outputs[0]][1] == shape):
+                bias = c
+                chain.append(nxt)
+                cur = g.nodes[nxt].outputs[0]
+        gelu = _match_gelu(g, cur, consumers, outputs, other)
+        if gelu is not None:
+            nodes, consts = gelu
+            attrs.update({"activation": "Gelu", "gelu_div": consts[0], "gelu_add": consts[1], "gelu_mul": consts[2]})
+            chain.extend(nodes)
+            cur = g.nodes[nodes[-1]].outputs[0]
+        if len(chain) == 1:
+            continue
+        last = max(chain)
+        for i in chain:
+            dropped.add(i)
+        dropped.discard(last)
+        replace[last] = Node("FusedMatMul", [n.inputs[0], n.inputs[1]] + ([bias] if bias else []), [cur], attrs,
+                             n.name)
+    nodes = [replace.get(i, nd) for i, nd in enumerate(g.nodes) if i not in dropped or i in replace]
+    return Graph(nodes=nodes, initializers=g.initializers, inputs=g.inputs, outputs=g.outputs, tensors=g.tensors)
+
+
+def _match_gelu(g: Graph, v: str, consumers, outputs, other):
+    """Div(v, c1) -> Erf -> Add(., c2) -> Mul(v, .) -> Mul(., c3) with v
+    consumed only by the Div and the first Mul; returns (node indices,
+    (c1, c2, c3)) or None."""
+    cons = consumers.get(v, [])
+    if v in outputs or len(cons) != 2:
+        return None
+    div = next((i for i in cons if g.nodes[i].op == "Div" and g.nodes[i].inputs[0] == v), None)
+    if div is None:
+        return None
+    c1 = _scalar(g, g.nodes[div].inputs[1])
+
+    def only(t):
+        c = consumers.get(t, [])
+        return c[0] if len(c) == 1 and t not in outputs else None
+
+    erf = only(g.nodes[div].outputs[0])
+    if c1 is None or erf is None or g.nodes[erf].op != "Erf":
+        return None
+    add = only(g.nodes[erf].outputs[0])
+    if add is None or g.nodes[add].op != "Add":
+        return None
+    c2n = other(g.nodes[add], g.nodes[erf].outputs[0])
+    c2 = _scalar(g, c2n) if c2n else None
+    mul1 = only(g.nodes[add].outputs[0])
+    if c2 is None or mul1 is None or g.nodes[mul1].op != "Mul" or mul1 not in cons:
+        return None
+    if other(g.nodes[mul1], g.nodes[add].outputs[0]) != v:
+        return None
+    mul2 = only(g.nodes[mul1].outputs[0])
+    if mul2 is None or g.nodes[mul2].op != "Mul":
+        return None
+    c3n = other(g.nodes[mul2], g.nodes[mul1].outputs[0])
+    c3 = _scalar(g, c3n) if c3n else None
+    if c3 is None:
+        return None
+    return [div, erf, add, mul1, mul2], (c1, c2, c3)
+
+
 class _PackedNode:
     __slots__ = ("op", "name", "attrs", "ins", "outs", "err")
 
@@ -183,7 +303,7 @@ class _PackedNode:
 class Program:
     def __init__(self, g: Graph, fuse: bool = True, views: bool = True):
         if fuse:
-            g = fuse_conv_chains(g)
+            g = fuse_matmul_chains(fuse_conv_chains(g))
         self.alias: dict[str, str] = {}
         if views:
             g, self.alias = alias_views(g)

@@ -269,6 +269,48 @@ def test_fused_conv_bit_identical(gpu, xs, ws, attrs, with_z):
             np.maximum(ref, 0).astype(F), what="FusedConv vs reference")
 
 
+@pytest.mark.parametrize("ashape,n,alpha,bias,gelu", [
+    ((2, 197, 64), 96, None, True, False),     # projection + bias
+    ((2, 197, 64), 96, None, True, True),      # fc1 + bias + Gelu
+    ((3, 4, 33, 16), 33, 0.125, False, False), # scaled attention scores
+    ((5, 40), 24, 2.0, True, True),
+])
+def test_fused_matmul_bit_identical(gpu, ashape, n, alpha, bias, gelu):
+    """FusedMatMul == MatMul, Mul(alpha), Add(bias), Div/Erf/Add/Mul/Mul rows."""
+    a = randn(ashape, seed=60)
+    w = randn((ashape[-1], n), seed=61, scale=0.2)
+    b = randn((n,), seed=62)
+    out = ashape[:-1] + (n,)
+    y = _hip("MatMul", [a, w], out)
+    if alpha is not None:
+        y = _hip("Mul", [y, np.array(alpha, F)], out)
+    if bias:
+        y = _hip("Add", [y, b], out)
+    attrs = {}
+    if alpha is not None:
+        attrs["alpha"] = alpha
+    if gelu:
+        c1, c2, c3 = np.float32(np.sqrt(2.0)), np.float32(1.0), np.float32(0.5)
+        e = _hip("Erf", [_hip("Div", [y, np.array(c1, F)], out)], out)
+        e = _hip("Add", [e, np.array(c2, F)], out)
+        y = _hip("Mul", [_hip("Mul", [y, e], out), np.array(c3, F)], out)
+        attrs.update({"activation": "Gelu", "gelu_div": float(c1), "gelu_add": float(c2), "gelu_mul": float(c3)})
+    got = _hip("FusedMatMul", [a, w] + ([b] if bias else []), out, attrs)
+    assert np.array_equal(got, y)
+
+
+def test_fused_matmul_errors(gpu):
+    from nert_amd.device import NertError
+
+    a, w = randn((4, 8)), randn((8, 6))
+    with pytest.raises(NertError, match=r"FusedMatMul \(node 'n'\): unsupported activation 'Tanh'"):
+        _hip("FusedMatMul", [a, w], (4, 6), {"activation": "Tanh"})
+    with pytest.raises(NertError, match=r"FusedMatMul \(node 'n'\): bias must be float32 \[N\]"):
+        _hip("FusedMatMul", [a, w, randn((5,))], (4, 6))
+    with pytest.raises(NertError, match=r"FusedMatMul \(node 'n'\): output shape does not match the operands"):
+        _hip("FusedMatMul", [a, w], (4, 7))
+
+
 def test_fused_conv_errors(gpu):
     from nert_amd.device import NertError
 

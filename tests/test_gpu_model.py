@@ -96,6 +96,21 @@ def test_reference_executor_on_hipdevice(resnet):
     compare(got, want, rtol=RTOL, atol=RTOL, what="drop-in logits")
 
 
+def test_fused_vit_program_is_bit_identical(gpu):
+    """The MatMul+scale+bias+Gelu fusion and the view aliasing change no
+    output bit (ViT-B/16, two layers, batch 2)."""
+    g, inputs = workloads.vit_b16(batch=2, layers=2)
+    outs = []
+    for fuse, views in ((False, False), (True, True)):
+        prog = Program(g, fuse=fuse, views=views)
+        prog.set_input("input", inputs["input"])
+        prog.run()
+        outs.append(prog.output(g.outputs[0]))
+        prog.close()
+    assert sum(1 for n in Program(g).graph.nodes if n.op == "FusedMatMul") == 10
+    assert np.array_equal(outs[0], outs[1])
+
+
 def test_fused_program_is_bit_identical(gpu):
     """The runner's Conv+Add+Relu fusion changes no output bit (batch 2)."""
     g, inputs = workloads.resnet18(batch=2)

@@ -119,3 +119,41 @@ def _valid_order_with(g, alias):
             assert not t or alias.get(t, t) in avail or t in avail, (n.op, t)
         avail.update(n.outputs)
         avail.update(v for v, o in alias.items() if o in avail)
+
+
+def test_vit_matmul_fusion():
+    from nert_amd.runner import fuse_matmul_chains
+
+    g, _ = workloads.vit_b16(batch=2, layers=2)
+    f = fuse_matmul_chains(g)
+    fused = [n for n in f.nodes if n.op == "FusedMatMul"]
+    # per layer: QKV + bias, QK^T * 1/8, projection + bias, fc1 + bias + Gelu, fc2 + bias
+    assert len(fused) == 10
+    assert sum(1 for n in fused if n.attrs.get("activation") == "Gelu") == 2
+    assert sum(1 for n in fused if n.attrs.get("alpha") == 0.125) == 2
+    assert not any(n.op in ("Erf", "Div") for n in f.nodes)
+    assert [n.op for n in f.nodes].count("MatMul") == 2  # A.V stays plain
+    _valid_order(f)
+
+
+def test_matmul_fusion_rules():
+    from nert_amd.runner import fuse_matmul_chains
+
+    def chain(extra=False, bias_shape=(6,)):
+        g = Graph()
+        a = g.add_input("a", F, (4, 8))
+        w = g.add_initializer("w", np.ones((8, 6), F))
+        b = g.add_initializer("b", np.ones(bias_shape, F))
+        y = g.add_node("MatMul", [a, w], [("y", F, (4, 6))])[0]
+        z = g.add_node("Add", [y, b], [("z", F, (4, 6))])[0]
+        g.outputs = [z]
+        if extra:
+            g.add_node("Relu", [y], [("r", F, (4, 6))])
+            g.outputs.append("r")
+        return g
+
+    assert [n.op for n in fuse_matmul_chains(chain()).nodes] == ["FusedMatMul"]
+    # the MatMul output has a second consumer: nothing fuses
+    assert [n.op for n in fuse_matmul_chains(chain(extra=True)).nodes] == ["MatMul", "Add", "Relu"]
+    # a bias that is not [N] stays a separate Add
+    assert [n.op for n in fuse_matmul_chains(chain(bias_shape=(4, 6))).nodes] == ["MatMul", "Add"]
