@@ -13,7 +13,9 @@ alignment, so intermediates whose lifetimes do not overlap share memory and
 the working set stays small enough to live in the 256 MB Infinity Cache where
 possible. Rows that only reinterpret a dense buffer's shape (Reshape, Flatten,
 Squeeze, Unsqueeze, Identity) become views: their output shares the input's
-arena block for the union of both lifetimes, and no copy is queued.
+arena block for the union of both lifetimes, and no copy is queued. So do the
+outputs of a Split whose parts are contiguous slabs of its input (every axis
+before the split axis has extent 1): each part is the input at a byte offset.
 """
 
 from __future__ import annotations
@@ -33,51 +35,70 @@ ALIGN = 256
 VIEW_OPS = {"Reshape", "Flatten", "Squeeze", "Unsqueeze", "Identity"}
 
 
-def alias_views(g: Graph) -> tuple[Graph, dict[str, str]]:
-    """Drops view rows whose output can share the input's buffer.
+def alias_views(g: Graph) -> tuple[Graph, dict[str, tuple[str, int]]]:
+    """Drops view rows whose outputs can share the input's buffer.
 
     A row qualifies when its first input is an intermediate (produced by a
-    node, not a graph input or initializer), neither tensor is a graph output,
-    and dtype and element count agree (a dense row-major buffer reads the same
-    under either shape). Returns the graph without those rows and a map from
-    each aliased output to the tensor that owns the storage.
+    node, not a graph input or initializer) and none of the tensors involved
+    is a graph output: a shape-only row whose dtype and element count agree
+    (a dense row-major buffer reads the same under either shape), or a Split
+    along an axis preceded only by unit axes (each part is a contiguous slab).
+    Returns the graph without those rows and a map from each aliased output
+    to (the tensor that owns the storage, byte offset into it).
     """
     produced = {t for n in g.nodes for t in n.outputs}
     outputs = set(g.outputs)
-    alias: dict[str, str] = {}
+    alias: dict[str, tuple[str, int]] = {}
     kept: list[Node] = []
+
+    def owner_of(x: str) -> tuple[str, int]:
+        return alias.get(x, (x, 0))
+
     for n in g.nodes:
-        if n.op in VIEW_OPS and n.inputs and n.inputs[0] and len(n.outputs) == 1:
-            x, y = n.inputs[0], n.outputs[0]
-            root = alias.get(x, x)
+        x = n.inputs[0] if n.inputs else ""
+        ok_input = bool(x) and x in produced and x not in g.initializers and x not in g.inputs and x not in outputs
+        if ok_input and n.op in VIEW_OPS and len(n.outputs) == 1:
+            y = n.outputs[0]
             (xd, xs), (yd, ys) = g.tensors[x], g.tensors[y]
-            if (x in produced and x not in g.initializers and x not in g.inputs and x not in outputs
-                    and y not in outputs and np.dtype(xd) == np.dtype(yd)
-                    and int(np.prod(xs)) == int(np.prod(ys))):
-                alias[y] = root
+            if y not in outputs and np.dtype(xd) == np.dtype(yd) and int(np.prod(xs)) == int(np.prod(ys)):
+                alias[y] = owner_of(x)
+                continue
+        if ok_input and n.op == "Split" and not any(o in outputs for o in n.outputs):
+            xd, xs = g.tensors[x]
+            axis = int(n.attrs.get("axis", 0)) % max(len(xs), 1)
+            parts = [g.tensors[o][1] for o in n.outputs]
+            contiguous = int(np.prod(xs[:axis])) == 1 and all(
+                np.dtype(g.tensors[o][0]) == np.dtype(xd) and len(sh) == len(xs) for o, sh in zip(n.outputs, parts))
+            if contiguous and sum(sh[axis] for sh in parts) == xs[axis]:
+                inner = int(np.prod(xs[axis + 1:])) * np.dtype(xd).itemsize
+                owner, base = owner_of(x)
+                pos = 0
+                for o, sh in zip(n.outputs, parts):
+                    alias[o] = (owner, base + pos * inner)
+                    pos += sh[axis]
                 continue
         kept.append(n)
     return (Graph(nodes=kept, initializers=g.initializers, inputs=g.inputs, outputs=g.outputs, tensors=g.tensors),
             alias)
 
 
-def plan_arena(g: Graph, alias: dict[str, str] | None = None) -> tuple[dict[str, int], int]:
+def plan_arena(g: Graph, alias: dict[str, tuple[str, int]] | None = None) -> tuple[dict[str, int], int]:
     """Offsets for every node output that is not a graph input/initializer;
-    aliased tensors get their owner's offset, and the owner stays live until
-    the last use of any of its views."""
+    an aliased tensor gets its owner's offset plus its byte offset, and the
+    owner stays live until the last use of any of its views."""
     alias = alias or {}
     produced: dict[str, int] = {}
     last_use: dict[str, int] = {}
     for idx, n in enumerate(g.nodes):
         for t in n.inputs:
             if t:
-                last_use[alias.get(t, t)] = idx
+                last_use[alias.get(t, (t, 0))[0]] = idx
         for t in n.outputs:
             produced.setdefault(t, idx)
             last_use.setdefault(t, idx)
     end = len(g.nodes)
     for t in g.outputs:
-        last_use[alias.get(t, t)] = end
+        last_use[alias.get(t, (t, 0))[0]] = end
     live: list[tuple[int, int, int]] = []  # (offset, size, last_use)
     offsets: dict[str, int] = {}
     arena = 0
@@ -96,9 +117,9 @@ def plan_arena(g: Graph, alias: dict[str, str] | None = None) -> tuple[dict[str,
         offsets[t] = cursor
         live.append((cursor, size, last_use[t]))
         arena = max(arena, cursor + size)
-    for view, owner in alias.items():
+    for view, (owner, byte_offset) in alias.items():
         if owner in offsets:
-            offsets[view] = offsets[owner]
+            offsets[view] = offsets[owner] + byte_offset
     return offsets, arena
 
 
@@ -304,7 +325,7 @@ class Program:
     def __init__(self, g: Graph, fuse: bool = True, views: bool = True):
         if fuse:
             g = fuse_matmul_chains(fuse_conv_chains(g))
-        self.alias: dict[str, str] = {}
+        self.alias: dict[str, tuple[str, int]] = {}
         if views:
             g, self.alias = alias_views(g)
         self.graph = g
