@@ -306,11 +306,18 @@ __global__ __launch_bounds__(256) void SoftmaxRowsRegKernel(const float* __restr
     }
     const float* p = x + row * dim;
     float* q = y + row * dim;
+    // Loads from clamped (always valid) addresses, then a select: every
+    // load of the row is in flight at once instead of one guarded load
+    // (and one memory round trip) after another.
     float v[PER];
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
         const int i = lane + 64 * k;
-        v[k] = i < dim ? p[i] : -__builtin_huge_valf();
+        v[k] = p[i < dim ? i : dim - 1];
+    }
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        v[k] = lane + 64 * k < dim ? v[k] : -__builtin_huge_valf();
     }
     // Peak rule of the reference (value > peak from element 0): see
     // SoftmaxRowsKernel.
@@ -425,12 +432,17 @@ __global__ __launch_bounds__(256) void LayerNormRegKernel(const float* __restric
     }
     const float* p = x + row * inner;
     float* q = y + row * inner;
+    // Clamped-address loads, then a select (see SoftmaxRowsRegKernel).
     float v[PER];
-    double sum = 0.0;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
         const int i = lane + 64 * k;
-        v[k] = i < inner ? p[i] : 0.0f;
+        v[k] = p[i < inner ? i : inner - 1];
+    }
+    double sum = 0.0;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        v[k] = lane + 64 * k < inner ? v[k] : 0.0f;
         sum += static_cast<double>(v[k]);
     }
     const double mean = WaveAllSum(sum) / static_cast<double>(inner);
@@ -443,14 +455,21 @@ __global__ __launch_bounds__(256) void LayerNormRegKernel(const float* __restric
         }
     }
     const double inv = 1.0 / sqrt(WaveAllSum(sq) / static_cast<double>(inner) + eps);
+    float sc[PER];
+    float bi[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = lane + 64 * k;
+        const int ic = i < inner ? i : inner - 1;
+        sc[k] = scale[scale_scalar ? 0 : ic];
+        bi[k] = bias != nullptr ? bias[bias_scalar ? 0 : ic] : 0.0f;
+    }
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
         const int i = lane + 64 * k;
         if (i < inner) {
-            const double scaled =
-                (static_cast<double>(v[k]) - mean) * inv * static_cast<double>(scale[scale_scalar ? 0 : i]);
-            q[i] = static_cast<float>(bias != nullptr ? scaled + static_cast<double>(bias[bias_scalar ? 0 : i])
-                                                      : scaled);
+            const double scaled = (static_cast<double>(v[k]) - mean) * inv * static_cast<double>(sc[k]);
+            q[i] = static_cast<float>(bias != nullptr ? scaled + static_cast<double>(bi[k]) : scaled);
         }
     }
     if (lane == 0) {
