@@ -49,16 +49,65 @@ __device__ __forceinline__ auto MakeOperand(const float* base, int64_t row0, int
 // separate rows' float results bit for bit. The division is IEEE (HIP's
 // default correctly rounded fp32 divide), as in the Div row, and erff is the
 // Erf row's function.
-__device__ __forceinline__ float FinishGemm(const GemmArgs& p, float acc, int64_t r, int64_t c) {
+__device__ __forceinline__ float FinishWith(const GemmArgs& p, float acc, float bias) {
     float value = __fmul_rn(p.alpha, acc);
     if (p.has_bias) {
-        value = __fadd_rn(value, __fmul_rn(p.beta, p.bias[r * p.bias_sm + c * p.bias_sn]));
+        value = __fadd_rn(value, __fmul_rn(p.beta, bias));
     }
     if (p.act == 1) {
         const float e = __fadd_rn(erff(value / p.act_div), p.act_add);
         value = __fmul_rn(__fmul_rn(value, e), p.act_mul);
     }
     return value;
+}
+
+__device__ __forceinline__ float FinishGemm(const GemmArgs& p, float acc, int64_t r, int64_t c) {
+    return FinishWith(p, acc, p.has_bias ? p.bias[r * p.bias_sm + c * p.bias_sn] : 0.0f);
+}
+
+// Writes a workgroup's accumulators: raw partial sums (finish = false) or
+// finished outputs. Per 32x32 block, every bias load comes from a clamped,
+// always-valid address and all sixteen addresses are formed before the first
+// store, so the loads and stores of a lane are in flight together instead
+// of one guarded access and one wait after another.
+template <class Shape>
+__device__ __forceinline__ void GemmEpilogue(const GemmArgs& p, const Accum<Shape>& acc, float* out, int64_t row0,
+                                             int64_t col0, bool finish) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wave_m = wave % Shape::kWavesM;
+    const int wave_n = wave / Shape::kWavesM;
+    const int half = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < Shape::kSubN; ++j) {
+        const int64_t gc = col0 + wave_n * Shape::kWaveN + 32 * j + (lane & 31);
+        const bool col_ok = gc < p.n;
+        const int64_t cc = col_ok ? gc : 0;
+#pragma unroll
+        for (int i = 0; i < Shape::kSubM; ++i) {
+            const int64_t r0 = row0 + wave_m * Shape::kWaveM + 32 * i + 4 * half;
+            float* base = out + r0 * p.n + cc;
+            float value[16];
+            bool ok[16];
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int64_t r = r0 + 8 * (v >> 2) + (v & 3);
+                ok[v] = col_ok && r < p.m;
+                float bias = 0.0f;
+                if (finish && p.has_bias) {
+                    const int64_t rr = r < p.m ? r : p.m - 1;
+                    bias = p.bias[rr * p.bias_sm + cc * p.bias_sn];
+                }
+                value[v] = finish ? FinishWith(p, acc.c[i][j][v], bias) : acc.c[i][j][v];
+            }
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                if (ok[v]) {
+                    base[(8 * (v >> 2) + (v & 3)) * p.n] = value[v];
+                }
+            }
+        }
+    }
 }
 
 template <class Shape, bool A_KCONTIG, bool B_NCONTIG>
@@ -117,24 +166,11 @@ __global__ __launch_bounds__(Shape::kThreads) void GemmKernel(GemmArgs p) {
 
     const int64_t plane = p.m * p.n;
     if (p.partial != nullptr) {
-        float* out = p.partial + (static_cast<int64_t>(split) * gridDim.y + batch) * plane;
-        ForEachAccum<Shape>(acc, [&](int r, int c, float v) {
-            const int64_t gr = row0 + r;
-            const int64_t gc = col0 + c;
-            if (gr < p.m && gc < p.n) {
-                out[gr * p.n + gc] = v;
-            }
-        });
+        GemmEpilogue<Shape>(p, acc, p.partial + (static_cast<int64_t>(split) * gridDim.y + batch) * plane, row0, col0,
+                            false);
         return;
     }
-    float* out = p.y + batch * plane;
-    ForEachAccum<Shape>(acc, [&](int r, int c, float v) {
-        const int64_t gr = row0 + r;
-        const int64_t gc = col0 + c;
-        if (gr < p.m && gc < p.n) {
-            out[gr * p.n + gc] = FinishGemm(p, v, gr, gc);
-        }
-    });
+    GemmEpilogue<Shape>(p, acc, p.y + batch * plane, row0, col0, true);
 }
 
 // Sums the split-K partials in split order (deterministic) and applies the
