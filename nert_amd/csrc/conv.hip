@@ -21,6 +21,8 @@
 // skip the gather and run as a batched GEMM on the same engine.
 
 #include <array>
+#include <cmath>
+#include <cstdlib>
 #include <map>
 #include <mutex>
 
@@ -605,6 +607,14 @@ struct HaloGeom {
     FastDiv div_pw;        // by pw
     FastDiv div_rows_full; // by the patch rows of a whole image
     int32_t rows_full;
+    // Tail split (group 1 only): workgroups 0 .. n_full-1 take tiles whole;
+    // the remaining tiles are cut into tail_pieces channel ranges of
+    // tail_bps blocks, one workgroup each, whose partial sums go to
+    // tail_partial[piece][BM][BN] for ConvTailReduceKernel.
+    int32_t n_full;
+    int32_t tail_pieces;
+    int32_t tail_bps;
+    float* tail_partial;
 };
 
 // Register budget: 128 VGPRs (four waves per SIMD, two workgroups per CU),
@@ -631,12 +641,20 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
     const int wave_n = wave / Shape::kWavesM;
     const int half = lane >> 5;
     const int64_t tiles_m = (p.mg + BM - 1) / BM;
-    const int64_t row0 = (blockIdx.x % tiles_m) * BM;
-    const int64_t col0 = (blockIdx.x / tiles_m) * BN;
+    int64_t tile = blockIdx.x;
     const int g = blockIdx.y;
     const int split = blockIdx.z;
-    const int cb_begin = split * h.blocks_per_split;
-    const int cb_end = min(cb_begin + h.blocks_per_split, h.blocks);
+    int cb_begin = split * h.blocks_per_split;
+    int cb_end = min(cb_begin + h.blocks_per_split, h.blocks);
+    int piece = -1; // >= 0: this workgroup computes a tail piece
+    if (h.tail_pieces > 0 && tile >= h.n_full) {
+        piece = static_cast<int>(tile - h.n_full);
+        tile = h.n_full + piece / h.tail_pieces;
+        cb_begin = (piece % h.tail_pieces) * h.tail_bps;
+        cb_end = min(cb_begin + h.tail_bps, h.blocks);
+    }
+    const int64_t row0 = (tile % tiles_m) * BM;
+    const int64_t col0 = (tile / tiles_m) * BN;
 
     // The tile's first and last pixels: image and output row of each.
     uint32_t rem;
@@ -825,7 +843,45 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
         }
         __syncthreads();
     }
+    if (piece >= 0) {
+        float* out = h.tail_partial + static_cast<int64_t>(piece) * BM * BN;
+        ForEachAccum<Shape>(acc, [&](int r, int c, float v) { out[r * BN + c] = v; });
+        return;
+    }
     ConvEpilogue<Shape>(p, acc, row0, col0, g, split);
+}
+
+// Sums each tail tile's pieces in piece order (deterministic) and applies the
+// epilogue the other workgroups apply (group 1).
+__global__ void ConvTailReduceKernel(ConvArgs p, int n_full, int pieces, int bm, int bn, const float* partial,
+                                     int64_t tail_tiles) {
+    const int64_t tiles_m = (p.mg + bm - 1) / bm;
+    const int64_t per_tile = static_cast<int64_t>(bm) * bn;
+    const int64_t total = tail_tiles * per_tile;
+    for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < total;
+         e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t t = e / per_tile;
+        const int64_t rc = e - t * per_tile;
+        const int64_t r = rc / bn;
+        const int64_t c = rc - r * bn;
+        const int64_t tile = n_full + t;
+        const int64_t gr = (tile % tiles_m) * bm + r;
+        const int64_t gc = (tile / tiles_m) * bn + c;
+        if (gr >= p.mg || gc >= p.n_total) {
+            continue;
+        }
+        const float* src = partial + t * pieces * per_tile + rc;
+        float v = src[0];
+        for (int q = 1; q < pieces; ++q) {
+            v += src[q * per_tile];
+        }
+        const int64_t b = gc / p.plane_out;
+        const int64_t yi = (b * p.m + gr) * p.plane_out + (gc - b * p.plane_out);
+        if (p.bias != nullptr) {
+            v = v + p.bias[gr];
+        }
+        p.y[yi] = Finish(p, v, yi);
+    }
 }
 
 // Tile shapes. Which one (and which split-K count) is fastest depends on how
@@ -845,8 +901,24 @@ void LaunchHalo(const ConvArgs& p, const HaloGeom& h, dim3 grid, size_t lds, hip
 // 3x3, 2-D, C_g a multiple of kHaloBK, stride no larger than the filter's
 // extent, everything addressable with 32-bit offsets, and one workgroup's
 // patch and weights within kHaloMaxLds.
+// A split-K count (up to 8) under which the workgroup count fills whole
+// rounds of 256 CUs best: the smallest s minimising ceil(T*s/256)/(T*s/256).
+inline int BalancedSplits(int64_t tiles, int blocks) {
+    int best = 1;
+    double best_loss = 1e30;
+    for (int s = 1; s <= std::min(8, blocks); ++s) {
+        const double units = static_cast<double>(tiles * s) / 256.0;
+        const double loss = std::ceil(units) / units;
+        if (loss < best_loss - 1e-9) {
+            best_loss = loss;
+            best = s;
+        }
+    }
+    return best;
+}
+
 template <class Shape>
-bool TryHaloShape(ConvArgs p, hipStream_t stream, int force_splits) {
+bool TryHaloShape(ConvArgs p, hipStream_t stream, int force_splits, bool tail = false) {
     constexpr int kTaps = 9;
     HaloGeom h{};
     h.pw = (p.out_w - 1) * p.s_w + 2 * p.d_w + 1;
@@ -872,8 +944,43 @@ bool TryHaloShape(ConvArgs p, hipStream_t stream, int force_splits) {
     h.div_pw = FastDiv::Make(static_cast<uint32_t>(h.pw));
     h.div_rows_full = FastDiv::Make(static_cast<uint32_t>(h.rows_full));
     const int64_t tiles = ((p.mg + Shape::kBM - 1) / Shape::kBM) * ((p.n_total + Shape::kBN - 1) / Shape::kBN);
-    const int splits = force_splits > 0 ? std::min(force_splits, static_cast<int>(h.blocks))
-                                        : PlanSplits(tiles * p.group, h.blocks, kResidentBlocks, 4);
+    if (tail) {
+        // Whole rounds of one tile per CU run whole; the rest is cut along
+        // the channel blocks into about one piece per CU.
+        constexpr int64_t kCUs = 256;
+        const int64_t rest = tiles % kCUs;
+        const int64_t n_full = tiles - rest;
+        if (p.group != 1 || n_full == 0 || rest == 0) {
+            return false;
+        }
+        const int pieces = static_cast<int>(std::min<int64_t>(h.blocks, std::max<int64_t>(2, kCUs / rest)));
+        h.tail_bps = (h.blocks + pieces - 1) / pieces;
+        h.tail_pieces = (h.blocks + h.tail_bps - 1) / h.tail_bps;
+        h.n_full = static_cast<int32_t>(n_full);
+        h.blocks_per_split = h.blocks;
+        const int64_t per_tile = static_cast<int64_t>(Shape::kBM) * Shape::kBN;
+        h.tail_partial = static_cast<float*>(
+            Workspace(rest * h.tail_pieces * per_tile * static_cast<int64_t>(sizeof(float)), stream));
+        p.k_per_split = 0;
+        p.partial = nullptr;
+        const dim3 grid(static_cast<unsigned>(n_full + rest * h.tail_pieces), 1, 1);
+        if (per_thread == 1) {
+            LaunchHalo<Shape, 1>(p, h, grid, static_cast<size_t>(lds), stream);
+        } else if (per_thread == 2) {
+            LaunchHalo<Shape, 2>(p, h, grid, static_cast<size_t>(lds), stream);
+        } else {
+            LaunchHalo<Shape, 4>(p, h, grid, static_cast<size_t>(lds), stream);
+        }
+        CheckLaunch("HaloConvKernel launch");
+        ConvTailReduceKernel<<<GridFor(rest * per_tile, 256, 4096), 256, 0, stream>>>(
+            p, h.n_full, h.tail_pieces, Shape::kBM, Shape::kBN, h.tail_partial, rest);
+        CheckLaunch("ConvTailReduceKernel launch");
+        return true;
+    }
+    // force_splits: > 0 a count, 0 PlanSplits' choice, -1 the balanced count.
+    const int splits = force_splits > 0    ? std::min(force_splits, static_cast<int>(h.blocks))
+                       : force_splits == 0 ? PlanSplits(tiles * p.group, h.blocks, kResidentBlocks, 4)
+                                           : BalancedSplits(tiles * p.group, h.blocks);
     h.blocks_per_split = (h.blocks + splits - 1) / splits;
     p.k_per_split = 0;
     p.partial = nullptr;
@@ -932,11 +1039,36 @@ int ChooseConvConfig(std::map<ConvKey, int>& cache, const ConvArgs& p, hipStream
 }
 
 // 3x3 candidates: tile shape i / 4 (0 W, 1 M, 2 Q, 3 N) with split-K count
-// {PlanSplits' choice, 1, 2, 4}[i % 4].
-constexpr int kHaloCandidates = 16;
+// {PlanSplits' choice, 1, 2, 4}[i % 4]; 16 + s: shape s with the tail split;
+// 20 + s: shape s with the balanced split count.
+constexpr int kHaloCandidates = 24;
 
 bool LaunchHaloCandidate(int i, const ConvArgs& p, hipStream_t stream) {
     static constexpr int kSplits[4] = {0, 1, 2, 4};
+    if (i >= 20) {
+        switch (i - 20) {
+        case 0:
+            return p.mg <= 64 && TryHaloShape<HaloShapeW>(p, stream, -1);
+        case 1:
+            return TryHaloShape<HaloShapeM>(p, stream, -1);
+        case 2:
+            return TryHaloShape<HaloShapeQ>(p, stream, -1);
+        default:
+            return TryHaloShape<HaloShapeN>(p, stream, -1);
+        }
+    }
+    if (i >= 16) {
+        switch (i - 16) {
+        case 0:
+            return p.mg <= 64 && TryHaloShape<HaloShapeW>(p, stream, 0, true);
+        case 1:
+            return TryHaloShape<HaloShapeM>(p, stream, 0, true);
+        case 2:
+            return TryHaloShape<HaloShapeQ>(p, stream, 0, true);
+        default:
+            return TryHaloShape<HaloShapeN>(p, stream, 0, true);
+        }
+    }
     const int splits = kSplits[i % 4];
     switch (i / 4) {
     case 0:
@@ -956,6 +1088,14 @@ bool TryHaloConv(const ConvArgs& p, hipStream_t stream) {
     }
     static std::map<ConvKey, int> chosen;
     const int fallback = p.mg <= 64 ? 0 : 4; // 64x256 tiles for M_g <= 64, else 64x128
+    // NERT_HIP_CONV_CANDIDATE=i forces candidate i wherever it fits (tests
+    // of every configuration use it); otherwise the per-geometry choice.
+    if (const char* forced = std::getenv("NERT_HIP_CONV_CANDIDATE")) {
+        const int i = std::atoi(forced);
+        if (i >= 0 && i < kHaloCandidates && LaunchHaloCandidate(i, p, stream)) {
+            return true;
+        }
+    }
     const int c = ChooseConvConfig(chosen, p, stream, kHaloCandidates, fallback, LaunchHaloCandidate);
     // Whether a candidate fits depends on the geometry alone, so a cached
     // choice fits; the default is tried next only as a safeguard.

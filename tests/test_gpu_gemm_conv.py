@@ -357,3 +357,51 @@ def test_small_channel_conv_nonfinite_inputs(gpu):
     w, b = randn((64, 3, 7, 7), seed=54), randn((64,), seed=55)
     attrs = {"pads": [3, 3, 3, 3], "strides": [2, 2]}
     assert_parity("Conv", [x, w, b], [(_conv_out(x.shape, w.shape, attrs), F)], attrs)
+
+
+# --- every 3x3 configuration, forced ----------------------------------------
+
+_FORCED = r"""
+import json, sys
+import numpy as np
+sys.path.insert(0, {root!r})
+from nert_amd.device import DeviceArray, run_node
+x = np.load({x!r}); w = np.load({w!r}); b = np.load({b!r}); z = np.load({z!r})
+def hip(op, ins, shape, attrs):
+    dev = [DeviceArray.from_host(a) for a in ins]
+    out = DeviceArray(shape, np.float32)
+    run_node(op, dev, [out], attrs)
+    return out.to_host()
+a = {{"pads": [1, 1, 1, 1]}}
+np.save({out1!r}, hip("Conv", [x, w, b], z.shape, a))
+np.save({out2!r}, hip("FusedConv", [x, w, b, z], z.shape, dict(a, activation="Relu")))
+"""
+
+
+@pytest.mark.parametrize("batch,hw", [(17, 32), (32, 28)])
+@pytest.mark.parametrize("cand", [0, 9, 14, 18, 19, 22, 23])
+def test_conv_lds_patch_forced_configs(gpu, tmp_path, batch, hw, cand):
+    """Each 3x3 configuration (tile shapes, split counts, and the tail split
+    that cuts the last partial round of tiles along the channels: 16 tiles in
+    8 pieces, or 136 tiles in halves) computes the same convolution: forced in
+    a child process, compared with the restatement and with the fused
+    epilogue applied by hand."""
+    import os
+    import subprocess
+    import sys
+
+    x = randn((batch, 64, hw, hw), seed=80)
+    w = randn((64, 64, 3, 3), seed=81, scale=0.06)
+    b = randn((64,), seed=82, scale=0.1)
+    z = randn((batch, 64, hw, hw), seed=83)
+    paths = {k: str(tmp_path / f"{k}.npy") for k in ("x", "w", "b", "z", "out1", "out2")}
+    for k, v in (("x", x), ("w", w), ("b", b), ("z", z)):
+        np.save(paths[k], v)
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, NERT_HIP_CONV_CANDIDATE=str(cand))
+    subprocess.run([sys.executable, "-c", _FORCED.format(root=root, **paths)], env=env, check=True, timeout=120)
+    conv = np.load(paths["out1"])
+    ref = restate.conv(x, w, b, None, None, [1, 1, 1, 1], 1, "NOTSET")
+    compare(conv, ref, what=f"candidate {cand}")
+    want = conv + z
+    assert np.array_equal(np.load(paths["out2"]), np.where(want > 0, want, np.float32(0)).astype(F))
