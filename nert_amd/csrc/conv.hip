@@ -953,7 +953,17 @@ bool TryHaloShape(ConvArgs p, hipStream_t stream, int force_splits, bool tail = 
         if (p.group != 1 || n_full == 0 || rest == 0) {
             return false;
         }
-        const int pieces = static_cast<int>(std::min<int64_t>(h.blocks, std::max<int64_t>(2, kCUs / rest)));
+        // Piece count: the CUs' last partial round, ceil(rest * P / 256)
+        // pieces of 1/P tile each, as short as possible.
+        int pieces = 2;
+        double best = 1e30;
+        for (int q = 2; q <= std::min(h.blocks, 16); ++q) {
+            const double round = std::ceil(static_cast<double>(rest * q) / kCUs) / q;
+            if (round < best - 1e-9) {
+                best = round;
+                pieces = q;
+            }
+        }
         h.tail_bps = (h.blocks + pieces - 1) / pieces;
         h.tail_pieces = (h.blocks + h.tail_bps - 1) / h.tail_bps;
         h.n_full = static_cast<int32_t>(n_full);
