@@ -1099,7 +1099,8 @@ bool TryHaloConv(const ConvArgs& p, hipStream_t stream) {
     static std::map<ConvKey, int> chosen;
     const int fallback = p.mg <= 64 ? 0 : 4; // 64x256 tiles for M_g <= 64, else 64x128
     // NERT_HIP_CONV_CANDIDATE=i forces candidate i wherever it fits (tests
-    // of every configuration use it); otherwise the per-geometry choice.
+    // of every configuration use it; 100 + i names the other kernels'
+    // candidate i); otherwise the per-geometry choice.
     if (const char* forced = std::getenv("NERT_HIP_CONV_CANDIDATE")) {
         const int i = std::atoi(forced);
         if (i >= 0 && i < kHaloCandidates && LaunchHaloCandidate(i, p, stream)) {
@@ -1112,7 +1113,116 @@ bool TryHaloConv(const ConvArgs& p, hipStream_t stream) {
     return LaunchHaloCandidate(c, p, stream) || LaunchHaloCandidate(fallback, p, stream);
 }
 
-// Tap-major and gather kernels: ConvShapeL, ConvShapeW, ConvShapeS.
+// ---- 1x1 convolutions with a short K, straight from memory --------------------
+//
+// A 1x1 convolution with few input channels (the ResNet downsampling convs:
+// 64-256 channels, stride 2) has too few K steps for an LDS pipeline to get
+// going. Here every wave owns a 32x32 output block (32 channels x 32 pixels)
+// and runs its whole K with MFMAs fed directly from memory: lane half h
+// takes channels 8j + 4h .. 8j + 4h + 3, so one 16-byte weight load and four
+// input loads (one per channel plane) feed four MFMA steps; nothing waits on
+// a barrier. The four waves of a workgroup cover four channel blocks of the
+// same pixels, so the input columns they share come from L1/L2.
+__global__ __launch_bounds__(256) void PointwiseDirectKernel(ConvArgs p) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int half = lane >> 5;
+    const int64_t m_blocks = (p.mg + 31) / 32;
+    const int64_t groups_m = (m_blocks + 3) / 4;
+    const int64_t mb = (blockIdx.x % groups_m) * 4 + wave;
+    const int64_t n0 = (blockIdx.x / groups_m) * 32;
+    const int g = blockIdx.y;
+    if (mb >= m_blocks) {
+        return;
+    }
+    const int64_t m0 = mb * 32;
+    // This lane's pixel (column) and weight row.
+    const int64_t n = n0 + (lane & 31);
+    const bool n_ok = n < p.n_total;
+    const int64_t nc = n_ok ? n : 0;
+    const int64_t b = nc / p.plane_out;
+    const int64_t opix = nc - b * p.plane_out;
+    const int64_t oh = opix / p.out_w;
+    const int64_t ow = opix - oh * p.out_w;
+    const int64_t ih = oh * p.s_h - p.p_h;
+    const int64_t iw = ow * p.s_w - p.p_w;
+    const bool in = n_ok && ih >= 0 && ih < p.in_h && iw >= 0 && iw < p.in_w;
+    const float* xp = p.x + (b * p.c + static_cast<int64_t>(g) * p.cg) * p.plane_in + (in ? ih * p.in_w + iw : 0) +
+                      4 * half * p.plane_in;
+    const int64_t m = m0 + (lane & 31);
+    const bool m_ok = m < p.mg;
+    const float* wp = p.w + (static_cast<int64_t>(g) * p.mg + (m_ok ? m : 0)) * p.cg + 4 * half;
+    nert_floatx16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        acc[v] = 0.0f;
+    }
+#pragma unroll 4
+    for (int64_t k = 0; k < p.cg; k += 8) {
+        nert_floatx4 a = *reinterpret_cast<const nert_floatx4*>(wp + k);
+        float bv[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            bv[q] = xp[(k + q) * p.plane_in];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(m_ok ? a[q] : 0.0f, in ? bv[q] : 0.0f, acc, 0, 0, 0);
+        }
+    }
+    // Epilogue as in ConvEpilogue: bias, then residual, then Relu.
+    const int64_t ybase = b * p.m * p.plane_out + opix;
+    float value[16];
+    int64_t yi[16];
+    bool ok[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int64_t r = m0 + 8 * (v >> 2) + 4 * half + (v & 3);
+        ok[v] = n_ok && r < p.mg;
+        const int64_t oc = static_cast<int64_t>(g) * p.mg + (ok[v] ? r : 0);
+        yi[v] = ybase + oc * p.plane_out;
+        value[v] = p.bias != nullptr ? acc[v] + p.bias[oc] : acc[v];
+    }
+    if (p.residual != nullptr) {
+        float res[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            res[v] = p.residual[ok[v] ? yi[v] : 0];
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            value[v] = value[v] + res[v];
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        float out = value[v];
+        if (p.relu) {
+            out = (0.0f < out) ? out : 0.0f;
+        }
+        if (ok[v]) {
+            p.y[yi[v]] = out;
+        }
+    }
+}
+
+bool TryPointwiseDirect(const ConvArgs& p, hipStream_t stream) {
+    if (p.k_d != 1 || p.k_h != 1 || p.k_w != 1 || p.in_d != 1 || p.out_d != 1 || p.cg % 8 != 0 ||
+        (reinterpret_cast<uintptr_t>(p.w) & 15) != 0 || p.group > 65535) {
+        return false;
+    }
+    const int64_t m_blocks = (p.mg + 31) / 32;
+    const int64_t blocks = ((m_blocks + 3) / 4) * ((p.n_total + 31) / 32);
+    if (blocks >= (int64_t{1} << 31)) {
+        return false;
+    }
+    PointwiseDirectKernel<<<dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(p.group)), 256, 0, stream>>>(p);
+    CheckLaunch("PointwiseDirectKernel launch");
+    return true;
+}
+
+// Tap-major and gather kernels: ConvShapeL, ConvShapeW, ConvShapeS; 3: the
+// direct 1x1 kernel.
 bool LaunchGatherCandidate(int i, const ConvArgs& p, hipStream_t stream) {
     switch (i) {
     case 0:
@@ -1121,16 +1231,27 @@ bool LaunchGatherCandidate(int i, const ConvArgs& p, hipStream_t stream) {
     case 1:
         LaunchConv<ConvShapeW>(p, stream);
         return true;
-    default:
+    case 2:
         LaunchConv<ConvShapeS>(p, stream);
         return true;
+    default:
+        return TryPointwiseDirect(p, stream);
     }
 }
 
 void LaunchGatherConv(const ConvArgs& p, hipStream_t stream) {
     static std::map<ConvKey, int> chosen;
     const int fallback = p.mg <= 32 ? 2 : (p.mg <= 64 ? 1 : 0);
-    LaunchGatherCandidate(ChooseConvConfig(chosen, p, stream, 3, fallback, LaunchGatherCandidate), p, stream);
+    if (const char* forced = std::getenv("NERT_HIP_CONV_CANDIDATE")) {
+        const int i = std::atoi(forced) - 100; // 100 + i: gather candidate i
+        if (i >= 0 && i < 4 && LaunchGatherCandidate(i, p, stream)) {
+            return;
+        }
+    }
+    const int c = ChooseConvConfig(chosen, p, stream, 4, fallback, LaunchGatherCandidate);
+    if (!LaunchGatherCandidate(c, p, stream)) {
+        LaunchGatherCandidate(fallback, p, stream);
+    }
 }
 
 // ---- Small-channel convolution from an LDS input patch -------------------------

@@ -372,7 +372,7 @@ def hip(op, ins, shape, attrs):
     out = DeviceArray(shape, np.float32)
     run_node(op, dev, [out], attrs)
     return out.to_host()
-a = {{"pads": [1, 1, 1, 1]}}
+a = json.loads({attrs!r})
 np.save({out1!r}, hip("Conv", [x, w, b], z.shape, a))
 np.save({out2!r}, hip("FusedConv", [x, w, b, z], z.shape, dict(a, activation="Relu")))
 """
@@ -386,10 +386,6 @@ def test_conv_lds_patch_forced_configs(gpu, tmp_path, batch, hw, cand):
     8 pieces, or 136 tiles in halves) computes the same convolution: forced in
     a child process, compared with the restatement and with the fused
     epilogue applied by hand."""
-    import os
-    import subprocess
-    import sys
-
     x = randn((batch, 64, hw, hw), seed=80)
     w = randn((64, 64, 3, 3), seed=81, scale=0.06)
     b = randn((64,), seed=82, scale=0.1)
@@ -397,11 +393,46 @@ def test_conv_lds_patch_forced_configs(gpu, tmp_path, batch, hw, cand):
     paths = {k: str(tmp_path / f"{k}.npy") for k in ("x", "w", "b", "z", "out1", "out2")}
     for k, v in (("x", x), ("w", w), ("b", b), ("z", z)):
         np.save(paths[k], v)
-    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    env = dict(os.environ, NERT_HIP_CONV_CANDIDATE=str(cand))
-    subprocess.run([sys.executable, "-c", _FORCED.format(root=root, **paths)], env=env, check=True, timeout=120)
+    _run_forced(cand, paths, {"pads": [1, 1, 1, 1]})
     conv = np.load(paths["out1"])
     ref = restate.conv(x, w, b, None, None, [1, 1, 1, 1], 1, "NOTSET")
     compare(conv, ref, what=f"candidate {cand}")
+    want = conv + z
+    assert np.array_equal(np.load(paths["out2"]), np.where(want > 0, want, np.float32(0)).astype(F))
+
+
+def _run_forced(cand, paths, attrs):
+    import json
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, NERT_HIP_CONV_CANDIDATE=str(cand))
+    subprocess.run([sys.executable, "-c", _FORCED.format(root=root, attrs=json.dumps(attrs), **paths)], env=env,
+                   check=True, timeout=120)
+
+
+@pytest.mark.parametrize("xs,ws,attrs", [
+    ((4, 64, 56, 56), (128, 64, 1, 1), {"strides": [2, 2]}),   # ResNet downsampling
+    ((2, 256, 14, 14), (512, 256, 1, 1), {"strides": [2, 2]}),
+    ((3, 24, 9, 11), (40, 24, 1, 1), {"strides": [1, 2], "pads": [1, 0, 0, 1]}),
+    ((2, 32, 8, 8), (48, 16, 1, 1), {"group": 2}),
+])
+@pytest.mark.parametrize("cand", [100, 101, 102, 103])
+def test_conv_1x1_forced_configs(gpu, tmp_path, xs, ws, attrs, cand):
+    """Every configuration of the other conv kernels, the direct 1x1 kernel
+    (103) included, forced: matches the restatement, and the fused epilogue
+    matches Conv + Add + Relu bit for bit."""
+    x, w, b = randn(xs, seed=90), randn(ws, seed=91, scale=0.1), randn((ws[0],), seed=92)
+    out = _conv_out(xs, ws, attrs)
+    z = randn(out, seed=93)
+    paths = {k: str(tmp_path / f"{k}.npy") for k in ("x", "w", "b", "z", "out1", "out2")}
+    for k, v in (("x", x), ("w", w), ("b", b), ("z", z)):
+        np.save(paths[k], v)
+    _run_forced(cand, paths, attrs)
+    conv = np.load(paths["out1"])
+    compare(conv, restate.conv(x, w, b, attrs.get("strides"), None, attrs.get("pads"), attrs.get("group", 1),
+                               "NOTSET"), what=f"candidate {cand}")
     want = conv + z
     assert np.array_equal(np.load(paths["out2"]), np.where(want > 0, want, np.float32(0)).astype(F))
