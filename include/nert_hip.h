@@ -44,9 +44,20 @@ void* nert_hip_malloc(int64_t bytes);
 int nert_hip_free(void* ptr);
 
 /* Blocking transfers on the layer stream; replace HIPTransfer
- * (src/hip_device.cpp:70-89). bytes == 0 is a no-op. */
+ * (src/hip_device.cpp:70-89). bytes == 0 is a no-op. Pageable host buffers
+ * of 1 MiB or more are staged through pinned bounce buffers (pieces of 1 MiB
+ * growing to 4 MiB, 2 host threads, host memcpy overlapped with the DMA);
+ * pinned host buffers and smaller copies go straight to the DMA engine.
+ * NERT_HIP_STAGING=0 turns the staging off. */
 int nert_hip_memcpy_h2d(void* dst, const void* src, int64_t bytes);
 int nert_hip_memcpy_d2h(void* dst, const void* src, int64_t bytes);
+/* Pinned (page-locked) host memory, for callers that keep their inputs and
+ * outputs where the DMA engine reads them directly. bytes <= 0 returns NULL;
+ * nert_hip_host_free(NULL) is a no-op. No reference counterpart: the
+ * reference's Transfer takes whatever host pointer the caller holds
+ * (src/hip_device.cpp:70-89). */
+void* nert_hip_host_alloc(int64_t bytes);
+int nert_hip_host_free(void* ptr);
 /* Asynchronous device-to-device copy (Identity/Reshape/Flatten payloads). */
 int nert_hip_memcpy_d2d(void* dst, const void* src, int64_t bytes, void* stream);
 

@@ -9,10 +9,12 @@
 #include "common.hpp"
 #include "../../include/nert_hip.h"
 
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 namespace nert_hip {
@@ -159,6 +161,167 @@ bool ShadowGet(const void* src, int64_t bytes, void* out) {
     return true;
 }
 
+namespace {
+
+// Pinned bounce buffers for transfers from and to pageable host memory.
+//
+// A pageable copy cannot be DMA'd directly; the runtime stages it through its
+// own buffers one piece at a time. Here the copy is cut into pieces (the
+// first kStageFirst bytes, doubling up to kStageChunk) dealt round-robin to
+// kStageLanes host threads. Each lane owns two pinned slots (hipHostMalloc,
+// allocated once, kept until the process ends): H2D, the lane memcpy's a
+// piece into a free slot and queues the slot's DMA, then fills its other slot
+// while that DMA runs; D2H, the lane queues the next piece's DMA before
+// copying the finished one out. Host memcpy and PCIe DMA overlap, and the
+// lanes' memcpy's run in parallel. Measured on MI355X for 18-38 MiB copies:
+// H2D 37-41 GB/s (the runtime's own pageable path 30-36), D2H 34-40 GB/s
+// (17.7), pinned-to-device 56 GB/s. Copies whose host side is already pinned
+// (or below kStageMin) go straight to hipMemcpyAsync. NERT_HIP_STAGING=0
+// turns staging off (every copy a plain hipMemcpyAsync).
+constexpr int64_t kStageChunk = 4 << 20;
+constexpr int64_t kStageFirst = 1 << 20;
+constexpr int kStageLanes = 2;
+constexpr int64_t kStageMin = 1 << 20;
+
+struct Staging {
+    std::mutex mutex;  // one staged transfer at a time
+    bool ready = false;
+    void* slot[2 * kStageLanes] = {};
+    hipEvent_t done[2 * kStageLanes] = {};
+};
+
+Staging& Stage() {
+    static Staging st;
+    return st;
+}
+
+bool StagingEnabled() {
+    const char* v = std::getenv("NERT_HIP_STAGING");
+    return v == nullptr || std::strcmp(v, "0") != 0;
+}
+
+bool HostIsPinned(const void* p) {
+    hipPointerAttribute_t attr{};
+    const hipError_t rc = hipPointerGetAttributes(&attr, p);
+    if (rc != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return attr.type == hipMemoryTypeHost;
+}
+
+void EnsureStaging(Staging& st) {
+    if (st.ready) {
+        return;
+    }
+    for (int i = 0; i < 2 * kStageLanes; ++i) {
+        Check(hipHostMalloc(&st.slot[i], static_cast<size_t>(kStageChunk), hipHostMallocDefault),
+              "hipHostMalloc(staging)");
+        Check(hipEventCreateWithFlags(&st.done[i], hipEventDisableTiming), "hipEventCreate(staging)");
+    }
+    st.ready = true;
+}
+
+// Piece boundaries of a staged copy: sizes double from kStageFirst up to
+// kStageChunk, so the first DMA starts after a short memcpy and the steady
+// state moves large pieces (each DMA carries a fixed submission cost).
+std::vector<int64_t> StagePieces(int64_t bytes) {
+    std::vector<int64_t> starts;
+    int64_t piece = kStageFirst < kStageChunk ? kStageFirst : kStageChunk;
+    for (int64_t off = 0; off < bytes; off += piece, piece = piece * 2 < kStageChunk ? piece * 2 : kStageChunk) {
+        starts.push_back(off);
+    }
+    starts.push_back(bytes);
+    return starts;
+}
+
+// Runs lane(0..lanes-1) on the calling thread and lanes-1 helper threads;
+// rethrows the first lane error after all lanes have stopped.
+template <class Lane>
+void RunLanes(int lanes, Lane lane) {
+    std::vector<std::string> errors(static_cast<size_t>(lanes));
+    auto guarded = [&](int t) {
+        try {
+            lane(t);
+        } catch (const std::exception& e) {
+            errors[static_cast<size_t>(t)] = e.what();
+        }
+    };
+    std::vector<std::thread> helpers;
+    for (int t = 1; t < lanes; ++t) {
+        helpers.emplace_back(guarded, t);
+    }
+    guarded(0);
+    for (auto& h : helpers) {
+        h.join();
+    }
+    for (const auto& e : errors) {
+        if (!e.empty()) {
+            throw Error(e);
+        }
+    }
+}
+
+void StagedH2D(char* dst, const char* src, int64_t bytes, hipStream_t s) {
+    Staging& st = Stage();
+    std::lock_guard<std::mutex> lock(st.mutex);
+    EnsureStaging(st);
+    const std::vector<int64_t> at = StagePieces(bytes);
+    const int64_t pieces = static_cast<int64_t>(at.size()) - 1;
+    const int lanes = static_cast<int>(pieces < kStageLanes ? pieces : kStageLanes);
+    RunLanes(lanes, [&](int t) {
+        int k = 0;
+        for (int64_t c = t; c < pieces; c += lanes, ++k) {
+            const int slot = 2 * t + (k & 1);
+            const int64_t off = at[static_cast<size_t>(c)];
+            const int64_t n = at[static_cast<size_t>(c) + 1] - off;
+            if (k >= 2) {
+                Check(hipEventSynchronize(st.done[slot]), "hipEventSynchronize(staging)");
+            }
+            std::memcpy(st.slot[slot], src + off, static_cast<size_t>(n));
+            Check(hipMemcpyAsync(dst + off, st.slot[slot], static_cast<size_t>(n), hipMemcpyHostToDevice, s),
+                  "hipMemcpyAsync(H2D)");
+            Check(hipEventRecord(st.done[slot], s), "hipEventRecord(staging)");
+        }
+    });
+    Check(hipStreamSynchronize(s), "hipStreamSynchronize");
+}
+
+void StagedD2H(char* dst, const char* src, int64_t bytes, hipStream_t s) {
+    Staging& st = Stage();
+    std::lock_guard<std::mutex> lock(st.mutex);
+    EnsureStaging(st);
+    const std::vector<int64_t> at = StagePieces(bytes);
+    const int64_t pieces = static_cast<int64_t>(at.size()) - 1;
+    const int lanes = static_cast<int>(pieces < kStageLanes ? pieces : kStageLanes);
+    RunLanes(lanes, [&](int t) {
+        auto issue = [&](int64_t c, int slot) {
+            const int64_t off = at[static_cast<size_t>(c)];
+            const int64_t n = at[static_cast<size_t>(c) + 1] - off;
+            Check(hipMemcpyAsync(st.slot[slot], src + off, static_cast<size_t>(n), hipMemcpyDeviceToHost, s),
+                  "hipMemcpyAsync(D2H)");
+            Check(hipEventRecord(st.done[slot], s), "hipEventRecord(staging)");
+        };
+        int k = 0;
+        issue(t, 2 * t);
+        for (int64_t c = t; c < pieces; c += lanes, ++k) {
+            const int slot = 2 * t + (k & 1);
+            if (c + lanes < pieces) {
+                issue(c + lanes, 2 * t + ((k + 1) & 1));
+            }
+            Check(hipEventSynchronize(st.done[slot]), "hipEventSynchronize(staging)");
+            const int64_t off = at[static_cast<size_t>(c)];
+            std::memcpy(dst + off, st.slot[slot], static_cast<size_t>(at[static_cast<size_t>(c) + 1] - off));
+        }
+    });
+}
+
+bool UseStaging(const void* host, int64_t bytes) {
+    return bytes >= kStageMin && StagingEnabled() && !HostIsPinned(host);
+}
+
+} // namespace
+
 } // namespace nert_hip
 
 using nert_hip::Guard;
@@ -208,15 +371,41 @@ int nert_hip_free(void* ptr) {
     });
 }
 
+void* nert_hip_host_alloc(int64_t bytes) {
+    if (bytes <= 0) {
+        return nullptr;
+    }
+    void* ptr = nullptr;
+    const int rc = Guard([&] {
+        nert_hip::EnsureReady();
+        nert_hip::Check(hipHostMalloc(&ptr, static_cast<size_t>(bytes), hipHostMallocDefault), "hipHostMalloc");
+    });
+    return rc == 0 ? ptr : nullptr;
+}
+
+int nert_hip_host_free(void* ptr) {
+    if (ptr == nullptr) {
+        return 0;
+    }
+    return Guard([&] {
+        nert_hip::Check(hipStreamSynchronize(nert_hip::DefaultStream()), "hipStreamSynchronize");
+        nert_hip::Check(hipHostFree(ptr), "hipHostFree");
+    });
+}
+
 int nert_hip_memcpy_h2d(void* dst, const void* src, int64_t bytes) {
     if (bytes == 0) {
         return 0;
     }
     return Guard([&] {
         hipStream_t s = nert_hip::DefaultStream();
-        nert_hip::Check(hipMemcpyAsync(dst, src, static_cast<size_t>(bytes), hipMemcpyHostToDevice, s),
-                        "hipMemcpyAsync(H2D)");
-        nert_hip::Check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        if (nert_hip::UseStaging(src, bytes)) {
+            nert_hip::StagedH2D(static_cast<char*>(dst), static_cast<const char*>(src), bytes, s);
+        } else {
+            nert_hip::Check(hipMemcpyAsync(dst, src, static_cast<size_t>(bytes), hipMemcpyHostToDevice, s),
+                            "hipMemcpyAsync(H2D)");
+            nert_hip::Check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        }
         nert_hip::ShadowPut(dst, src, bytes);
     });
 }
@@ -227,9 +416,13 @@ int nert_hip_memcpy_d2h(void* dst, const void* src, int64_t bytes) {
     }
     return Guard([&] {
         hipStream_t s = nert_hip::DefaultStream();
-        nert_hip::Check(hipMemcpyAsync(dst, src, static_cast<size_t>(bytes), hipMemcpyDeviceToHost, s),
-                        "hipMemcpyAsync(D2H)");
-        nert_hip::Check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        if (nert_hip::UseStaging(dst, bytes)) {
+            nert_hip::StagedD2H(static_cast<char*>(dst), static_cast<const char*>(src), bytes, s);
+        } else {
+            nert_hip::Check(hipMemcpyAsync(dst, src, static_cast<size_t>(bytes), hipMemcpyDeviceToHost, s),
+                            "hipMemcpyAsync(D2H)");
+            nert_hip::Check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        }
     });
 }
 

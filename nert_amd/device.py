@@ -48,6 +48,9 @@ def lib() -> C.CDLL:
     L.nert_hip_malloc.restype = vp
     L.nert_hip_malloc.argtypes = [i64]
     L.nert_hip_free.argtypes = [vp]
+    L.nert_hip_host_alloc.restype = vp
+    L.nert_hip_host_alloc.argtypes = [i64]
+    L.nert_hip_host_free.argtypes = [vp]
     L.nert_hip_memcpy_h2d.argtypes = [vp, vp, i64]
     L.nert_hip_memcpy_d2h.argtypes = [vp, vp, i64]
     L.nert_hip_memcpy_d2d.argtypes = [vp, vp, i64, vp]
@@ -86,6 +89,36 @@ def init() -> None:
 
 def synchronize() -> None:
     check(lib().nert_hip_stream_sync(None), "nert_hip_stream_sync")
+
+
+class PinnedArray:
+    """A numpy array over pinned host memory (nert_hip_host_alloc): copies
+    to and from it go straight to the DMA engine, with no bounce buffer."""
+
+    def __init__(self, shape: Sequence[int], dtype: Any):
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        self.ptr = lib().nert_hip_host_alloc(self.nbytes) if self.nbytes > 0 else None
+        if self.nbytes > 0 and not self.ptr:
+            raise NertError(abi.OTHER_ERROR, f"nert_hip_host_alloc({self.nbytes}): {last_error()}")
+        if self.ptr:
+            raw = (C.c_uint8 * self.nbytes).from_address(self.ptr)
+            self.array = np.frombuffer(raw, np.uint8).view(self.dtype).reshape(self.shape)
+        else:
+            self.array = np.empty(self.shape, self.dtype)
+
+    def close(self) -> None:
+        if self.ptr:
+            self.array = None
+            lib().nert_hip_host_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class DeviceArray:
