@@ -350,7 +350,13 @@ int nert_hip_grid_sample_f32(const float* x, const float* grid, float* y, int64_
  * element sums, in double, the product of the operands over the summed labels
  * (sum_size, odometer order, last fastest). Strides are per label and operand,
  * in elements; a repeated label (diagonal) carries the sum of its strides
- * (src/kernels/einsum.cpp:205-258). At most 16 labels of each kind. */
+ * (src/kernels/einsum.cpp:205-258). At most 16 labels of each kind.
+ * Two-operand equations that are batched matrix products (batch labels, then
+ * row labels of a, then column labels of b -- or columns before rows -- each
+ * group mergeable into one strided index, every summed label in both
+ * operands, at most four batch groups) run on the MFMA GEMM engine with fp32
+ * accumulation instead (within 1e-4 of the double sums); the environment
+ * variable NERT_HIP_EINSUM_EXACT=1 keeps every equation on the double path. */
 int nert_hip_einsum_f32(const float* a, const float* b, float* y, int n_out, const int64_t* out_size,
                         const int64_t* out_stride_a, const int64_t* out_stride_b, int n_sum, const int64_t* sum_size,
                         const int64_t* sum_stride_a, const int64_t* sum_stride_b, void* stream);

@@ -1,11 +1,20 @@
 // Einsum over one or two float32 operands, and ConvTranspose.
 //
 // Einsum: the host resolves the equation into per-label extents and strides
-// (output labels, then summed labels in alphabetical order); one thread per
-// output element walks the summed labels as an odometer, last label
-// fastest, multiplying the operands in double and accumulating in double, so
-// each output sums its terms in the same order as the reference's odometer
-// over all labels (src/kernels/einsum.cpp:205-258) and rounds once.
+// (output labels, then summed labels in alphabetical order). A two-operand
+// equation whose labels fall into the batched-GEMM classes -- batch labels
+// (in both operands and the output), row labels (first operand and output),
+// column labels (second operand and output), contracted labels (both
+// operands, not the output) -- with each class mergeable into one strided
+// index, and the output ordered [batch][rows][columns] (or columns before
+// rows, which swaps the operands), runs on the MFMA GEMM engine with fp32
+// accumulation. Every other equation (one operand, diagonals that do not
+// merge, labels summed in one operand only, broadcast output labels,
+// interleaved row/column labels) takes the exact path: one thread per output
+// element walks the summed labels as an odometer, last label fastest,
+// multiplying the operands in double and accumulating in double, so each
+// output sums its terms in the same order as the reference's odometer over
+// all labels (src/kernels/einsum.cpp:205-258) and rounds once.
 //
 // ConvTranspose: the reference scatters every input pixel into the output
 // (src/kernels/conv_transpose.cpp:160-188). Here each output element gathers
@@ -14,7 +23,13 @@
 // the input. No atomics, one write per output; sums run in double.
 
 #include "common.hpp"
+#include "gemm_engine.hpp"
 #include "../../include/nert_hip.h"
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
 
 namespace nert_hip {
 namespace {
@@ -125,6 +140,194 @@ __global__ void ConvTransposeKernel(const float* __restrict__ x, const float* __
     }
 }
 
+struct Label {
+    int64_t size, sa, sb;
+};
+
+// Merges labels (outer to inner) into one index of extent prod(size) whose
+// stride in an operand is the innermost label's: each outer stride must equal
+// the next inner one times its extent. `which` 0 checks the first operand's
+// strides, 1 the second's.
+bool Mergeable(const std::vector<Label>& g, int which) {
+    for (size_t i = 0; i + 1 < g.size(); ++i) {
+        const int64_t outer = which == 0 ? g[i].sa : g[i].sb;
+        const int64_t inner = which == 0 ? g[i + 1].sa : g[i + 1].sb;
+        if (outer != inner * g[i + 1].size) {
+            return false;
+        }
+    }
+    return true;
+}
+
+Label Merged(const std::vector<Label>& g) {
+    Label m{1, 0, 0};
+    for (const Label& l : g) {
+        m.size *= l.size;
+    }
+    if (!g.empty()) {
+        m.sa = g.back().sa;
+        m.sb = g.back().sb;
+    }
+    return m;
+}
+
+// The batched-GEMM lowering; false when the equation does not fit it.
+bool TryEinsumGemm(const float* a, const float* b, float* y, int n_out, const int64_t* out_size,
+                   const int64_t* out_sa, const int64_t* out_sb, int n_sum, const int64_t* sum_size,
+                   const int64_t* sum_sa, const int64_t* sum_sb, hipStream_t stream) {
+    if (b == nullptr) {
+        return false;
+    }
+    enum Kind { kBatch, kRow, kCol };
+    std::vector<Label> batch, first, second;
+    int first_kind = -1;
+    bool in_second = false;
+    for (int d = 0; d < n_out; ++d) {
+        const Label l{out_size[d], out_sa[d], out_sb[d]};
+        if (l.size == 1) {
+            continue;
+        }
+        int kind;
+        if (l.sa != 0 && l.sb != 0) {
+            kind = kBatch;
+        } else if (l.sa != 0) {
+            kind = kRow;
+        } else if (l.sb != 0) {
+            kind = kCol;
+        } else {
+            return false; // output label present in neither operand
+        }
+        if (kind == kBatch) {
+            if (first_kind >= 0) {
+                return false; // batch labels must lead the output
+            }
+            batch.push_back(l);
+            continue;
+        }
+        if (first_kind < 0) {
+            first_kind = kind;
+        }
+        if (kind == first_kind) {
+            if (in_second) {
+                return false; // row and column labels interleave
+            }
+            first.push_back(l);
+        } else {
+            in_second = true;
+            second.push_back(l);
+        }
+    }
+    std::vector<Label> contracted;
+    for (int d = 0; d < n_sum; ++d) {
+        const Label l{sum_size[d], sum_sa[d], sum_sb[d]};
+        if (l.size == 1) {
+            continue;
+        }
+        if (l.sa == 0 || l.sb == 0) {
+            return false; // summed in one operand only
+        }
+        contracted.push_back(l);
+    }
+    std::stable_sort(contracted.begin(), contracted.end(),
+                     [](const Label& x, const Label& y) { return x.sa > y.sa; });
+    // The GEMM's rows are the output's first non-batch group; when those are
+    // the second operand's labels, the operands swap roles.
+    const bool swap = first_kind == kCol;
+    const std::vector<Label>& rows = first;
+    const std::vector<Label>& cols = second;
+    if (!Mergeable(rows, swap ? 1 : 0) || !Mergeable(cols, swap ? 0 : 1) || !Mergeable(contracted, 0) ||
+        !Mergeable(contracted, 1)) {
+        return false;
+    }
+    // Adjacent batch labels merge when both operands allow it; at most four remain.
+    std::vector<std::vector<Label>> bgroups;
+    for (const Label& l : batch) {
+        if (!bgroups.empty()) {
+            std::vector<Label> trial = bgroups.back();
+            trial.push_back(l);
+            if (Mergeable(trial, 0) && Mergeable(trial, 1)) {
+                bgroups.back() = trial;
+                continue;
+            }
+        }
+        bgroups.push_back({l});
+    }
+    if (bgroups.size() > 4) {
+        return false;
+    }
+    const Label m = Merged(rows);
+    const Label n = Merged(cols);
+    const Label k = Merged(contracted);
+    GemmArgs p{};
+    // Operand roles: A(m, k) from the rows' operand, B(k, n) from the other.
+    p.a = swap ? b : a;
+    p.b = swap ? a : b;
+    p.y = y;
+    p.m = m.size;
+    p.n = n.size;
+    p.k = k.size;
+    p.a_sm = swap ? m.sb : m.sa;
+    p.a_sk = swap ? k.sb : k.sa;
+    p.b_sk = swap ? k.sa : k.sb;
+    p.b_sn = swap ? n.sa : n.sb;
+    // A unit extent has no stride of its own; give it the unit stride the
+    // engine's layouts expect.
+    if (p.m == 1 && p.a_sk != 1) {
+        p.a_sm = 1;
+    }
+    if (p.k == 1) {
+        if (p.a_sm != 1) {
+            p.a_sk = 1;
+        }
+        if (p.b_sn != 1) {
+            p.b_sk = 1;
+        }
+    }
+    if (p.n == 1 && p.b_sk != 1) {
+        p.b_sn = 1;
+    }
+    if ((p.a_sm != 1 && p.a_sk != 1) || (p.b_sk != 1 && p.b_sn != 1)) {
+        return false;
+    }
+    p.alpha = 1.0f;
+    p.beta = 0.0f;
+    p.batch_rank = static_cast<int>(bgroups.size());
+    int64_t batches = 1;
+    for (size_t d = 0; d < bgroups.size(); ++d) {
+        const Label l = Merged(bgroups[d]);
+        p.bdims[d] = l.size;
+        p.a_bs[d] = swap ? l.sb : l.sa;
+        p.b_bs[d] = swap ? l.sa : l.sb;
+        batches *= l.size;
+    }
+    if (batches > 65535) {
+        return false;
+    }
+    // The lowered walk must span exactly the elements the label walk reads:
+    // the largest offset into each operand agrees, so the GEMM stays inside
+    // the operands whenever the equation's own strides do.
+    int64_t reach_a = 0, reach_b = 0;
+    for (int d = 0; d < n_out; ++d) {
+        reach_a += (out_size[d] - 1) * out_sa[d];
+        reach_b += (out_size[d] - 1) * out_sb[d];
+    }
+    for (int d = 0; d < n_sum; ++d) {
+        reach_a += (sum_size[d] - 1) * sum_sa[d];
+        reach_b += (sum_size[d] - 1) * sum_sb[d];
+    }
+    int64_t lowered_a = (p.m - 1) * p.a_sm + (p.k - 1) * p.a_sk;
+    int64_t lowered_b = (p.k - 1) * p.b_sk + (p.n - 1) * p.b_sn;
+    for (int d = 0; d < p.batch_rank; ++d) {
+        lowered_a += (p.bdims[d] - 1) * p.a_bs[d];
+        lowered_b += (p.bdims[d] - 1) * p.b_bs[d];
+    }
+    if (lowered_a != (swap ? reach_b : reach_a) || lowered_b != (swap ? reach_a : reach_b)) {
+        return false;
+    }
+    LaunchGemm(p, batches, stream);
+    return true;
+}
+
 } // namespace
 } // namespace nert_hip
 
@@ -158,6 +361,12 @@ int nert_hip_einsum_f32(const float* a, const float* b, float* y, int n_out, con
             e.sum_total *= sum_size[d];
         }
         if (n <= 0) {
+            return;
+        }
+        const char* exact = std::getenv("NERT_HIP_EINSUM_EXACT");
+        const bool force_exact = exact != nullptr && std::strcmp(exact, "1") == 0;
+        if (!force_exact && TryEinsumGemm(a, b, y, n_out, out_size, out_stride_a, out_stride_b, n_sum, sum_size,
+                                          sum_stride_a, sum_stride_b, StreamOr(stream))) {
             return;
         }
         EinsumKernel<<<GridFor(n, 256, 16384), 256, 0, StreamOr(stream)>>>(a, b != nullptr ? b : a, y, e, n);

@@ -127,6 +127,35 @@ def test_einsum(gpu, equation, shapes):
     assert_parity("Einsum", xs, [(want.shape, F)], {"equation": equation})
 
 
+# (equation, shapes, lowered onto the GEMM engine). Contracted extents of 64
+# and more make the fp32 MFMA sums differ from the double sums of the exact
+# path in some bits, which is how the routing is observed.
+EINSUM_ROUTES = [
+    ("ij,jk->ik", [(96, 200), (200, 80)], True),
+    ("ij,jk->ki", [(64, 128), (128, 96)], True),             # columns first: operands swap
+    ("bij,bjk->bik", [(6, 64, 96), (6, 96, 48)], True),
+    ("bhqd,bhkd->bhqk", [(2, 4, 64, 64), (2, 4, 80, 64)], True),
+    ("bqhd,bkhd->bhqk", [(2, 64, 4, 32), (2, 48, 4, 32)], True),  # two batch groups, strided rows
+    ("ijk,jkl->il", [(32, 16, 8), (16, 8, 40)], True),       # two contracted labels merge
+    ("bi,bij->bj", [(8, 128), (8, 128, 64)], True),          # no row labels
+    ("...ij,jk->...ik", [(7, 30, 64), (64, 20)], True),       # ellipsis rows merge
+    ("ijk,kjl->il", [(16, 12, 10), (10, 12, 20)], False),    # contracted labels do not merge
+    ("ij,kl->ikjl", [(8, 9), (10, 11)], False),              # rows and columns interleave
+    ("ij,jk->i", [(32, 64), (64, 16)], False),               # k summed in one operand only
+    ("ij->ji", [(30, 40)], False),                           # one operand
+]
+
+
+@pytest.mark.parametrize("equation,shapes,lowered", EINSUM_ROUTES)
+def test_einsum_gemm_lowering(gpu, equation, shapes, lowered, monkeypatch):
+    xs = [randn(s, seed=20 + i) for i, s in enumerate(shapes)]
+    want = np.einsum(equation, *[x.astype(np.float64) for x in xs])
+    got = assert_parity("Einsum", xs, [(want.shape, F)], {"equation": equation})[0]
+    monkeypatch.setenv("NERT_HIP_EINSUM_EXACT", "1")
+    exact = assert_parity("Einsum", xs, [(want.shape, F)], {"equation": equation})[0]
+    assert np.array_equal(got, exact) != lowered, "lowered" if lowered else "exact path expected"
+
+
 def test_einsum_errors(gpu):
     a, b = randn((3, 4)), randn((4, 5))
     assert_same_error("Einsum", [a, b], [((3, 5), F)], {"equation": "ij,jk->iq"})
