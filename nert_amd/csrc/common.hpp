@@ -32,10 +32,13 @@ inline hipStream_t StreamOr(void* stream) {
     return stream != nullptr ? static_cast<hipStream_t>(stream) : DefaultStream();
 }
 
-// Reusable device workspace on the default device: grows on demand (a
-// stream-synchronised reallocation), never shrinks. Kernels that need
-// scratch (split-K partials, TopK candidates, error flags) take it from here.
-void* Workspace(int64_t bytes, hipStream_t stream);
+// Reusable device workspaces on the default device: each slot grows on
+// demand (a stream-synchronised reallocation), never shrinks. Kernels that
+// need scratch (split-K partials, TopK candidates, error flags) take slot 0;
+// a row that keeps an intermediate alive across a GEMM launch (which may take
+// slot 0 for its partials) holds it in slot 1.
+constexpr int kWorkspaceSlots = 2;
+void* Workspace(int64_t bytes, hipStream_t stream, int slot = 0);
 
 // A 64-byte device flag block (zeroed at creation) used by rows that must
 // report data-dependent errors (out-of-range indices, integer division by

@@ -17,10 +17,16 @@
 // all labels (src/kernels/einsum.cpp:205-258) and rounds once.
 //
 // ConvTranspose: the reference scatters every input pixel into the output
-// (src/kernels/conv_transpose.cpp:160-188). Here each output element gathers
-// the (channel, tap) pairs that land on it: tap kh contributes when
+// (src/kernels/conv_transpose.cpp:160-188). Here it is a GEMM plus a gather.
+// Per (image, group), one batched MFMA GEMM forms
+// Z[(m, kh, kw)][ih, iw] = sum_c W[c][m, kh, kw] * X[c][ih, iw]
+// (the weights are read in place as the transposed operand), then each output
+// element gathers the taps that land on it -- tap kh contributes when
 // oh + pad - kh * dilation is a non-negative multiple of the stride inside
-// the input. No atomics, one write per output; sums run in double.
+// the input -- adds the bias and is written once; no atomics. fp32 sums, as
+// the reference's. Groups of fewer than 8 input channels, and problems whose
+// Z would pass 2 GiB, keep the direct kernel: one thread per output gathering
+// (channel, tap) pairs with double sums.
 
 #include "common.hpp"
 #include "gemm_engine.hpp"
@@ -328,6 +334,109 @@ bool TryEinsumGemm(const float* a, const float* b, float* y, int n_out, const in
     return true;
 }
 
+// Output element i (row-major over [batch, out_c, out_h, out_w]) sums the
+// Z entries of its valid taps. With unit dilation the valid kh are
+// kh0, kh0 + stride, ... where kh0 = (oh + pad) mod stride.
+__global__ __launch_bounds__(256) void ConvTransposeGatherKernel(const float* __restrict__ z,
+                                                                 const float* __restrict__ bias, float* __restrict__ y,
+                                                                 ConvTArgs p, FastDiv fw, FastDiv fh, FastDiv fc,
+                                                                 uint32_t n) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= n) {
+        return;
+    }
+    uint32_t ow, oh, m;
+    uint32_t t = DivMod(fw, i, ow);
+    t = DivMod(fh, t, oh);
+    const uint32_t b = DivMod(fc, t, m);
+    const int mg = static_cast<int>(p.out_c / p.group);
+    const int g = static_cast<int>(m) / mg;
+    const int ml = static_cast<int>(m) - g * mg;
+    const int64_t plane = p.in_h * p.in_w;
+    const float* zb = z + ((static_cast<int64_t>(b) * p.group + g) * mg + ml) * (p.k_h * p.k_w) * plane;
+    const int sh = static_cast<int>(p.stride_h), sw = static_cast<int>(p.stride_w);
+    const int dh = static_cast<int>(p.dil_h), dw = static_cast<int>(p.dil_w);
+    const int kh_n = static_cast<int>(p.k_h), kw_n = static_cast<int>(p.k_w);
+    const int ih_n = static_cast<int>(p.in_h), iw_n = static_cast<int>(p.in_w);
+    const int th0 = static_cast<int>(oh) + static_cast<int>(p.pad_h);
+    const int tw0 = static_cast<int>(ow) + static_cast<int>(p.pad_w);
+    const int kh_first = dh == 1 ? (th0 % sh) : 0;
+    const int kh_step = dh == 1 ? sh : 1;
+    const int kw_first = dw == 1 ? (tw0 % sw) : 0;
+    const int kw_step = dw == 1 ? sw : 1;
+    float acc = 0.0f;
+    for (int kh = kh_first; kh < kh_n; kh += kh_step) {
+        const int th = th0 - kh * dh;
+        if (th < 0) {
+            break;
+        }
+        if (th % sh != 0) {
+            continue;
+        }
+        const int ih = th / sh;
+        if (ih >= ih_n) {
+            continue;
+        }
+        for (int kw = kw_first; kw < kw_n; kw += kw_step) {
+            const int tw = tw0 - kw * dw;
+            if (tw < 0) {
+                break;
+            }
+            if (tw % sw != 0) {
+                continue;
+            }
+            const int iw = tw / sw;
+            if (iw >= iw_n) {
+                continue;
+            }
+            acc += zb[(kh * kw_n + kw) * plane + ih * iw_n + iw];
+        }
+    }
+    y[i] = bias != nullptr ? bias[m] + acc : acc;
+}
+
+bool TryConvTransposeGemm(const float* x, const float* w, const float* bias, float* y, const ConvTArgs& p,
+                          hipStream_t stream) {
+    const int64_t cg = p.in_c / p.group;
+    const int64_t mg = p.out_c / p.group;
+    const int64_t rows = mg * p.k_h * p.k_w;
+    const int64_t plane = p.in_h * p.in_w;
+    const int64_t batches = p.batch * p.group;
+    const int64_t outputs = p.batch * p.out_c * p.out_h * p.out_w;
+    const int64_t z_bytes = batches * rows * plane * static_cast<int64_t>(sizeof(float));
+    if (cg < 8 || batches > 65535 || z_bytes > (int64_t{1} << 31) || outputs >= (int64_t{1} << 31) ||
+        plane <= 0 || rows <= 0 || p.pad_h < 0 || p.pad_w < 0 || p.dil_h < 1 || p.dil_w < 1) {
+        return false;
+    }
+    float* z = static_cast<float*>(Workspace(z_bytes, stream, 1));
+    GemmArgs g{};
+    g.a = w; // A(r, c) = W[g*cg + c][r]
+    g.b = x; // B(c, q) = X[b][g*cg + c][q]
+    g.y = z;
+    g.m = rows;
+    g.n = plane;
+    g.k = cg;
+    g.a_sm = 1;
+    g.a_sk = rows;
+    g.b_sk = plane;
+    g.b_sn = 1;
+    g.alpha = 1.0f;
+    g.beta = 0.0f;
+    g.batch_rank = 2;
+    g.bdims[0] = p.batch;
+    g.a_bs[0] = 0;
+    g.b_bs[0] = p.in_c * plane;
+    g.bdims[1] = p.group;
+    g.a_bs[1] = cg * rows;
+    g.b_bs[1] = cg * plane;
+    LaunchGemm(g, batches, stream);
+    ConvTransposeGatherKernel<<<GridFor(outputs, 256, outputs), 256, 0, stream>>>(
+        z, bias, y, p, FastDiv::Make(static_cast<uint32_t>(p.out_w)), FastDiv::Make(static_cast<uint32_t>(p.out_h)),
+        FastDiv::Make(static_cast<uint32_t>(p.out_c)), static_cast<uint32_t>(outputs));
+    CheckLaunch("conv_transpose gather launch");
+    return true;
+}
+
 } // namespace
 } // namespace nert_hip
 
@@ -387,6 +496,11 @@ int nert_hip_conv_transpose_f32(const float* x, const float* w, const float* bia
         }
         const int64_t n = p.batch * p.out_c * p.out_h * p.out_w;
         if (n <= 0) {
+            return;
+        }
+        const char* exact = std::getenv("NERT_HIP_CONVT_EXACT");
+        const bool force_exact = exact != nullptr && std::strcmp(exact, "1") == 0;
+        if (!force_exact && TryConvTransposeGemm(x, w, bias, y, p, StreamOr(stream))) {
             return;
         }
         ConvTransposeKernel<<<GridFor(n, 256, 16384), 256, 0, StreamOr(stream)>>>(x, w, bias, y, p, n);

@@ -25,8 +25,8 @@ thread_local std::string g_last_error;
 struct Context {
     bool ready = false;
     hipStream_t stream = nullptr;
-    void* workspace = nullptr;
-    int64_t workspace_bytes = 0;
+    void* workspace[kWorkspaceSlots] = {};
+    int64_t workspace_bytes[kWorkspaceSlots] = {};
     int32_t* flags = nullptr;
 };
 
@@ -71,28 +71,31 @@ hipStream_t DefaultStream() {
     return Ctx().stream;
 }
 
-void* Workspace(int64_t bytes, hipStream_t stream) {
+void* Workspace(int64_t bytes, hipStream_t stream, int slot) {
     EnsureReady();
+    if (slot < 0 || slot >= kWorkspaceSlots) {
+        throw Error("workspace slot out of range");
+    }
     Context& ctx = Ctx();
-    if (bytes <= ctx.workspace_bytes) {
-        return ctx.workspace;
+    if (bytes <= ctx.workspace_bytes[slot]) {
+        return ctx.workspace[slot];
     }
     // Grow geometrically; the old buffer may still be read by queued work.
-    int64_t want = ctx.workspace_bytes * 2;
+    int64_t want = ctx.workspace_bytes[slot] * 2;
     if (want < bytes) {
         want = bytes;
     }
     want = (want + 0xFFFFF) & ~static_cast<int64_t>(0xFFFFF);
-    if (ctx.workspace != nullptr) {
+    if (ctx.workspace[slot] != nullptr) {
         Check(hipStreamSynchronize(stream), "hipStreamSynchronize(workspace)");
         Check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize(workspace)");
-        Check(hipFree(ctx.workspace), "hipFree(workspace)");
-        ctx.workspace = nullptr;
-        ctx.workspace_bytes = 0;
+        Check(hipFree(ctx.workspace[slot]), "hipFree(workspace)");
+        ctx.workspace[slot] = nullptr;
+        ctx.workspace_bytes[slot] = 0;
     }
-    Check(hipMalloc(&ctx.workspace, static_cast<size_t>(want)), "hipMalloc(workspace)");
-    ctx.workspace_bytes = want;
-    return ctx.workspace;
+    Check(hipMalloc(&ctx.workspace[slot], static_cast<size_t>(want)), "hipMalloc(workspace)");
+    ctx.workspace_bytes[slot] = want;
+    return ctx.workspace[slot];
 }
 
 int32_t* ErrorFlags() {

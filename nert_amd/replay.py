@@ -9,6 +9,13 @@ captures it into a HIP graph and replays it N times between HIP events on
 the layer stream. Prints one line: workload, ms per replay, and the
 algorithmic GFLOP of the graph.
 
+    python3 -m nert_amd.replay contractions [--runs N]
+
+Times ConvTranspose and Einsum rows at decoder / attention sizes on their
+MFMA GEMM paths and on the exact double-sum paths (NERT_HIP_CONVT_EXACT=1,
+NERT_HIP_EINSUM_EXACT=1): microseconds per row between HIP events, TFLOP/s,
+and the largest difference between the two paths relative to the 1e-4 bar.
+
     python3 -m nert_amd.replay transfer [--runs N]
 
 Times the blocking host<->device copies (nert_hip_memcpy_h2d/d2h) at the
@@ -70,14 +77,81 @@ def _transfer(runs: int) -> None:
         pinned.close()
 
 
+def _contractions(runs: int) -> None:
+    import os
+
+    import numpy as np
+
+    from .graph import Graph
+
+    rng = np.random.default_rng(0)
+    cases = []
+    for (b, c, h, m, k, s, p) in [(4, 64, 64, 32, 4, 2, 1), (8, 256, 32, 128, 2, 2, 0), (2, 128, 56, 64, 3, 1, 1)]:
+        g = Graph()
+        g.add_input("x", np.float32, (b, c, h, h))
+        g.add_initializer("w", (rng.standard_normal((c, m, k, k)) * 0.05).astype(np.float32))
+        g.add_initializer("bias", rng.standard_normal(m).astype(np.float32))
+        o = s * (h - 1) + k - 2 * p
+        g.add_node("ConvTranspose", ["x", "w", "bias"], [("y", np.float32, (b, m, o, o))],
+                   {"strides": [s, s], "pads": [p, p, p, p]})
+        g.outputs = ["y"]
+        cases.append((f"ConvTranspose x{(b, c, h, h)} w{(c, m, k, k)} stride {s} pad {p}", g,
+                       {"x": rng.standard_normal((b, c, h, h)).astype(np.float32)}, 2 * b * c * h * h * m * k * k,
+                       "NERT_HIP_CONVT_EXACT"))
+    for eq, sa, sb in [("bhqd,bhkd->bhqk", (16, 12, 197, 64), (16, 12, 197, 64)),
+                       ("bhqk,bhkd->bhqd", (16, 12, 197, 197), (16, 12, 197, 64)),
+                       ("ij,jk->ik", (1024, 1024), (1024, 1024))]:
+        g = Graph()
+        g.add_input("a", np.float32, sa)
+        g.add_input("b", np.float32, sb)
+        out = np.einsum(eq, np.zeros(sa, np.float32), np.zeros(sb, np.float32)).shape
+        g.add_node("Einsum", ["a", "b"], [("y", np.float32, out)], {"equation": eq})
+        g.outputs = ["y"]
+        cases.append((f"Einsum {eq} {sa} {sb}", g, {"a": rng.standard_normal(sa).astype(np.float32),
+                                                    "b": rng.standard_normal(sb).astype(np.float32)},
+                      2 * int(np.prod(out)) * sa[-1], "NERT_HIP_EINSUM_EXACT"))
+
+    def timed(g, inputs, env, reps):
+        os.environ.update(env)
+        try:
+            prog = Program(g, fuse=False)
+            for n in g.inputs:
+                prog.set_input(n, inputs[n])
+            prog.run()
+            device.synchronize()
+            start, stop = Event(), Event()
+            start.record()
+            for _ in range(reps):
+                prog.run()
+            stop.record()
+            ms = start.elapsed_ms(stop) / reps
+            out = prog.output(g.outputs[0])
+            prog.close()
+        finally:
+            for k in env:
+                os.environ.pop(k, None)
+        return ms, out
+
+    for name, g, inputs, flops, var in cases:
+        ms_fast, y_fast = timed(g, inputs, {}, runs)
+        ms_exact, y_exact = timed(g, inputs, {var: "1"}, max(1, runs // 5))
+        ratio = float(np.max(np.abs(y_fast.astype(np.float64) - y_exact) / (1e-4 + 1e-4 * np.abs(y_exact))))
+        print(f"{name}: MFMA path {ms_fast * 1e3:.1f} us ({flops / ms_fast / 1e9:.1f} TFLOP/s), exact path "
+              f"{ms_exact * 1e3:.1f} us ({flops / ms_exact / 1e9:.2f} TFLOP/s), {ms_exact / ms_fast:.0f}x; "
+              f"max |diff| / (1e-4 + 1e-4 |exact|) = {ratio:.3f}", flush=True)
+
+
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("workload", choices=sorted(BUILDERS) + ["transfer"])
+    ap.add_argument("workload", choices=sorted(BUILDERS) + ["contractions", "transfer"])
     ap.add_argument("--runs", type=int, default=10)
     args = ap.parse_args(argv)
     device.init()
     if args.workload == "transfer":
         _transfer(max(args.runs, 1))
+        return 0
+    if args.workload == "contractions":
+        _contractions(max(args.runs, 1))
         return 0
     g, inputs = BUILDERS[args.workload]()
     prog = Program(g)

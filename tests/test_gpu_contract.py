@@ -4,8 +4,11 @@ reference CpuDevice rows.
 Resize nearest is a copy and must be bit-exact; linear Resize and
 GridSample follow the reference's double-precision coordinate and weight
 arithmetic step for step, so they are held to the same float32 bar as the
-other float rows (|d| <= 1e-4 + 1e-4 |ref|). ConvTranspose accumulates in
-double where the reference scatters in float32 (same bar)."""
+other float rows (|d| <= 1e-4 + 1e-4 |ref|). ConvTranspose runs as an MFMA
+GEMM plus a tap gather in float32 (groups of 8+ input channels) or as a
+direct kernel summing in double, where the reference scatters in float32
+(same bar for both). Einsum equations that are batched matrix products run on
+the GEMM engine, the rest on a double-sum walk (same bar)."""
 
 import numpy as np
 import pytest
@@ -180,6 +183,11 @@ def test_einsum_errors(gpu):
 ])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_conv_transpose(gpu, geom, with_bias):
+    inputs, spec, a = _conv_transpose_case(geom, with_bias)
+    assert_parity("ConvTranspose", inputs, spec, a)
+
+
+def _conv_transpose_case(geom, with_bias):
     a = geom["attrs"]
     x, w = randn(geom["x"], seed=20), randn(geom["w"], seed=21)
     s, d = a.get("strides", [1, 1]), a.get("dilations", [1, 1])
@@ -190,7 +198,33 @@ def test_conv_transpose(gpu, geom, with_bias):
     oh = s[0] * (x.shape[2] - 1) + op[0] + d[0] * (w.shape[2] - 1) + 1 - p[0] - p[2]
     ow = s[1] * (x.shape[3] - 1) + op[1] + d[1] * (w.shape[3] - 1) + 1 - p[1] - p[3]
     inputs = [x, w] + ([randn((m,), seed=22)] if with_bias else [])
-    assert_parity("ConvTranspose", inputs, [((x.shape[0], m, oh, ow), F)], a)
+    return inputs, [((x.shape[0], m, oh, ow), F)], a
+
+
+# Groups of 8 or more input channels run as an MFMA GEMM plus a tap gather;
+# (geometry, lowered). The exact path (NERT_HIP_CONVT_EXACT=1) sums in double,
+# so with 64 channels per group the two differ in some bits.
+CONVT_GEMM_GEOMS = [
+    (dict(x=(2, 16, 9, 11), w=(16, 8, 3, 3), attrs={"strides": [2, 2], "pads": [1, 1, 1, 1]}), True),
+    (dict(x=(1, 32, 8, 8), w=(32, 6, 4, 4), attrs={"strides": [2, 2], "pads": [1, 1, 1, 1], "group": 2}), True),
+    (dict(x=(2, 8, 7, 6), w=(8, 5, 3, 3), attrs={"dilations": [2, 2]}), True),
+    (dict(x=(1, 12, 5, 5), w=(12, 4, 3, 3), attrs={"strides": [3, 2], "pads": [1, 0, 2, 1],
+                                                   "output_padding": [2, 1], "dilations": [1, 2]}), True),
+    (dict(x=(4, 64, 16, 16), w=(64, 32, 4, 4), attrs={"strides": [2, 2], "pads": [1, 1, 1, 1]}), True),
+    (dict(x=(2, 4, 5, 6), w=(4, 3, 3, 3), attrs={"strides": [2, 2]}), False),
+]
+
+
+@pytest.mark.parametrize("geom,lowered", CONVT_GEMM_GEOMS)
+def test_conv_transpose_gemm_path(gpu, geom, lowered, monkeypatch):
+    inputs, spec, a = _conv_transpose_case(geom, True)
+    got = assert_parity("ConvTranspose", inputs, spec, a)[0]
+    monkeypatch.setenv("NERT_HIP_CONVT_EXACT", "1")
+    exact = assert_parity("ConvTranspose", inputs, spec, a)[0]
+    if lowered and geom["x"][1] // geom["attrs"].get("group", 1) >= 64:
+        assert not np.array_equal(got, exact), "expected the GEMM path"
+    if not lowered:
+        assert np.array_equal(got, exact), "expected the direct path"
 
 
 def test_conv_transpose_errors(gpu):
