@@ -526,6 +526,141 @@ __global__ __launch_bounds__(256) void InstanceNormKernel(const float* __restric
     }
 }
 
+// Register-resident InstanceNorm: a group of GROUP threads (one wave, or the
+// whole 256-thread block) owns a plane of at most GROUP * PER elements, reads
+// it once into registers (clamped loads, masked afterwards), and forms the
+// double mean, then the double sum of squared deviations, from the registers:
+// one HBM read and one write per element.
+template <int GROUP, int PER>
+__global__ __launch_bounds__(256) void InstanceNormResidentKernel(const float* __restrict__ x,
+                                                                  const float* __restrict__ scale,
+                                                                  const float* __restrict__ bias,
+                                                                  float* __restrict__ y, int64_t channels,
+                                                                  int64_t spatial, int64_t planes, double eps) {
+    __shared__ double smem[4];
+    constexpr int kPlanesPerBlock = 256 / GROUP;
+    const int t = static_cast<int>(threadIdx.x) % GROUP;
+    const int64_t plane = static_cast<int64_t>(blockIdx.x) * kPlanesPerBlock + threadIdx.x / GROUP;
+    if (GROUP == 64 && plane >= planes) {
+        return; // whole waves leave; the wave kernel has no block barrier
+    }
+    const int64_t c = plane % channels;
+    const float* p = x + plane * spatial;
+    float v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int64_t i = t + static_cast<int64_t>(k) * GROUP;
+        v[k] = p[i < spatial ? i : spatial - 1];
+    }
+    double sum = 0.0;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        if (t + static_cast<int64_t>(k) * GROUP < spatial) {
+            sum += static_cast<double>(v[k]);
+        }
+    }
+    sum = GROUP == 64 ? WaveAllSum(sum) : BlockSum(sum, smem);
+    const double mean = sum / static_cast<double>(spatial);
+    double sq = 0.0;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        if (t + static_cast<int64_t>(k) * GROUP < spatial) {
+            const double d = static_cast<double>(v[k]) - mean;
+            sq += d * d;
+        }
+    }
+    sq = GROUP == 64 ? WaveAllSum(sq) : BlockSum(sq, smem);
+    const double inv = 1.0 / sqrt(sq / static_cast<double>(spatial) + eps);
+    const double sc = static_cast<double>(scale[c]);
+    const double bi = static_cast<double>(bias[c]);
+    float* q = y + plane * spatial;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int64_t i = t + static_cast<int64_t>(k) * GROUP;
+        if (i < spatial) {
+            q[i] = static_cast<float>((static_cast<double>(v[k]) - mean) * inv * sc + bi);
+        }
+    }
+}
+
+// Split-plane InstanceNorm for planes larger than one block holds: blockIdx.y
+// is the plane, blockIdx.x a chunk of kInChunk elements. PASS 0 writes each
+// chunk's double sum; PASS 1 forms the mean from those (in chunk order) and
+// writes each chunk's sum of squared deviations; PASS 2 forms mean and
+// inverse deviation the same way and normalises the chunk.
+constexpr int kInPer = 16;
+constexpr int kInChunk = 256 * kInPer;
+
+template <int PASS>
+__global__ __launch_bounds__(256) void InstanceNormSplitKernel(const float* __restrict__ x,
+                                                               const float* __restrict__ scale,
+                                                               const float* __restrict__ bias, float* __restrict__ y,
+                                                               double* __restrict__ partial, int64_t channels,
+                                                               int64_t spatial, int chunks, double eps) {
+    __shared__ double smem[4];
+    __shared__ double stats[2];
+    const int64_t plane = blockIdx.y;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kInChunk;
+    const float* p = x + plane * spatial;
+    double* sums = partial + plane * chunks;
+    double* sqs = partial + (static_cast<int64_t>(gridDim.y) + plane) * chunks;
+    float v[kInPer];
+#pragma unroll
+    for (int k = 0; k < kInPer; ++k) {
+        const int64_t i = base + threadIdx.x + k * 256;
+        v[k] = p[i < spatial ? i : spatial - 1];
+    }
+    if (PASS > 0) {
+        // Every block of the plane folds the chunk partials the same way
+        // (strided per thread, then the block tree), so all agree bit for bit.
+        double total = 0.0;
+        double sq = 0.0;
+        for (int j = threadIdx.x; j < chunks; j += 256) {
+            total += sums[j];
+            if (PASS == 2) {
+                sq += sqs[j];
+            }
+        }
+        total = BlockSum(total, smem);
+        if (PASS == 2) {
+            sq = BlockSum(sq, smem);
+        }
+        if (threadIdx.x == 0) {
+            stats[0] = total / static_cast<double>(spatial);
+            stats[1] = PASS == 2 ? 1.0 / sqrt(sq / static_cast<double>(spatial) + eps) : 0.0;
+        }
+        __syncthreads();
+    }
+    const double mean = PASS > 0 ? stats[0] : 0.0;
+    if (PASS < 2) {
+        double acc = 0.0;
+#pragma unroll
+        for (int k = 0; k < kInPer; ++k) {
+            if (base + threadIdx.x + k * 256 < spatial) {
+                const double d = static_cast<double>(v[k]) - mean;
+                acc += PASS == 0 ? static_cast<double>(v[k]) : d * d;
+            }
+        }
+        acc = BlockSum(acc, smem);
+        if (threadIdx.x == 0) {
+            (PASS == 0 ? sums : sqs)[blockIdx.x] = acc;
+        }
+        return;
+    }
+    const int64_t c = plane % channels;
+    const double inv = stats[1];
+    const double sc = static_cast<double>(scale[c]);
+    const double bi = static_cast<double>(bias[c]);
+    float* q = y + plane * spatial;
+#pragma unroll
+    for (int k = 0; k < kInPer; ++k) {
+        const int64_t i = base + threadIdx.x + k * 256;
+        if (i < spatial) {
+            q[i] = static_cast<float>((static_cast<double>(v[k]) - mean) * inv * sc + bi);
+        }
+    }
+}
+
 // ---- ArgMax ----------------------------------------------------------------
 // Sequential rule: index i replaces the best when v > best, or (last) when
 // v == best; so NaN never wins after index 0 and a NaN at index 0 wins.
@@ -730,8 +865,34 @@ int nert_hip_instancenorm_f32(const float* x, const float* scale, const float* b
         if (planes > 0x7FFFFFFF) {
             throw Error("instancenorm: too many planes");
         }
-        InstanceNormKernel<<<static_cast<unsigned>(planes), 256, 0, StreamOr(stream)>>>(x, scale, bias, y, channels,
-                                                                                        spatial, epsilon);
+        hipStream_t s = StreamOr(stream);
+        const unsigned wave_blocks = static_cast<unsigned>((planes + 3) / 4);
+        const unsigned plane_blocks = static_cast<unsigned>(planes);
+        if (spatial <= 256) {
+            InstanceNormResidentKernel<64, 4><<<wave_blocks, 256, 0, s>>>(x, scale, bias, y, channels, spatial,
+                                                                          planes, epsilon);
+        } else if (spatial <= 1024) {
+            InstanceNormResidentKernel<64, 16><<<wave_blocks, 256, 0, s>>>(x, scale, bias, y, channels, spatial,
+                                                                           planes, epsilon);
+        } else if (spatial <= 4096) {
+            InstanceNormResidentKernel<256, 16><<<plane_blocks, 256, 0, s>>>(x, scale, bias, y, channels, spatial,
+                                                                             planes, epsilon);
+        } else if (spatial <= 8192) {
+            InstanceNormResidentKernel<256, 32><<<plane_blocks, 256, 0, s>>>(x, scale, bias, y, channels, spatial,
+                                                                             planes, epsilon);
+        } else if (planes <= 65535 && (spatial + kInChunk - 1) / kInChunk <= 0x7FFFFFFF) {
+            const int chunks = static_cast<int>((spatial + kInChunk - 1) / kInChunk);
+            auto* partial = static_cast<double*>(Workspace(2 * planes * chunks * 8, s));
+            const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(planes));
+            InstanceNormSplitKernel<0><<<grid, 256, 0, s>>>(x, scale, bias, y, partial, channels, spatial, chunks,
+                                                            epsilon);
+            InstanceNormSplitKernel<1><<<grid, 256, 0, s>>>(x, scale, bias, y, partial, channels, spatial, chunks,
+                                                            epsilon);
+            InstanceNormSplitKernel<2><<<grid, 256, 0, s>>>(x, scale, bias, y, partial, channels, spatial, chunks,
+                                                            epsilon);
+        } else {
+            InstanceNormKernel<<<plane_blocks, 256, 0, s>>>(x, scale, bias, y, channels, spatial, epsilon);
+        }
         CheckLaunch("instancenorm launch");
     });
 }

@@ -269,6 +269,80 @@ __global__ void GridSampleKernel(const float* __restrict__ x, const float* __res
     }
 }
 
+// GridSample with the channels spread over blockIdx.y in groups of
+// kGsChannels: thread = output pixel, as in GridSampleKernel, with the same
+// double coordinate and weight arithmetic in the same order (so the results
+// are identical), but the four taps of every channel of the group are loaded
+// up front from clamped, always-valid offsets and masked afterwards, so the
+// loads overlap instead of each waiting on a branch.
+constexpr int kGsChannels = 4;
+
+__global__ __launch_bounds__(256) void GridSampleGroupKernel(const float* __restrict__ x,
+                                                             const float* __restrict__ grid, float* __restrict__ y,
+                                                             int64_t c, int64_t h, int64_t w, int64_t ho, int64_t wo,
+                                                             int nearest, int padding, int align, FastDiv fwo,
+                                                             FastDiv fho, uint32_t pixels) {
+    const uint32_t p = blockIdx.x * 256u + threadIdx.x;
+    if (p >= pixels) {
+        return;
+    }
+    uint32_t j, i;
+    const uint32_t b = DivMod(fho, DivMod(fwo, p, j), i);
+    const float* g = grid + static_cast<int64_t>(p) * 2;
+    const double px = GridCoord(static_cast<double>(g[0]), w, align != 0, padding);
+    const double py = GridCoord(static_cast<double>(g[1]), h, align != 0, padding);
+    int64_t x0, y0;
+    double wx = 0.0, wy = 0.0;
+    if (nearest) {
+        x0 = ToI64(rint(px));
+        y0 = ToI64(rint(py));
+    } else {
+        const double fx = floor(px);
+        const double fy = floor(py);
+        x0 = ToI64(fx);
+        y0 = ToI64(fy);
+        wx = px - fx;
+        wy = py - fy;
+    }
+    const bool inx0 = x0 >= 0 && x0 < w, inx1 = x0 + 1 >= 0 && x0 + 1 < w;
+    const bool iny0 = y0 >= 0 && y0 < h, iny1 = y0 + 1 >= 0 && y0 + 1 < h;
+    const int64_t cx0 = x0 < 0 ? 0 : (x0 >= w ? w - 1 : x0);
+    const int64_t cx1 = x0 + 1 < 0 ? 0 : (x0 + 1 >= w ? w - 1 : x0 + 1);
+    const int64_t cy0 = y0 < 0 ? 0 : (y0 >= h ? h - 1 : y0);
+    const int64_t cy1 = y0 + 1 < 0 ? 0 : (y0 + 1 >= h ? h - 1 : y0 + 1);
+    const int64_t o00 = cy0 * w + cx0, o01 = cy0 * w + cx1, o10 = cy1 * w + cx0, o11 = cy1 * w + cx1;
+    const int64_t ch0 = static_cast<int64_t>(blockIdx.y) * kGsChannels;
+    float a[kGsChannels][4];
+#pragma unroll
+    for (int k = 0; k < kGsChannels; ++k) {
+        const int64_t ch = ch0 + k < c ? ch0 + k : c - 1;
+        const float* plane = x + (static_cast<int64_t>(b) * c + ch) * h * w;
+        a[k][0] = plane[o00];
+        a[k][1] = plane[o01];
+        a[k][2] = plane[o10];
+        a[k][3] = plane[o11];
+    }
+    const int64_t out_plane = ho * wo;
+    float* out = y + (static_cast<int64_t>(b) * c + ch0) * out_plane + static_cast<int64_t>(i) * wo + j;
+#pragma unroll
+    for (int k = 0; k < kGsChannels; ++k) {
+        if (ch0 + k >= c) {
+            break;
+        }
+        const double v00 = iny0 && inx0 ? static_cast<double>(a[k][0]) : 0.0;
+        double value;
+        if (nearest) {
+            value = v00;
+        } else {
+            const double v01 = iny0 && inx1 ? static_cast<double>(a[k][1]) : 0.0;
+            const double v10 = iny1 && inx0 ? static_cast<double>(a[k][2]) : 0.0;
+            const double v11 = iny1 && inx1 ? static_cast<double>(a[k][3]) : 0.0;
+            value = v00 * (1.0 - wx) * (1.0 - wy) + v01 * wx * (1.0 - wy) + v10 * (1.0 - wx) * wy + v11 * wx * wy;
+        }
+        out[k * out_plane] = static_cast<float>(value);
+    }
+}
+
 } // namespace
 } // namespace nert_hip
 
@@ -340,8 +414,17 @@ int nert_hip_grid_sample_f32(const float* x, const float* grid, float* y, int64_
         if (pixels <= 0 || c <= 0) {
             return;
         }
-        GridSampleKernel<<<GridFor(pixels, 256, 16384), 256, 0, StreamOr(stream)>>>(x, grid, y, n, c, h, w, ho, wo,
-                                                                                    nearest, padding, align_corners);
+        const int64_t groups = (c + kGsChannels - 1) / kGsChannels;
+        if (pixels < (int64_t{1} << 31) && groups <= 65535 && h > 0 && w > 0) {
+            const dim3 blocks(static_cast<unsigned>((pixels + 255) / 256), static_cast<unsigned>(groups));
+            GridSampleGroupKernel<<<blocks, 256, 0, StreamOr(stream)>>>(
+                x, grid, y, c, h, w, ho, wo, nearest, padding, align_corners,
+                FastDiv::Make(static_cast<uint32_t>(wo)), FastDiv::Make(static_cast<uint32_t>(ho)),
+                static_cast<uint32_t>(pixels));
+        } else {
+            GridSampleKernel<<<GridFor(pixels, 256, 16384), 256, 0, StreamOr(stream)>>>(
+                x, grid, y, n, c, h, w, ho, wo, nearest, padding, align_corners);
+        }
         CheckLaunch("grid_sample launch");
     });
 }

@@ -9,12 +9,14 @@ captures it into a HIP graph and replays it N times between HIP events on
 the layer stream. Prints one line: workload, ms per replay, and the
 algorithmic GFLOP of the graph.
 
-    python3 -m nert_amd.replay contractions [--runs N]
+    python3 -m nert_amd.replay rows [--runs N]
 
 Times ConvTranspose and Einsum rows at decoder / attention sizes on their
 MFMA GEMM paths and on the exact double-sum paths (NERT_HIP_CONVT_EXACT=1,
 NERT_HIP_EINSUM_EXACT=1): microseconds per row between HIP events, TFLOP/s,
-and the largest difference between the two paths relative to the 1e-4 bar.
+and the largest difference between the two paths relative to the 1e-4 bar;
+then InstanceNormalization and GridSample rows: microseconds and TB/s of
+their algorithmic bytes (one read of X and the grid, one write of Y).
 
     python3 -m nert_amd.replay transfer [--runs N]
 
@@ -77,7 +79,7 @@ def _transfer(runs: int) -> None:
         pinned.close()
 
 
-def _contractions(runs: int) -> None:
+def _rows(runs: int) -> None:
     import os
 
     import numpy as np
@@ -140,18 +142,43 @@ def _contractions(runs: int) -> None:
               f"{ms_exact * 1e3:.1f} us ({flops / ms_exact / 1e9:.2f} TFLOP/s), {ms_exact / ms_fast:.0f}x; "
               f"max |diff| / (1e-4 + 1e-4 |exact|) = {ratio:.3f}", flush=True)
 
+    for shp in [(1, 64, 256, 256), (8, 128, 64, 64), (4, 256, 32, 32), (16, 32, 128, 128), (2, 512, 16, 16)]:
+        g = Graph()
+        g.add_input("x", np.float32, shp)
+        g.add_initializer("s", rng.standard_normal(shp[1]).astype(np.float32))
+        g.add_initializer("b", rng.standard_normal(shp[1]).astype(np.float32))
+        g.add_node("InstanceNormalization", ["x", "s", "b"], [("y", np.float32, shp)], {"epsilon": 1e-5})
+        g.outputs = ["y"]
+        ms, _ = timed(g, {"x": rng.standard_normal(shp).astype(np.float32)}, {}, runs)
+        nbytes = 8 * int(np.prod(shp))
+        print(f"InstanceNormalization {shp}: {ms * 1e3:.1f} us, {nbytes / ms / 1e9:.2f} TB/s", flush=True)
+    for (n, c, h, w, ho, wo) in [(1, 64, 128, 128, 128, 128), (4, 32, 64, 64, 96, 96), (8, 256, 16, 16, 32, 32)]:
+        for mode, pad in [("bilinear", "zeros"), ("nearest", "border"), ("bilinear", "reflection")]:
+            g = Graph()
+            g.add_input("x", np.float32, (n, c, h, w))
+            g.add_input("grid", np.float32, (n, ho, wo, 2))
+            g.add_node("GridSample", ["x", "grid"], [("y", np.float32, (n, c, ho, wo))],
+                       {"mode": mode, "padding_mode": pad, "align_corners": 0})
+            g.outputs = ["y"]
+            feeds = {"x": rng.standard_normal((n, c, h, w)).astype(np.float32),
+                     "grid": rng.uniform(-1.1, 1.1, (n, ho, wo, 2)).astype(np.float32)}
+            ms, _ = timed(g, feeds, {}, runs)
+            nbytes = 4 * (n * c * h * w + n * ho * wo * 2 + n * c * ho * wo)
+            print(f"GridSample {mode}/{pad} x{(n, c, h, w)} -> {ho}x{wo}: {ms * 1e3:.1f} us, "
+                  f"{nbytes / ms / 1e9:.2f} TB/s", flush=True)
+
 
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("workload", choices=sorted(BUILDERS) + ["contractions", "transfer"])
+    ap.add_argument("workload", choices=sorted(BUILDERS) + ["rows", "transfer"])
     ap.add_argument("--runs", type=int, default=10)
     args = ap.parse_args(argv)
     device.init()
     if args.workload == "transfer":
         _transfer(max(args.runs, 1))
         return 0
-    if args.workload == "contractions":
-        _contractions(max(args.runs, 1))
+    if args.workload == "rows":
+        _rows(max(args.runs, 1))
         return 0
     g, inputs = BUILDERS[args.workload]()
     prog = Program(g)

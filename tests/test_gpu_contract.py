@@ -88,6 +88,21 @@ def test_grid_sample(gpu, mode, padding, align):
     assert_parity("GridSample", [x, grid], [((2, 3, 5, 7), F)], attrs)
 
 
+@pytest.mark.parametrize("mode", ["bilinear", "nearest"])
+@pytest.mark.parametrize("padding", ["zeros", "border", "reflection"])
+@pytest.mark.parametrize("shape", [(1, 6, 33, 40, 21, 50), (3, 9, 16, 16, 40, 8), (2, 1, 5, 5, 3, 3)])
+def test_grid_sample_channel_groups(gpu, mode, padding, shape):
+    """Channel counts that do not fill the last group of four, and
+    non-finite grid points (their taps fall outside the input)."""
+    n, c, h, w, ho, wo = shape
+    x = randn((n, c, h, w), seed=8)
+    grid = (randn((n, ho, wo, 2), seed=9) * 0.9).astype(F)
+    grid[0, 0, 0] = [np.inf, 0.5]
+    grid[-1, -1, -1] = [-0.25, -np.inf]
+    attrs = {"mode": mode, "padding_mode": padding, "align_corners": 0}
+    assert_parity("GridSample", [x, grid], [((n, c, ho, wo), F)], attrs)
+
+
 def test_grid_sample_errors(gpu):
     x = randn((1, 2, 4, 4))
     g = np.zeros((1, 3, 3, 2), F)

@@ -110,6 +110,19 @@ def test_instancenorm(gpu):
     assert_parity("InstanceNormalization", [x2, randn((4,), seed=15), randn((4,), seed=16)], [(x2.shape, F)])
 
 
+# One case per kernel path: a wave per plane (spatial <= 256, <= 1024; plane
+# counts that leave the last block part-filled), a block per plane (<= 4096,
+# <= 8192), and the split-plane path (whole and ragged 4096-element chunks).
+@pytest.mark.parametrize("shape", [(3, 5, 7, 9), (2, 3, 17, 19), (2, 3, 40, 50), (1, 6, 80, 90), (1, 4, 40960),
+                                   (2, 3, 100, 123), (1, 2, 3, 1)])
+@pytest.mark.parametrize("offset", [0.0, 300.0])
+def test_instancenorm_paths(gpu, shape, offset):
+    x = (randn(shape, seed=31) + np.float32(offset)).astype(F)
+    c = shape[1]
+    assert_parity("InstanceNormalization", [x, randn((c,), seed=32), randn((c,), seed=33)], [(shape, F)],
+                  {"epsilon": 1e-5})
+
+
 @pytest.mark.parametrize("shape,axis,keepdims,last", [
     ((1024, 1024), 1, 1, 0), ((1024, 1024), 1, 0, 1), ((4, 5, 6), 1, 1, 0), ((4, 5, 6), 0, 0, 1), ((7,), 0, 0, 0),
 ])
