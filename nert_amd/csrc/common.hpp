@@ -130,5 +130,6 @@ inline void CheckLaunch(const char* what) { Check(hipGetLastError(), what); }
 } // namespace nert_hip
 
 // Device-side vector types for the MFMA builtins.
+typedef float nert_floatx2 __attribute__((ext_vector_type(2)));
 typedef float nert_floatx4 __attribute__((ext_vector_type(4)));
 typedef float nert_floatx16 __attribute__((ext_vector_type(16)));

@@ -1485,10 +1485,303 @@ bool LaunchPatch(const ConvArgs& p, const PatchGeom& pg, dim3 grid, size_t lds, 
     return true;
 }
 
+// ---- Stride-2 image stems: four taps per lane per operand read ---------------
+//
+// The patch kernel above feeds every MFMA with two 4-byte LDS reads. For the
+// stride-2 stems with filter rows of 5 to 8 taps (the 7x7 ResNet stem) the
+// rows are padded to 8 taps and split the way the 3x3 kernel splits its
+// channels: MFMA step kk of a filter row takes tap kk in lanes 0-31 and tap
+// 4 + kk in lanes 32-63. A lane's four taps are then consecutive input
+// columns 2 * ox + 4 * half + kk, 8-byte aligned because the stride is 2, so
+// two 8-byte reads per pixel column and one 16-byte weight read feed the
+// row's eight MFMAs. Taps past the filter's width have zero weights and their
+// input values are replaced by zero in registers (a 0 * inf would be NaN).
+constexpr int kStemTaps = 8;
+
+struct StemGeom {
+    int32_t rows;          // C_g * KH filter rows
+    int32_t wpitch;        // LDS weight row pitch (rows * 8 + 4 floats)
+    int32_t ph, pitch;     // patch rows, LDS patch row pitch (a multiple of 4)
+    int32_t pw;            // patch columns read from the input
+    int32_t tiles_w, tiles_h;
+    int32_t patch_floats;  // C_g * ph * pitch
+    int32_t blocks;        // batch * tiles_h * tiles_w
+    FastDiv div_plane;     // by ph * pitch
+    FastDiv div_pitch;     // by pitch
+};
+
+__global__ __launch_bounds__(512, 4) void StemQuadKernel(ConvArgs p, StemGeom sg) {
+    // Dynamic LDS: weights [kPatchM][wpitch], bias [kPatchM], two patches.
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    float* const ws = smem;
+    float* const bias_s = ws + kPatchM * sg.wpitch;
+    float* const patches = bias_s + kPatchM;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int g = blockIdx.z;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kPatchM;
+    const int cg = static_cast<int>(p.cg);
+    const int kh_n = p.k_h, kw_n = p.k_w;
+    const int knat = cg * kh_n * kw_n;
+
+    // Weights, rows padded to 8 taps with zeros (zero rows past M_g).
+    const float* wg = p.w + (static_cast<int64_t>(g) * p.mg + m0) * knat;
+    for (int m = wave; m < kPatchM; m += 8) {
+        const bool ok = m0 + m < p.mg;
+        for (int k = lane; k < sg.rows * kStemTaps; k += 64) {
+            const int row = k >> 3;
+            const int t = k & 7;
+            ws[m * sg.wpitch + k] = ok && t < kw_n ? wg[static_cast<int64_t>(m) * knat + row * kw_n + t] : 0.0f;
+        }
+    }
+    if (tid < kPatchM) {
+        const int64_t m = m0 + tid;
+        bias_s[tid] = p.bias != nullptr && m < p.mg ? p.bias[static_cast<int64_t>(g) * p.mg + m] : 0.0f;
+    }
+
+    // Patch element e = tid + i * 512 is channel, row, column of the padded
+    // [C][ph][pitch] layout; columns past pw and positions outside the image
+    // load zero. Straight from memory into LDS, 64 consecutive floats a wave.
+    auto load_patch = [&](int blk, float* dst) {
+        const int tx0 = (blk % sg.tiles_w) * kPatchTile;
+        const int rest = blk / sg.tiles_w;
+        const int ty0 = (rest % sg.tiles_h) * kPatchTile;
+        const int64_t b = rest / sg.tiles_h;
+        const int ih0 = ty0 * p.s_h - p.p_h;
+        const int iw0 = tx0 * p.s_w - p.p_w;
+        const __amdgpu_buffer_rsrc_t xr = MakeRsrc(p.x + (b * p.c + static_cast<int64_t>(g) * cg) * p.plane_in,
+                                                   static_cast<uint32_t>(cg * p.plane_in * 4));
+        const int plane_in = static_cast<int>(p.plane_in);
+        for (int w0 = wave * 64; w0 < sg.patch_floats; w0 += 512) {
+            const int e = w0 + lane;
+            if (e < sg.patch_floats) {
+                uint32_t rem, x;
+                const uint32_t c = DivMod(sg.div_plane, static_cast<uint32_t>(e), rem);
+                const int ih = ih0 + static_cast<int>(DivMod(sg.div_pitch, rem, x));
+                const int iw = iw0 + static_cast<int>(x);
+                const bool in = static_cast<int>(x) < sg.pw &&
+                                static_cast<unsigned>(ih) < static_cast<unsigned>(p.in_h) &&
+                                static_cast<unsigned>(iw) < static_cast<unsigned>(p.in_w);
+                const uint32_t off =
+                    in ? static_cast<uint32_t>((static_cast<int>(c) * plane_in + ih * p.in_w + iw) * 4) : kOutOfRange;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*)(dst + w0), 4,
+                                                         static_cast<int>(off), 0, 0, 0);
+            }
+        }
+    };
+
+    // 8 waves: 2 along M (32 rows each) x 4 along N (64 pixels = 4 block rows).
+    const int wave_m = wave & 1;
+    const int wave_n = wave >> 1;
+    const int half = lane >> 5;
+    const int col = lane & 31;
+    int boff[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = wave_n * 64 + j * 32 + col;
+        boff[j] = (n / kPatchTile) * p.s_h * sg.pitch + (n % kPatchTile) * 2 + 4 * half;
+    }
+    bool zero_tap[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+        zero_tap[kk] = 4 * half + kk >= kw_n;
+    }
+    const float* const wrow = ws + (wave_m * 32 + col) * sg.wpitch + 4 * half;
+    const int plane_patch = sg.ph * sg.pitch;
+    const int row_step = p.d_h * sg.pitch;
+
+    float bias_r[16];
+    bool bias_read = false;
+    int blk = blockIdx.x;
+    if (blk < sg.blocks) {
+        load_patch(blk, patches);
+    }
+    for (int buf = 0; blk < sg.blocks; blk += gridDim.x, buf ^= 1) {
+        float* const patch = patches + buf * sg.patch_floats;
+        // This wave's copies of the current patch are complete; after the
+        // barrier everyone's are, and nobody still reads the other buffer.
+        // After the first block the copies are followed by the previous
+        // block's 32 output stores, of which the newest 16 may still be in
+        // flight: vector memory operations complete in issue order, so
+        // vmcnt <= 16 already implies the copies are done (simm16 0x4070:
+        // vmcnt 16, expcnt untouched, lgkmcnt 0). The stores then drain
+        // under this block's MFMAs.
+        // A plain s_barrier: the waits above already cover the LDS writes
+        // (the copies through vmcnt, ordinary LDS stores through lgkmcnt),
+        // and __syncthreads' release fence would wait for every store.
+        if (bias_read) {
+            __builtin_amdgcn_s_waitcnt(0x4070);
+        } else {
+            __builtin_amdgcn_s_waitcnt(0);
+        }
+        __builtin_amdgcn_s_barrier();
+        if (!bias_read) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    bias_r[4 * r + v] = bias_s[wave_m * 32 + 8 * r + 4 * half + v];
+                }
+            }
+            bias_read = true;
+        }
+        const int next = blk + static_cast<int>(gridDim.x);
+        if (next < sg.blocks) {
+            load_patch(next, patches + (buf ^ 1) * sg.patch_floats);
+        }
+        nert_floatx16 acc[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                acc[j][v] = 0.0f;
+            }
+        }
+        for (int c = 0; c < cg; ++c) {
+            const float* prow = patch + c * plane_patch;
+            const float* wr = wrow + c * kh_n * kStemTaps;
+            for (int kh = 0; kh < kh_n; ++kh) {
+                const nert_floatx4 a = *reinterpret_cast<const nert_floatx4*>(wr + kh * kStemTaps);
+                float bq[2][4];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const float* src = prow + kh * row_step + boff[j];
+                    const nert_floatx2 lo = *reinterpret_cast<const nert_floatx2*>(src);
+                    const nert_floatx2 hi = *reinterpret_cast<const nert_floatx2*>(src + 2);
+                    bq[j][0] = zero_tap[0] ? 0.0f : lo[0];
+                    bq[j][1] = zero_tap[1] ? 0.0f : lo[1];
+                    bq[j][2] = zero_tap[2] ? 0.0f : hi[0];
+                    bq[j][3] = zero_tap[3] ? 0.0f : hi[1];
+                }
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk], bq[j][kk], acc[j], 0, 0, 0);
+                    }
+                }
+            }
+        }
+
+        // Epilogue, as in the patch kernel, but every lane issues all 32 of
+        // its stores (buffer stores; a lane without an output element stores
+        // to an out-of-range offset, which the hardware drops), so the store
+        // count behind the next block's copies is fixed.
+        const int tx0 = (blk % sg.tiles_w) * kPatchTile;
+        const int rest = blk / sg.tiles_w;
+        const int ty0 = (rest % sg.tiles_h) * kPatchTile;
+        const int64_t b = rest / sg.tiles_h;
+        const uint32_t image_bytes = static_cast<uint32_t>(p.m * p.plane_out * 4);
+        const __amdgpu_buffer_rsrc_t yr = MakeRsrc(p.y + b * p.m * p.plane_out, image_bytes);
+        const bool has_residual = p.residual != nullptr;
+        const __amdgpu_buffer_rsrc_t zr =
+            MakeRsrc(has_residual ? p.residual + b * p.m * p.plane_out : p.y, has_residual ? image_bytes : 0u);
+        const int plane_out = static_cast<int>(p.plane_out);
+        const bool has_bias = p.bias != nullptr;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int n = wave_n * 64 + j * 32 + col;
+            const int oy = ty0 + n / kPatchTile;
+            const int ox = tx0 + n % kPatchTile;
+            const bool pix_ok = oy < p.out_h && ox < p.out_w;
+            const int pix = pix_ok ? oy * p.out_w + ox : 0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int ml0 = wave_m * 32 + 8 * r + 4 * half;
+                float value[4];
+                int yi[4];
+                bool ok[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int ml = ml0 + v;
+                    ok[v] = pix_ok && m0 + ml < p.mg;
+                    const int oc = g * static_cast<int>(p.mg) + (ok[v] ? static_cast<int>(m0) + ml : 0);
+                    yi[v] = oc * plane_out + pix;
+                    value[v] = has_bias ? acc[j][4 * r + v] + bias_r[4 * r + v] : acc[j][4 * r + v];
+                }
+                if (has_residual) {
+                    float res[4];
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        res[v] = BufferLoad(zr, ok[v] ? static_cast<uint32_t>(yi[v]) * 4u : kOutOfRange, 0);
+                    }
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        value[v] = value[v] + res[v];
+                    }
+                }
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    float out = value[v];
+                    if (p.relu) {
+                        out = (0.0f < out) ? out : 0.0f; // std::max(0.0f, v)
+                    }
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out), yr,
+                                                          static_cast<int>(ok[v] ? static_cast<uint32_t>(yi[v]) * 4u
+                                                                                 : kOutOfRange),
+                                                          0, 0);
+                }
+            }
+        }
+    }
+}
+
+// Stride-2, undilated-along-W stems with 5..8 taps per filter row whose
+// weights and two padded patches fit in 160 KiB of LDS.
+bool TryStemQuad(const ConvArgs& p, hipStream_t stream) {
+    if (p.k_d != 1 || p.in_d != 1 || p.out_d != 1 || p.cg > 4 || p.s_w != 2 || p.d_w != 1 || p.k_w < 5 ||
+        p.k_w > kStemTaps) {
+        return false;
+    }
+    StemGeom sg{};
+    sg.rows = static_cast<int32_t>(p.cg) * p.k_h;
+    sg.wpitch = sg.rows * kStemTaps + 4;
+    sg.ph = (kPatchTile - 1) * p.s_h + (p.k_h - 1) * p.d_h + 1;
+    sg.pw = (kPatchTile - 1) * 2 + kStemTaps;
+    sg.pitch = (sg.pw + 3) / 4 * 4;
+    const int64_t patch_floats = p.cg * sg.ph * sg.pitch;
+    const size_t lds_bytes =
+        (static_cast<size_t>(kPatchM) * sg.wpitch + kPatchM + 2 * static_cast<size_t>(patch_floats)) * sizeof(float);
+    if (lds_bytes > 160 * 1024) {
+        return false;
+    }
+    sg.patch_floats = static_cast<int32_t>(patch_floats);
+    sg.tiles_w = (p.out_w + kPatchTile - 1) / kPatchTile;
+    sg.tiles_h = (p.out_h + kPatchTile - 1) / kPatchTile;
+    const int64_t blocks = p.batch * sg.tiles_w * sg.tiles_h;
+    const int64_t m_blocks = (p.mg + kPatchM - 1) / kPatchM;
+    if (blocks > 0x7FFFFFFF || m_blocks > 65535 || p.group > 65535 || p.cg * p.plane_in * 4 >= (int64_t{1} << 31) ||
+        p.m * p.plane_out * 4 >= (int64_t{1} << 31)) {
+        return false;
+    }
+    sg.blocks = static_cast<int32_t>(blocks);
+    sg.div_plane = FastDiv::Make(static_cast<uint32_t>(sg.ph * sg.pitch));
+    sg.div_pitch = FastDiv::Make(static_cast<uint32_t>(sg.pitch));
+    static const bool allowed = hipFuncSetAttribute(reinterpret_cast<const void*>(&StemQuadKernel),
+                                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                    160 * 1024) == hipSuccess;
+    if (!allowed) {
+        (void)hipGetLastError();
+        if (lds_bytes > 64 * 1024) {
+            return false;
+        }
+    }
+    const int64_t per_slot = std::max<int64_t>(1, kResidentBlocks / (m_blocks * p.group));
+    const dim3 grid(static_cast<unsigned>(std::min(blocks, per_slot)), static_cast<unsigned>(m_blocks),
+                    static_cast<unsigned>(p.group));
+    StemQuadKernel<<<grid, 512, lds_bytes, stream>>>(p, sg);
+    CheckLaunch("StemQuadKernel launch");
+    return true;
+}
+
 // True when the patch kernel applies: 2-D, few channels per group, filter
 // rows of up to 8 taps, and a workgroup's weights and two input patches fit
 // in 160 KiB of LDS.
 bool TryPatchConv(const ConvArgs& p, hipStream_t stream) {
+    if (TryStemQuad(p, stream)) {
+        return true;
+    }
     if (p.k_d != 1 || p.in_d != 1 || p.out_d != 1 || p.cg > 4 || p.k_w > 8) {
         return false;
     }

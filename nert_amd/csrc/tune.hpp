@@ -12,12 +12,22 @@
 
 #include "common.hpp"
 
+#include <cstdio>
 #include <cstdlib>
 #include <map>
 #include <mutex>
 #include <string>
 
 namespace nert_hip {
+
+// NERT_HIP_TUNE_LOG=1: print every candidate's time and the choice to stderr.
+inline bool TuneLogEnabled() {
+    static const bool enabled = [] {
+        const char* e = std::getenv("NERT_HIP_TUNE_LOG");
+        return e != nullptr && std::string(e) == "1";
+    }();
+    return enabled;
+}
 
 inline bool TuningEnabled() {
     static const bool enabled = [] {
@@ -60,6 +70,9 @@ int ChooseConfig(std::map<Key, int>& cache, std::mutex& mu, const Key& key, size
                 Check(hipEventSynchronize(stop), "hipEventSynchronize");
                 float ms = 0.0f;
                 Check(hipEventElapsedTime(&ms, start, stop), "hipEventElapsedTime");
+                if (TuneLogEnabled()) {
+                    std::fprintf(stderr, "nert_hip tune: candidate %d %.1f us\n", i, ms * 1000.0f / 3.0f);
+                }
                 if (best_ms < 0.0f || ms < best_ms) {
                     best_ms = ms;
                     best = i;
@@ -76,6 +89,9 @@ int ChooseConfig(std::map<Key, int>& cache, std::mutex& mu, const Key& key, size
         Check(hipEventDestroy(start), "hipEventDestroy");
         Check(hipEventDestroy(stop), "hipEventDestroy");
         Check(hipFree(scratch), "hipFree(tuning output)");
+    }
+    if (TuneLogEnabled()) {
+        std::fprintf(stderr, "nert_hip tune: chose %d of %d\n", best, count);
     }
     cache.emplace(key, best);
     return best;

@@ -240,7 +240,8 @@ def test_config1c_skinny_gemm(gpu):
 FUSED_CASES = [
     ((2, 64, 14, 14), (64, 64, 3, 3), {"pads": [1, 1, 1, 1]}),                      # tap-major, split-K
     ((1, 256, 7, 7), (512, 256, 3, 3), {"pads": [1, 1, 1, 1]}),                     # deep split-K
-    ((2, 3, 32, 32), (16, 3, 7, 7), {"pads": [3, 3, 3, 3], "strides": [2, 2]}),     # gather path (C=3)
+    ((2, 3, 32, 32), (16, 3, 7, 7), {"pads": [3, 3, 3, 3], "strides": [2, 2]}),     # stem kernel (C=3)
+    ((24, 3, 224, 224), (64, 3, 7, 7), {"pads": [3, 3, 3, 3], "strides": [2, 2]}),  # stem, 2-3 blocks per workgroup
     ((2, 32, 9, 9), (48, 32, 1, 1), {}),                                            # pointwise shape
     ((1, 64, 20, 20), (64, 16, 3, 3), {"pads": [1, 1, 1, 1], "group": 4}),          # groups
 ]
@@ -343,10 +344,15 @@ def _restate_args(attrs):
     ((2, 3, 70, 50), (16, 3, 3, 3), {"pads": [1, 1, 1, 1], "strides": [2, 2]}),     # detector stem, ragged
     ((2, 1, 33, 31), (100, 1, 5, 4), {"pads": [2, 1, 2, 2], "dilations": [2, 1]}),  # M > 64, even KW
     ((2, 4, 20, 20), (8, 2, 3, 3), {"pads": [1, 1, 1, 1], "group": 2}),             # groups
+    ((3, 3, 45, 61), (100, 3, 7, 7), {"pads": [3, 3, 3, 3], "strides": [2, 2]}),    # 7x7, two channel blocks
+    ((1, 2, 30, 30), (64, 2, 7, 7), {"pads": [2, 3, 1, 3], "dilations": [1, 2]}),   # 7x7, C=2, dilated
+    ((2, 3, 40, 40), (24, 3, 3, 5), {"pads": [2, 2, 2, 2], "strides": [1, 2], "dilations": [2, 1]}),  # 5 taps
+    ((1, 4, 36, 36), (32, 4, 4, 8), {"pads": [1, 3, 2, 4], "strides": [2, 2]}),     # 8 taps, C=4
 ])
 def test_small_channel_conv(gpu, xs, ws, attrs):
     x, w, b = randn(xs, seed=50), randn(ws, seed=51), randn((ws[0],), seed=52)
     assert_parity("Conv", [x, w, b], [(_conv_out(xs, ws, attrs), F)], attrs)
+    assert_parity("Conv", [x, w], [(_conv_out(xs, ws, attrs), F)], attrs)  # no bias
 
 
 def test_small_channel_conv_nonfinite_inputs(gpu):
