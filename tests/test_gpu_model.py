@@ -96,6 +96,37 @@ def test_reference_executor_on_hipdevice(resnet):
     compare(got, want, rtol=RTOL, atol=RTOL, what="drop-in logits")
 
 
+def test_dropin_end_to_end_bs32(resnet):
+    """The drop-in at the benchmark's batch: nert::Model(graph, dims,
+    HipDevice()).RunTyped on all 32 images (per run: the executor's input
+    staging through the seam's Transfer, every row launched eagerly, the
+    blocking output copy). Images 0-1 match the oracle; the wall time per warm
+    run is printed beside the device-only time of the runner's graph replay
+    (the benchmark's step)."""
+    g, x, lg, want = resnet
+    _dropin_run(lg, x, runs=1)  # first run: per-geometry kernel choices, allocator warm-up
+    got, secs, _ = _dropin_run(lg, x, runs=5)
+    compare(got[:2], want, rtol=RTOL, atol=RTOL, what="drop-in bs32 logits, images 0-1")
+    prog = Program(g)
+    prog.set_input("input", x)
+    prog.capture()
+    for _ in range(5):
+        prog.replay()
+    from nert_amd.device import Event, synchronize
+    synchronize()
+    e0, e1 = Event(), Event()
+    e0.record()
+    for _ in range(20):
+        prog.replay()
+    e1.record()
+    device_ms = e0.elapsed_ms(e1) / 20
+    compare(prog.output(g.outputs[0]), got, rtol=RTOL, atol=RTOL, what="runner vs drop-in bs32 logits")
+    prog.close()
+    print(f"\nModel::RunTyped on HipDevice, ResNet-18 bs32: {secs * 1e3:.3f} ms wall per run "
+          f"({32 / secs:.0f} img/s, host input staged each run); runner graph replay, inputs resident: "
+          f"{device_ms:.3f} ms per step ({32 / device_ms * 1e3:.0f} img/s)")
+
+
 def test_fused_vit_program_is_bit_identical(gpu):
     """The MatMul+scale+bias+Gelu fusion and the view aliasing change no
     output bit (ViT-B/16, two layers, batch 2)."""
