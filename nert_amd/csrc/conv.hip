@@ -515,6 +515,47 @@ __global__ void ConvSplitReduceKernel(ConvArgs p, int splits, int vec) {
     }
 }
 
+// The same sums for partial planes whose element count is a multiple of 4 and
+// under 2^31: four consecutive elements per thread, 16-byte partial loads,
+// 32-bit index decoding; the output index is decoded per element, so the four
+// may straddle an image boundary (planes of 49 pixels). Same order of
+// additions as ConvSplitReduceKernel, so the results are identical.
+__global__ __launch_bounds__(256) void ConvSplitReduceQuadKernel(ConvArgs p, int splits, FastDiv div_n,
+                                                                 FastDiv div_plane) {
+    const uint32_t per_split = static_cast<uint32_t>(p.group * p.mg * p.n_total);
+    const uint32_t quads = per_split / 4;
+    const int plane_out = static_cast<int>(p.plane_out);
+    for (uint32_t q = blockIdx.x * 256u + threadIdx.x; q < quads; q += gridDim.x * 256u) {
+        const uint32_t i = q * 4u;
+        nert_floatx4 sum = *reinterpret_cast<const nert_floatx4*>(p.partial + i);
+        for (int s = 1; s < splits; ++s) {
+            sum += *reinterpret_cast<const nert_floatx4*>(p.partial + static_cast<int64_t>(s) * per_split + i);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            uint32_t gc, pix;
+            const uint32_t oc = DivMod(div_n, i + e, gc); // g * mg + m
+            const uint32_t b = DivMod(div_plane, gc, pix);
+            const int64_t yi = (static_cast<int64_t>(b) * p.m + oc) * plane_out + pix;
+            const float bias = p.bias != nullptr ? p.bias[oc] : 0.f;
+            p.y[yi] = Finish(p, sum[e] + bias, yi);
+        }
+    }
+}
+
+void LaunchSplitReduce(const ConvArgs& p, int splits, hipStream_t stream) {
+    const int64_t per_split = p.group * p.mg * p.n_total;
+    const int vec = (p.plane_out % 4 == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0) ? 4 : 1;
+    if (vec == 1 && per_split % 4 == 0 && per_split < (int64_t{1} << 31)) {
+        ConvSplitReduceQuadKernel<<<GridFor(per_split / 4, 256, 8192), 256, 0, stream>>>(
+            p, splits, FastDiv::Make(static_cast<uint32_t>(p.n_total)),
+            FastDiv::Make(static_cast<uint32_t>(p.plane_out)));
+    } else {
+        ConvSplitReduceKernel<<<GridFor(per_split / vec, 256, 8192), 256, 0, stream>>>(p, splits, vec);
+    }
+    CheckLaunch("ConvSplitReduceKernel launch");
+}
+
 // Eight waves per workgroup, 64x32 or 32x64 each: measured on the ResNet-18
 // bs32 layers, two waves per SIMD from one workgroup hide the gather latency
 // better than four waves with 64x64 tiles (1.3-1.5x faster per layer).
@@ -562,10 +603,7 @@ void LaunchConv(ConvArgs p, hipStream_t stream) {
     }
     CheckLaunch("ConvKernel launch");
     if (splits > 1) {
-        const int vec = (p.plane_out % 4 == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0) ? 4 : 1;
-        const int64_t work = p.group * p.mg * p.n_total / vec;
-        ConvSplitReduceKernel<<<GridFor(work, 256, 8192), 256, 0, stream>>>(p, splits, vec);
-        CheckLaunch("ConvSplitReduceKernel launch");
+        LaunchSplitReduce(p, splits, stream);
     }
 }
 
@@ -852,7 +890,61 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
 }
 
 // Sums each tail tile's pieces in piece order (deterministic) and applies the
-// epilogue the other workgroups apply (group 1).
+// epilogue the other workgroups apply (group 1). Four consecutive columns of
+// a tile row per thread (16-byte loads of every piece, issued together),
+// 32-bit index decoding; the same additions in the same order as
+// ConvTailReduceKernel below, so the results are identical.
+__global__ __launch_bounds__(256) void ConvTailReduceQuadKernel(ConvArgs p, int n_full, int pieces, int bm, int bn,
+                                                                const float* partial, uint32_t quads,
+                                                                FastDiv div_tile_quads, FastDiv div_row_quads,
+                                                                FastDiv div_tiles_m, FastDiv div_plane) {
+    const uint32_t per_tile = static_cast<uint32_t>(bm * bn);
+    const int plane_out = static_cast<int>(p.plane_out);
+    for (uint32_t q = blockIdx.x * 256u + threadIdx.x; q < quads; q += gridDim.x * 256u) {
+        uint32_t rc4, c4, tm;
+        const uint32_t t = DivMod(div_tile_quads, q, rc4);
+        const uint32_t r = DivMod(div_row_quads, rc4, c4);
+        const uint32_t tn = DivMod(div_tiles_m, static_cast<uint32_t>(n_full) + t, tm);
+        const uint32_t gr = tm * bm + r;
+        if (gr >= p.mg) {
+            continue;
+        }
+        const uint32_t gc0 = tn * bn + 4 * c4;
+        const float* src = partial + static_cast<int64_t>(t) * pieces * per_tile + r * bn + 4 * c4;
+        nert_floatx4 v = *reinterpret_cast<const nert_floatx4*>(src);
+        int qp = 1;
+        for (; qp + 3 < pieces; qp += 4) {
+            const nert_floatx4 a = *reinterpret_cast<const nert_floatx4*>(src + qp * per_tile);
+            const nert_floatx4 b = *reinterpret_cast<const nert_floatx4*>(src + (qp + 1) * per_tile);
+            const nert_floatx4 c = *reinterpret_cast<const nert_floatx4*>(src + (qp + 2) * per_tile);
+            const nert_floatx4 d = *reinterpret_cast<const nert_floatx4*>(src + (qp + 3) * per_tile);
+            v += a;
+            v += b;
+            v += c;
+            v += d;
+        }
+        for (; qp < pieces; ++qp) {
+            v += *reinterpret_cast<const nert_floatx4*>(src + qp * per_tile);
+        }
+        const float bias = p.bias != nullptr ? p.bias[gr] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t gc = gc0 + e;
+            if (gc >= p.n_total) {
+                break;
+            }
+            uint32_t pix;
+            const uint32_t b = DivMod(div_plane, gc, pix);
+            const int64_t yi = (static_cast<int64_t>(b) * p.m + gr) * plane_out + pix;
+            float out = v[e];
+            if (p.bias != nullptr) {
+                out = out + bias;
+            }
+            p.y[yi] = Finish(p, out, yi);
+        }
+    }
+}
+
 __global__ void ConvTailReduceKernel(ConvArgs p, int n_full, int pieces, int bm, int bn, const float* partial,
                                      int64_t tail_tiles) {
     const int64_t tiles_m = (p.mg + bm - 1) / bm;
@@ -982,8 +1074,17 @@ bool TryHaloShape(ConvArgs p, hipStream_t stream, int force_splits, bool tail = 
             LaunchHalo<Shape, 4>(p, h, grid, static_cast<size_t>(lds), stream);
         }
         CheckLaunch("HaloConvKernel launch");
-        ConvTailReduceKernel<<<GridFor(rest * per_tile, 256, 4096), 256, 0, stream>>>(
-            p, h.n_full, h.tail_pieces, Shape::kBM, Shape::kBN, h.tail_partial, rest);
+        const int64_t tiles_m = (p.mg + Shape::kBM - 1) / Shape::kBM;
+        if (rest * per_tile < (int64_t{1} << 31) && p.n_total < (int64_t{1} << 31) && Shape::kBN % 4 == 0) {
+            const auto quads = static_cast<uint32_t>(rest * per_tile / 4);
+            ConvTailReduceQuadKernel<<<GridFor(quads, 256, 8192), 256, 0, stream>>>(
+                p, h.n_full, h.tail_pieces, Shape::kBM, Shape::kBN, h.tail_partial, quads,
+                FastDiv::Make(static_cast<uint32_t>(per_tile / 4)), FastDiv::Make(Shape::kBN / 4),
+                FastDiv::Make(static_cast<uint32_t>(tiles_m)), FastDiv::Make(static_cast<uint32_t>(p.plane_out)));
+        } else {
+            ConvTailReduceKernel<<<GridFor(rest * per_tile, 256, 4096), 256, 0, stream>>>(
+                p, h.n_full, h.tail_pieces, Shape::kBM, Shape::kBN, h.tail_partial, rest);
+        }
         CheckLaunch("ConvTailReduceKernel launch");
         return true;
     }
@@ -1008,10 +1109,7 @@ bool TryHaloShape(ConvArgs p, hipStream_t stream, int force_splits, bool tail = 
     }
     CheckLaunch("HaloConvKernel launch");
     if (splits > 1) {
-        const int vec = (p.plane_out % 4 == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0) ? 4 : 1;
-        const int64_t work = p.group * p.mg * p.n_total / vec;
-        ConvSplitReduceKernel<<<GridFor(work, 256, 8192), 256, 0, stream>>>(p, splits, vec);
-        CheckLaunch("ConvSplitReduceKernel launch");
+        LaunchSplitReduce(p, splits, stream);
     }
     return true;
 }
