@@ -661,13 +661,15 @@ template <class Shape, int KH, int KW, int NPOS>
 __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKernel(ConvArgs p, HaloGeom h) {
     constexpr int BM = Shape::kBM;
     constexpr int BN = Shape::kBN;
-    constexpr int BK = kHaloBK;
+    constexpr int BK = Shape::kBK;      // channels per K step: 8 or 16
+    constexpr int CS = BK + 4;          // LDS floats per patch position
+    constexpr int KG = BK / 8;          // groups of 8 channels (one k-quad pair each)
     constexpr int THREADS = Shape::kThreads;
     constexpr int kTaps = KH * KW;
     constexpr int kAPitch = kTaps * BK + 4;                        // [m][tap][c] rows, 16-byte aligned
     constexpr int kQuadsRow = kTaps * BK / 4;                      // 16-byte weight loads per row and block
     constexpr int kAQuads = (BM * kQuadsRow + THREADS - 1) / THREADS; // weight loads per thread
-    static_assert(BK == 8 && (kTaps * BK) % 4 == 0, "weight rows must split into 16-byte loads");
+    static_assert(BK % 8 == 0 && (kTaps * BK) % 4 == 0, "weight rows must split into 16-byte loads");
     extern __shared__ __attribute__((aligned(16))) float smem[];
     float* const as = smem;
     float* const bs = smem + BM * kAPitch;
@@ -770,10 +772,10 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
             const int32_t first = seg == 0 ? oh_first : 0;
             pos = (start + (oh - first) * p.s_h) * h.pw + static_cast<int32_t>(ow) * p.s_w;
         }
-        b_lane[j] = pos * kHaloCS + half * 4;
+        b_lane[j] = pos * CS + half * 4;
     }
-    const int row_step = p.d_h * h.pw * kHaloCS;
-    const int col_step = p.d_w * kHaloCS;
+    const int row_step = p.d_h * h.pw * CS;
+    const int col_step = p.d_w * CS;
 
     float bv[NPOS][BK];
     nert_floatx4 av[kAQuads];
@@ -798,9 +800,12 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
         for (int i = 0; i < NPOS; ++i) {
             const int q = tid + i * THREADS;
             if (q < h.positions) {
-                float* dst = bs + q * kHaloCS;
-                *reinterpret_cast<nert_floatx4*>(dst) = nert_floatx4{bv[i][0], bv[i][1], bv[i][2], bv[i][3]};
-                *reinterpret_cast<nert_floatx4*>(dst + 4) = nert_floatx4{bv[i][4], bv[i][5], bv[i][6], bv[i][7]};
+                float* dst = bs + q * CS;
+#pragma unroll
+                for (int c4 = 0; c4 < BK / 4; ++c4) {
+                    *reinterpret_cast<nert_floatx4*>(dst + 4 * c4) =
+                        nert_floatx4{bv[i][4 * c4], bv[i][4 * c4 + 1], bv[i][4 * c4 + 2], bv[i][4 * c4 + 3]};
+                }
             }
         }
         // Weight float k of a row slice is channel k / kTaps, tap k % kTaps.
@@ -833,47 +838,61 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
         // Operands of tap t + 1 are read while the MFMAs of tap t run; the
         // scheduling barriers keep the compiler from sinking the reads back
         // behind the MFMAs.
-        nert_floatx4 a_next[Shape::kSubM];
-        nert_floatx4 b_next[Shape::kSubN];
+        nert_floatx4 a_next[Shape::kSubM][KG];
+        nert_floatx4 b_next[Shape::kSubN][KG];
 #pragma unroll
-        for (int i = 0; i < Shape::kSubM; ++i) {
-            a_next[i] = *reinterpret_cast<const nert_floatx4*>(as + a_lane + i * 32 * kAPitch);
-        }
-#pragma unroll
-        for (int j = 0; j < Shape::kSubN; ++j) {
-            b_next[j] = *reinterpret_cast<const nert_floatx4*>(bs + b_lane[j]);
-        }
-#pragma unroll
-        for (int t = 0; t < kTaps; ++t) {
-            nert_floatx4 a[Shape::kSubM];
-            nert_floatx4 b[Shape::kSubN];
+        for (int g = 0; g < KG; ++g) {
 #pragma unroll
             for (int i = 0; i < Shape::kSubM; ++i) {
-                a[i] = a_next[i];
+                a_next[i][g] = *reinterpret_cast<const nert_floatx4*>(as + a_lane + i * 32 * kAPitch + 8 * g);
             }
 #pragma unroll
             for (int j = 0; j < Shape::kSubN; ++j) {
-                b[j] = b_next[j];
+                b_next[j][g] = *reinterpret_cast<const nert_floatx4*>(bs + b_lane[j] + 8 * g);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < kTaps; ++t) {
+            nert_floatx4 a[Shape::kSubM][KG];
+            nert_floatx4 b[Shape::kSubN][KG];
+#pragma unroll
+            for (int g = 0; g < KG; ++g) {
+#pragma unroll
+                for (int i = 0; i < Shape::kSubM; ++i) {
+                    a[i][g] = a_next[i][g];
+                }
+#pragma unroll
+                for (int j = 0; j < Shape::kSubN; ++j) {
+                    b[j][g] = b_next[j][g];
+                }
             }
             if (t + 1 < kTaps) {
                 const int toff = ((t + 1) / KW) * row_step + ((t + 1) % KW) * col_step;
 #pragma unroll
-                for (int i = 0; i < Shape::kSubM; ++i) {
-                    a_next[i] = *reinterpret_cast<const nert_floatx4*>(as + a_lane + i * 32 * kAPitch + (t + 1) * BK);
-                }
+                for (int g = 0; g < KG; ++g) {
 #pragma unroll
-                for (int j = 0; j < Shape::kSubN; ++j) {
-                    b_next[j] = *reinterpret_cast<const nert_floatx4*>(bs + b_lane[j] + toff);
+                    for (int i = 0; i < Shape::kSubM; ++i) {
+                        a_next[i][g] = *reinterpret_cast<const nert_floatx4*>(as + a_lane + i * 32 * kAPitch +
+                                                                              (t + 1) * BK + 8 * g);
+                    }
+#pragma unroll
+                    for (int j = 0; j < Shape::kSubN; ++j) {
+                        b_next[j][g] = *reinterpret_cast<const nert_floatx4*>(bs + b_lane[j] + toff + 8 * g);
+                    }
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
+            for (int g = 0; g < KG; ++g) {
 #pragma unroll
-                for (int i = 0; i < Shape::kSubM; ++i) {
+                for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
-                    for (int j = 0; j < Shape::kSubN; ++j) {
-                        acc.c[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][kk], b[j][kk], acc.c[i][j], 0, 0, 0);
+                    for (int i = 0; i < Shape::kSubM; ++i) {
+#pragma unroll
+                        for (int j = 0; j < Shape::kSubN; ++j) {
+                            acc.c[i][j] =
+                                __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][g][kk], b[j][g][kk], acc.c[i][j], 0, 0, 0);
+                        }
                     }
                 }
             }
@@ -984,10 +1003,38 @@ using HaloShapeW = TileShape<64, 256, kHaloBK, 2, 4>; // 8 waves, 32x64 each (M_
 using HaloShapeM = TileShape<64, 128, kHaloBK, 2, 4>; // 8 waves, 32x32 each
 using HaloShapeQ = TileShape<64, 64, kHaloBK, 2, 2>;  // 4 waves, 32x32 each
 using HaloShapeN = TileShape<32, 128, kHaloBK, 1, 4>; // 4 waves, 32x32 each
+// The same 32x32-per-wave shapes with 16 channels per K step: twice the MFMAs
+// per LDS-store/barrier phase, twice the LDS.
+using HaloShapeM16 = TileShape<64, 128, 16, 2, 4>;
+using HaloShapeQ16 = TileShape<64, 64, 16, 2, 2>;
+using HaloShapeN16 = TileShape<32, 128, 16, 1, 4>;
 
 template <class Shape, int NPOS>
 void LaunchHalo(const ConvArgs& p, const HaloGeom& h, dim3 grid, size_t lds, hipStream_t stream) {
     HaloConvKernel<Shape, 3, 3, NPOS><<<grid, Shape::kThreads, lds, stream>>>(p, h);
+}
+
+// Shapes with 16-channel K steps need more than the 64 KiB default of
+// dynamic LDS (up to kHaloMaxLds16, two workgroups per CU): raised once per
+// process for the shape's kernels; false when the runtime refuses.
+constexpr int kHaloMaxLds16 = 80 * 1024;
+
+template <class Shape>
+bool AllowHaloLds() {
+    static const bool allowed = [] {
+        bool ok = true;
+        ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(&HaloConvKernel<Shape, 3, 3, 1>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kHaloMaxLds16) == hipSuccess;
+        ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(&HaloConvKernel<Shape, 3, 3, 2>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kHaloMaxLds16) == hipSuccess;
+        ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(&HaloConvKernel<Shape, 3, 3, 4>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kHaloMaxLds16) == hipSuccess;
+        if (!ok) {
+            (void)hipGetLastError();
+        }
+        return ok;
+    }();
+    return allowed;
 }
 
 // 3x3, 2-D, C_g a multiple of kHaloBK, stride no larger than the filter's
@@ -1021,8 +1068,12 @@ bool TryHaloShape(ConvArgs p, hipStream_t stream, int force_splits, bool tail = 
     const int64_t s_max = std::min<int64_t>((r_max - 1 + p.out_h - 1) / p.out_h + 1, p.batch);
     const int64_t rows = r_max * p.s_h + s_max * (2 * p.d_h + 1 - p.s_h);
     const int64_t positions = rows * h.pw;
-    const int64_t lds = (static_cast<int64_t>(Shape::kBM) * (kTaps * kHaloBK + 4) + positions * kHaloCS) * 4;
-    if (lds > kHaloMaxLds) {
+    constexpr int BK = Shape::kBK;
+    if (p.cg % BK != 0) {
+        return false;
+    }
+    const int64_t lds = (static_cast<int64_t>(Shape::kBM) * (kTaps * BK + 4) + positions * (BK + 4)) * 4;
+    if (lds > (BK > 8 ? kHaloMaxLds16 : kHaloMaxLds) || (lds > kHaloMaxLds && !AllowHaloLds<Shape>())) {
         return false;
     }
     const int64_t per_thread = (positions + Shape::kThreads - 1) / Shape::kThreads;
@@ -1030,7 +1081,7 @@ bool TryHaloShape(ConvArgs p, hipStream_t stream, int force_splits, bool tail = 
         return false;
     }
     h.positions = static_cast<int32_t>(positions);
-    h.blocks = static_cast<int32_t>(p.cg / kHaloBK);
+    h.blocks = static_cast<int32_t>(p.cg / BK);
     h.div_plane_out = FastDiv::Make(static_cast<uint32_t>(p.plane_out));
     h.div_out_w = FastDiv::Make(static_cast<uint32_t>(p.out_w));
     h.div_pw = FastDiv::Make(static_cast<uint32_t>(h.pw));
@@ -1148,11 +1199,25 @@ int ChooseConvConfig(std::map<ConvKey, int>& cache, const ConvArgs& p, hipStream
 
 // 3x3 candidates: tile shape i / 4 (0 W, 1 M, 2 Q, 3 N) with split-K count
 // {PlanSplits' choice, 1, 2, 4}[i % 4]; 16 + s: shape s with the tail split;
-// 20 + s: shape s with the balanced split count.
-constexpr int kHaloCandidates = 24;
+// 20 + s: shape s with the balanced split count; 24 + 3 s + v: the
+// 16-channel shape s (0 M16, 1 Q16, 2 N16) with v = 0 PlanSplits' choice,
+// 1 the tail split, 2 the balanced split count.
+constexpr int kHaloCandidates = 33;
+
+template <class Shape>
+bool TryHalo16(const ConvArgs& p, hipStream_t stream, int v) {
+    return v == 0 ? TryHaloShape<Shape>(p, stream, 0)
+                  : (v == 1 ? TryHaloShape<Shape>(p, stream, 0, true) : TryHaloShape<Shape>(p, stream, -1));
+}
 
 bool LaunchHaloCandidate(int i, const ConvArgs& p, hipStream_t stream) {
     static constexpr int kSplits[4] = {0, 1, 2, 4};
+    if (i >= 24) {
+        const int s16 = (i - 24) / 3;
+        const int v = (i - 24) % 3;
+        return s16 == 0 ? TryHalo16<HaloShapeM16>(p, stream, v)
+                        : (s16 == 1 ? TryHalo16<HaloShapeQ16>(p, stream, v) : TryHalo16<HaloShapeN16>(p, stream, v));
+    }
     if (i >= 20) {
         switch (i - 20) {
         case 0:

@@ -385,11 +385,12 @@ np.save({out2!r}, hip("FusedConv", [x, w, b, z], z.shape, dict(a, activation="Re
 
 
 @pytest.mark.parametrize("batch,hw", [(17, 32), (32, 28)])
-@pytest.mark.parametrize("cand", [0, 9, 14, 18, 19, 22, 23])
+@pytest.mark.parametrize("cand", [0, 9, 14, 18, 19, 22, 23] + list(range(24, 33)))
 def test_conv_lds_patch_forced_configs(gpu, tmp_path, batch, hw, cand):
-    """Each 3x3 configuration (tile shapes, split counts, and the tail split
-    that cuts the last partial round of tiles along the channels: 16 tiles in
-    8 pieces, or 136 tiles in halves) computes the same convolution: forced in
+    """Each 3x3 configuration (tile shapes with 8- and 16-channel K steps,
+    split counts, and the tail split that cuts the last partial round of tiles
+    along the channels: 16 tiles in 8 pieces, or 136 tiles in halves)
+    computes the same convolution: forced in
     a child process, compared with the restatement and with the fused
     epilogue applied by hand."""
     x = randn((batch, 64, hw, hw), seed=80)
