@@ -681,7 +681,17 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
     const int wave_n = wave / Shape::kWavesM;
     const int half = lane >> 5;
     const int64_t tiles_m = (p.mg + BM - 1) / BM;
+    // Workgroups are dispatched round-robin over the 8 XCDs (workgroup i on
+    // XCD i % 8), each with its own L2. Remap so that each XCD takes one
+    // contiguous run of tiles: neighbouring tiles share their input patch
+    // (the next channel tile) or its halo rows (the next pixel tile).
     int64_t tile = blockIdx.x;
+    {
+        const int64_t whole = (h.tail_pieces > 0 ? h.n_full : static_cast<int64_t>(gridDim.x)) / 8 * 8;
+        if (tile < whole) {
+            tile = (tile % 8) * (whole / 8) + tile / 8;
+        }
+    }
     const int g = blockIdx.y;
     const int split = blockIdx.z;
     int cb_begin = split * h.blocks_per_split;
