@@ -174,6 +174,16 @@ struct ConvBLoader {
 // clamped addresses, and no separate edge path. Requires both tensors under
 // 2 GiB (32-bit buffer offsets); the host checks.
 
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup i on XCD
+// i % 8), each with its own L2. Workgroup i of the first `count` rounded down
+// to a multiple of 8 takes tile (i % 8) * (whole / 8) + i / 8, so each XCD
+// works through one contiguous run of tiles, whose neighbours share operand
+// rows or columns in that XCD's L2; the rest keep their index.
+__device__ __forceinline__ int64_t XcdTile(int64_t i, int64_t count) {
+    const int64_t whole = count / 8 * 8;
+    return i < whole ? (i % 8) * (whole / 8) + i / 8 : i;
+}
+
 constexpr uint32_t kBufferWord3 = 0x00020000; // raw 32-bit dword buffer (gfx9 family)
 constexpr uint32_t kOutOfRange = 0x80000000u; // >= every num_records used here
 
@@ -384,7 +394,7 @@ template <class Shape, int KH, int KW>
 __global__ __launch_bounds__(Shape::kThreads) void ConvTapKernel(ConvArgs p) {
     __shared__ __attribute__((aligned(16))) float lds[2 * (Shape::kLdsA + Shape::kLdsB)];
     const int64_t tiles_m = (p.mg + Shape::kBM - 1) / Shape::kBM;
-    const int64_t tile = blockIdx.x;
+    const int64_t tile = XcdTile(blockIdx.x, gridDim.x);
     const int64_t row0 = (tile % tiles_m) * Shape::kBM;
     const int64_t col0 = (tile / tiles_m) * Shape::kBN;
     const int g = blockIdx.y;
@@ -408,7 +418,7 @@ template <class Shape, int KH, int KW>
 __global__ __launch_bounds__(Shape::kThreads) void ConvKernel(ConvArgs p) {
     __shared__ __attribute__((aligned(16))) float lds[2 * (Shape::kLdsA + Shape::kLdsB)];
     const int64_t tiles_m = (p.mg + Shape::kBM - 1) / Shape::kBM;
-    const int64_t tile = blockIdx.x;
+    const int64_t tile = XcdTile(blockIdx.x, gridDim.x);
     const int64_t tm = tile % tiles_m;
     const int64_t tn = tile / tiles_m;
     const int64_t row0 = tm * Shape::kBM;
@@ -685,13 +695,7 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
     // XCD i % 8), each with its own L2. Remap so that each XCD takes one
     // contiguous run of tiles: neighbouring tiles share their input patch
     // (the next channel tile) or its halo rows (the next pixel tile).
-    int64_t tile = blockIdx.x;
-    {
-        const int64_t whole = (h.tail_pieces > 0 ? h.n_full : static_cast<int64_t>(gridDim.x)) / 8 * 8;
-        if (tile < whole) {
-            tile = (tile % 8) * (whole / 8) + tile / 8;
-        }
-    }
+    int64_t tile = XcdTile(blockIdx.x, h.tail_pieces > 0 ? h.n_full : static_cast<int64_t>(gridDim.x));
     const int g = blockIdx.y;
     const int split = blockIdx.z;
     int cb_begin = split * h.blocks_per_split;
