@@ -432,12 +432,23 @@ __global__ __launch_bounds__(256) void LayerNormRegKernel(const float* __restric
     }
     const float* p = x + row * inner;
     float* q = y + row * inner;
-    // Clamped-address loads, then a select (see SoftmaxRowsRegKernel).
+    // Clamped-address loads, then a select (see SoftmaxRowsRegKernel). Scale
+    // and bias are read in the same batch as the row, unconditionally (a
+    // scalar or absent operand reads element 0 of a valid array), so the three
+    // streams of loads share one round trip to memory.
+    const float* bsrc = bias != nullptr ? bias : scale;
+    const int sstep = scale_scalar ? 0 : 1;
+    const int bstep = bias == nullptr || bias_scalar ? 0 : 1;
     float v[PER];
+    float sc[PER];
+    float bi[PER];
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
         const int i = lane + 64 * k;
-        v[k] = p[i < inner ? i : inner - 1];
+        const int ic = i < inner ? i : inner - 1;
+        v[k] = p[ic];
+        sc[k] = scale[ic * sstep];
+        bi[k] = bsrc[ic * bstep];
     }
     double sum = 0.0;
 #pragma unroll
@@ -455,15 +466,6 @@ __global__ __launch_bounds__(256) void LayerNormRegKernel(const float* __restric
         }
     }
     const double inv = 1.0 / sqrt(WaveAllSum(sq) / static_cast<double>(inner) + eps);
-    float sc[PER];
-    float bi[PER];
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        const int i = lane + 64 * k;
-        const int ic = i < inner ? i : inner - 1;
-        sc[k] = scale[scale_scalar ? 0 : ic];
-        bi[k] = bias != nullptr ? bias[bias_scalar ? 0 : ic] : 0.0f;
-    }
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
         const int i = lane + 64 * k;

@@ -99,6 +99,8 @@ def test_layernorm(gpu, shape, axis):
     mean_shape = shape[:ax] + (1,) * (len(shape) - ax)
     assert_parity("LayerNormalization", [x, np.array([1.5], F)], [(shape, F), (mean_shape, F), (mean_shape, F)],
                   {"axis": axis})
+    assert_parity("LayerNormalization", [x, np.array([0.75], F), np.array([-0.25], F)], [(shape, F)],
+                  {"axis": axis})
     assert outer > 0
 
 
