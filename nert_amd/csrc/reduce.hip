@@ -293,14 +293,17 @@ __global__ __launch_bounds__(256) void SoftmaxRowsKernel(const float* __restrict
     }
 }
 
-// Rows of at most 64 * PER elements: the row is read once into registers and
-// each exponential is computed once (the reference evaluates the same exp
-// twice, so reusing it gives the same values).
-template <int PER>
+// Rows of at most LANES * PER elements: the row is read once into registers
+// and each exponential is computed once (the reference evaluates the same exp
+// twice, so reusing it gives the same values). LANES = 32 puts two rows on
+// each wave (shuffles of width 32 stay within a row's half): short rows then
+// run on half as many waves, with twice the independent work per wave.
+template <int PER, int LANES = 64>
 __global__ __launch_bounds__(256) void SoftmaxRowsRegKernel(const float* __restrict__ x, float* __restrict__ y,
                                                             int64_t rows, int dim) {
-    const int lane = threadIdx.x & 63;
-    const int64_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    static_assert(LANES == 32 || LANES == 64, "a row takes a whole wave or half of one");
+    const int lane = threadIdx.x & (LANES - 1);
+    const int64_t row = blockIdx.x * static_cast<int64_t>(256 / LANES) + (threadIdx.x / LANES);
     if (row >= rows) {
         return;
     }
@@ -312,24 +315,24 @@ __global__ __launch_bounds__(256) void SoftmaxRowsRegKernel(const float* __restr
     float v[PER];
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-        const int i = lane + 64 * k;
+        const int i = lane + LANES * k;
         v[k] = p[i < dim ? i : dim - 1];
     }
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-        v[k] = lane + 64 * k < dim ? v[k] : -__builtin_huge_valf();
+        v[k] = lane + LANES * k < dim ? v[k] : -__builtin_huge_valf();
     }
     // Peak rule of the reference (value > peak from element 0): see
     // SoftmaxRowsKernel.
-    const float first = __shfl(v[0], 0, 64);
+    const float first = __shfl(v[0], 0, LANES);
     float peak = first;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
         peak = v[k] > peak ? v[k] : peak;
     }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float o = __shfl_xor(peak, off, 64);
+    for (int off = LANES / 2; off > 0; off >>= 1) {
+        const float o = __shfl_xor(peak, off, LANES);
         peak = o > peak ? o : peak;
     }
     if (first != first) {
@@ -340,13 +343,16 @@ __global__ __launch_bounds__(256) void SoftmaxRowsRegKernel(const float* __restr
     double total = 0.0;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-        e[k] = lane + 64 * k < dim ? exp(static_cast<double>(v[k]) - dp) : 0.0;
+        e[k] = lane + LANES * k < dim ? exp(static_cast<double>(v[k]) - dp) : 0.0;
         total += e[k];
     }
-    total = WaveAllSum(total);
+#pragma unroll
+    for (int off = LANES / 2; off > 0; off >>= 1) {
+        total += __shfl_xor(total, off, LANES);
+    }
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-        const int i = lane + 64 * k;
+        const int i = lane + LANES * k;
         if (i < dim) {
             q[i] = static_cast<float>(e[k] / total);
         }
@@ -774,6 +780,15 @@ unsigned RowBlocks(int64_t rows) {
     return static_cast<unsigned>(b < 1 ? 1 : b);
 }
 
+// Blocks of 256 threads for two rows per wave (eight rows per block).
+unsigned PairRowBlocks(int64_t rows) {
+    const int64_t b = (rows + 7) / 8;
+    if (b > 0x7FFFFFFF) {
+        throw Error("too many rows");
+    }
+    return static_cast<unsigned>(b < 1 ? 1 : b);
+}
+
 } // namespace
 } // namespace nert_hip
 
@@ -820,7 +835,9 @@ int nert_hip_softmax_f32(const float* x, float* y, int64_t outer, int64_t dim, i
             return;
         }
         hipStream_t s = StreamOr(stream);
-        if (inner == 1 && dim <= 256) {
+        if (inner == 1 && dim <= 224) {
+            SoftmaxRowsRegKernel<7, 32><<<PairRowBlocks(outer), 256, 0, s>>>(x, y, outer, static_cast<int>(dim));
+        } else if (inner == 1 && dim <= 256) {
             SoftmaxRowsRegKernel<4><<<RowBlocks(outer), 256, 0, s>>>(x, y, outer, static_cast<int>(dim));
         } else if (inner == 1 && dim <= 1024) {
             SoftmaxRowsRegKernel<16><<<RowBlocks(outer), 256, 0, s>>>(x, y, outer, static_cast<int>(dim));
