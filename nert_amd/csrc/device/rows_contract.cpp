@@ -1,9 +1,7 @@
 // Resampling and contraction rows: Resize, GridSample, Einsum,
-// ConvTranspose. Validation mirrors src/kernels/{resize,grid_sample,einsum,
-// conv_transpose}.cpp; the Einsum equation front end (ellipsis expansion,
-// implicit output, label binding) restates src/kernels/einsum.cpp:24-258
-// and its nert::einsum helpers (:291-492) so that the same equations resolve to the
-// same labels, sizes, strides and messages.
+// ConvTranspose. Each row rejects the nodes its reference row rejects
+// (src/kernels/{resize,grid_sample,einsum,conv_transpose}.cpp), in the same
+// order and with the same messages, before it queues any work.
 
 #include "rows.hpp"
 
@@ -201,191 +199,117 @@ NERT_HIP_ROW(GridSample) {
 }
 
 // ---- Einsum -------------------------------------------------------------------
+//
+// Front end, from the ONNX Einsum rules: the equation is scanned once into
+// terms of integer label ids. Letters keep their ASCII order as ids
+// ('A'..'Z' = 0..25, 'a'..'z' = 26..51), so "alphabetical" (the implicit
+// output, the summation order) is id order. An ellipsis stands for up to W
+// batch slots, W being the widest ellipsis over the operands; slot s has id
+// kSlotId + s, after every letter. Each operand's ellipsis dims fill the
+// last slots (right-aligned, NumPy broadcasting); the slots it does not
+// reach, and all slots of an operand without an ellipsis, are virtual:
+// extent 1, stride 0, no storage. Slots broadcast (1 against n); letters
+// must agree exactly. The row then hands the kernel one extent and one
+// stride per operand for every output label and every summed label.
+// Rejections, their order and their text follow src/kernels/einsum.cpp
+// (the seam compares messages verbatim).
 
 namespace {
 
-bool IsLabel(char c) { return (c >= 'a' && c <= 'z') || (c >= 'A' && c <= 'Z'); }
+constexpr int kLetterIds = 52;
+constexpr int kSlotId = 64;
 
-std::vector<std::string> SplitOperands(const std::string& lhs) {
-    std::vector<std::string> subs;
-    size_t start = 0;
-    while (true) {
-        const size_t comma = lhs.find(',', start);
-        subs.push_back(lhs.substr(start, comma == std::string::npos ? std::string::npos : comma - start));
-        if (comma == std::string::npos) {
-            return subs;
-        }
-        start = comma + 1;
+int LetterId(char c) {
+    if (c >= 'A' && c <= 'Z') {
+        return c - 'A';
     }
+    if (c >= 'a' && c <= 'z') {
+        return 26 + (c - 'a');
+    }
+    return -1;
 }
 
-// One subscript around its "...": false when the dots are not exactly one
-// "..." group (nert::einsum SplitEllipsis, src/kernels/einsum.cpp:291-315).
-bool SplitDots(const std::string& sub, std::string& left, std::string& right, bool& has) {
-    has = false;
-    left.clear();
-    right.clear();
-    size_t i = 0;
-    while (i < sub.size() && sub[i] != '.') {
-        left.push_back(sub[i++]);
-    }
-    if (i < sub.size()) {
-        if (sub.compare(i, 3, "...") != 0) {
-            return false;
-        }
-        has = true;
-        i += 3;
-        while (i < sub.size() && sub[i] != '.') {
-            right.push_back(sub[i++]);
-        }
-        if (i < sub.size()) {
-            return false;
-        }
-    }
-    return true;
-}
+// One subscript: its letters in order and where "..." sits among them.
+struct Term {
+    std::vector<int> ids;  // letter ids; -1 for a character that is no letter
+    int dots_at = -1;      // index into ids before which "..." stands, -1 if none
+    bool malformed_dots = false;  // dots other than exactly one "..." group
+    bool foreign_char = false;    // a character that is neither a letter nor a dot
 
-// An equation with every "..." replaced by fresh labels.
-struct Expanded {
-    std::string error;
-    std::vector<std::string> inputs;
-    std::string output;
-    std::vector<char> fresh;
-    std::vector<size_t> pads;
-    std::vector<size_t> lefts;
-    size_t width = 0;
+    const char* SyntaxError() const {
+        if (malformed_dots) {
+            return "dots must form exactly one '...' per subscript";
+        }
+        if (foreign_char) {
+            return "invalid character in the equation";
+        }
+        return nullptr;
+    }
 };
 
-// nert::einsum::EllipsisSyntaxError + ExpandEllipsis (src/kernels/einsum.cpp:317-459).
-Expanded ExpandDots(const std::string& text, const std::vector<size_t>& ranks) {
-    Expanded r;
+Term ScanTerm(const std::string& text, size_t begin, size_t end) {
+    Term t;
+    size_t dots = 0;
+    size_t first_dot = end;
+    for (size_t i = begin; i < end; ++i) {
+        const char c = text[i];
+        if (c == '.') {
+            if (dots++ == 0) {
+                first_dot = i;
+                t.dots_at = static_cast<int>(t.ids.size());
+            }
+            continue;
+        }
+        const int id = LetterId(c);
+        t.foreign_char = t.foreign_char || id < 0;
+        t.ids.push_back(id);
+    }
+    // Valid only as no dot at all or exactly three adjacent ones.
+    if (dots != 0 && !(dots == 3 && text[first_dot + 1] == '.' && text[first_dot + 2] == '.')) {
+        t.malformed_dots = true;
+    }
+    if (dots == 0) {
+        t.dots_at = -1;
+    }
+    return t;
+}
+
+struct Equation {
+    std::vector<Term> operands;
+    Term output;
+    bool explicit_output = false;
+    bool any_dots = false;
+};
+
+Equation ScanEquation(const std::string& text) {
+    Equation eq;
     const size_t arrow = text.find("->");
-    const std::string lhs = arrow == std::string::npos ? text : text.substr(0, arrow);
-    const std::vector<std::string> subs = SplitOperands(lhs);
-    std::vector<std::string> checked = subs;
-    if (arrow != std::string::npos) {
-        checked.push_back(text.substr(arrow + 2));
-    }
-    for (const std::string& sub : checked) {
-        std::string left, right;
-        bool has = false;
-        if (!SplitDots(sub, left, right, has)) {
-            r.error = "dots must form exactly one '...' per subscript";
-            return r;
+    const size_t lhs_end = arrow == std::string::npos ? text.size() : arrow;
+    size_t begin = 0;
+    for (size_t i = 0; i <= lhs_end; ++i) {
+        if (i == lhs_end || text[i] == ',') {
+            eq.operands.push_back(ScanTerm(text, begin, i));
+            begin = i + 1;
         }
-        for (char c : left + right) {
-            if (!IsLabel(c)) {
-                r.error = "invalid character in the equation";
-                return r;
-            }
-        }
-    }
-    if (subs.size() != ranks.size()) {
-        r.error = "operand count does not match the equation";
-        return r;
-    }
-    bool used[256] = {false};
-    for (char c : text) {
-        if (IsLabel(c)) {
-            used[static_cast<unsigned char>(c)] = true;
-        }
-    }
-    std::vector<std::string> lefts, rights;
-    std::vector<size_t> counts;
-    for (size_t i = 0; i < subs.size(); ++i) {
-        std::string left, right;
-        bool has = false;
-        SplitDots(subs[i], left, right, has);
-        if (ranks[i] < left.size() + right.size()) {
-            r.error = "operand rank is smaller than its explicit labels";
-            return r;
-        }
-        if (!has && ranks[i] != left.size() + right.size()) {
-            r.error = "operand rank does not match its subscript";
-            return r;
-        }
-        const size_t count = has ? ranks[i] - left.size() - right.size() : 0;
-        r.width = std::max(r.width, count);
-        lefts.push_back(left);
-        rights.push_back(right);
-        counts.push_back(count);
-    }
-    std::string pool;
-    for (char c = 'a'; c <= 'z'; ++c) {
-        if (!used[static_cast<unsigned char>(c)]) {
-            pool.push_back(c);
-        }
-    }
-    for (char c = 'A'; c <= 'Z'; ++c) {
-        if (!used[static_cast<unsigned char>(c)]) {
-            pool.push_back(c);
-        }
-    }
-    if (pool.size() < r.width) {
-        r.error = "equation leaves no fresh labels for the ellipsis";
-        return r;
-    }
-    const std::string fresh = pool.substr(0, r.width);
-    r.fresh.assign(fresh.begin(), fresh.end());
-    for (size_t i = 0; i < subs.size(); ++i) {
-        r.pads.push_back(r.width - counts[i]);
-        r.lefts.push_back(lefts[i].size());
-        r.inputs.push_back(lefts[i] + fresh + rights[i]);
     }
     if (arrow != std::string::npos) {
-        std::string left, right;
-        bool has = false;
-        SplitDots(text.substr(arrow + 2), left, right, has);
-        r.output = left + (has ? fresh : "") + right;
-    } else {
-        r.output = fresh;
+        eq.explicit_output = true;
+        eq.output = ScanTerm(text, arrow + 2, text.size());
     }
-    return r;
+    eq.any_dots = text.find('.') != std::string::npos;
+    return eq;
 }
 
-struct Mapped {
-    char label;
-    int64_t dim;
-    bool virtual_pad;
+// One storage (or virtual) axis of an operand, outermost first.
+struct Axis {
+    int label;
+    int64_t extent;
+    bool is_virtual;
 };
-
-// nert::einsum::MapOperand (src/kernels/einsum.cpp:461-492).
-bool MapDims(const std::string& sub, size_t left, size_t pad, size_t width, const std::vector<int64_t>& dims,
-             std::vector<Mapped>& mapped) {
-    mapped.clear();
-    size_t d = 0;
-    for (size_t q = 0; q < left && q < sub.size(); ++q) {
-        if (d >= dims.size()) {
-            return false;
-        }
-        mapped.push_back(Mapped{sub[q], dims[d++], false});
-    }
-    for (size_t p = 0; p < width; ++p) {
-        const size_t q = left + p;
-        if (q >= sub.size()) {
-            return false;
-        }
-        if (p < pad) {
-            mapped.push_back(Mapped{sub[q], 1, true});
-        } else {
-            if (d >= dims.size()) {
-                return false;
-            }
-            mapped.push_back(Mapped{sub[q], dims[d++], false});
-        }
-    }
-    for (size_t q = left + width; q < sub.size(); ++q) {
-        if (d >= dims.size()) {
-            return false;
-        }
-        mapped.push_back(Mapped{sub[q], dims[d++], false});
-    }
-    return d == dims.size();
-}
 
 } // namespace
 
-// src/kernels/einsum.cpp:36-132 (equation), 134-258 (row)
+// src/kernels/einsum.cpp:134-258 (row), equation rules :36-132, ellipsis :291-459
 NERT_HIP_ROW(Einsum) {
     const std::string context = "Einsum (node '" + node.name + "')";
     const Attribute* attr = nullptr;
@@ -407,151 +331,217 @@ NERT_HIP_ROW(Einsum) {
             text.push_back(c);
         }
     }
-    std::string eq_text = text;
-    std::vector<char> fresh;
-    std::vector<size_t> pads, lefts;
-    size_t width = 0;
-    if (text.find('.') != std::string::npos) {
-        if (text.find("->") == std::string::npos) {
-            throw InferenceException(context + ": implicit output with ellipsis is not supported");
+    const Equation eq = ScanEquation(text);
+    auto fail = [&](const char* why) { throw InferenceException(context + ": " + why); };
+
+    // Ellipsis slots: the widest operand ellipsis, checked against the ranks
+    // before anything else about the labels.
+    size_t slots = 0;
+    std::vector<size_t> covered(eq.operands.size(), 0);  // dims each operand's ellipsis covers
+    if (eq.any_dots) {
+        if (!eq.explicit_output) {
+            fail("implicit output with ellipsis is not supported");
         }
-        std::vector<size_t> ranks;
-        for (const TensorView& in : inputs) {
-            ranks.push_back(in.dims.size());
-        }
-        const Expanded ex = ExpandDots(text, ranks);
-        if (!ex.error.empty()) {
-            throw InferenceException(context + ": " + ex.error);
-        }
-        eq_text.clear();
-        for (size_t i = 0; i < ex.inputs.size(); ++i) {
-            if (i != 0) {
-                eq_text.push_back(',');
+        for (const Term& t : eq.operands) {
+            if (const char* why = t.SyntaxError()) {
+                fail(why);
             }
-            eq_text += ex.inputs[i];
         }
-        eq_text += "->" + ex.output;
-        fresh = ex.fresh;
-        pads = ex.pads;
-        lefts = ex.lefts;
-        width = ex.width;
-    }
-    const size_t arrow = eq_text.find("->");
-    const bool explicit_output = arrow != std::string::npos;
-    const std::vector<std::string> subs = SplitOperands(explicit_output ? eq_text.substr(0, arrow) : eq_text);
-    std::map<char, int> counts;
-    for (const std::string& sub : subs) {
-        for (char c : sub) {
-            if (!IsLabel(c)) {
-                throw InferenceException(context + ": invalid character in the equation");
-            }
-            ++counts[c];
+        if (const char* why = eq.output.SyntaxError()) {
+            fail(why);
         }
-    }
-    std::string output;
-    if (explicit_output) {
-        output = eq_text.substr(arrow + 2);
-        for (size_t i = 0; i < output.size(); ++i) {
-            if (counts.find(output[i]) == counts.end()) {
-                throw InferenceException(context + ": output label does not appear in the inputs");
+        if (eq.operands.size() != inputs.size()) {
+            fail("operand count does not match the equation");
+        }
+        for (size_t i = 0; i < eq.operands.size(); ++i) {
+            const Term& t = eq.operands[i];
+            const size_t rank = inputs[i].dims.size();
+            if (rank < t.ids.size()) {
+                fail("operand rank is smaller than its explicit labels");
             }
-            if (output.find(output[i]) != i) {
-                throw InferenceException(context + ": output label repeated");
+            if (t.dots_at < 0 && rank != t.ids.size()) {
+                fail("operand rank does not match its subscript");
             }
+            covered[i] = t.dots_at < 0 ? 0 : rank - t.ids.size();
+            slots = std::max(slots, covered[i]);
+        }
+        // The slots must fit in the letters the equation leaves unused: an
+        // equation that needs more is rejected.
+        bool seen[kLetterIds] = {false};
+        size_t letters = 0;
+        for (char c : text) {
+            const int id = LetterId(c);
+            if (id >= 0 && !seen[id]) {
+                seen[id] = true;
+                ++letters;
+            }
+        }
+        if (slots > kLetterIds - letters) {
+            fail("equation leaves no fresh labels for the ellipsis");
         }
     } else {
-        for (const auto& entry : counts) {
-            if (entry.second == 1) {
-                output.push_back(entry.first);
+        for (const Term& t : eq.operands) {
+            if (t.foreign_char) {
+                fail("invalid character in the equation");
             }
         }
     }
-    if (subs.size() != inputs.size() || inputs.empty() || inputs.size() > 2 || outputs.size() != 1) {
-        throw InferenceException(context + ": operand count does not match the equation");
+
+    // How often each label appears over the operands (every operand spells
+    // every slot once when the equation has an ellipsis).
+    std::map<int, int> uses;
+    for (const Term& t : eq.operands) {
+        for (int id : t.ids) {
+            ++uses[id];
+        }
+        for (size_t s = 0; s < slots; ++s) {
+            ++uses[kSlotId + static_cast<int>(s)];
+        }
+    }
+    std::vector<int> out_labels;
+    if (eq.explicit_output) {
+        // The output ids in spelling order, its "..." expanded to every slot.
+        std::vector<int> spelled;
+        const Term& o = eq.output;
+        for (size_t q = 0; q <= o.ids.size(); ++q) {
+            if (static_cast<int>(q) == o.dots_at) {
+                for (size_t s = 0; s < slots; ++s) {
+                    spelled.push_back(kSlotId + static_cast<int>(s));
+                }
+            }
+            if (q < o.ids.size()) {
+                spelled.push_back(o.ids[q]);
+            }
+        }
+        for (size_t q = 0; q < spelled.size(); ++q) {
+            if (spelled[q] < 0 || uses.count(spelled[q]) == 0) {
+                fail("output label does not appear in the inputs");
+            }
+            if (std::find(spelled.begin(), spelled.begin() + static_cast<std::ptrdiff_t>(q), spelled[q]) !=
+                spelled.begin() + static_cast<std::ptrdiff_t>(q)) {
+                fail("output label repeated");
+            }
+        }
+        out_labels = spelled;
+    } else {
+        for (const auto& [id, n] : uses) {
+            if (n == 1) {
+                out_labels.push_back(id);
+            }
+        }
+    }
+    if (eq.operands.size() != inputs.size() || inputs.empty() || inputs.size() > 2 || outputs.size() != 1) {
+        fail("operand count does not match the equation");
     }
     const TensorView& out = outputs[0];
     if (out.dtype != DataType::Float32) {
-        throw InferenceException(context + ": tensors must be float32");
+        fail("tensors must be float32");
     }
-    auto is_fresh = [&](char c) { return std::find(fresh.begin(), fresh.end(), c) != fresh.end(); };
-    std::vector<std::vector<Mapped>> mapped(inputs.size());
-    std::map<char, int64_t> sizes;
+
+    // Bind every label to one extent, operand by operand.
+    std::vector<std::vector<Axis>> axes(inputs.size());
+    std::map<int, int64_t> extent;
     for (size_t i = 0; i < inputs.size(); ++i) {
-        if (inputs[i].dtype != DataType::Float32) {
-            throw InferenceException(context + ": tensors must be float32");
+        const TensorView& in = inputs[i];
+        if (in.dtype != DataType::Float32) {
+            fail("tensors must be float32");
         }
-        if (inputs[i].data == nullptr) {
-            throw InferenceException(context + ": null buffer");
+        if (in.data == nullptr) {
+            fail("null buffer");
         }
-        const size_t left = i < lefts.size() ? lefts[i] : subs[i].size();
-        const size_t pad = i < pads.size() ? pads[i] : 0;
-        if (!MapDims(subs[i], left, pad, width, inputs[i].dims, mapped[i])) {
-            throw InferenceException(context + ": operand rank does not match its subscript");
+        const Term& t = eq.operands[i];
+        const size_t rank = in.dims.size();
+        const size_t real_slots = t.dots_at < 0 ? 0 : covered[i];
+        if (rank != t.ids.size() + real_slots) {
+            fail("operand rank does not match its subscript");
         }
-        for (const Mapped& entry : mapped[i]) {
-            if (entry.virtual_pad) {
-                sizes.emplace(entry.label, 1);
+        size_t d = 0;
+        const size_t before = t.dots_at < 0 ? t.ids.size() : static_cast<size_t>(t.dots_at);
+        for (size_t q = 0; q < before; ++q) {
+            axes[i].push_back(Axis{t.ids[q], in.dims[d++], false});
+        }
+        for (size_t s = 0; s < slots; ++s) {
+            const bool real = s + real_slots >= slots;
+            axes[i].push_back(Axis{kSlotId + static_cast<int>(s), real ? in.dims[d++] : 1, !real});
+        }
+        for (size_t q = before; q < t.ids.size(); ++q) {
+            axes[i].push_back(Axis{t.ids[q], in.dims[d++], false});
+        }
+        for (const Axis& a : axes[i]) {
+            if (a.is_virtual) {
+                extent.emplace(a.label, 1);
                 continue;
             }
-            if (entry.dim <= 0) {
-                throw InferenceException(context + ": non-positive dimension");
+            if (a.extent <= 0) {
+                fail("non-positive dimension");
             }
-            const auto inserted = sizes.emplace(entry.label, entry.dim);
-            if (!inserted.second && inserted.first->second != entry.dim) {
-                if (!is_fresh(entry.label) || (inserted.first->second != 1 && entry.dim != 1)) {
-                    throw InferenceException(context + ": label bound to two different sizes");
+            auto [it, fresh] = extent.emplace(a.label, a.extent);
+            if (!fresh && it->second != a.extent) {
+                const bool broadcasts = a.label >= kSlotId && (it->second == 1 || a.extent == 1);
+                if (!broadcasts) {
+                    fail("label bound to two different sizes");
                 }
-                inserted.first->second = std::max(inserted.first->second, entry.dim);
+                it->second = std::max(it->second, a.extent);
             }
         }
     }
-    std::vector<int64_t> expected;
-    for (char c : output) {
-        expected.push_back(sizes.at(c));
+    std::vector<int64_t> out_size;
+    for (int id : out_labels) {
+        out_size.push_back(extent.at(id));
     }
-    if (out.dims != expected) {
-        throw InferenceException(context + ": output shape does not match the operands");
+    if (out.dims != out_size) {
+        fail("output shape does not match the operands");
     }
     if (out.data == nullptr) {
-        throw InferenceException(context + ": null buffer");
+        fail("null buffer");
     }
-    // Per-label strides of each operand; repeated labels (diagonals) add up,
-    // broadcast ellipsis planes contribute none.
-    std::map<char, int64_t> stride_a, stride_b;
+
+    // Element strides per label and operand: a repeated label (a diagonal)
+    // adds its strides; a virtual or broadcast (extent 1) slot adds none.
+    std::vector<std::map<int, int64_t>> stride(2);
     for (size_t i = 0; i < inputs.size(); ++i) {
-        std::map<char, int64_t>& st = i == 0 ? stride_a : stride_b;
-        int64_t stride = 1;
-        for (size_t k = mapped[i].size(); k-- > 0;) {
-            const Mapped& entry = mapped[i][k];
-            if (entry.virtual_pad || entry.dim != sizes.at(entry.label)) {
-                if (!entry.virtual_pad && (!is_fresh(entry.label) || entry.dim != 1)) {
-                    throw InferenceException(context + ": broadcast diagonal is not supported");
-                }
-            } else {
-                st[entry.label] += stride;
+        int64_t step = 1;
+        for (size_t k = axes[i].size(); k-- > 0;) {
+            const Axis& a = axes[i][k];
+            if (!a.is_virtual && a.extent == extent.at(a.label)) {
+                stride[i][a.label] += step;
+            } else if (!a.is_virtual && !(a.label >= kSlotId && a.extent == 1)) {
+                fail("broadcast diagonal is not supported");
             }
-            stride *= entry.dim;
+            step *= a.extent;
         }
     }
-    auto at = [](const std::map<char, int64_t>& m, char c) {
-        const auto it = m.find(c);
-        return it == m.end() ? int64_t{0} : it->second;
+    auto stride_of = [&](size_t i, int id) {
+        const auto it = stride[i].find(id);
+        return it == stride[i].end() ? int64_t{0} : it->second;
     };
-    std::vector<int64_t> out_size, out_sa, out_sb, sum_size, sum_sa, sum_sb;
-    for (char c : output) {
-        out_size.push_back(sizes.at(c));
-        out_sa.push_back(at(stride_a, c));
-        out_sb.push_back(at(stride_b, c));
+    std::vector<int64_t> out_sa, out_sb, sum_size, sum_sa, sum_sb;
+    for (int id : out_labels) {
+        out_sa.push_back(stride_of(0, id));
+        out_sb.push_back(stride_of(1, id));
     }
-    for (const auto& entry : sizes) { // alphabetical, as the reference odometer
-        if (output.find(entry.first) == std::string::npos) {
-            sum_size.push_back(entry.second);
-            sum_sa.push_back(at(stride_a, entry.first));
-            sum_sb.push_back(at(stride_b, entry.first));
+    for (const auto& [id, n] : extent) {  // summed labels in id order
+        if (std::find(out_labels.begin(), out_labels.end(), id) == out_labels.end()) {
+            sum_size.push_back(n);
+            sum_sa.push_back(stride_of(0, id));
+            sum_sb.push_back(stride_of(1, id));
         }
     }
     if (out_size.size() > 16 || sum_size.size() > 16) {
-        throw InferenceException(context + ": more than 16 output or summed labels");
+        fail("more than 16 output or summed labels");
+    }
+    // Every offset the kernel forms must stay inside its operand.
+    for (size_t i = 0; i < inputs.size(); ++i) {
+        int64_t last = 0;
+        for (size_t d = 0; d < out_size.size(); ++d) {
+            last += (out_size[d] - 1) * (i == 0 ? out_sa[d] : out_sb[d]);
+        }
+        for (size_t d = 0; d < sum_size.size(); ++d) {
+            last += (sum_size[d] - 1) * (i == 0 ? sum_sa[d] : sum_sb[d]);
+        }
+        if (last >= ElementCount(inputs[i].dims, context)) {
+            fail("internal error: operand strides exceed the operand");
+        }
     }
     CheckStatus(nert_hip_einsum_f32(static_cast<const float*>(inputs[0].data),
                                     inputs.size() == 2 ? static_cast<const float*>(inputs[1].data) : nullptr,

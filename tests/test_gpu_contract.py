@@ -186,6 +186,84 @@ def test_einsum_errors(gpu):
     assert_same_error("Einsum", [a, b], [((3, 5), F)], {"equation": "ijk,jk->ik"})
     assert_same_error("Einsum", [a, b], [((3, 6), F)], {"equation": "ij,jk->ik"})
     assert_same_error("Einsum", [a, b], [((3, 5), F)], {})
+    c3 = randn((2, 3, 4))
+    assert_same_error("Einsum", [c3, b], [((3, 5), F)], {"equation": "...ij,jk"})           # implicit + ellipsis
+    assert_same_error("Einsum", [c3, b], [((3, 5), F)], {"equation": "abcd...,jk->...k"})   # rank below labels
+    assert_same_error("Einsum", [c3, b], [((3, 5), F)], {"equation": "...ij,j->...i"})      # no ellipsis, rank off
+    assert_same_error("Einsum", [c3, b], [((3, 5), F)], {"equation": "....ij,jk->...ik"})   # four dots
+    assert_same_error("Einsum", [c3, b], [((3, 5), F)], {"equation": "...ij,jk->...i.k"})   # dots in output
+    assert_same_error("Einsum", [c3, b], [((3, 5), F)], {"equation": "...ij,jk->...i1"})    # foreign output char
+    assert_same_error("Einsum", [c3, b], [((3, 5), F)], {"equation": "...ij,jk->...ii"})    # repeated output label
+    assert_same_error("Einsum", [c3, b], [((3, 5), F)], {"equation": "...ij,jk->...iq"})    # unknown output label
+    assert_same_error("Einsum", [c3], [((3, 5), F)], {"equation": "...ij,jk->...ik"})       # operand count (dots)
+    assert_same_error("Einsum", [c3, randn((3, 4, 5))], [((2, 3, 5), F)],
+                      {"equation": "...ij,...jk->...ik"})                                   # slots 2 vs 3
+    wide = "".join(chr(c) for c in range(ord("a"), ord("z") + 1)) + "".join(
+        chr(c) for c in range(ord("A"), ord("Y") + 1))                                      # 51 letters used
+    assert_same_error("Einsum", [randn((1,) * 53)], [((1,), F)],
+                      {"equation": wide + "...->" + "..."})                                 # no fresh labels left
+
+
+def _einsum_outcome(equation, xs, out_shape):
+    from rowcheck import run_hip, run_ref
+
+    specs = [(out_shape, F)]
+    want, ref_err = run_ref("Einsum", xs, specs, {"equation": equation}, name="fz")
+    got, hip_err = run_hip("Einsum", xs, specs, {"equation": equation}, name="fz")
+    if ref_err is not None or hip_err is not None:
+        assert ref_err is not None and hip_err is not None, (equation, ref_err, hip_err)
+        assert hip_err.message == ref_err.message, (equation, hip_err.message, ref_err.message)
+        return False
+    from rowcheck import compare
+
+    compare(got[0], want[0], what=equation)
+    return True
+
+
+def test_einsum_random_equations(gpu):
+    """Random equations, valid and not, over a small alphabet: the HIP row
+    accepts exactly what the reference row accepts, rejects with the same
+    message, and agrees with it on the result."""
+    r = rng(77)
+    letters = "ijkAB"
+    accepted = 0
+    for case in range(300):
+        n_ops = int(r.integers(1, 3)) if case % 17 else int(r.integers(1, 4))
+        subs, shapes = [], []
+        extents = {c: int(r.integers(1, 4)) for c in letters}
+        batch = [int(r.integers(1, 4)) for _ in range(3)]
+        for _ in range(n_ops):
+            labels = [letters[int(k)] for k in r.integers(0, len(letters), int(r.integers(0, 4)))]
+            dims = [extents[c] for c in labels]
+            if r.random() < 0.4:
+                nb = int(r.integers(0, 3))
+                pos = int(r.integers(0, len(labels) + 1))
+                bd = [1 if r.random() < 0.3 else b for b in batch[3 - nb:]]
+                labels = labels[:pos] + ["..."] + labels[pos:]
+                dims = dims[:pos] + bd + dims[pos:]
+            if r.random() < 0.08 and dims:
+                dims[int(r.integers(0, len(dims)))] += 1          # size clash
+            if r.random() < 0.05:
+                labels.append(r.choice(["1", ".", "..", "_"]))     # syntax error
+            subs.append("".join(labels))
+            shapes.append(tuple(dims))
+        eq = ",".join(subs)
+        if r.random() < 0.85:
+            out = sorted({c for s in subs for c in s if c.isalpha()})
+            out = list(r.permutation(out))[: int(r.integers(0, len(out) + 1))]
+            if any("..." in s for s in subs) and r.random() < 0.8:
+                out.insert(int(r.integers(0, len(out) + 1)), "...")
+            if r.random() < 0.05:
+                out.append(r.choice(["q", "i", "."]))
+            eq += "->" + "".join(out)
+        xs = [randn(s, seed=case * 7 + i) if len(s) else np.array(randn((1,), seed=case)[0], F) for i, s in
+              enumerate(shapes)]
+        try:
+            out_shape = np.einsum(eq, *[x.astype(np.float64) for x in xs]).shape
+        except Exception:  # numpy rejects it too: any output shape, errors are compared
+            out_shape = (1,)
+        accepted += _einsum_outcome(eq, xs, out_shape)
+    assert accepted > 100, f"only {accepted} of 300 random equations were accepted"
 
 
 @pytest.mark.parametrize("geom", [
