@@ -74,9 +74,13 @@ int nert_hip_event_destroy(void* event);
  * copies) becomes one replayable graph; rows that must read device memory on
  * the host (control operands without a host shadow) cannot be captured and
  * fail the capture, while data-dependent error checks are deferred (see
- * nert_hip_take_error_flags). Workspace growth must happen before capture
- * (run the sequence once eagerly first). No reference counterpart: the
- * reference executor launches rows one by one (src/executor.cpp:480-535). */
+ * nert_hip_take_error_flags; begin clears the error word first, eagerly).
+ * Workspaces (split-K partials, TopK state, ...) must reach their size before
+ * capture: run the sequence once eagerly first. A later eager call may still
+ * grow a workspace; while any graph exec is alive the replaced buffer is kept
+ * (not freed) until the last graph exec is destroyed, so replays never touch
+ * freed memory. No reference counterpart: the reference executor launches
+ * rows one by one (src/executor.cpp:480-535). */
 int nert_hip_capture_begin(void);
 int nert_hip_capture_end(void** graph_exec);
 int nert_hip_graph_launch(void* graph_exec, void* stream);
@@ -86,8 +90,22 @@ int nert_hip_graph_destroy(void* graph_exec);
  * data-dependent failures raise: bit 0 = integer division by zero,
  * bit 1 = index out of range. Synchronises `stream`. While `stream` is being
  * captured into a graph it reports 0 without reading: the flag stays raised
- * and the first call after a replay reports it. */
+ * and the first call after a replay reports it. A caller that replays graphs
+ * holding such rows calls this after the replay to see their errors. */
 int nert_hip_take_error_flags(int32_t* flags_out, void* stream);
+
+/* Host shadows. nert_hip_memcpy_h2d keeps a host copy of every upload of at
+ * most 64 KiB, keyed by device address, so rows read control operands
+ * (shapes, axes, K, scales, pads, indices they validate) without a D2H round
+ * trip. Writes through the node level (nert_hip_run_node, the HipDevice()
+ * rows), nert_hip_memcpy_d2d and nert_hip_free drop the shadows they overlap.
+ * The kernel-level entry points below do not: a C caller that writes a
+ * buffer with one of them and then passes that buffer to nert_hip_run_node
+ * as a control operand calls nert_hip_forget_host_shadow(buffer, bytes)
+ * first, or the row reads the uploaded (stale) values. No reference
+ * counterpart (the reference rows read control operands back with a
+ * blocking D2H copy, e.g. src/hip/gather.cu:160). */
+int nert_hip_forget_host_shadow(const void* ptr, int64_t bytes);
 
 /* ---------------------------------------------------------- node level --- */
 

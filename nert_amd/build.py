@@ -4,7 +4,9 @@
     python -m nert_amd.build --force    # rebuild everything
 
 Outputs (git-ignored, shipped with the tree to the GPU box):
-    nert_amd/lib/libnert_hip.so   C-ABI kernels + runtime + nert::HipDevice()
+    nert_amd/lib/libnert_hip.so      C-ABI kernels + runtime + nert::HipDevice()
+    nert_amd/lib/libnert_core.so     the NERT host library a seam user links
+    nert_amd/lib/libnert_seamrun.so  (nert_amd/host/): Model on HipDevice()
 
 The seam rows compile against NERT's public headers and its header-only form
 helpers (include/nert/*.hpp, src/{softmax_form,reduce_axes,axes_form}.hpp of
@@ -112,6 +114,17 @@ def build_oracle(force: bool = False) -> None:
     subprocess.run(args, check=True, capture_output=True, text=True)
 
 
+def build_host(force: bool = False) -> None:
+    """Builds the NERT host side a seam user links (nert_amd/host/Makefile):
+    nert_amd/lib/libnert_core.so and the drop-in C-ABI libnert_seamrun.so."""
+    if not (NERT_REF / "src" / "executor.cpp").exists():
+        return  # the reference is absent (GPU box): use the prebuilt libraries
+    args = ["make", "-C", str(PKG / "host"), "-j8"]
+    if force:
+        args.insert(1, "-B")
+    subprocess.run(args, check=True, capture_output=True, text=True)
+
+
 def build_tests(force: bool = False) -> None:
     """Builds the C++ test harness libraries under tests/_build."""
     mk = ROOT / "tests" / "cpp" / "Makefile"
@@ -125,6 +138,7 @@ def build_tests(force: bool = False) -> None:
 
 def build_all(force: bool = False) -> None:
     build_device_layer(force=force)
+    build_host(force=force)
     build_oracle(force=force)
     build_tests(force=force)
 
@@ -132,11 +146,13 @@ def build_all(force: bool = False) -> None:
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--force", action="store_true")
-    ap.add_argument("--only", choices=["device", "oracle", "tests", "all"], default="all")
+    ap.add_argument("--only", choices=["device", "host", "oracle", "tests", "all"], default="all")
     a = ap.parse_args(argv)
     try:
         if a.only in ("device", "all"):
             print(build_device_layer(force=a.force))
+        if a.only in ("host", "all"):
+            build_host(force=a.force)
         if a.only in ("oracle", "all"):
             build_oracle(force=a.force)
         if a.only in ("tests", "all"):

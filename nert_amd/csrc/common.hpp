@@ -44,6 +44,9 @@ void* Workspace(int64_t bytes, hipStream_t stream, int slot = 0);
 // report data-dependent errors (out-of-range indices, integer division by
 // zero) back to the host.
 int32_t* ErrorFlags();
+// Live graph execs keep replaced workspaces alive (workspace_book.hpp).
+void GraphCreated();
+void GraphDestroyed();
 
 // Host shadows of small host-to-device uploads (<= 64 KiB), keyed by device
 // address. nert_hip_memcpy_h2d records them; device-side writes that go

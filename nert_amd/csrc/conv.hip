@@ -1200,11 +1200,11 @@ ConvKey KeyOf(const ConvArgs& p) {
 }
 
 template <class Launch>
-int ChooseConvConfig(std::map<ConvKey, int>& cache, const ConvArgs& p, hipStream_t stream, int count, int fallback,
-                     Launch launch) {
+int ChooseConvConfig(const char* family, std::map<ConvKey, int>& cache, const ConvArgs& p, hipStream_t stream,
+                     int count, int fallback, Launch launch) {
     static std::mutex mu;
     const size_t y_bytes = static_cast<size_t>(p.batch * p.m * p.plane_out) * sizeof(float);
-    return ChooseConfig(cache, mu, KeyOf(p), y_bytes, stream, count, fallback, [&](int i, float* scratch) {
+    return ChooseConfig(family, cache, mu, KeyOf(p), y_bytes, stream, count, fallback, [&](int i, float* scratch) {
         ConvArgs q = p;
         q.y = scratch;
         return launch(i, q, stream);
@@ -1284,7 +1284,7 @@ bool TryHaloConv(const ConvArgs& p, hipStream_t stream) {
             return true;
         }
     }
-    const int c = ChooseConvConfig(chosen, p, stream, kHaloCandidates, fallback, LaunchHaloCandidate);
+    const int c = ChooseConvConfig("conv3x3", chosen, p, stream, kHaloCandidates, fallback, LaunchHaloCandidate);
     // Whether a candidate fits depends on the geometry alone, so a cached
     // choice fits; the default is tried next only as a safeguard.
     return LaunchHaloCandidate(c, p, stream) || LaunchHaloCandidate(fallback, p, stream);
@@ -1425,7 +1425,7 @@ void LaunchGatherConv(const ConvArgs& p, hipStream_t stream) {
             return;
         }
     }
-    const int c = ChooseConvConfig(chosen, p, stream, 4, fallback, LaunchGatherCandidate);
+    const int c = ChooseConvConfig("conv", chosen, p, stream, 4, fallback, LaunchGatherCandidate);
     if (!LaunchGatherCandidate(c, p, stream)) {
         LaunchGatherCandidate(fallback, p, stream);
     }

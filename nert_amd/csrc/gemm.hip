@@ -383,7 +383,7 @@ void LaunchGemm(GemmArgs p, int64_t batches, hipStream_t stream) {
     const size_t y_bytes = static_cast<size_t>(batches * p.m * p.n) * sizeof(float);
     // Candidates 0-11: tile shape x split count; 12: the skinny kernel.
     const bool skinny = SkinnyApplies(p, batches);
-    const int c = ChooseConfig(chosen, mu, key, y_bytes, stream, 13, 4 * fallback_shape, [&](int i, float* scratch) {
+    const int c = ChooseConfig("gemm", chosen, mu, key, y_bytes, stream, 13, 4 * fallback_shape, [&](int i, float* scratch) {
         GemmArgs q = p;
         q.y = scratch;
         if (i == 12) {

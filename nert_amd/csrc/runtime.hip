@@ -7,6 +7,7 @@
 // synchronisation points are blocking transfers and explicit syncs.
 
 #include "common.hpp"
+#include "workspace_book.hpp"
 #include "../../include/nert_hip.h"
 
 #include <cstdlib>
@@ -27,6 +28,7 @@ struct Context {
     hipStream_t stream = nullptr;
     void* workspace[kWorkspaceSlots] = {};
     int64_t workspace_bytes[kWorkspaceSlots] = {};
+    WorkspaceBook book;  // replaced workspaces stay alive while graph execs may use them
     int32_t* flags = nullptr;
 };
 
@@ -86,21 +88,44 @@ void* Workspace(int64_t bytes, hipStream_t stream, int slot) {
         want = bytes;
     }
     want = (want + 0xFFFFF) & ~static_cast<int64_t>(0xFFFFF);
-    if (ctx.workspace[slot] != nullptr) {
+    void* grown = nullptr;
+    Check(hipMalloc(&grown, static_cast<size_t>(want)), "hipMalloc(workspace)");
+    std::lock_guard<std::mutex> lock(Mutex());
+    const std::vector<void*> free_now = ctx.book.Replaced(ctx.workspace[slot]);
+    if (!free_now.empty()) {
         Check(hipStreamSynchronize(stream), "hipStreamSynchronize(workspace)");
         Check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize(workspace)");
-        Check(hipFree(ctx.workspace[slot]), "hipFree(workspace)");
-        ctx.workspace[slot] = nullptr;
-        ctx.workspace_bytes[slot] = 0;
+        for (void* p : free_now) {
+            Check(hipFree(p), "hipFree(workspace)");
+        }
     }
-    Check(hipMalloc(&ctx.workspace[slot], static_cast<size_t>(want)), "hipMalloc(workspace)");
+    ctx.workspace[slot] = grown;
     ctx.workspace_bytes[slot] = want;
-    return ctx.workspace[slot];
+    return grown;
 }
 
 int32_t* ErrorFlags() {
     EnsureReady();
     return Ctx().flags;
+}
+
+void GraphCreated() {
+    std::lock_guard<std::mutex> lock(Mutex());
+    Ctx().book.GraphCreated();
+}
+
+void GraphDestroyed() {
+    std::vector<void*> free_now;
+    {
+        std::lock_guard<std::mutex> lock(Mutex());
+        free_now = Ctx().book.GraphDestroyed();
+    }
+    if (!free_now.empty()) {
+        Check(hipStreamSynchronize(Ctx().stream), "hipStreamSynchronize(workspace)");
+        for (void* p : free_now) {
+            Check(hipFree(p), "hipFree(workspace)");
+        }
+    }
 }
 
 namespace {
@@ -429,6 +454,10 @@ int nert_hip_memcpy_d2h(void* dst, const void* src, int64_t bytes) {
     });
 }
 
+int nert_hip_forget_host_shadow(const void* ptr, int64_t bytes) {
+    return Guard([&] { nert_hip::ShadowDrop(ptr, bytes); });
+}
+
 int nert_hip_memcpy_d2d(void* dst, const void* src, int64_t bytes, void* stream) {
     if (bytes == 0) {
         return 0;
@@ -480,8 +509,15 @@ int nert_hip_event_destroy(void* event) {
 
 int nert_hip_capture_begin(void) {
     return Guard([&] {
-        nert_hip::Check(hipStreamBeginCapture(nert_hip::DefaultStream(), hipStreamCaptureModeThreadLocal),
-                        "hipStreamBeginCapture");
+        // The graph's deferred checks report through the error word: start
+        // it cleared (eagerly, before the capture; no memset node is
+        // recorded into the graph).
+        hipStream_t s = nert_hip::DefaultStream();
+        const int32_t zero = 0;
+        nert_hip::Check(hipMemcpyAsync(nert_hip::ErrorFlags(), &zero, sizeof(zero), hipMemcpyHostToDevice, s),
+                        "hipMemcpyAsync(flags)");
+        nert_hip::Check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        nert_hip::Check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
     });
 }
 
@@ -494,6 +530,7 @@ int nert_hip_capture_end(void** graph_exec) {
         const hipError_t status = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
         (void)hipGraphDestroy(graph);
         nert_hip::Check(status, "hipGraphInstantiate");
+        nert_hip::GraphCreated();
         *graph_exec = exec;
     });
 }
@@ -511,6 +548,7 @@ int nert_hip_graph_destroy(void* graph_exec) {
     }
     return Guard([&] {
         nert_hip::Check(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)), "hipGraphExecDestroy");
+        nert_hip::GraphDestroyed();
     });
 }
 

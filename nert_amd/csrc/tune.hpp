@@ -1,25 +1,41 @@
 #pragma once
-// Per-geometry choice among kernel configurations, made by timing.
+// Per-geometry choice among kernel configurations, made by timing or read
+// from a committed table.
 //
 // Which tile shape and split-K count is fastest depends on how a problem's
 // tile count falls against the 256 CUs, which no simple rule captures across
-// shapes. So the first eager call of each geometry runs every candidate that
-// fits on a scratch output (one warm-up and three timed launches each, HIP
-// events on the caller's stream) and keeps the fastest; later calls of the
-// geometry reuse it, so within a process a geometry is always computed the
-// same way. The four fastest of that pass are timed again (two interleaved
-// rounds of five launches) before the choice, since the leaders are often
-// closer than one pass's noise. A first call under stream capture cannot time anything and fixes
-// the fallback instead, as does NERT_HIP_CONV_TUNE=0 in the environment.
+// shapes. A choice fixes the order in which a geometry's sums are formed, so
+// it also fixes the rounding: to make results reproducible across processes
+// and machines, choices come first from a table (one line per geometry,
+// nert_amd/tuning/gfx950.tsv next to the library, or the file that
+// NERT_HIP_TUNE_TABLE names). A geometry the table lacks is timed on its
+// first eager call: every candidate that fits runs on a scratch output (one
+// warm-up and three timed launches each, HIP events on the caller's stream);
+// the four fastest are timed again (two interleaved rounds of five launches)
+// since the leaders are often closer than one pass's noise, and the fastest
+// is kept for the rest of the process. NERT_HIP_TUNE_RECORD=<file> appends
+// each such timed choice to <file> in the table's format. A first call
+// under stream capture cannot time anything and fixes the fallback instead,
+// as does NERT_HIP_CONV_TUNE=0 in the environment.
+//
+// Table line: <family> <candidate count> <key integers, comma separated>
+// <choice>; '#' starts a comment. A line whose family or candidate count no
+// longer matches the caller is ignored, so a changed candidate list falls
+// back to timing rather than to a wrong index.
 
 #include "common.hpp"
 
+#include <dlfcn.h>
+
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
-#include <algorithm>
+#include <fstream>
 #include <map>
 #include <mutex>
+#include <sstream>
 #include <string>
+#include <unordered_map>
 #include <utility>
 #include <vector>
 
@@ -42,20 +58,89 @@ inline bool TuningEnabled() {
     return enabled;
 }
 
+template <class Key>
+std::string TableKey(const char* family, int count, const Key& key) {
+    std::string s = std::string(family) + " " + std::to_string(count) + " ";
+    for (size_t i = 0; i < key.size(); ++i) {
+        s += (i != 0 ? "," : "") + std::to_string(key[i]);
+    }
+    return s;
+}
+
+// The committed choices: <dir of libnert_hip.so>/../tuning/gfx950.tsv, or
+// $NERT_HIP_TUNE_TABLE. Read once; a missing file is an empty table.
+inline const std::unordered_map<std::string, int>& TuneTable() {
+    static const std::unordered_map<std::string, int> table = [] {
+        std::unordered_map<std::string, int> t;
+        std::string path;
+        if (const char* e = std::getenv("NERT_HIP_TUNE_TABLE")) {
+            path = e;
+        } else {
+            Dl_info info{};
+            if (dladdr(reinterpret_cast<const void*>(&TuneLogEnabled), &info) != 0 && info.dli_fname != nullptr) {
+                std::string lib = info.dli_fname;
+                const size_t slash = lib.rfind('/');
+                path = (slash == std::string::npos ? std::string(".") : lib.substr(0, slash)) + "/../tuning/gfx950.tsv";
+            }
+        }
+        std::ifstream in(path);
+        std::string line;
+        while (std::getline(in, line)) {
+            const size_t hash = line.find('#');
+            if (hash != std::string::npos) {
+                line.resize(hash);
+            }
+            std::istringstream fields(line);
+            std::string family, count, key;
+            int choice = -1;
+            if (fields >> family >> count >> key >> choice && choice >= 0) {
+                t[family + " " + count + " " + key] = choice;
+            }
+        }
+        return t;
+    }();
+    return table;
+}
+
+inline void RecordChoice(const std::string& table_key, int choice) {
+    const char* path = std::getenv("NERT_HIP_TUNE_RECORD");
+    if (path == nullptr || *path == 0) {
+        return;
+    }
+    static std::mutex mu;
+    std::lock_guard<std::mutex> lock(mu);
+    if (FILE* f = std::fopen(path, "a")) {
+        std::fprintf(f, "%s %d\n", table_key.c_str(), choice);
+        std::fclose(f);
+    }
+}
+
 // launch(i, scratch_y) -> false when candidate i does not fit; it must write
 // its output to scratch_y (scratch_bytes long) instead of the caller's.
 template <class Key, class Launch>
-int ChooseConfig(std::map<Key, int>& cache, std::mutex& mu, const Key& key, size_t scratch_bytes,
-                 hipStream_t stream, int count, int fallback, Launch launch) {
+int ChooseConfig(const char* family, std::map<Key, int>& cache, std::mutex& mu, const Key& key,
+                 size_t scratch_bytes, hipStream_t stream, int count, int fallback, Launch launch) {
     std::lock_guard<std::mutex> lock(mu);
     auto it = cache.find(key);
     if (it != cache.end()) {
         return it->second;
     }
+    const std::string table_key = TableKey(family, count, key);
+    const auto& table = TuneTable();
+    const auto row = table.find(table_key);
+    if (row != table.end() && row->second < count) {
+        if (TuneLogEnabled()) {
+            std::fprintf(stderr, "nert_hip tune: table %s -> %d\n", table_key.c_str(), row->second);
+        }
+        cache.emplace(key, row->second);
+        return row->second;
+    }
     int best = fallback;
+    bool timed = false;
     hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
     Check(hipStreamIsCapturing(stream, &capture), "hipStreamIsCapturing");
     if (TuningEnabled() && capture == hipStreamCaptureStatusNone && count > 1 && scratch_bytes > 0) {
+        timed = true;
         float* scratch = nullptr;
         Check(hipMalloc(&scratch, scratch_bytes), "hipMalloc(tuning output)");
         hipEvent_t start = nullptr, stop = nullptr;
@@ -122,7 +207,10 @@ int ChooseConfig(std::map<Key, int>& cache, std::mutex& mu, const Key& key, size
         Check(hipFree(scratch), "hipFree(tuning output)");
     }
     if (TuneLogEnabled()) {
-        std::fprintf(stderr, "nert_hip tune: chose %d of %d\n", best, count);
+        std::fprintf(stderr, "nert_hip tune: chose %d of %d for %s\n", best, count, table_key.c_str());
+    }
+    if (timed) {
+        RecordChoice(table_key, best);
     }
     cache.emplace(key, best);
     return best;

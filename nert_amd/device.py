@@ -69,6 +69,7 @@ def lib() -> C.CDLL:
     L.nert_hip_capture_end.argtypes = [C.POINTER(C.c_void_p)]
     L.nert_hip_graph_launch.argtypes = [vp, vp]
     L.nert_hip_graph_destroy.argtypes = [vp]
+    L.nert_hip_take_error_flags.argtypes = [C.POINTER(C.c_int32), vp]
     _lib = L
     return L
 
@@ -89,6 +90,17 @@ def init() -> None:
 
 def synchronize() -> None:
     check(lib().nert_hip_stream_sync(None), "nert_hip_stream_sync")
+
+
+ERROR_FLAG_TEXT = {1: "integer division by zero", 2: "index out of range"}
+
+
+def take_error_flags() -> int:
+    """Reads and clears the device error word (synchronises the layer
+    stream): bit 0 integer division by zero, bit 1 index out of range."""
+    flags = C.c_int32(0)
+    check(lib().nert_hip_take_error_flags(C.byref(flags), None), "nert_hip_take_error_flags")
+    return int(flags.value)
 
 
 class PinnedArray:

@@ -1,0 +1,134 @@
+"""Op-level measurement cases: the reference's published op-bench fixtures
+(olibartfast/nert bench/runtime/main.cpp:331-674, the twelve quoted with
+MI300X figures) plus BASELINE.json configs[0] and configs[1](a)(b)(c).
+
+Each case is one node with the fixture's shapes, attributes and value ranges
+(values drawn from this package's seeded generator; the reference draws from
+std::mt19937_64(0xC0FFEE), whose values do not change the work). `work` is
+the algorithmic amount the roofline uses: 2*M*N*K (or the conv's
+2*N*M*(C/g)*kh*kw*OH*OW) flops for MFMA-bound cases, input + output bytes
+for bandwidth-bound ones. `mi300x_ms` is the reference HIP layer's published
+dev_ms on MI300X (specs/2026-10-23-amd-devcloud/bench-results.txt; it
+includes a host-to-device zero fill of the output inside the timed loop).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Any, Callable
+
+import numpy as np
+
+from .graph import Graph
+from .workloads import Rng
+
+F32, I64 = np.float32, np.int64
+
+
+@dataclass
+class OpCase:
+    name: str
+    op: str
+    inputs_spec: list[tuple[str, tuple[int, ...], Any, Callable[[Rng, tuple[int, ...]], np.ndarray]]]
+    outputs_spec: list[tuple[str, tuple[int, ...], Any]]
+    bound: str            # "mfma" or "hbm"
+    work: float           # flops (mfma) or bytes (hbm) per launch
+    attrs: dict = field(default_factory=dict)
+    initializers: dict = field(default_factory=dict)
+    mi300x_ms: float | None = None
+    source: str = ""
+
+    def graph(self) -> Graph:
+        g = Graph()
+        for n, shape, dtype, _ in self.inputs_spec:
+            g.add_input(n, dtype, shape)
+        for n, v in self.initializers.items():
+            g.add_initializer(n, v)
+        names = [s[0] for s in self.inputs_spec] + list(self.initializers)
+        outs = g.add_node(self.op, names, [(n, d, s) for n, s, d in self.outputs_spec], self.attrs, name=self.name)
+        g.outputs.extend(outs)
+        return g
+
+    def inputs(self, seed: int = 0xC0FFEE) -> dict[str, np.ndarray]:
+        rng = Rng(seed)
+        return {n: make(rng, shape).astype(dtype) for n, shape, dtype, make in self.inputs_spec}
+
+
+def _u(lo, hi):
+    return lambda rng, shape: rng.uniform(shape, lo, hi)
+
+
+def _nrm(std):
+    return lambda rng, shape: rng.normal(shape, 0.0, std)
+
+
+def _bytes(*shapes_dtypes) -> float:
+    return float(sum(int(np.prod(s)) * np.dtype(d).itemsize for s, d in shapes_dtypes))
+
+
+K_BIG, K_NEW = 4 * 1024 * 1024, 1024 * 1024
+
+
+def _cases() -> list[OpCase]:
+    c: list[OpCase] = []
+    src = "bench/runtime/main.cpp"
+    # --- the reference's published fixtures ---
+    c.append(OpCase("gemm_512", "Gemm", [("a", (512, 512), F32, _u(-1, 1)), ("b", (512, 512), F32, _u(-1, 1))],
+                    [("y", (512, 512), F32)], "mfma", 2.0 * 512 ** 3, mi300x_ms=0.15, source=f"{src}:337-346"))
+    c.append(OpCase("conv_8x16x64x64", "Conv",
+                    [("x", (8, 16, 64, 64), F32, _u(-1, 1)), ("w", (32, 16, 3, 3), F32, _u(-1, 1)),
+                     ("b", (32,), F32, _u(-1, 1))],
+                    [("y", (8, 32, 62, 62), F32)], "mfma", 2.0 * 8 * 32 * 62 * 62 * 16 * 9,
+                    mi300x_ms=0.21, source=f"{src}:409-419"))
+    c.append(OpCase("softmax_256x4096", "Softmax", [("x", (256, 4096), F32, _u(-3, 3))], [("y", (256, 4096), F32)],
+                    "hbm", _bytes(((256, 4096), F32), ((256, 4096), F32)), {"axis": -1}, mi300x_ms=5.38,
+                    source=f"{src}:388-396"))
+    c.append(OpCase("layernorm_1024x1024", "LayerNormalization", [("x", (1024, 1024), F32, _u(-3, 3))],
+                    [("y", (1024, 1024), F32)], "hbm", _bytes(((1024, 1024), F32), ((1024,), F32), ((1024, 1024), F32)),
+                    {"axis": 1}, {"scale": np.ones(1024, F32)}, mi300x_ms=1.45, source=f"{src}:614-623"))
+    c.append(OpCase("reducemean_1024x1024", "ReduceMean", [("x", (1024, 1024), F32, _u(-3, 3))],
+                    [("y", (1024, 1), F32)], "hbm", _bytes(((1024, 1024), F32), ((1024, 1), F32)), {},
+                    {"axes": np.array([1], I64)}, mi300x_ms=0.59, source=f"{src}:568-577"))
+    c.append(OpCase("gap_8x64x112x112", "GlobalAveragePool", [("x", (8, 64, 112, 112), F32, _u(-3, 3))],
+                    [("y", (8, 64, 1, 1), F32)], "hbm", _bytes(((8, 64, 112, 112), F32), ((8, 64, 1, 1), F32)),
+                    mi300x_ms=3.35, source=f"{src}:624-632"))
+    c.append(OpCase("maxpool_8x64x112x112", "MaxPool", [("x", (8, 64, 112, 112), F32, _u(-3, 3))],
+                    [("y", (8, 64, 55, 55), F32)], "hbm", _bytes(((8, 64, 112, 112), F32), ((8, 64, 55, 55), F32)),
+                    {"kernel_shape": [3, 3], "strides": [2, 2]}, mi300x_ms=0.16, source=f"{src}:376-387"))
+    c.append(OpCase("relu_4m", "Relu", [("x", (K_BIG,), F32, _u(-6, 6))], [("y", (K_BIG,), F32)], "hbm",
+                    _bytes(((K_BIG,), F32), ((K_BIG,), F32)), mi300x_ms=0.35, source=f"{src}:347-355"))
+    c.append(OpCase("add_2048x2048", "Add", [("a", (2048, 2048), F32, _u(-3, 3)), ("b", (2048,), F32, _u(-3, 3))],
+                    [("y", (2048, 2048), F32)], "hbm",
+                    _bytes(((2048, 2048), F32), ((2048,), F32), ((2048, 2048), F32)), mi300x_ms=0.37,
+                    source=f"{src}:356-364"))
+    c.append(OpCase("sigmoid_4m", "Sigmoid", [("x", (K_BIG,), F32, _u(-6, 6))], [("y", (K_BIG,), F32)], "hbm",
+                    _bytes(((K_BIG,), F32), ((K_BIG,), F32)), mi300x_ms=0.35, source=f"{src}:347-355"))
+    c.append(OpCase("erf_1m", "Erf", [("x", (K_NEW,), F32, _u(-4, 4))], [("y", (K_NEW,), F32)], "hbm",
+                    _bytes(((K_NEW,), F32), ((K_NEW,), F32)), mi300x_ms=0.10, source=f"{src}:429-440"))
+    c.append(OpCase("argmax_1024x1024", "ArgMax", [("x", (1024, 1024), F32, _u(-3, 3))], [("y", (1024, 1), I64)],
+                    "hbm", _bytes(((1024, 1024), F32), ((1024, 1), I64)), {"axis": 1}, mi300x_ms=0.27,
+                    source=f"{src}:578-586"))
+    # --- BASELINE.json configs[0] and configs[1] ---
+    c.append(OpCase("cfg0_conv_1x64x56x56", "Conv",
+                    [("x", (1, 64, 56, 56), F32, _nrm(1.0)), ("w", (64, 64, 3, 3), F32, _nrm(np.sqrt(2 / 576))),
+                     ("b", (64,), F32, _nrm(0.01))],
+                    [("y", (1, 64, 56, 56), F32)], "mfma", 2.0 * 64 * 56 * 56 * 64 * 9,
+                    {"kernel_shape": [3, 3], "pads": [1, 1, 1, 1]}, source="BASELINE.json configs[0]"))
+    c.append(OpCase("cfg1a_matmul_8x1024", "MatMul",
+                    [("a", (8, 1024, 1024), F32, _u(-1, 1)), ("b", (8, 1024, 1024), F32, _u(-1, 1))],
+                    [("y", (8, 1024, 1024), F32)], "mfma", 2.0 * 8 * 1024 ** 3, source="BASELINE.json configs[1](a)"))
+    c.append(OpCase("cfg1b_gemm_2048x1024x4096", "Gemm",
+                    [("a", (2048, 4096), F32, _u(-1, 1)), ("b", (1024, 4096), F32, _u(-1, 1)),
+                     ("c", (1024,), F32, _u(-1, 1))],
+                    [("y", (2048, 1024), F32)], "mfma", 2.0 * 2048 * 1024 * 4096,
+                    {"transB": 1, "alpha": 1.0, "beta": 1.0}, source="BASELINE.json configs[1](b)"))
+    c.append(OpCase("cfg1c_gemm_32x1000x512", "Gemm",
+                    [("a", (32, 512), F32, _u(-1, 1)), ("b", (1000, 512), F32, _u(-1, 1)),
+                     ("c", (1000,), F32, _u(-1, 1))],
+                    [("y", (32, 1000), F32)], "hbm", _bytes(((32, 512), F32), ((1000, 512), F32), ((1000,), F32),
+                                                           ((32, 1000), F32)),
+                    {"transB": 1, "alpha": 1.0, "beta": 1.0}, source="BASELINE.json configs[1](c)"))
+    return c
+
+
+CASES: list[OpCase] = _cases()

@@ -26,7 +26,7 @@ from typing import Any, Iterable
 import numpy as np
 
 from . import abi
-from .device import DeviceArray, Event, NertError, check, lib
+from .device import ERROR_FLAG_TEXT, DeviceArray, Event, NertError, check, lib, take_error_flags
 from .graph import Graph, Node
 
 ALIGN = 256
@@ -340,6 +340,7 @@ class Program:
         self.nodes = [self._pack(n) for n in g.nodes]
         self.exec_graph = None
         self._events: list[Event] = []
+        self._control: dict[str, np.ndarray] = {}
 
     def ptr(self, name: str) -> int:
         if name in self.resident:
@@ -357,11 +358,32 @@ class Program:
                            abi.TensorPack([self._entry(t) for t in n.outputs]))
 
     def set_input(self, name: str, value: np.ndarray) -> None:
+        """Uploads a graph input. Rows read small integer operands (indices,
+        shapes, divisors) on the host when they launch, so once the program
+        is captured, a new value for an int64 or bool input re-captures it:
+        the graph then carries launches checked against the new values."""
         d = self.resident[name]
         a = np.asarray(value, dtype=d.dtype, order="C")
         if a.shape != d.shape:
             raise ValueError(f"input {name}: shape {a.shape} != {d.shape}")
+        control = d.dtype in (np.dtype(np.int64), np.dtype(np.bool_))
+        changed = control and not np.array_equal(self._control.get(name), a)
         check(lib().nert_hip_memcpy_h2d(d.ptr, a.ctypes.data, d.nbytes), "h2d")
+        if control:
+            self._control[name] = a.copy()
+        if changed and self.exec_graph is not None:
+            self.close()
+            self.capture()
+
+    def check_errors(self) -> None:
+        """Raises NertError when rows run since the last check (a replayed
+        graph's deferred checks included) raised the device error word: an
+        out-of-range Gather/GatherElements/ScatterND index or an int64
+        division by zero. Synchronises the layer stream."""
+        flags = take_error_flags()
+        if flags:
+            what = ", ".join(t for bit, t in ERROR_FLAG_TEXT.items() if flags & bit) or f"flags {flags:#x}"
+            raise NertError(abi.INFERENCE_ERROR, f"device error raised by the replayed rows: {what}")
 
     def output(self, name: str) -> np.ndarray:
         dtype, shape = self.graph.tensors[name]
@@ -401,6 +423,38 @@ class Program:
             else:
                 self._call(p)
         return {idx: e0.elapsed_ms(e1) for idx, e0, e1 in marks}
+
+    def time_rows(self, indices: Iterable[int], reps: int = 20) -> dict[int, float]:
+        """Per-row device time as the replayed step sees it: for each node
+        index, `reps` back-to-back launches of that row alone are captured
+        into one HIP graph, which is replayed twice (warm) and then once
+        between HIP events on the layer stream. Returns {index: ms per
+        launch}. Rows run on the operands the last full run left in place, so
+        call it after run() or replay(); the output buffers are rewritten
+        with the same values."""
+        result: dict[int, float] = {}
+        e0, e1 = Event(), Event()
+        for idx in indices:
+            p = self.nodes[idx]
+            check(lib().nert_hip_stream_sync(None), "sync")
+            check(lib().nert_hip_capture_begin(), "capture begin")
+            try:
+                for _ in range(reps):
+                    self._call(p)
+            finally:
+                handle = C.c_void_p()
+                rc = lib().nert_hip_capture_end(C.byref(handle))
+            check(rc, "capture end")
+            try:
+                for _ in range(2):
+                    check(lib().nert_hip_graph_launch(handle, None), "graph launch")
+                e0.record()
+                check(lib().nert_hip_graph_launch(handle, None), "graph launch")
+                e1.record()
+                result[idx] = e0.elapsed_ms(e1) / reps
+            finally:
+                lib().nert_hip_graph_destroy(handle)
+        return result
 
     def capture(self) -> None:
         """Captures the node sequence into one HIP graph (after a warm run so

@@ -1,0 +1,94 @@
+"""Regenerates nert_amd/tuning/gfx950.tsv, the committed per-geometry kernel
+choices (tile shape, split-K count) that make results reproducible across
+processes (nert_amd/csrc/tune.hpp reads it).
+
+    python3 -m nert_amd.tuning.make_table [--rounds 3] [--out nert_amd/tuning/gfx950.tsv]
+
+Each round is a fresh process that ignores the current table and times
+every candidate of every geometry the seeded workloads reach (the
+BASELINE.json configs, the batch sizes the parity tests use, and the
+op-level cases), recording its choices (NERT_HIP_TUNE_RECORD). Per
+geometry the table keeps the choice most rounds made (ties: the earliest
+round). Needs the GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import collections
+import os
+import subprocess
+import sys
+import tempfile
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parent.parent
+
+WORKLOADS = [
+    ("resnet18", {"batch": 32}), ("resnet18", {"batch": 2}),
+    ("vit_b16", {"batch": 16}), ("vit_b16", {"batch": 2, "layers": 1}),
+    ("detector", {"batch": 8}), ("detector", {"batch": 2}),
+]
+
+
+def _round() -> None:
+    """One tuning pass in this process (the table is disabled by the parent)."""
+    sys.path.insert(0, str(ROOT))
+    from nert_amd import device, opcases, workloads
+    from nert_amd.runner import Program
+
+    device.init()
+    for name, kwargs in WORKLOADS:
+        g, inputs = getattr(workloads, name)(**kwargs)
+        prog = Program(g)  # fused and unfused rows share their geometry keys
+        for n in g.inputs:
+            prog.set_input(n, inputs[n])
+        prog.run()
+        device.synchronize()
+        prog.close()
+        print(f"tuned {name} {kwargs}", flush=True)
+    for case in opcases.CASES:
+        prog = Program(case.graph())
+        for n, v in case.inputs().items():
+            prog.set_input(n, v)
+        prog.run()
+        device.synchronize()
+        prog.close()
+    print("tuned op cases", flush=True)
+
+
+def main(argv: list[str] | None = None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--rounds", type=int, default=3)
+    ap.add_argument("--out", default=str(HERE / "gfx950.tsv"))
+    ap.add_argument("--_round", action="store_true", help=argparse.SUPPRESS)
+    a = ap.parse_args(argv)
+    if a._round:
+        _round()
+        return 0
+    votes: dict[str, list[int]] = collections.defaultdict(list)
+    with tempfile.TemporaryDirectory() as tmp:
+        for r in range(a.rounds):
+            rec = os.path.join(tmp, f"round{r}.tsv")
+            env = dict(os.environ, NERT_HIP_TUNE_TABLE=os.devnull, NERT_HIP_TUNE_RECORD=rec)
+            subprocess.run([sys.executable, "-m", "nert_amd.tuning.make_table", "--_round"], cwd=ROOT, env=env,
+                           check=True)
+            for line in Path(rec).read_text().splitlines():
+                key, choice = line.rsplit(" ", 1)
+                votes[key].append(int(choice))
+    lines = ["# Per-geometry kernel choices for gfx950 (MI355X): <family> <candidates> <geometry key> <choice>.",
+             f"# Written by `python3 -m nert_amd.tuning.make_table --rounds {a.rounds}`: the choice most of "
+             f"{a.rounds} timing rounds made.", ""]
+    for key in sorted(votes):
+        counts = collections.Counter(votes[key])
+        top = max(counts.values())
+        choice = next(c for c in votes[key] if counts[c] == top)
+        lines.append(f"{key} {choice}")
+    Path(a.out).write_text("\n".join(lines) + "\n")
+    print(f"wrote {len(votes)} geometries to {a.out}", flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

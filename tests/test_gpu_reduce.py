@@ -101,6 +101,10 @@ def test_layernorm(gpu, shape, axis):
                   {"axis": axis})
     assert_parity("LayerNormalization", [x, np.array([0.75], F), np.array([-0.25], F)], [(shape, F)],
                   {"axis": axis})
+    # Per-element Scale with no B, and with a scalar B (the kernels read an
+    # absent or scalar operand through a zero step).
+    assert_parity("LayerNormalization", [x, scale], [(shape, F)], {"axis": axis, "epsilon": 1e-6})
+    assert_parity("LayerNormalization", [x, scale, np.array([-0.25], F)], [(shape, F)], {"axis": axis})
     assert outer > 0
 
 

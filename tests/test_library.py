@@ -60,3 +60,22 @@ def test_hip_table_rows():
     assert device.has_row("FusedMatMul")
     assert not device.has_row("BatchNormalization")
     assert not device.has_row("")
+
+
+def test_hip_device_without_gpu_throws_inference_exception():
+    """HipDevice() throws nert::InferenceException when no GPU is usable
+    (src/hip_device.cpp:33-44; test/device_test_helpers.hpp:22-29 treats that
+    as the device being absent). This container has no GPU."""
+    import os
+
+    from nert_amd import abi as _abi
+
+    if device.gpu_available() and os.environ.get("NERT_FORCE_NO_GPU") != "1":
+        pytest.skip("a GPU is present: the no-device path cannot be observed here")
+    lib = ctypes.CDLL(str(ROOT / "tests" / "_build" / "libnert_contract.so"))
+    name = ctypes.create_string_buffer(64)
+    is_host, offsets = ctypes.c_int(), ctypes.c_int()
+    err = ctypes.create_string_buffer(1024)
+    rc = lib.contract_device_facts(name, 64, ctypes.byref(is_host), ctypes.byref(offsets), err, 1024)
+    assert rc == _abi.INFERENCE_ERROR, (rc, err.value)
+    assert err.value.decode(), "the exception names its cause"
