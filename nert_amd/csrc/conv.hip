@@ -2016,8 +2016,27 @@ bool TryPatchConv(const ConvArgs& p, hipStream_t stream) {
     return launched;
 }
 
+// y = relu?(y + residual) in place: the fused pointwise convolution's
+// epilogue, run after the GEMM has written conv + bias (each step rounded
+// like the Add and Relu rows).
+__global__ void ResidualReluKernel(float* y, const float* residual, int relu, int64_t n) {
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        float v = y[i];
+        if (residual != nullptr) {
+            v = __fadd_rn(v, residual[i]);
+        }
+        if (relu) {
+            v = (0.0f < v) ? v : 0.0f;
+        }
+        y[i] = v;
+    }
+}
+
 // A 1x1, stride-1, unpadded, ungrouped convolution is Y[b] = W[M,C] * X[b][C,P]
-// with P = D*H*W: a batched GEMM whose B batches are the images.
+// with P = D*H*W: a batched GEMM whose B batches are the images. The fused
+// form (residual, Relu) runs the same GEMM and then ResidualReluKernel, so a
+// Conv and a FusedConv of one geometry sum in the same order.
 bool TryPointwise(const ConvArgs& p, hipStream_t stream) {
     const bool unit = p.k_d == 1 && p.k_h == 1 && p.k_w == 1 && p.s_d == 1 && p.s_h == 1 && p.s_w == 1 &&
                       p.p_d == 0 && p.p_h == 0 && p.p_w == 0 && p.group == 1 && p.plane_in == p.plane_out;
@@ -2046,6 +2065,11 @@ bool TryPointwise(const ConvArgs& p, hipStream_t stream) {
     g.a_bs[0] = 0;
     g.b_bs[0] = p.c * p.plane_in;
     LaunchGemm(g, p.batch, stream);
+    if (p.residual != nullptr || p.relu) {
+        const int64_t n = p.batch * p.m * p.plane_out;
+        ResidualReluKernel<<<GridFor(n, 256, 16384), 256, 0, stream>>>(p.y, p.residual, p.relu, n);
+        CheckLaunch("ResidualReluKernel launch");
+    }
     return true;
 }
 
@@ -2106,7 +2130,7 @@ extern "C" int nert_hip_conv_fused_f32(const float* x, const float* w, const flo
             return;
         }
         hipStream_t s = nert_hip::StreamOr(stream);
-        if (p.residual == nullptr && !p.relu && nert_hip::TryPointwise(p, s)) {
+        if (nert_hip::TryPointwise(p, s)) {
             return;
         }
         if (nert_hip::TryPatchConv(p, s)) {

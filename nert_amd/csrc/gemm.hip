@@ -110,7 +110,7 @@ __device__ __forceinline__ void GemmEpilogue(const GemmArgs& p, const Accum<Shap
     }
 }
 
-template <class Shape, bool A_KCONTIG, bool B_NCONTIG>
+template <class Shape, bool A_KCONTIG, bool B_NCONTIG, int FLUSH>
 __global__ __launch_bounds__(Shape::kThreads) void GemmKernel(GemmArgs p) {
     __shared__ __attribute__((aligned(16))) float lds[2 * (Shape::kLdsA + Shape::kLdsB)];
     const int64_t tiles_m = (p.m + Shape::kBM - 1) / Shape::kBM;
@@ -154,14 +154,14 @@ __global__ __launch_bounds__(Shape::kThreads) void GemmKernel(GemmArgs p) {
             a, row0, p.a_sm, p.a_sk, p.m, k_full);
         const auto bload = MakeOperand<Shape::kBN, Shape::kBK, Shape::kThreads, Shape::kPitchB, !B_NCONTIG, false>(
             b, col0, p.b_sn, p.b_sk, p.n, k_full);
-        MainLoop<Shape>(aload, bload, k_begin, k_full, lds, acc);
+        MainLoop<Shape, FLUSH>(aload, bload, k_begin, k_full, lds, acc);
     }
     if (k_full < k_end) {
         const auto aload = MakeOperand<Shape::kBM, Shape::kBK, Shape::kThreads, Shape::kPitchA, A_KCONTIG, true>(
             a, row0, p.a_sm, p.a_sk, p.m, k_end);
         const auto bload = MakeOperand<Shape::kBN, Shape::kBK, Shape::kThreads, Shape::kPitchB, !B_NCONTIG, true>(
             b, col0, p.b_sn, p.b_sk, p.n, k_end);
-        MainLoop<Shape>(aload, bload, k_full, k_end, lds, acc);
+        MainLoop<Shape, FLUSH>(aload, bload, k_full, k_end, lds, acc);
     }
 
     const int64_t plane = p.m * p.n;
@@ -173,8 +173,9 @@ __global__ __launch_bounds__(Shape::kThreads) void GemmKernel(GemmArgs p) {
     GemmEpilogue<Shape>(p, acc, p.y + batch * plane, row0, col0, true);
 }
 
-// Sums the split-K partials in split order (deterministic) and applies the
-// epilogue, four outputs per thread when rows hold whole quads.
+// Sums the split-K partials in split order (deterministic), in double with
+// one rounding, and applies the epilogue, four outputs per thread when rows
+// hold whole quads.
 __global__ void SplitReduceKernel(GemmArgs p, int splits, int64_t batches, int vec) {
     const int64_t plane = p.m * p.n;
     const int64_t total = plane * batches;
@@ -186,11 +187,11 @@ __global__ void SplitReduceKernel(GemmArgs p, int splits, int64_t batches, int v
         const int64_t r = e / p.n;
         const int64_t c = e % p.n;
         for (int v = 0; v < vec; ++v) {
-            float sum = p.partial[i + v];
+            double sum = p.partial[i + v];
             for (int s = 1; s < splits; ++s) {
                 sum += p.partial[s * total + i + v];
             }
-            p.y[i + v] = FinishGemm(p, sum, r, c + v);
+            p.y[i + v] = FinishGemm(p, static_cast<float>(sum), r, c + v);
         }
     }
 }
@@ -278,6 +279,8 @@ void LaunchSkinny(const GemmArgs& p, hipStream_t stream) {
 // the ViT projections on MI355X: 8 waves of 64x32 for problems with at least
 // 1024 such tiles (4096^3: 135 TFLOP/s), 4 waves of 32x64 below that (more
 // workgroups in flight hide the load latency), 2 waves for M <= 32.
+constexpr int64_t kTwoLevelK = 1024;
+constexpr int64_t kChunkK = 512;
 using ShapeL = TileShape<128, 128, 16, 2, 4>; // 8 waves, 64x32 per wave
 using ShapeM = TileShape<64, 128, 16, 2, 2>;  // 4 waves, 32x64 per wave
 using ShapeS = TileShape<32, 64, 32, 1, 2>;   // 2 waves, skinny M
@@ -289,14 +292,23 @@ void LaunchShape(GemmArgs p, int64_t batches, int splits, hipStream_t stream) {
     dim3 block(Shape::kThreads);
     const bool a_k = p.a_sk == 1;
     const bool b_n = p.b_sn == 1;
+    // K ranges beyond kTwoLevelK accumulate in chunks of kChunkK (see
+    // MainLoop); shorter ones keep one set of accumulators (the second set
+    // costs occupancy).
+    const bool two_level = p.k_per_split > kTwoLevelK;
+    constexpr int kFlush = kChunkK / Shape::kBK;
     if (a_k && b_n) {
-        GemmKernel<Shape, true, true><<<grid, block, 0, stream>>>(p);
+        two_level ? GemmKernel<Shape, true, true, kFlush><<<grid, block, 0, stream>>>(p)
+                  : GemmKernel<Shape, true, true, 0><<<grid, block, 0, stream>>>(p);
     } else if (a_k) {
-        GemmKernel<Shape, true, false><<<grid, block, 0, stream>>>(p);
+        two_level ? GemmKernel<Shape, true, false, kFlush><<<grid, block, 0, stream>>>(p)
+                  : GemmKernel<Shape, true, false, 0><<<grid, block, 0, stream>>>(p);
     } else if (b_n) {
-        GemmKernel<Shape, false, true><<<grid, block, 0, stream>>>(p);
+        two_level ? GemmKernel<Shape, false, true, kFlush><<<grid, block, 0, stream>>>(p)
+                  : GemmKernel<Shape, false, true, 0><<<grid, block, 0, stream>>>(p);
     } else {
-        GemmKernel<Shape, false, false><<<grid, block, 0, stream>>>(p);
+        two_level ? GemmKernel<Shape, false, false, kFlush><<<grid, block, 0, stream>>>(p)
+                  : GemmKernel<Shape, false, false, 0><<<grid, block, 0, stream>>>(p);
     }
     CheckLaunch("GemmKernel launch");
 }

@@ -94,16 +94,36 @@ __device__ __forceinline__ void MmaTile(const float* __restrict__ as, const floa
     }
 }
 
+// Adds `part` into `sum` element by element.
+template <class Shape>
+__device__ __forceinline__ void AddAccum(Accum<Shape>& sum, const Accum<Shape>& part) {
+#pragma unroll
+    for (int i = 0; i < Shape::kSubM; ++i) {
+#pragma unroll
+        for (int j = 0; j < Shape::kSubN; ++j) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                sum.c[i][j][v] += part.c[i][j][v];
+            }
+        }
+    }
+}
+
 // The K loop: ALoader/BLoader stage K tiles [k_begin, k_end) through LDS and
 // accumulate into `acc` (the caller zeroes it once, so a block may run an
 // unchecked interior loop and a checked tail loop into the same registers).
+// FLUSH > 0 accumulates in two levels: every FLUSH K tiles are summed in a
+// fresh set of registers that is then added to `acc`, so the fp32 rounding
+// error of a long dot product grows with the chunk length rather than with
+// all of K (about 2.5 times smaller at K = 4096 with 512-element chunks). It
+// costs a second set of accumulators, hence only for long K ranges.
 // Loader interface:
 //   typename Stage;                       registers for one thread's share
 //   void load(int64_t k0, Stage&)         global -> registers (zero-padded)
 //   void store(const Stage&, float* lds)  registers -> k-major LDS tile
-template <class Shape, class ALoader, class BLoader>
+template <class Shape, int FLUSH = 0, class ALoader, class BLoader>
 __device__ __forceinline__ void MainLoop(const ALoader& aload, const BLoader& bload, int64_t k_begin, int64_t k_end,
-                                         float* lds, Accum<Shape>& acc) {
+                                         float* lds, Accum<Shape>& sum) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -127,6 +147,21 @@ __device__ __forceinline__ void MainLoop(const ALoader& aload, const BLoader& bl
     aload.store(sa, a0);
     bload.store(sb, b0);
     __syncthreads();
+    Accum<Shape> chunk_regs;
+    Accum<Shape>& acc = FLUSH > 0 ? chunk_regs : sum;
+    if constexpr (FLUSH > 0) {
+        chunk_regs.zero();
+    }
+    int in_chunk = 0;
+    auto after_tile = [&]() {
+        if constexpr (FLUSH > 0) {
+            if (++in_chunk == FLUSH) {
+                AddAccum(sum, chunk_regs);
+                chunk_regs.zero();
+                in_chunk = 0;
+            }
+        }
+    };
     int64_t k0 = k_begin;
     while (true) {
         bool more = k0 + Shape::kBK < k_end;
@@ -135,6 +170,7 @@ __device__ __forceinline__ void MainLoop(const ALoader& aload, const BLoader& bl
             bload.load(k0 + Shape::kBK, sb);
         }
         MmaTile<Shape>(a0, b0, acc, wave_m, wave_n, lane);
+        after_tile();
         if (more) {
             aload.store(sa, a1);
             bload.store(sb, b1);
@@ -150,6 +186,7 @@ __device__ __forceinline__ void MainLoop(const ALoader& aload, const BLoader& bl
             bload.load(k0 + Shape::kBK, sb);
         }
         MmaTile<Shape>(a1, b1, acc, wave_m, wave_n, lane);
+        after_tile();
         if (more) {
             aload.store(sa, a0);
             bload.store(sb, b0);
@@ -159,6 +196,11 @@ __device__ __forceinline__ void MainLoop(const ALoader& aload, const BLoader& bl
             break;
         }
         k0 += Shape::kBK;
+    }
+    if constexpr (FLUSH > 0) {
+        if (in_chunk != 0) {
+            AddAccum(sum, chunk_regs);
+        }
     }
 }
 
