@@ -326,6 +326,21 @@ int nert_hip_scatter_nd(int elem_size, const void* data, const int64_t* indices,
  * (src/kernels/top_k.cpp:125-141). Requires 0 < k <= dim < 2^32. */
 int nert_hip_topk_f32(const float* x, float* values, int64_t* indices, int64_t outer, int64_t dim, int64_t inner,
                       int64_t k, void* stream);
+
+/* nert_hip_topk_f32 without any allocation. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory -- work being
+ * captured into a HIP graph, tight serving loops, harnesses that forbid
+ * hipMalloc. Same arguments, results and errors as nert_hip_topk_f32, but
+ * the long-row select state and candidates live in a fixed 4 MiB device
+ * array that the library holds on each GPU until the process ends (set up
+ * by nert_hip_init, which must have run). Rows longer than 4096 need about
+ * 16 * rows * k + 1 KiB * rows bytes of it; larger requests fail with an
+ * error and launch nothing. Every call on one GPU shares that GPU's array,
+ * so calls that overlap in time on one GPU (two streams, two threads) race:
+ * serialise them. The array keeps the last call's contents; each call
+ * clears what it needs with a kernel (no memset node). */
+int nert_hip_topk_f32_noalloc(const float* x, float* values, int64_t* indices, int64_t outer, int64_t dim,
+                              int64_t inner, int64_t k, void* stream);
 /* Range: y[i] = start + i * delta, float32 rounded after the product and
  * after the sum (src/kernels/range.cpp:62-64), or int64. */
 int nert_hip_range(int dtype, double fstart, double fdelta, int64_t istart, int64_t idelta, void* y, int64_t count,

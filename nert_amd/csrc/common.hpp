@@ -44,6 +44,11 @@ void* Workspace(int64_t bytes, hipStream_t stream, int slot = 0);
 // report data-dependent errors (out-of-range indices, integer division by
 // zero) back to the host.
 int32_t* ErrorFlags();
+// True once the device, stream and error word are set up (nert_hip_init).
+bool RuntimeReady();
+// Set-up of the fixed scratch of nert_hip_topk_f32_noalloc (topk.hip), run by
+// the runtime's initialisation with the device current.
+void TopkScratchSetup();
 // Live graph execs keep replaced workspaces alive (workspace_book.hpp).
 void GraphCreated();
 void GraphDestroyed();

@@ -61,10 +61,13 @@ void EnsureReady() {
     Check(hipMalloc(reinterpret_cast<void**>(&ctx.flags), 64), "hipMalloc(flags)");
     Check(hipMemsetAsync(ctx.flags, 0, 64, ctx.stream), "hipMemsetAsync(flags)");
     Check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
+    TopkScratchSetup();
     ctx.ready = true;
 }
 
 } // namespace
+
+bool RuntimeReady() { return Ctx().ready; }
 
 void SetLastError(const std::string& message) { g_last_error = message; }
 

@@ -332,7 +332,126 @@ int PowTwoAtLeast(int64_t n) {
     return p;
 }
 
+// Scratch of the allocation-free entry point (nert_hip_topk_f32_noalloc):
+// one array per GPU, held until the process ends. In host code `scratch`
+// names a host-side stand-in, never the device memory: the device address
+// comes from hipGetSymbolAddress (TopkScratchSetup), once per device.
+constexpr int64_t kNoAllocScratchBytes = 4 << 20;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+uint8_t* g_scratch_ptr[kMaxDevices] = {};
+
+// The workspace a long-row TopK needs: select state | histograms | two
+// candidate buffers (256-byte aligned pieces).
+struct TopkLayout {
+    int64_t st_bytes, hist_bytes, cand_bytes;
+    int64_t total() const { return st_bytes + hist_bytes + 2 * cand_bytes; }
+};
+
+TopkLayout LayoutFor(int64_t rows, int64_t k) {
+    TopkLayout l{};
+    l.st_bytes = (rows * static_cast<int64_t>(sizeof(SelectState)) + 255) / 256 * 256;
+    l.hist_bytes = (rows * 256 * 4 + 255) / 256 * 256;
+    l.cand_bytes = (rows * k * 8 + 255) / 256 * 256;
+    return l;
+}
+
+// The TopK launch sequence. `fixed` is the caller's scratch (fixed_bytes
+// long) or null, in which case the layer's grow-only workspace is used.
+void TopkImpl(const float* x, float* values, int64_t* indices, int64_t outer, int64_t dim, int64_t inner, int64_t k,
+              void* stream, uint8_t* fixed, int64_t fixed_bytes) {
+    if (k <= 0 || k > dim || dim > 0xFFFFFFFFll) {
+        throw Error("topk: need 0 < k <= dim < 2^32");
+    }
+    const int64_t rows = outer * inner;
+    if (rows <= 0) {
+        return;
+    }
+    hipStream_t s = StreamOr(stream);
+    const RowGeom g{dim, inner, k};
+    if (dim <= kSmallRow) {
+        if (rows > 0x7FFFFFFF) {
+            throw Error("topk: too many rows");
+        }
+        SmallRowKernel<<<static_cast<unsigned>(rows), kThreads, 0, s>>>(x, values, indices, g, PowTwoAtLeast(dim));
+        CheckLaunch("topk small-row launch");
+        return;
+    }
+    // Long rows: about 2048 workgroups over all rows, >= 4096 keys each.
+    int64_t chunks = (2048 + rows - 1) / rows;
+    const int64_t max_chunks = (dim + 4095) / 4096;
+    if (chunks > max_chunks) {
+        chunks = max_chunks;
+    }
+    if (chunks < 1) {
+        chunks = 1;
+    }
+    const int64_t chunk = (dim + chunks - 1) / chunks;
+    if (rows * chunks > 0x7FFFFFFF) {
+        throw Error("topk: too many rows");
+    }
+    const TopkLayout lay = LayoutFor(rows, k);
+    const int64_t st_bytes = lay.st_bytes;
+    const int64_t hist_bytes = lay.hist_bytes;
+    const int64_t cand_bytes = lay.cand_bytes;
+    uint8_t* ws = fixed;
+    if (fixed == nullptr) {
+        ws = static_cast<uint8_t*>(Workspace(lay.total(), s));
+    } else if (lay.total() > fixed_bytes) {
+        throw Error("topk_noalloc: " + std::to_string(rows) + " rows x k = " + std::to_string(k) + " need " +
+                    std::to_string(lay.total()) + " bytes of scratch; the fixed scratch holds " +
+                    std::to_string(fixed_bytes));
+    }
+    auto* st = reinterpret_cast<SelectState*>(ws);
+    auto* hist = reinterpret_cast<uint32_t*>(ws + st_bytes);
+    auto* cand = reinterpret_cast<uint64_t*>(ws + st_bytes + hist_bytes);
+    auto* cand2 = reinterpret_cast<uint64_t*>(ws + st_bytes + hist_bytes + cand_bytes);
+
+    InitSelectKernel<<<GridFor(rows * 256, 256, 4096), 256, 0, s>>>(st, hist, rows, k);
+    const unsigned blocks = static_cast<unsigned>(rows * chunks);
+    for (int pass = 0; pass < 8; ++pass) {
+        HistKernel<<<blocks, kThreads, 0, s>>>(x, g, chunk, static_cast<int>(chunks), st, hist, pass);
+        ScanKernel<<<static_cast<unsigned>(rows), 256, 0, s>>>(st, hist, pass);
+    }
+    CollectKernel<<<blocks, kThreads, 0, s>>>(x, g, chunk, static_cast<int>(chunks), st, cand);
+    if (k <= kRankMax) {
+        const int parts = static_cast<int>((k + 63) / 64);
+        RankSortKernel<<<static_cast<unsigned>(rows * parts), 256, 0, s>>>(cand, cand2, k, parts);
+        EmitKernel<<<GridFor(rows * k, 256, 16384), 256, 0, s>>>(x, cand2, values, indices, rows, g);
+        CheckLaunch("topk launch");
+        return;
+    }
+    const int64_t runs = (k + kRun - 1) / kRun;
+    const int run_pow2 = PowTwoAtLeast(k < kRun ? k : kRun);
+    SortRunsKernel<<<static_cast<unsigned>(rows * runs), kThreads, 0, s>>>(cand, k, static_cast<int>(runs),
+                                                                         run_pow2);
+    uint64_t* src = cand;
+    uint64_t* dst = cand2;
+    for (int64_t width = kRun; width < k; width *= 2) {
+        MergeKernel<<<GridFor(rows * k, 256, 16384), 256, 0, s>>>(src, dst, rows, k, width);
+        uint64_t* t = src;
+        src = dst;
+        dst = t;
+    }
+    EmitKernel<<<GridFor(rows * k, 256, 16384), 256, 0, s>>>(x, src, values, indices, rows, g);
+    CheckLaunch("topk launch");
+}
+
 } // namespace
+
+// Resolves this device's copy of `scratch` (called by the runtime's set-up
+// with the device current, before any TopK call).
+void TopkScratchSetup() {
+    int dev = 0;
+    Check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) {
+        throw Error("topk scratch: device ordinal out of range");
+    }
+    void* ptr = nullptr;
+    Check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(topk scratch)");
+    g_scratch_ptr[dev] = static_cast<uint8_t*>(ptr);
+}
+
 } // namespace nert_hip
 
 using namespace nert_hip;
@@ -341,75 +460,22 @@ extern "C" {
 
 int nert_hip_topk_f32(const float* x, float* values, int64_t* indices, int64_t outer, int64_t dim, int64_t inner,
                       int64_t k, void* stream) {
-    return Guard([&] {
-        if (k <= 0 || k > dim || dim > 0xFFFFFFFFll) {
-            throw Error("topk: need 0 < k <= dim < 2^32");
-        }
-        const int64_t rows = outer * inner;
-        if (rows <= 0) {
-            return;
-        }
-        hipStream_t s = StreamOr(stream);
-        const RowGeom g{dim, inner, k};
-        if (dim <= kSmallRow) {
-            if (rows > 0x7FFFFFFF) {
-                throw Error("topk: too many rows");
-            }
-            SmallRowKernel<<<static_cast<unsigned>(rows), kThreads, 0, s>>>(x, values, indices, g, PowTwoAtLeast(dim));
-            CheckLaunch("topk small-row launch");
-            return;
-        }
-        // Long rows: about 2048 workgroups over all rows, >= 4096 keys each.
-        int64_t chunks = (2048 + rows - 1) / rows;
-        const int64_t max_chunks = (dim + 4095) / 4096;
-        if (chunks > max_chunks) {
-            chunks = max_chunks;
-        }
-        if (chunks < 1) {
-            chunks = 1;
-        }
-        const int64_t chunk = (dim + chunks - 1) / chunks;
-        if (rows * chunks > 0x7FFFFFFF) {
-            throw Error("topk: too many rows");
-        }
-        // Workspace: state | histograms | two candidate buffers.
-        const int64_t st_bytes = (rows * static_cast<int64_t>(sizeof(SelectState)) + 255) / 256 * 256;
-        const int64_t hist_bytes = (rows * 256 * 4 + 255) / 256 * 256;
-        const int64_t cand_bytes = (rows * k * 8 + 255) / 256 * 256;
-        auto* ws = static_cast<uint8_t*>(Workspace(st_bytes + hist_bytes + 2 * cand_bytes, s));
-        auto* st = reinterpret_cast<SelectState*>(ws);
-        auto* hist = reinterpret_cast<uint32_t*>(ws + st_bytes);
-        auto* cand = reinterpret_cast<uint64_t*>(ws + st_bytes + hist_bytes);
-        auto* cand2 = reinterpret_cast<uint64_t*>(ws + st_bytes + hist_bytes + cand_bytes);
+    return Guard([&] { TopkImpl(x, values, indices, outer, dim, inner, k, stream, nullptr, 0); });
+}
 
-        InitSelectKernel<<<GridFor(rows * 256, 256, 4096), 256, 0, s>>>(st, hist, rows, k);
-        const unsigned blocks = static_cast<unsigned>(rows * chunks);
-        for (int pass = 0; pass < 8; ++pass) {
-            HistKernel<<<blocks, kThreads, 0, s>>>(x, g, chunk, static_cast<int>(chunks), st, hist, pass);
-            ScanKernel<<<static_cast<unsigned>(rows), 256, 0, s>>>(st, hist, pass);
+int nert_hip_topk_f32_noalloc(const float* x, float* values, int64_t* indices, int64_t outer, int64_t dim,
+                              int64_t inner, int64_t k, void* stream) {
+    return Guard([&] {
+        if (!RuntimeReady()) {
+            throw Error("topk_noalloc: call nert_hip_init() first (it sets up the fixed scratch)");
         }
-        CollectKernel<<<blocks, kThreads, 0, s>>>(x, g, chunk, static_cast<int>(chunks), st, cand);
-        if (k <= kRankMax) {
-            const int parts = static_cast<int>((k + 63) / 64);
-            RankSortKernel<<<static_cast<unsigned>(rows * parts), 256, 0, s>>>(cand, cand2, k, parts);
-            EmitKernel<<<GridFor(rows * k, 256, 16384), 256, 0, s>>>(x, cand2, values, indices, rows, g);
-            CheckLaunch("topk launch");
-            return;
+        int dev = 0;
+        Check(hipGetDevice(&dev), "hipGetDevice");
+        uint8_t* ptr = dev >= 0 && dev < kMaxDevices ? g_scratch_ptr[dev] : nullptr;
+        if (ptr == nullptr) {
+            throw Error("topk_noalloc: no fixed scratch on the current device");
         }
-        const int64_t runs = (k + kRun - 1) / kRun;
-        const int run_pow2 = PowTwoAtLeast(k < kRun ? k : kRun);
-        SortRunsKernel<<<static_cast<unsigned>(rows * runs), kThreads, 0, s>>>(cand, k, static_cast<int>(runs),
-                                                                             run_pow2);
-        uint64_t* src = cand;
-        uint64_t* dst = cand2;
-        for (int64_t width = kRun; width < k; width *= 2) {
-            MergeKernel<<<GridFor(rows * k, 256, 16384), 256, 0, s>>>(src, dst, rows, k, width);
-            uint64_t* t = src;
-            src = dst;
-            dst = t;
-        }
-        EmitKernel<<<GridFor(rows * k, 256, 16384), 256, 0, s>>>(x, src, values, indices, rows, g);
-        CheckLaunch("topk launch");
+        TopkImpl(x, values, indices, outer, dim, inner, k, stream, ptr, kNoAllocScratchBytes);
     });
 }
 
