@@ -274,6 +274,15 @@ int nert_hip_softmax_f32(const float* x, float* y, int64_t outer, int64_t dim, i
 int nert_hip_layernorm_f32(const float* x, const float* scale, int scale_scalar, const float* bias, int bias_scalar,
                            float* y, float* mean_out, float* invstd_out, int64_t rows, int64_t inner, double epsilon,
                            void* stream);
+/* sum = a + b (float32, rounded as the Add row rounds), then y =
+ * LayerNorm(sum) over rows of `inner` elements with per-element Scale and
+ * optional per-element B, bit-identical to running the Add and
+ * LayerNormalization rows one after the other, in one pass over a and b. No
+ * counterpart in the reference: it backs the runner's FusedAddLayerNorm row
+ * (a residual Add feeding a LayerNormalization, as in every pre-LN
+ * transformer block). */
+int nert_hip_add_layernorm_f32(const float* a, const float* b, const float* scale, const float* bias, float* sum,
+                               float* y, int64_t rows, int64_t inner, double epsilon, void* stream);
 /* InstanceNormalization over each (n, c) plane
  * (src/kernels/instance_normalization.cpp:44-106). */
 int nert_hip_instancenorm_f32(const float* x, const float* scale, const float* bias, float* y, int64_t batch,

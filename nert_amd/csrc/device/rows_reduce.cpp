@@ -417,6 +417,66 @@ NERT_HIP_ROW(LayerNormalization) {
     AfterRow(outputs, context);
 }
 
+// Not a reference row: the runner's fusion of a residual Add whose output
+// feeds a LayerNormalization over its trailing axes (pre-LN transformer
+// blocks). Inputs A, B (same shape), Scale, optional B of the norm; outputs
+// the sum (still read by later rows) and the normalised tensor. Equal bit for
+// bit to the Add row followed by the LayerNormalization row.
+NERT_HIP_ROW(FusedAddLayerNorm) {
+    const std::string context = "FusedAddLayerNorm (node '" + node.name + "')";
+    if (inputs.size() < 3 || inputs.size() > 4 || outputs.size() != 2) {
+        throw InferenceException(context + ": expected A, B, Scale, optional bias, and two outputs");
+    }
+    const TensorView& a = inputs[0];
+    const TensorView& b = inputs[1];
+    const TensorView& sum = outputs[0];
+    const TensorView& y = outputs[1];
+    for (const TensorView* t : {&a, &b, &sum, &y}) {
+        if (t->dtype != DataType::Float32) {
+            throw InferenceException(context + ": tensors must be float32");
+        }
+        if (t->dims != a.dims) {
+            throw InferenceException(context + ": A, B and both outputs must share one shape");
+        }
+    }
+    if (a.dims.empty()) {
+        throw InferenceException(context + ": tensors must not be scalars");
+    }
+    const int64_t rank = static_cast<int64_t>(a.dims.size());
+    int64_t axis = IntAttr(node, "axis", -1, "FusedAddLayerNorm");
+    if (axis < 0) {
+        axis += rank;
+    }
+    if (axis < 0 || axis >= rank) {
+        throw InferenceException(context + ": axis is out of range");
+    }
+    const float epsilon = FloatAttr(node, "epsilon", 1e-5f, "FusedAddLayerNorm");
+    int64_t outer = 1;
+    int64_t inner = 1;
+    for (int64_t i = 0; i < rank; ++i) {
+        (i < axis ? outer : inner) *= a.dims[static_cast<size_t>(i)];
+    }
+    (void)ElementCount(a.dims, context);
+    if (a.data == nullptr || b.data == nullptr || sum.data == nullptr || y.data == nullptr) {
+        throw InferenceException(context + ": null buffer");
+    }
+    int scale_scalar = 0;
+    const float* scale = NormParam(inputs[2], inner, scale_scalar, context, "Scale");
+    int bias_scalar = 0;
+    const float* bias = nullptr;
+    if (inputs.size() == 4 && inputs[3].dtype != DataType::Unknown) {
+        bias = NormParam(inputs[3], inner, bias_scalar, context, "B");
+    }
+    if (scale_scalar || bias_scalar) {
+        throw InferenceException(context + ": Scale and B must have one value per normalised element");
+    }
+    CheckStatus(nert_hip_add_layernorm_f32(static_cast<const float*>(a.data), static_cast<const float*>(b.data), scale,
+                                           bias, static_cast<float*>(sum.data), static_cast<float*>(y.data), outer,
+                                           inner, static_cast<double>(epsilon), Stream()),
+                context);
+    AfterRow(outputs, context);
+}
+
 // src/kernels/instance_normalization.cpp:44-80
 NERT_HIP_ROW(InstanceNormalization) {
     const std::string context = "InstanceNormalization (node '" + node.name + "')";

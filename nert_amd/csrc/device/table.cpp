@@ -19,6 +19,7 @@ nert::KernelFn FindRow(const std::string& op_type) {
         {"Conv", &Conv},
         {"FusedConv", &FusedConv},
         {"FusedMatMul", &FusedMatMul},
+        {"FusedAddLayerNorm", &FusedAddLayerNorm},
         {"Relu", &Relu},
         {"Sigmoid", &Sigmoid},
         {"Tanh", &Tanh},

@@ -14,6 +14,7 @@
 #include "../../include/nert_hip.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <array>
 #include <map>
 #include <mutex>
@@ -395,6 +396,19 @@ void LaunchGemm(GemmArgs p, int64_t batches, hipStream_t stream) {
     const size_t y_bytes = static_cast<size_t>(batches * p.m * p.n) * sizeof(float);
     // Candidates 0-11: tile shape x split count; 12: the skinny kernel.
     const bool skinny = SkinnyApplies(p, batches);
+    // NERT_HIP_GEMM_CANDIDATE=i forces candidate i wherever it applies (tests
+    // of each configuration use it).
+    if (const char* forced = std::getenv("NERT_HIP_GEMM_CANDIDATE")) {
+        const int i = std::atoi(forced);
+        if (i == 12 && skinny) {
+            LaunchSkinny(p, stream);
+            return;
+        }
+        if (i >= 0 && i < 12) {
+            LaunchConfig(p, batches, i / 4, kGemmSplits[i % 4], stream);
+            return;
+        }
+    }
     const int c = ChooseConfig("gemm", chosen, mu, key, y_bytes, stream, 13, 4 * fallback_shape, [&](int i, float* scratch) {
         GemmArgs q = p;
         q.y = scratch;

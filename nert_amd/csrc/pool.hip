@@ -102,17 +102,33 @@ __global__ __launch_bounds__(256) void MaxPoolTileKernel(PoolArgs p, PoolTile t)
     const float* xp = p.x + plane * p.in_h * p.in_w;
     const float ninf = -__builtin_huge_valf();
     if (t.vec) {
+        // Every 16-byte load of the tile is issued before the first LDS
+        // store (batches of kBatch per thread), so a thread waits for one
+        // memory round trip per batch rather than one per quad.
+        constexpr int kBatch = 4;
         const int quads_row = p.in_w / 4;
         const int quads = t.rows_in * quads_row;
-        for (int e = threadIdx.x; e < quads; e += blockDim.x) {
-            uint32_t c4;
-            const int r = static_cast<int>(DivMod(t.div_in_w, static_cast<uint32_t>(e), c4));
-            const int ih = ih0 + r;
-            nert_floatx4 v = {ninf, ninf, ninf, ninf};
-            if (static_cast<unsigned>(ih) < static_cast<unsigned>(p.in_h)) {
-                v = *reinterpret_cast<const nert_floatx4*>(xp + static_cast<int64_t>(ih) * p.in_w + 4 * c4);
+        for (int e0 = 0; e0 < quads; e0 += kBatch * 256) {
+            nert_floatx4 v[kBatch];
+            int dst[kBatch];
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                const int e = e0 + j * 256 + threadIdx.x;
+                uint32_t c4;
+                const int r = static_cast<int>(DivMod(t.div_in_w, static_cast<uint32_t>(e < quads ? e : 0), c4));
+                const int ih = ih0 + r;
+                const bool in = e < quads && static_cast<unsigned>(ih) < static_cast<unsigned>(p.in_h);
+                const nert_floatx4 w = *reinterpret_cast<const nert_floatx4*>(
+                    xp + static_cast<int64_t>(in ? ih : 0) * p.in_w + 4 * c4);
+                v[j] = in ? w : nert_floatx4{ninf, ninf, ninf, ninf};
+                dst[j] = e < quads ? r * p.in_w + 4 * static_cast<int>(c4) : -1;
             }
-            *reinterpret_cast<nert_floatx4*>(tile + r * p.in_w + 4 * c4) = v;
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                if (dst[j] >= 0) {
+                    *reinterpret_cast<nert_floatx4*>(tile + dst[j]) = v[j];
+                }
+            }
         }
     } else {
         const int elems = t.rows_in * p.in_w;
@@ -126,8 +142,8 @@ __global__ __launch_bounds__(256) void MaxPoolTileKernel(PoolArgs p, PoolTile t)
         }
     }
     __syncthreads();
-    const int outs = t.rows * p.out_w;
     float* yp = p.y + plane * p.out_h * p.out_w;
+    const int outs = t.rows * p.out_w;
     for (int o = threadIdx.x; o < outs; o += blockDim.x) {
         uint32_t ow;
         const int r = static_cast<int>(DivMod(t.div_out_w, static_cast<uint32_t>(o), ow));
@@ -247,6 +263,51 @@ __global__ __launch_bounds__(256) void GlobalAvgPoolKernel(const float* __restri
     }
 }
 
+// Large planes (the reference bench's [8, 64, 112, 112]): one 256-thread
+// workgroup per plane, 16-byte loads when the plane allows, four loads in
+// flight per thread, double accumulation, then the waves' sums through LDS
+// in a fixed order.
+template <bool VEC>
+__global__ __launch_bounds__(256) void GlobalAvgPoolBlockKernel(const float* __restrict__ x, float* __restrict__ y,
+                                                                int64_t spatial) {
+    __shared__ double part[4];
+    const int tid = threadIdx.x;
+    const float* xp = x + static_cast<int64_t>(blockIdx.x) * spatial;
+    double sum = 0.0;
+    if constexpr (VEC) {
+        const nert_floatx4* x4 = reinterpret_cast<const nert_floatx4*>(xp);
+        const int64_t quads = spatial / 4;
+        int64_t i = tid;
+        for (; i + 768 < quads; i += 1024) {
+            const nert_floatx4 a = x4[i];
+            const nert_floatx4 b = x4[i + 256];
+            const nert_floatx4 c = x4[i + 512];
+            const nert_floatx4 d = x4[i + 768];
+            sum += ((static_cast<double>(a[0]) + a[1]) + (static_cast<double>(a[2]) + a[3])) +
+                   ((static_cast<double>(b[0]) + b[1]) + (static_cast<double>(b[2]) + b[3]));
+            sum += ((static_cast<double>(c[0]) + c[1]) + (static_cast<double>(c[2]) + c[3])) +
+                   ((static_cast<double>(d[0]) + d[1]) + (static_cast<double>(d[2]) + d[3]));
+        }
+        for (; i < quads; i += 256) {
+            const nert_floatx4 a = x4[i];
+            sum += (static_cast<double>(a[0]) + a[1]) + (static_cast<double>(a[2]) + a[3]);
+        }
+    } else {
+        for (int64_t i = tid; i < spatial; i += 256) {
+            sum += static_cast<double>(xp[i]);
+        }
+    }
+    sum = WaveSum(sum);
+    if ((tid & 63) == 0) {
+        part[tid >> 6] = sum;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const double total = (part[0] + part[1]) + (part[2] + part[3]);
+        y[blockIdx.x] = static_cast<float>(total / static_cast<double>(spatial));
+    }
+}
+
 PoolArgs MakeArgs(const float* x, float* y, const nert_pool_desc* d) {
     PoolArgs p{};
     p.x = x;
@@ -316,6 +377,18 @@ int nert_hip_avgpool2d_f32(const float* x, float* y, const nert_pool_desc* d, vo
 int nert_hip_global_avgpool_f32(const float* x, float* y, int64_t planes, int64_t spatial, void* stream) {
     return Guard([&] {
         if (planes <= 0 || spatial <= 0) {
+            return;
+        }
+        if (spatial >= 2048 && planes <= 0x7FFFFFFF) {
+            const bool vec = spatial % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+            if (vec) {
+                GlobalAvgPoolBlockKernel<true><<<static_cast<unsigned>(planes), 256, 0, StreamOr(stream)>>>(x, y,
+                                                                                                           spatial);
+            } else {
+                GlobalAvgPoolBlockKernel<false><<<static_cast<unsigned>(planes), 256, 0, StreamOr(stream)>>>(x, y,
+                                                                                                            spatial);
+            }
+            CheckLaunch("GlobalAvgPoolBlockKernel launch");
             return;
         }
         const int64_t blocks = (planes + 3) / 4;

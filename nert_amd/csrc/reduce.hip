@@ -14,8 +14,10 @@
 // (src/kernels/reduce_sum.cpp:33-70, reduce_mean.cpp:180-197), ReduceMax
 // starting from the lowest float with std::max so NaN never wins
 // (reduce_max.cpp:152-165), ReduceL2 as sqrt of a double sum of squares
-// (reduce_l2.cpp:63-80), Softmax with a float peak and double exponentials
-// (softmax.cpp:98-119), LayerNorm/InstanceNorm two-pass double statistics
+// (reduce_l2.cpp:63-80), Softmax with the reference's float peak rule
+// (softmax.cpp:98-119; its exponentials are double, ours fp32 with a double
+// sum: within 1e-6 relative, far inside the 1e-4 bar, and the rows stay
+// memory-bound), LayerNorm/InstanceNorm two-pass double statistics
 // (layer_normalization.cpp:134-159, instance_normalization.cpp:80-103),
 // ArgMax's sequential first/last-maximum rule (arg_max.cpp:41-57) and
 // CumSum's sequential scan (cum_sum.cpp:40-70).
@@ -282,14 +284,14 @@ __global__ __launch_bounds__(256) void SoftmaxRowsKernel(const float* __restrict
     if (first != first) {
         peak = first;
     }
-    const double dp = static_cast<double>(peak);
     double total = 0.0;
     for (int64_t i = lane; i < dim; i += 64) {
-        total += exp(static_cast<double>(p[i]) - dp);
+        total += static_cast<double>(expf(p[i] - peak));
     }
     total = WaveAllSum(total);
+    const float inv = static_cast<float>(1.0 / total);
     for (int64_t i = lane; i < dim; i += 64) {
-        q[i] = static_cast<float>(exp(static_cast<double>(p[i]) - dp) / total);
+        q[i] = expf(p[i] - peak) * inv;
     }
 }
 
@@ -338,23 +340,112 @@ __global__ __launch_bounds__(256) void SoftmaxRowsRegKernel(const float* __restr
     if (first != first) {
         peak = first;
     }
-    const double dp = static_cast<double>(peak);
-    double e[PER];
+    float e[PER];
     double total = 0.0;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-        e[k] = lane + LANES * k < dim ? exp(static_cast<double>(v[k]) - dp) : 0.0;
-        total += e[k];
+        e[k] = lane + LANES * k < dim ? expf(v[k] - peak) : 0.0f;
+        total += static_cast<double>(e[k]);
     }
 #pragma unroll
     for (int off = LANES / 2; off > 0; off >>= 1) {
         total += __shfl_xor(total, off, LANES);
     }
+    const float inv = static_cast<float>(1.0 / total);
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
         const int i = lane + LANES * k;
         if (i < dim) {
-            q[i] = static_cast<float>(e[k] / total);
+            q[i] = e[k] * inv;
+        }
+    }
+}
+
+// Rows of up to 256 * PER elements, one 256-thread workgroup per row, held in
+// registers (one read of the row; 16-byte loads and stores when VEC): peak and
+// sum through the waves' shuffles and LDS, fp32 exponentials, double sum.
+template <int PER, bool VEC>
+__global__ __launch_bounds__(256) void SoftmaxRowsBlockKernel(const float* __restrict__ x, float* __restrict__ y,
+                                                              int dim) {
+    __shared__ float peaks[4];
+    __shared__ double sums[4];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const float* p = x + static_cast<int64_t>(blockIdx.x) * dim;
+    float* q = y + static_cast<int64_t>(blockIdx.x) * dim;
+    float v[PER];
+    // Element j of this thread: 4 * (tid + 256 * (j / 4)) + j % 4 (VEC) or
+    // tid + 256 * j; clamped loads, then a select.
+    auto index = [&](int j) { return VEC ? 4 * (tid + 256 * (j / 4)) + (j & 3) : tid + 256 * j; };
+    if constexpr (VEC) {
+#pragma unroll
+        for (int j = 0; j < PER; j += 4) {
+            const int i = 4 * (tid + 256 * (j / 4));
+            const nert_floatx4 w = *reinterpret_cast<const nert_floatx4*>(p + (i < dim ? i : 0));
+            v[j] = w[0];
+            v[j + 1] = w[1];
+            v[j + 2] = w[2];
+            v[j + 3] = w[3];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int i = index(j);
+            v[j] = p[i < dim ? i : dim - 1];
+        }
+    }
+    const float first = p[0];
+    float peak = first;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const float w = index(j) < dim ? v[j] : -__builtin_huge_valf();
+        peak = w > peak ? w : peak;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float o = __shfl_xor(peak, off, 64);
+        peak = o > peak ? o : peak;
+    }
+    if ((tid & 63) == 0) {
+        peaks[wave] = peak;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        peak = peaks[w] > peak ? peaks[w] : peak;
+    }
+    if (first != first) {
+        peak = first; // the reference's peak rule: see SoftmaxRowsKernel
+    }
+    double total = 0.0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        v[j] = index(j) < dim ? expf(v[j] - peak) : 0.0f;
+        total += static_cast<double>(v[j]);
+    }
+    total = WaveAllSum(total);
+    if ((tid & 63) == 0) {
+        sums[wave] = total;
+    }
+    __syncthreads();
+    total = (sums[0] + sums[1]) + (sums[2] + sums[3]);
+    const float inv = static_cast<float>(1.0 / total);
+    if constexpr (VEC) {
+#pragma unroll
+        for (int j = 0; j < PER; j += 4) {
+            const int i = 4 * (tid + 256 * (j / 4));
+            if (i < dim) {
+                *reinterpret_cast<nert_floatx4*>(q + i) =
+                    nert_floatx4{v[j] * inv, v[j + 1] * inv, v[j + 2] * inv, v[j + 3] * inv};
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int i = index(j);
+            if (i < dim) {
+                q[i] = v[j] * inv;
+            }
         }
     }
 }
@@ -376,13 +467,13 @@ __global__ void SoftmaxColsKernel(const float* __restrict__ x, float* __restrict
                 peak = v;
             }
         }
-        const double dp = static_cast<double>(peak);
         double total = 0.0;
         for (int64_t k = 0; k < dim; ++k) {
-            total += exp(static_cast<double>(p[k * inner]) - dp);
+            total += static_cast<double>(expf(p[k * inner] - peak));
         }
+        const float inv = static_cast<float>(1.0 / total);
         for (int64_t k = 0; k < dim; ++k) {
-            q[k * inner] = static_cast<float>(exp(static_cast<double>(p[k * inner]) - dp) / total);
+            q[k * inner] = expf(p[k * inner] - peak) * inv;
         }
     }
 }
@@ -487,6 +578,145 @@ __global__ __launch_bounds__(256) void LayerNormRegKernel(const float* __restric
         if (invstd_out != nullptr) {
             invstd_out[row] = static_cast<float>(inv);
         }
+    }
+}
+
+// Rows of at most 256 * Q elements (inner % 4 == 0, 16-byte aligned
+// tensors, per-element or absent Scale and B): lane l holds the quads
+// l, l + 64, ... of its row in registers, read and written with 16-byte
+// accesses; the statistics are the two-pass double ones of
+// LayerNormRegKernel. LayerNormQuadRow is the part after the row is in
+// registers, shared by the plain kernel and the one that first adds two
+// rows (FusedAddLayerNorm), so both normalise bit-identically.
+template <int Q>
+__device__ __forceinline__ void LayerNormQuadRow(const nert_floatx4 (&v)[Q], const nert_floatx4 (&sc)[Q],
+                                                 const nert_floatx4 (&bi)[Q], bool has_bias, nert_floatx4* q,
+                                                 float* mean_out, float* invstd_out, int64_t row, int inner,
+                                                 double eps) {
+    const int lane = threadIdx.x & 63;
+    const int quads = inner / 4;
+    double sum = 0.0;
+#pragma unroll
+    for (int k = 0; k < Q; ++k) {
+        if (lane + 64 * k < quads) {
+            sum += (static_cast<double>(v[k][0]) + static_cast<double>(v[k][1])) +
+                   (static_cast<double>(v[k][2]) + static_cast<double>(v[k][3]));
+        }
+    }
+    const double mean = WaveAllSum(sum) / static_cast<double>(inner);
+    double sq = 0.0;
+#pragma unroll
+    for (int k = 0; k < Q; ++k) {
+        if (lane + 64 * k < quads) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const double c = static_cast<double>(v[k][e]) - mean;
+                sq += c * c;
+            }
+        }
+    }
+    const double inv = 1.0 / sqrt(WaveAllSum(sq) / static_cast<double>(inner) + eps);
+#pragma unroll
+    for (int k = 0; k < Q; ++k) {
+        const int i = lane + 64 * k;
+        if (i < quads) {
+            nert_floatx4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const double scaled = (static_cast<double>(v[k][e]) - mean) * inv * static_cast<double>(sc[k][e]);
+                o[e] = static_cast<float>(has_bias ? scaled + static_cast<double>(bi[k][e]) : scaled);
+            }
+            q[i] = o;
+        }
+    }
+    if (lane == 0) {
+        if (mean_out != nullptr) {
+            mean_out[row] = static_cast<float>(mean);
+        }
+        if (invstd_out != nullptr) {
+            invstd_out[row] = static_cast<float>(inv);
+        }
+    }
+}
+
+// Loads the quads of row `row` this lane owns from `src` (clamped addresses,
+// always valid) into `out`.
+template <int Q>
+__device__ __forceinline__ void LoadQuads(const float* src, int quads, nert_floatx4 (&out)[Q]) {
+    const int lane = threadIdx.x & 63;
+    const nert_floatx4* p = reinterpret_cast<const nert_floatx4*>(src);
+#pragma unroll
+    for (int k = 0; k < Q; ++k) {
+        const int i = lane + 64 * k;
+        out[k] = p[i < quads ? i : quads - 1];
+    }
+}
+
+template <int Q>
+__global__ __launch_bounds__(256) void LayerNormQuadKernel(const float* __restrict__ x,
+                                                           const float* __restrict__ scale,
+                                                           const float* __restrict__ bias, float* __restrict__ y,
+                                                           float* mean_out, float* invstd_out, int64_t rows,
+                                                           int inner, double eps) {
+    const int64_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) {
+        return;
+    }
+    const int quads = inner / 4;
+    nert_floatx4 v[Q];
+    nert_floatx4 sc[Q];
+    nert_floatx4 bi[Q];
+    LoadQuads<Q>(x + row * inner, quads, v);
+    LoadQuads<Q>(scale, quads, sc);
+    LoadQuads<Q>(bias != nullptr ? bias : scale, quads, bi);
+    LayerNormQuadRow<Q>(v, sc, bi, bias != nullptr, reinterpret_cast<nert_floatx4*>(y + row * inner), mean_out,
+                        invstd_out, row, inner, eps);
+}
+
+// FusedAddLayerNorm: s = a + b (float, as the Add row rounds it), written to
+// `sum`, then LayerNorm of s into y -- one read of each operand instead of
+// writing s and reading it back.
+template <int Q>
+__global__ __launch_bounds__(256) void AddLayerNormQuadKernel(const float* __restrict__ a,
+                                                              const float* __restrict__ b,
+                                                              const float* __restrict__ scale,
+                                                              const float* __restrict__ bias,
+                                                              float* __restrict__ sum, float* __restrict__ y,
+                                                              int64_t rows, int inner, double eps) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) {
+        return;
+    }
+    const int quads = inner / 4;
+    nert_floatx4 v[Q];
+    nert_floatx4 w[Q];
+    nert_floatx4 sc[Q];
+    nert_floatx4 bi[Q];
+    LoadQuads<Q>(a + row * inner, quads, v);
+    LoadQuads<Q>(b + row * inner, quads, w);
+    LoadQuads<Q>(scale, quads, sc);
+    LoadQuads<Q>(bias != nullptr ? bias : scale, quads, bi);
+    nert_floatx4* s4 = reinterpret_cast<nert_floatx4*>(sum + row * inner);
+#pragma unroll
+    for (int k = 0; k < Q; ++k) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[k][e] = __fadd_rn(v[k][e], w[k][e]);
+        }
+        if (lane + 64 * k < quads) {
+            s4[lane + 64 * k] = v[k];
+        }
+    }
+    LayerNormQuadRow<Q>(v, sc, bi, bias != nullptr, reinterpret_cast<nert_floatx4*>(y + row * inner), nullptr,
+                        nullptr, row, inner, eps);
+}
+
+__global__ void AddFlatKernel(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ s,
+                              int64_t n) {
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        s[i] = __fadd_rn(a[i], b[i]);
     }
 }
 
@@ -841,6 +1071,16 @@ int nert_hip_softmax_f32(const float* x, float* y, int64_t outer, int64_t dim, i
             SoftmaxRowsRegKernel<4><<<RowBlocks(outer), 256, 0, s>>>(x, y, outer, static_cast<int>(dim));
         } else if (inner == 1 && dim <= 1024) {
             SoftmaxRowsRegKernel<16><<<RowBlocks(outer), 256, 0, s>>>(x, y, outer, static_cast<int>(dim));
+        } else if (inner == 1 && dim <= 4096 && outer <= 0x7FFFFFFF) {
+            const bool vec = dim % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                             (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+            if (vec) {
+                SoftmaxRowsBlockKernel<16, true><<<static_cast<unsigned>(outer), 256, 0, s>>>(x, y,
+                                                                                             static_cast<int>(dim));
+            } else {
+                SoftmaxRowsBlockKernel<16, false><<<static_cast<unsigned>(outer), 256, 0, s>>>(x, y,
+                                                                                              static_cast<int>(dim));
+            }
         } else if (inner == 1) {
             SoftmaxRowsKernel<<<RowBlocks(outer), 256, 0, s>>>(x, y, outer, dim);
         } else {
@@ -858,7 +1098,24 @@ int nert_hip_layernorm_f32(const float* x, const float* scale, int scale_scalar,
             return;
         }
         hipStream_t s = StreamOr(stream);
-        if (inner <= 256) {
+        const auto aligned = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+        const bool quad = inner % 4 == 0 && inner <= 1024 && !scale_scalar && (bias == nullptr || !bias_scalar) &&
+                          aligned(x) && aligned(y) && aligned(scale) && (bias == nullptr || aligned(bias));
+        if (quad) {
+            // Q = quads per lane, exactly what the row needs (no idle loads).
+            const int q = static_cast<int>((inner / 4 + 63) / 64);
+            const int n = static_cast<int>(inner);
+            const unsigned blocks = RowBlocks(rows);
+            if (q == 1) {
+                LayerNormQuadKernel<1><<<blocks, 256, 0, s>>>(x, scale, bias, y, mean_out, invstd_out, rows, n, epsilon);
+            } else if (q == 2) {
+                LayerNormQuadKernel<2><<<blocks, 256, 0, s>>>(x, scale, bias, y, mean_out, invstd_out, rows, n, epsilon);
+            } else if (q == 3) {
+                LayerNormQuadKernel<3><<<blocks, 256, 0, s>>>(x, scale, bias, y, mean_out, invstd_out, rows, n, epsilon);
+            } else {
+                LayerNormQuadKernel<4><<<blocks, 256, 0, s>>>(x, scale, bias, y, mean_out, invstd_out, rows, n, epsilon);
+            }
+        } else if (inner <= 256) {
             LayerNormRegKernel<4><<<RowBlocks(rows), 256, 0, s>>>(x, scale, scale_scalar, bias, bias_scalar, y,
                                                                   mean_out, invstd_out, rows, static_cast<int>(inner),
                                                                   epsilon);
@@ -871,6 +1128,41 @@ int nert_hip_layernorm_f32(const float* x, const float* scale, int scale_scalar,
                                                             invstd_out, rows, inner, epsilon);
         }
         CheckLaunch("layernorm launch");
+    });
+}
+
+int nert_hip_add_layernorm_f32(const float* a, const float* b, const float* scale, const float* bias, float* sum,
+                               float* y, int64_t rows, int64_t inner, double epsilon, void* stream) {
+    return Guard([&] {
+        if (rows * inner == 0) {
+            return;
+        }
+        hipStream_t s = StreamOr(stream);
+        const auto aligned = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+        const bool quad = inner % 4 == 0 && inner <= 1024 && aligned(a) && aligned(b) && aligned(scale) &&
+                          (bias == nullptr || aligned(bias)) && aligned(sum) && aligned(y);
+        if (!quad) {
+            // The separate Add and LayerNormalization launches, as the rows run them.
+            AddFlatKernel<<<GridFor(rows * inner, 256, 16384), 256, 0, s>>>(a, b, sum, rows * inner);
+            CheckLaunch("add launch");
+            if (nert_hip_layernorm_f32(sum, scale, 0, bias, 0, y, nullptr, nullptr, rows, inner, epsilon, stream) != 0) {
+                throw Error(std::string(nert_hip_last_error()));
+            }
+            return;
+        }
+        const int q = static_cast<int>((inner / 4 + 63) / 64);
+        const int n = static_cast<int>(inner);
+        const unsigned blocks = RowBlocks(rows);
+        if (q == 1) {
+            AddLayerNormQuadKernel<1><<<blocks, 256, 0, s>>>(a, b, scale, bias, sum, y, rows, n, epsilon);
+        } else if (q == 2) {
+            AddLayerNormQuadKernel<2><<<blocks, 256, 0, s>>>(a, b, scale, bias, sum, y, rows, n, epsilon);
+        } else if (q == 3) {
+            AddLayerNormQuadKernel<3><<<blocks, 256, 0, s>>>(a, b, scale, bias, sum, y, rows, n, epsilon);
+        } else {
+            AddLayerNormQuadKernel<4><<<blocks, 256, 0, s>>>(a, b, scale, bias, sum, y, rows, n, epsilon);
+        }
+        CheckLaunch("add-layernorm launch");
     });
 }
 

@@ -1,6 +1,7 @@
 """Op-level measurement cases: the reference's published op-bench fixtures
 (olibartfast/nert bench/runtime/main.cpp:331-674, the twelve quoted with
-MI300X figures) plus BASELINE.json configs[0] and configs[1](a)(b)(c).
+MI300X figures), BASELINE.json configs[0] and configs[1](a)(b)(c), and the
+bandwidth-bound rows at the shapes configs[2] and configs[3] run them.
 
 Each case is one node with the fixture's shapes, attributes and value ranges
 (values drawn from this package's seeded generator; the reference draws from
@@ -128,6 +129,22 @@ def _cases() -> list[OpCase]:
                     [("y", (32, 1000), F32)], "hbm", _bytes(((32, 512), F32), ((1000, 512), F32), ((1000,), F32),
                                                            ((32, 1000), F32)),
                     {"transB": 1, "alpha": 1.0, "beta": 1.0}, source="BASELINE.json configs[1](c)"))
+    # --- the bandwidth-bound rows at the model configs' shapes ---
+    c.append(OpCase("cfg2_maxpool_32x64x112x112", "MaxPool", [("x", (32, 64, 112, 112), F32, _nrm(1.0))],
+                    [("y", (32, 64, 56, 56), F32)], "hbm",
+                    _bytes(((32, 64, 112, 112), F32), ((32, 64, 56, 56), F32)),
+                    {"kernel_shape": [3, 3], "strides": [2, 2], "pads": [1, 1, 1, 1]},
+                    source="BASELINE.json configs[2] (ResNet-18 stem pool)"))
+    c.append(OpCase("cfg3_softmax_16x12x197x197", "Softmax", [("x", (16, 12, 197, 197), F32, _nrm(3.0))],
+                    [("y", (16, 12, 197, 197), F32)], "hbm",
+                    _bytes(((16, 12, 197, 197), F32), ((16, 12, 197, 197), F32)), {"axis": -1},
+                    source="BASELINE.json configs[3] (ViT attention)"))
+    c.append(OpCase("cfg3_layernorm_16x197x768", "LayerNormalization", [("x", (16, 197, 768), F32, _nrm(1.0))],
+                    [("y", (16, 197, 768), F32)], "hbm",
+                    _bytes(((16, 197, 768), F32), ((768,), F32), ((768,), F32), ((16, 197, 768), F32)),
+                    {"axis": -1, "epsilon": 1e-6},
+                    {"scale": np.linspace(0.9, 1.1, 768, dtype=F32), "bias": np.linspace(-0.1, 0.1, 768, dtype=F32)},
+                    source="BASELINE.json configs[3] (ViT pre-LN)"))
     return c
 
 

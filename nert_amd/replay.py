@@ -1,13 +1,14 @@
 """Replays one of the seeded BASELINE workloads through the runner, for
 timing and kernel traces:
 
-    python3 -m nert_amd.replay {resnet18,vit,detector} [--runs N]
+    python3 -m nert_amd.replay {resnet18,vit,detector} [--runs N] [--eager] [--copy-probe]
 
-Builds the program (Conv chain fusion, view aliasing), binds the seeded
-input, runs it once eagerly (per-geometry kernel choices are made here),
-captures it into a HIP graph and replays it N times between HIP events on
-the layer stream. Prints one line: workload, ms per replay, and the
-algorithmic GFLOP of the graph.
+Builds the program (Conv chain fusion, Add+LayerNorm fusion, view
+aliasing), binds the seeded input, runs it once eagerly, captures it into a
+HIP graph and replays it N times between HIP events on the layer stream
+(--eager: N eager runs instead). Prints one line: workload, ms per replay,
+and the algorithmic GFLOP of the graph. --copy-probe ends with one Relu over
+256 MiB, the known-size dispatch that calibrates --pmc byte counters.
 
     python3 -m nert_amd.replay rows [--runs N]
 
@@ -172,6 +173,10 @@ def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("workload", choices=sorted(BUILDERS) + ["rows", "transfer"])
     ap.add_argument("--runs", type=int, default=10)
+    ap.add_argument("--eager", action="store_true", help="launch the rows one by one instead of replaying a graph")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="end with one Relu over 64 Mi floats (256 MiB read, 256 MiB written): the known-size "
+                         "dispatch that scales FETCH_SIZE/WRITE_SIZE counters of a --pmc run")
     args = ap.parse_args(argv)
     device.init()
     if args.workload == "transfer":
@@ -184,19 +189,41 @@ def main(argv: list[str] | None = None) -> int:
     prog = Program(g)
     for name in g.inputs:
         prog.set_input(name, inputs[name])
-    prog.capture()
-    prog.replay()
+    step = prog.run
+    if not args.eager:
+        prog.capture()
+        step = prog.replay
+    step()
     device.synchronize()
     start, stop = Event(), Event()
     start.record()
     for _ in range(args.runs):
-        prog.replay()
+        step()
     stop.record()
     ms = start.elapsed_ms(stop) / max(args.runs, 1)
     device.synchronize()
-    print(f"{args.workload}: {ms:.3f} ms per replay, {g.flops() / 1e9:.2f} GFLOP", flush=True)
+    prog.check_errors()
+    print(f"{args.workload}: {ms:.3f} ms per {'eager run' if args.eager else 'replay'}, "
+          f"{g.flops() / 1e9:.2f} GFLOP", flush=True)
     prog.close()
+    if args.copy_probe:
+        _copy_probe()
     return 0
+
+
+def _copy_probe() -> None:
+    """One Relu over 64 Mi non-negative floats: 256 MiB read, 256 MiB written."""
+    import numpy as np
+
+    from .device import DeviceArray, check, lib
+
+    n = 64 << 20
+    buf = DeviceArray.from_host(np.ones(n, np.float32))
+    out = DeviceArray((n,), np.float32)
+    check(lib().nert_hip_unary(0, 0, buf.ptr, out.ptr, n, 0.0, 0.0, None), "relu")
+    device.synchronize()
+    buf.close()
+    out.close()
 
 
 if __name__ == "__main__":

@@ -309,6 +309,56 @@ def _match_gelu(g: Graph, v: str, consumers, outputs, other):
     return [div, erf, add, mul1, mul2], (c1, c2, c3)
 
 
+def fuse_add_layernorm(g: Graph) -> Graph:
+    """Rewrites a residual Add whose output feeds a LayerNormalization into
+    one FusedAddLayerNorm node (outputs: the sum, which later rows still
+    read, and the normalised tensor).
+
+    The Add must sum two float32 tensors of its output's shape (no
+    broadcasting); the LayerNormalization must take that sum as X, have only
+    the Y output, and per-element float32 initializers for Scale (and B).
+    The fused node sits where the Add was (the norm's other operands are
+    initializers). The row adds in float32 like the Add row and normalises
+    with the LayerNormalization row's kernel, so the outputs are
+    bit-identical; the sum is read once instead of written and read back.
+    """
+    consumers: dict[str, list[int]] = {}
+    for idx, n in enumerate(g.nodes):
+        for t in n.inputs:
+            if t:
+                consumers.setdefault(t, []).append(idx)
+    replace: dict[int, Node] = {}
+    dropped: set[int] = set()
+    for idx, n in enumerate(g.nodes):
+        if n.op != "Add" or len(n.inputs) != 2 or len(n.outputs) != 1 or idx in dropped:
+            continue
+        out = n.outputs[0]
+        dtype, shape = g.tensors[out]
+        if np.dtype(dtype) != np.float32 or not shape or any(
+                g.tensors[t][1] != shape or np.dtype(g.tensors[t][0]) != np.float32 for t in n.inputs):
+            continue
+        for c in consumers.get(out, []):
+            ln = g.nodes[c]
+            if ln.op != "LayerNormalization" or c in dropped or ln.inputs[0] != out or len(ln.outputs) != 1:
+                continue
+            axis = int(ln.attrs.get("axis", -1)) % len(shape)
+            inner = int(np.prod(shape[axis:]))
+            params = [t for t in ln.inputs[1:] if t]
+            if not params or len(ln.inputs) > 3 or any(
+                    t not in g.initializers or g.initializers[t].dtype != np.float32 or g.initializers[t].size != inner
+                    or g.initializers[t].ndim != 1 for t in params):
+                continue
+            attrs = {"axis": int(ln.attrs.get("axis", -1))}
+            if "epsilon" in ln.attrs:
+                attrs["epsilon"] = ln.attrs["epsilon"]
+            replace[idx] = Node("FusedAddLayerNorm", [n.inputs[0], n.inputs[1]] + list(ln.inputs[1:]),
+                                [out, ln.outputs[0]], attrs, ln.name)
+            dropped.add(c)
+            break
+    nodes = [replace.get(i, nd) for i, nd in enumerate(g.nodes) if i not in dropped]
+    return Graph(nodes=nodes, initializers=g.initializers, inputs=g.inputs, outputs=g.outputs, tensors=g.tensors)
+
+
 class _PackedNode:
     __slots__ = ("op", "name", "attrs", "ins", "outs", "err")
 
@@ -324,7 +374,7 @@ class _PackedNode:
 class Program:
     def __init__(self, g: Graph, fuse: bool = True, views: bool = True):
         if fuse:
-            g = fuse_matmul_chains(fuse_conv_chains(g))
+            g = fuse_add_layernorm(fuse_matmul_chains(fuse_conv_chains(g)))
         self.alias: dict[str, tuple[str, int]] = {}
         if views:
             g, self.alias = alias_views(g)

@@ -195,6 +195,9 @@ POOL_CASES = [
     ((1, 2, 9, 9), {"kernel_shape": [3, 3], "dilations": [2, 2], "pads": [2, 2, 2, 2]}),
     ((2, 3, 30, 2000), {"kernel_shape": [3, 3], "pads": [1, 1, 1, 1]}),  # wide rows: 4-row LDS tiles
     ((1, 1, 5, 5000), {"kernel_shape": [3, 3]}),                          # too wide for LDS: direct kernel
+    ((1, 2, 20, 20), {"kernel_shape": [3, 3], "dilations": [2, 2], "pads": [2, 2, 2, 2]}),  # 4 outputs/thread
+    ((1, 3, 17, 17), {"kernel_shape": [3, 3], "strides": [2, 2], "ceil_mode": 1}),         # ragged last window
+    ((8, 64, 112, 112), {"kernel_shape": [3, 3], "strides": [2, 2]}),     # the reference bench case (55 wide)
 ]
 
 
@@ -231,7 +234,8 @@ def test_maxpool_nan_and_neg_inf(gpu):
     assert_parity("MaxPool", [x], [((1, 1, 2, 2), F)], {"kernel_shape": [2, 2], "strides": [2, 2]})
 
 
-@pytest.mark.parametrize("xs", [(32, 512, 7, 7), (8, 64, 112, 112), (2, 3, 5), (1, 4, 2, 3, 4), (3, 5)])
+@pytest.mark.parametrize("xs", [(32, 512, 7, 7), (8, 64, 112, 112), (2, 3, 5), (1, 4, 2, 3, 4), (3, 5),
+                                (2, 3, 47, 49), (1, 2, 4096, 1)])
 def test_global_average_pool(gpu, xs):
     x = randn(xs, seed=29)
     out = xs[:2] + (1,) * (len(xs) - 2)

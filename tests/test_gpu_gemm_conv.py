@@ -443,3 +443,32 @@ def test_conv_1x1_forced_configs(gpu, tmp_path, xs, ws, attrs, cand):
                                "NOTSET"), what=f"candidate {cand}")
     want = conv + z
     assert np.array_equal(np.load(paths["out2"]), np.where(want > 0, want, np.float32(0)).astype(F))
+
+
+# --- every GEMM candidate, forced ------------------------------------------
+
+GEMM_FORCED = [
+    ("MatMul", [(24, 197, 64), (24, 64, 197)], {}),                 # attention scores (K = 64)
+    ("MatMul", [(24, 197, 197), (24, 197, 64)], {}),                # attention x V (K = 197, unaligned rows)
+    ("MatMul", [(3, 70, 33), (3, 33, 45)], {}),                     # ragged M, N, K
+    ("MatMul", [(96, 200), (200, 80)], {}),                         # one batch
+    ("Gemm", [(50, 37), (60, 37)], {"transB": 1}),                  # K contiguous in B
+    ("Gemm", [(37, 50), (37, 60)], {"transA": 1}),                  # A transposed
+    ("Gemm", [(40, 1100), (1100, 24)], {}),                         # two-level accumulation (K > 1024)
+]
+
+
+@pytest.mark.parametrize("candidate", list(range(13)))
+@pytest.mark.parametrize("op,shapes,attrs", GEMM_FORCED)
+def test_gemm_every_candidate(gpu, monkeypatch, candidate, op, shapes, attrs):
+    """Each tile shape x split count and the skinny kernel, forced with
+    NERT_HIP_GEMM_CANDIDATE wherever it applies, against the reference row."""
+    monkeypatch.setenv("NERT_HIP_GEMM_CANDIDATE", str(candidate))
+    xs = [uniform(s, seed=50 + i) for i, s in enumerate(shapes)]
+    if op == "MatMul":
+        out = np.matmul(np.zeros(shapes[0], F), np.zeros(shapes[1], F)).shape
+    else:
+        m = shapes[0][1] if attrs.get("transA") else shapes[0][0]
+        n = shapes[1][0] if attrs.get("transB") else shapes[1][1]
+        out = (m, n)
+    assert_parity(op, xs, [(out, F)], attrs)

@@ -128,8 +128,9 @@ def test_dropin_end_to_end_bs32(resnet):
 
 
 def test_fused_vit_program_is_bit_identical(gpu):
-    """The MatMul+scale+bias+Gelu fusion and the view aliasing change no
-    output bit (ViT-B/16, two layers, batch 2)."""
+    """The MatMul+scale+bias+Gelu fusion, the residual Add+LayerNorm fusion
+    and the view aliasing change no output bit (ViT-B/16, two layers,
+    batch 2)."""
     g, inputs = workloads.vit_b16(batch=2, layers=2)
     outs = []
     for fuse, views in ((False, False), (True, True)):
@@ -138,7 +139,9 @@ def test_fused_vit_program_is_bit_identical(gpu):
         prog.run()
         outs.append(prog.output(g.outputs[0]))
         prog.close()
-    assert sum(1 for n in Program(g).graph.nodes if n.op == "FusedMatMul") == 10
+    fused = Program(g).graph.nodes
+    assert sum(1 for n in fused if n.op == "FusedMatMul") == 10
+    assert sum(1 for n in fused if n.op == "FusedAddLayerNorm") == 4
     assert np.array_equal(outs[0], outs[1])
 
 

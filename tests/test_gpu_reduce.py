@@ -68,7 +68,8 @@ def test_reduce_noop_and_special(gpu):
 
 
 SOFTMAX_CASES = [((16, 12, 197, 197), -1), ((4, 4096), -1), ((3, 5, 7), 1), ((2, 3, 4), 0), ((1000,), 0),
-                 ((7, 300), -1), ((5, 64), -1), ((9, 224), -1), ((3, 225), -1), ((11, 1), -1)]
+                 ((7, 300), -1), ((5, 64), -1), ((9, 224), -1), ((3, 225), -1), ((11, 1), -1),
+                 ((5, 2001), -1), ((3, 1028), -1), ((2, 4097), -1), ((256, 4096), -1)]  # workgroup-per-row paths
 
 
 @pytest.mark.parametrize("shape,axis", SOFTMAX_CASES)

@@ -160,3 +160,34 @@ def test_matmul_fusion_rules():
     assert [n.op for n in fuse_matmul_chains(chain(extra=True)).nodes] == ["MatMul", "Add", "Relu"]
     # a bias that is not [N] stays a separate Add
     assert [n.op for n in fuse_matmul_chains(chain(bias_shape=(4, 6))).nodes] == ["MatMul", "Add"]
+
+
+def test_add_layernorm_fusion_rules():
+    """A same-shape float Add feeding a LayerNormalization with per-element
+    initializer Scale/B fuses (at the Add's place, keeping the sum as an
+    output); a broadcasting Add, a norm with Mean output, or a non-initializer
+    Scale do not."""
+    from nert_amd.graph import Graph
+    from nert_amd.runner import fuse_add_layernorm
+
+    F = np.float32
+
+    def build(b_shape=(2, 3, 8), extra_out=False, scale_init=True):
+        g = Graph()
+        a = g.add_input("a", F, (2, 3, 8))
+        b = g.add_input("b", F, b_shape)
+        sc = g.add_initializer("sc", np.ones(8, F)) if scale_init else g.add_input("sc", F, (8,))
+        bi = g.add_initializer("bi", np.zeros(8, F))
+        s_ = g.add_node("Add", [a, b], [("s", F, (2, 3, 8))], name="add")[0]
+        outs = [("y", F, (2, 3, 8))] + ([("mean", F, (2, 3, 1))] if extra_out else [])
+        y = g.add_node("LayerNormalization", [s_, sc, bi], outs, {"axis": -1, "epsilon": 1e-6}, name="ln")[0]
+        z = g.add_node("Add", [s_, y], [("z", F, (2, 3, 8))], name="res")[0]
+        g.outputs.append(z)
+        return g
+
+    f = fuse_add_layernorm(build())
+    assert [n.op for n in f.nodes] == ["FusedAddLayerNorm", "Add"]
+    assert f.nodes[0].outputs == ["s", "y"] and f.nodes[0].inputs == ["a", "b", "sc", "bi"]
+    assert f.nodes[0].attrs == {"axis": -1, "epsilon": 1e-6}
+    for g in (build(b_shape=(8,)), build(extra_out=True), build(scale_init=False)):
+        assert [n.op for n in fuse_add_layernorm(g).nodes] == ["Add", "LayerNormalization", "Add"]
