@@ -3,9 +3,9 @@
  *
  * These mirror the reference seam types field for field so that a caller with
  * no C++ (ctypes, cgo, JNI) can describe a node and hand it to a device:
- *   nert_tensor_desc  <->  nert::TensorView  (include/nert/device.hpp:22-26)
- *   nert_attr_desc    <->  nert::Attribute   (include/nert/graph.hpp:159-174)
- *   dtype codes       <->  nert::DataType    (include/nert/graph.hpp:140-145)
+ *   nert_tensor_desc  <->  nert::TensorView  (include/nert/device.hpp:21-25)
+ *   nert_attr_desc    <->  nert::Attribute   (include/nert/graph.hpp:61-76)
+ *   dtype codes       <->  nert::DataType    (include/nert/graph.hpp:42-47)
  * The references are to files of olibartfast/nert.
  */
 #ifndef NERT_ABI_H
