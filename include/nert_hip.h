@@ -283,6 +283,21 @@ int nert_hip_layernorm_f32(const float* x, const float* scale, int scale_scalar,
  * transformer block). */
 int nert_hip_add_layernorm_f32(const float* a, const float* b, const float* scale, const float* bias, float* sum,
                                float* y, int64_t rows, int64_t inner, double epsilon, void* stream);
+/* Scaled-dot-product attention, per (batch b, head h):
+ *   O = Softmax(scale * Q K^T, last axis) V,
+ * Q/K/V element (b, token t, head h, dim d) at q/k/v + b*in_strides[0] +
+ * t*in_strides[1] + h*in_strides[2] + d (one stride set for all three: a
+ * packed QKV projection output), O's at out + b*out_strides[0] +
+ * t*out_strides[1] + h*out_strides[2] + d. head_dim must be 64; Q, K and
+ * out 16-byte aligned with strides that are multiples of 4; the token stride
+ * at least head_dim and one (batch, head) slice under 2^32 bytes. The same
+ * values as the reference's MatMul(Q, K^T), Mul(scale), Softmax and
+ * MatMul(P, V) rows (src/kernels/mat_mul.cpp, mul.cpp, softmax.cpp) within
+ * the fp32 parity bar; no counterpart of its own in the reference: it backs
+ * the runner's FusedAttention row. */
+int nert_hip_attention_f32(const float* q, const float* k, const float* v, float* out, int64_t batch, int64_t heads,
+                           int64_t seq, int64_t head_dim, const int64_t* in_strides, const int64_t* out_strides,
+                           float scale, void* stream);
 /* InstanceNormalization over each (n, c) plane
  * (src/kernels/instance_normalization.cpp:44-106). */
 int nert_hip_instancenorm_f32(const float* x, const float* scale, const float* bias, float* y, int64_t batch,

@@ -184,6 +184,18 @@ __device__ __forceinline__ int64_t XcdTile(int64_t i, int64_t count) {
     return i < whole ? (i % 8) * (whole / 8) + i / 8 : i;
 }
 
+// For `count` = tiles_m * tiles_n tiles numbered row tile fastest, with
+// tiles_m a multiple of 8: workgroup i (on XCD i % 8) takes row tile
+// (i % 8) * (tiles_m / 8) + j % (tiles_m / 8) of column tile j / (tiles_m / 8),
+// j = i / 8, so each XCD covers one eighth of the row tiles (of the weights)
+// and every column tile.
+__device__ __forceinline__ int64_t XcdTileByRow(int64_t i, int64_t count, int64_t tiles_m) {
+    const int64_t per = tiles_m / 8;
+    const int64_t j = i / 8;
+    (void)count;
+    return (i % 8) * per + j % per + tiles_m * (j / per);
+}
+
 constexpr uint32_t kBufferWord3 = 0x00020000; // raw 32-bit dword buffer (gfx9 family)
 constexpr uint32_t kOutOfRange = 0x80000000u; // >= every num_records used here
 
@@ -525,6 +537,28 @@ __global__ void ConvSplitReduceKernel(ConvArgs p, int splits, int vec) {
     }
 }
 
+// The sum of `count` >= 1 float4 slices `stride` floats apart, added in slice
+// order. The loads of up to eight slices are issued before the first addition
+// (slots past the last slice re-read its address and are not added), so a
+// thread waits for memory once per eight slices instead of once per slice.
+__device__ __forceinline__ nert_floatx4 SumSlicesQuad(const float* src, int64_t stride, int count) {
+    nert_floatx4 sum = *reinterpret_cast<const nert_floatx4*>(src);
+    for (int s0 = 0; s0 < count; s0 += 8) {
+        nert_floatx4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            v[j] = *reinterpret_cast<const nert_floatx4*>(src + static_cast<int64_t>(min(s0 + j, count - 1)) * stride);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (s0 + j > 0 && s0 + j < count) {
+                sum += v[j];
+            }
+        }
+    }
+    return sum;
+}
+
 // The same sums for partial planes whose element count is a multiple of 4 and
 // under 2^31: four consecutive elements per thread, 16-byte partial loads,
 // 32-bit index decoding; the output index is decoded per element, so the four
@@ -537,10 +571,7 @@ __global__ __launch_bounds__(256) void ConvSplitReduceQuadKernel(ConvArgs p, int
     const int plane_out = static_cast<int>(p.plane_out);
     for (uint32_t q = blockIdx.x * 256u + threadIdx.x; q < quads; q += gridDim.x * 256u) {
         const uint32_t i = q * 4u;
-        nert_floatx4 sum = *reinterpret_cast<const nert_floatx4*>(p.partial + i);
-        for (int s = 1; s < splits; ++s) {
-            sum += *reinterpret_cast<const nert_floatx4*>(p.partial + static_cast<int64_t>(s) * per_split + i);
-        }
+        const nert_floatx4 sum = SumSlicesQuad(p.partial + i, per_split, splits);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             uint32_t gc, pix;
@@ -572,6 +603,12 @@ void LaunchSplitReduce(const ConvArgs& p, int splits, hipStream_t stream) {
 using ConvShapeL = TileShape<128, 128, 16, 2, 4>; // 8 waves, 64x32 each
 using ConvShapeW = TileShape<64, 256, 16, 2, 4>;  // 8 waves, 32x64 each, for M_g <= 64
 using ConvShapeS = TileShape<32, 128, 16, 1, 4>;  // 4 waves, 32x32 each, for M_g <= 32
+// Small tiles for short K (the 1x1 stride-2 downsampling convs, K = C_g =
+// 64..256): a few K steps per tile, so the load latency is hidden by more
+// resident workgroups rather than by the pipeline; 4 x 392 .. 8 x 49 tiles
+// on the ResNet-18 bs32 shapes instead of 196 .. 208.
+using ConvShapeQ = TileShape<64, 64, 16, 2, 2>;  // 4 waves, 32x32 each
+using ConvShapeT = TileShape<32, 64, 32, 1, 2>;  // 2 waves, 32x32 each
 
 template <class Shape>
 int64_t ConvTiles(const ConvArgs& p) {
@@ -663,6 +700,10 @@ struct HaloGeom {
     int32_t tail_pieces;
     int32_t tail_bps;
     float* tail_partial;
+    // Channel-major XCD order (no tail split, tiles_m % 8 == 0): each XCD
+    // takes tiles_m / 8 channel tiles and every pixel tile, so it reads only
+    // its eighth of the weights; set where the weights outweigh the input.
+    int32_t xcd_by_channel;
 };
 
 // Register budget: 128 VGPRs (four waves per SIMD, two workgroups per CU),
@@ -695,7 +736,8 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
     // XCD i % 8), each with its own L2. Remap so that each XCD takes one
     // contiguous run of tiles: neighbouring tiles share their input patch
     // (the next channel tile) or its halo rows (the next pixel tile).
-    int64_t tile = XcdTile(blockIdx.x, h.tail_pieces > 0 ? h.n_full : static_cast<int64_t>(gridDim.x));
+    int64_t tile = h.xcd_by_channel ? XcdTileByRow(blockIdx.x, gridDim.x, tiles_m)
+                                    : XcdTile(blockIdx.x, h.tail_pieces > 0 ? h.n_full : static_cast<int64_t>(gridDim.x));
     const int g = blockIdx.y;
     const int split = blockIdx.z;
     int cb_begin = split * h.blocks_per_split;
@@ -944,21 +986,7 @@ __global__ __launch_bounds__(256) void ConvTailReduceQuadKernel(ConvArgs p, int 
         }
         const uint32_t gc0 = tn * bn + 4 * c4;
         const float* src = partial + static_cast<int64_t>(t) * pieces * per_tile + r * bn + 4 * c4;
-        nert_floatx4 v = *reinterpret_cast<const nert_floatx4*>(src);
-        int qp = 1;
-        for (; qp + 3 < pieces; qp += 4) {
-            const nert_floatx4 a = *reinterpret_cast<const nert_floatx4*>(src + qp * per_tile);
-            const nert_floatx4 b = *reinterpret_cast<const nert_floatx4*>(src + (qp + 1) * per_tile);
-            const nert_floatx4 c = *reinterpret_cast<const nert_floatx4*>(src + (qp + 2) * per_tile);
-            const nert_floatx4 d = *reinterpret_cast<const nert_floatx4*>(src + (qp + 3) * per_tile);
-            v += a;
-            v += b;
-            v += c;
-            v += d;
-        }
-        for (; qp < pieces; ++qp) {
-            v += *reinterpret_cast<const nert_floatx4*>(src + qp * per_tile);
-        }
+        const nert_floatx4 v = SumSlicesQuad(src, per_tile, pieces);
         const float bias = p.bias != nullptr ? p.bias[gr] : 0.0f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -1165,6 +1193,7 @@ bool TryHaloShape(ConvArgs p, hipStream_t stream, int force_splits, bool tail = 
             static_cast<float*>(Workspace(static_cast<int64_t>(splits) * p.group * p.mg * p.n_total * 4, stream));
     }
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(p.group), static_cast<unsigned>(splits));
+    h.xcd_by_channel = ((p.mg + Shape::kBM - 1) / Shape::kBM) % 8 == 0 && p.m * p.kg > p.batch * p.c * p.plane_in;
     if (per_thread == 1) {
         LaunchHalo<Shape, 1>(p, h, grid, static_cast<size_t>(lds), stream);
     } else if (per_thread == 2) {
@@ -1398,8 +1427,10 @@ bool TryPointwiseDirect(const ConvArgs& p, hipStream_t stream) {
     return true;
 }
 
-// Tap-major and gather kernels: ConvShapeL, ConvShapeW, ConvShapeS; 3: the
-// direct 1x1 kernel.
+// Tap-major and gather kernels: 0-2 ConvShapeL, ConvShapeW, ConvShapeS;
+// 3: the direct 1x1 kernel; 4-5: ConvShapeQ, ConvShapeT.
+constexpr int kGatherCandidates = 6;
+
 bool LaunchGatherCandidate(int i, const ConvArgs& p, hipStream_t stream) {
     switch (i) {
     case 0:
@@ -1411,6 +1442,12 @@ bool LaunchGatherCandidate(int i, const ConvArgs& p, hipStream_t stream) {
     case 2:
         LaunchConv<ConvShapeS>(p, stream);
         return true;
+    case 4:
+        LaunchConv<ConvShapeQ>(p, stream);
+        return true;
+    case 5:
+        LaunchConv<ConvShapeT>(p, stream);
+        return true;
     default:
         return TryPointwiseDirect(p, stream);
     }
@@ -1421,11 +1458,11 @@ void LaunchGatherConv(const ConvArgs& p, hipStream_t stream) {
     const int fallback = p.mg <= 32 ? 2 : (p.mg <= 64 ? 1 : 0);
     if (const char* forced = std::getenv("NERT_HIP_CONV_CANDIDATE")) {
         const int i = std::atoi(forced) - 100; // 100 + i: gather candidate i
-        if (i >= 0 && i < 4 && LaunchGatherCandidate(i, p, stream)) {
+        if (i >= 0 && i < kGatherCandidates && LaunchGatherCandidate(i, p, stream)) {
             return;
         }
     }
-    const int c = ChooseConvConfig("conv", chosen, p, stream, 4, fallback, LaunchGatherCandidate);
+    const int c = ChooseConvConfig("conv", chosen, p, stream, kGatherCandidates, fallback, LaunchGatherCandidate);
     if (!LaunchGatherCandidate(c, p, stream)) {
         LaunchGatherCandidate(fallback, p, stream);
     }

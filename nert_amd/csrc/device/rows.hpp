@@ -19,6 +19,7 @@ NERT_HIP_ROW(Conv);
 NERT_HIP_ROW(FusedConv); // not a reference row: the runner's Conv+Add+Relu fusion
 NERT_HIP_ROW(FusedMatMul); // not a reference row: the runner's MatMul+scale+bias+Gelu fusion
 NERT_HIP_ROW(FusedAddLayerNorm); // not a reference row: the runner's residual Add + LayerNormalization fusion
+NERT_HIP_ROW(FusedAttention); // not a reference row: the runner's MatMul/Mul/Softmax/MatMul attention fusion
 
 // Window helpers shared by Conv, ConvTranspose and the pools
 // (src/kernels/conv.cpp:78-134, src/kernels/max_pool.cpp).

@@ -273,6 +273,53 @@ void FusedMatMul(const Node& node, const Views& inputs, const Views& outputs) {
     MatMulCore(context, inputs[0], inputs[1], out, outputs, bias, alpha, act, params);
 }
 
+// Not a reference row: the runner's fusion of a transformer encoder's
+// attention block. Input: the packed QKV projection [B, S, 3 * H * D]
+// (token-major, the Reshape to [B, S, 3, H, D] it replaces); attributes heads
+// (H) and scale (the Mul's scalar). Output [B, S, H * D]: the heads of
+// Softmax(scale * Q K^T) V side by side, as the Transpose + Reshape after the
+// second MatMul lays them out. The reference runs MatMul, Mul, Softmax and
+// MatMul (src/kernels/mat_mul.cpp, mul.cpp, softmax.cpp) plus the copies
+// that split Q, K and V apart; the values agree within the fp32 parity bar.
+void FusedAttention(const Node& node, const Views& inputs, const Views& outputs) {
+    const std::string context = "FusedAttention (node '" + node.name + "')";
+    if (inputs.size() != 1 || outputs.size() != 1) {
+        throw InferenceException(context + ": expected one input (packed QKV) and one output");
+    }
+    const TensorView& qkv = inputs[0];
+    const TensorView& out = outputs[0];
+    if (qkv.dtype != DataType::Float32 || out.dtype != DataType::Float32) {
+        throw InferenceException(context + ": tensors must be float32");
+    }
+    if (qkv.dims.size() != 3 || out.dims.size() != 3 || out.dims[0] != qkv.dims[0] || out.dims[1] != qkv.dims[1]) {
+        throw InferenceException(context + ": expected QKV [B, S, 3*H*D] and output [B, S, H*D]");
+    }
+    const int64_t heads = IntAttrC(node, "heads", 0, context);
+    const float scale = FloatAttrC(node, "scale", 1.0f, context);
+    const int64_t width = out.dims[2];
+    if (heads <= 0 || width % heads != 0 || qkv.dims[2] != 3 * width) {
+        throw InferenceException(context + ": QKV width must be 3 * heads * head_dim and the output heads * head_dim");
+    }
+    const int64_t batch = qkv.dims[0];
+    const int64_t seq = qkv.dims[1];
+    const int64_t head_dim = width / heads;
+    (void)ElementCount(qkv.dims, context);
+    if (batch * seq * width == 0) {
+        AfterRow(outputs, context);
+        return;
+    }
+    if (qkv.data == nullptr || out.data == nullptr) {
+        throw InferenceException(context + ": null buffer");
+    }
+    const float* base = static_cast<const float*>(qkv.data);
+    const int64_t in_strides[3] = {seq * 3 * width, 3 * width, head_dim};
+    const int64_t out_strides[3] = {seq * width, width, head_dim};
+    CheckStatus(nert_hip_attention_f32(base, base + width, base + 2 * width, static_cast<float*>(out.data), batch,
+                                       heads, seq, head_dim, in_strides, out_strides, scale, Stream()),
+                context);
+    AfterRow(outputs, context);
+}
+
 namespace {
 
 // src/kernels/conv.cpp:78-119.

@@ -20,6 +20,7 @@ nert::KernelFn FindRow(const std::string& op_type) {
         {"FusedConv", &FusedConv},
         {"FusedMatMul", &FusedMatMul},
         {"FusedAddLayerNorm", &FusedAddLayerNorm},
+        {"FusedAttention", &FusedAttention},
         {"Relu", &Relu},
         {"Sigmoid", &Sigmoid},
         {"Tanh", &Tanh},

@@ -197,6 +197,51 @@ __global__ void SplitReduceKernel(GemmArgs p, int splits, int64_t batches, int v
     }
 }
 
+// The same sums for rows of whole quads under 2^31 outputs: four consecutive
+// outputs of one row per thread, 32-bit index decoding, and the 16-byte loads
+// of up to eight splits issued before the first addition (splits past the
+// last re-read the last one's address and are not added), so a thread waits
+// for memory once per eight splits rather than once per split. The additions
+// are SplitReduceKernel's, in the same order, so the results are identical.
+__global__ __launch_bounds__(256) void SplitReduceQuadKernel(GemmArgs p, int splits, uint32_t quads, uint32_t total,
+                                                             FastDiv div_row_quads, FastDiv div_m) {
+    for (uint32_t q = blockIdx.x * 256u + threadIdx.x; q < quads; q += gridDim.x * 256u) {
+        uint32_t cq, r;
+        const uint32_t row = DivMod(div_row_quads, q, cq); // over all batches
+        DivMod(div_m, row, r);
+        const uint32_t i = 4 * q;
+        double sum[4];
+        for (int s0 = 0; s0 < splits; s0 += 8) {
+            nert_floatx4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int s = min(s0 + j, splits - 1);
+                v[j] = *reinterpret_cast<const nert_floatx4*>(p.partial + static_cast<int64_t>(s) * total + i);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (s0 + j == 0) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        sum[e] = v[j][e];
+                    }
+                } else if (s0 + j < splits) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        sum[e] += v[j][e];
+                    }
+                }
+            }
+        }
+        nert_floatx4 out;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            out[e] = FinishGemm(p, static_cast<float>(sum[e]), r, 4 * cq + e);
+        }
+        *reinterpret_cast<nert_floatx4*>(p.y + i) = out;
+    }
+}
+
 // Skinny GEMM (M <= 32, K contiguous in both operands: the ResNet classifier
 // and Gemm with transB): one workgroup per 32 output columns; each of its 4
 // waves takes a quarter of K and runs MFMAs straight from 16-byte global loads
@@ -365,8 +410,15 @@ void LaunchConfig(GemmArgs p, int64_t batches, int shape, int force_splits, hipS
     }
     if (splits > 1) {
         const int vec = p.n % 4 == 0 ? 4 : 1;
-        const int64_t work = batches * p.m * p.n / vec;
-        SplitReduceKernel<<<GridFor(work, 256, 8192), 256, 0, stream>>>(p, splits, batches, vec);
+        const int64_t total = batches * p.m * p.n;
+        const int64_t work = total / vec;
+        if (vec == 4 && total < (int64_t{1} << 31) && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0) {
+            SplitReduceQuadKernel<<<GridFor(work, 256, 8192), 256, 0, stream>>>(
+                p, splits, static_cast<uint32_t>(work), static_cast<uint32_t>(total),
+                FastDiv::Make(static_cast<uint32_t>(p.n / 4)), FastDiv::Make(static_cast<uint32_t>(p.m)));
+        } else {
+            SplitReduceKernel<<<GridFor(work, 256, 8192), 256, 0, stream>>>(p, splits, batches, vec);
+        }
         CheckLaunch("SplitReduceKernel launch");
     }
 }

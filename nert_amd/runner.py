@@ -359,6 +359,133 @@ def fuse_add_layernorm(g: Graph) -> Graph:
     return Graph(nodes=nodes, initializers=g.initializers, inputs=g.inputs, outputs=g.outputs, tensors=g.tensors)
 
 
+ATTENTION_HEAD_DIM = 64   # what nert_hip_attention_f32 computes
+
+
+def _ints(g: Graph, name: str) -> list[int] | None:
+    v = g.initializers.get(name)
+    if v is None or v.dtype != np.int64:
+        return None
+    return [int(x) for x in v.reshape(-1)]
+
+
+def fuse_attention(g: Graph) -> Graph:
+    """Rewrites a transformer encoder's attention block into one
+    FusedAttention node:
+
+        qkv [B,S,3*H*D] -Reshape-> [B,S,3,H,D] -Transpose(2,0,3,1,4)-> Split
+        (axis 0, three parts) -> Squeeze(axis 0) -> q, k, v [B,H,S,D];
+        MatMul(q, Transpose(k, 0,1,3,2)) -> Mul by a float32 scalar ->
+        Softmax(last axis) -> MatMul(., v) -> Transpose(0,2,1,3) ->
+        Reshape [B,S,H*D]
+
+    becomes FusedAttention(qkv) -> [B,S,H*D] with attributes heads and
+    scale, placed where the final Reshape was. Every intermediate must have
+    exactly the consumer the pattern names and not be a graph output; D must
+    be 64 (what the kernel computes). The fused row keeps Q,
+    K and V where the projection wrote them and never materialises the
+    scores in HBM; its values agree with the separate rows within the fp32
+    parity bar (not bit for bit: the products accumulate in another order).
+    """
+    consumers: dict[str, list[int]] = {}
+    producer: dict[str, int] = {}
+    for idx, n in enumerate(g.nodes):
+        for t in n.inputs:
+            if t:
+                consumers.setdefault(t, []).append(idx)
+        for t in n.outputs:
+            producer[t] = idx
+    outputs = set(g.outputs)
+
+    def sole(t: str) -> int | None:
+        c = consumers.get(t, [])
+        return c[0] if len(c) == 1 and t not in outputs else None
+
+    def made_by(t: str, op: str, consumer: int) -> int | None:
+        """Index of t's producer if it is an `op` node whose only output t
+        feeds only `consumer`."""
+        i = producer.get(t)
+        if i is None or g.nodes[i].op != op or sole(t) != consumer:
+            return None
+        return i
+
+    def perm(i: int) -> list[int] | None:
+        p = g.nodes[i].attrs.get("perm")
+        return [int(x) for x in p] if p is not None else None
+
+    replace: dict[int, Node] = {}
+    dropped: set[int] = set()
+    for si, sm in enumerate(g.nodes):
+        if sm.op != "Softmax" or si in dropped or len(sm.inputs) != 1 or len(sm.outputs) != 1:
+            continue
+        p = sm.outputs[0]
+        dt, pshape = g.tensors[p]
+        if np.dtype(dt) != np.float32 or len(pshape) != 4 or int(sm.attrs.get("axis", -1)) not in (-1, 3):
+            continue
+        mul = made_by(sm.inputs[0], "Mul", si)
+        if mul is None or len(g.nodes[mul].inputs) != 2:
+            continue
+        a0, a1 = g.nodes[mul].inputs
+        scale, s = (_scalar(g, a1), a0) if _scalar(g, a1) is not None else (_scalar(g, a0), a1)
+        if scale is None:
+            continue
+        mm1 = made_by(s, "MatMul", mul)
+        if mm1 is None:
+            continue
+        q, kt = g.nodes[mm1].inputs
+        tk = made_by(kt, "Transpose", mm1)
+        if tk is None or perm(tk) != [0, 1, 3, 2]:
+            continue
+        k = g.nodes[tk].inputs[0]
+        mm2 = sole(p)
+        if mm2 is None or g.nodes[mm2].op != "MatMul" or g.nodes[mm2].inputs[0] != p:
+            continue
+        v = g.nodes[mm2].inputs[1]
+        to = sole(g.nodes[mm2].outputs[0])
+        if to is None or g.nodes[to].op != "Transpose" or perm(to) != [0, 2, 1, 3]:
+            continue
+        rs = sole(g.nodes[to].outputs[0])
+        if rs is None or g.nodes[rs].op != "Reshape":
+            continue
+        out = g.nodes[rs].outputs[0]
+        # q, k, v: the three parts of one Split, each through Squeeze(axis 0).
+        sq = [made_by(t, "Squeeze", c) for t, c in ((q, mm1), (k, tk), (v, mm2))]
+        if any(i is None for i in sq):
+            continue
+        parts = [g.nodes[i].inputs[0] for i in sq]
+        if any(_ints(g, g.nodes[i].inputs[1]) != [0] if len(g.nodes[i].inputs) > 1 and g.nodes[i].inputs[1]
+               else [int(x) for x in g.nodes[i].attrs.get("axes", [])] != [0] for i in sq):
+            continue
+        sp = producer.get(parts[0])
+        if sp is None or g.nodes[sp].op != "Split" or g.nodes[sp].outputs != parts or any(
+                sole(t) != i for t, i in zip(parts, sq)) or int(g.nodes[sp].attrs.get("axis", 0)) != 0:
+            continue
+        split_sizes = (_ints(g, g.nodes[sp].inputs[1]) if len(g.nodes[sp].inputs) > 1 and g.nodes[sp].inputs[1]
+                       else g.nodes[sp].attrs.get("split"))
+        if split_sizes is not None and [int(x) for x in split_sizes] != [1, 1, 1]:
+            continue
+        t5 = made_by(g.nodes[sp].inputs[0], "Transpose", sp)
+        if t5 is None or perm(t5) != [2, 0, 3, 1, 4]:
+            continue
+        r5 = made_by(g.nodes[t5].inputs[0], "Reshape", t5)
+        if r5 is None:
+            continue
+        qkv = g.nodes[r5].inputs[0]
+        qdt, qkv_shape = g.tensors[qkv]
+        _, shape5 = g.tensors[g.nodes[r5].outputs[0]]
+        if np.dtype(qdt) != np.float32 or len(qkv_shape) != 3 or len(shape5) != 5:
+            continue
+        b_, s_, three, h_, d_ = shape5
+        if (three != 3 or tuple(qkv_shape) != (b_, s_, 3 * h_ * d_) or d_ != ATTENTION_HEAD_DIM
+                or s_ <= 0 or tuple(g.tensors[out][1]) != (b_, s_, h_ * d_)
+                or tuple(pshape) != (b_, h_, s_, s_)):
+            continue
+        replace[rs] = Node("FusedAttention", [qkv], [out], {"heads": int(h_), "scale": float(scale)}, sm.name)
+        dropped.update([r5, t5, sp, *sq, tk, mm1, mul, si, mm2, to])
+    nodes = [replace.get(i, nd) for i, nd in enumerate(g.nodes) if i not in dropped]
+    return Graph(nodes=nodes, initializers=g.initializers, inputs=g.inputs, outputs=g.outputs, tensors=g.tensors)
+
+
 class _PackedNode:
     __slots__ = ("op", "name", "attrs", "ins", "outs", "err")
 
@@ -371,10 +498,20 @@ class _PackedNode:
         self.err = C.create_string_buffer(1024)
 
 
+def fuse_rows(g: Graph, attention: bool = True) -> Graph:
+    """The runner's fusions in order: Conv chains, attention blocks (when
+    `attention`; the only fusion whose outputs are not bit-identical to the
+    separate rows), MatMul chains, residual Add + LayerNorm."""
+    g = fuse_conv_chains(g)
+    if attention:
+        g = fuse_attention(g)
+    return fuse_add_layernorm(fuse_matmul_chains(g))
+
+
 class Program:
-    def __init__(self, g: Graph, fuse: bool = True, views: bool = True):
+    def __init__(self, g: Graph, fuse: bool = True, views: bool = True, attention: bool = True):
         if fuse:
-            g = fuse_add_layernorm(fuse_matmul_chains(fuse_conv_chains(g)))
+            g = fuse_rows(g, attention)
         self.alias: dict[str, tuple[str, int]] = {}
         if views:
             g, self.alias = alias_views(g)

@@ -41,12 +41,16 @@ def _round() -> None:
     device.init()
     for name, kwargs in WORKLOADS:
         g, inputs = getattr(workloads, name)(**kwargs)
-        prog = Program(g)  # fused and unfused rows share their geometry keys
-        for n in g.inputs:
-            prog.set_input(n, inputs[n])
-        prog.run()
-        device.synchronize()
-        prog.close()
+        # Fused and unfused Conv/MatMul rows share their geometry keys; the
+        # attention fusion removes the QK^T and PV products, which the
+        # unfused rows (the seam's executor) still run.
+        for attention in (True, False):
+            prog = Program(g, attention=attention)
+            for n in g.inputs:
+                prog.set_input(n, inputs[n])
+            prog.run()
+            device.synchronize()
+            prog.close()
         print(f"tuned {name} {kwargs}", flush=True)
     for case in opcases.CASES:
         prog = Program(case.graph())

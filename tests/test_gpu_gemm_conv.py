@@ -426,11 +426,12 @@ def _run_forced(cand, paths, attrs):
     ((3, 24, 9, 11), (40, 24, 1, 1), {"strides": [1, 2], "pads": [1, 0, 0, 1]}),
     ((2, 32, 8, 8), (48, 16, 1, 1), {"group": 2}),
 ])
-@pytest.mark.parametrize("cand", [100, 101, 102, 103])
+@pytest.mark.parametrize("cand", [100, 101, 102, 103, 104, 105])
 def test_conv_1x1_forced_configs(gpu, tmp_path, xs, ws, attrs, cand):
     """Every configuration of the other conv kernels, the direct 1x1 kernel
-    (103) included, forced: matches the restatement, and the fused epilogue
-    matches Conv + Add + Relu bit for bit."""
+    (103) and the small-tile shapes (104, 105) included, forced: matches the
+    restatement, and the fused epilogue matches Conv + Add + Relu bit for
+    bit."""
     x, w, b = randn(xs, seed=90), randn(ws, seed=91, scale=0.1), randn((ws[0],), seed=92)
     out = _conv_out(xs, ws, attrs)
     z = randn(out, seed=93)

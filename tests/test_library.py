@@ -53,13 +53,14 @@ def test_reference_table_is_73_rows():
 
 def test_hip_table_rows():
     """Every reference row has a HIP row, plus the runner's internal fused
-    rows FusedConv, FusedMatMul and FusedAddLayerNorm (lookup only; no device
-    call)."""
+    rows FusedConv, FusedMatMul, FusedAddLayerNorm and FusedAttention (lookup
+    only; no device call)."""
     missing = [op for op in REFERENCE_ROWS if not device.has_row(op)]
     assert missing == [], f"rows without a HIP kernel: {missing}"
     assert device.has_row("FusedConv")
     assert device.has_row("FusedMatMul")
     assert device.has_row("FusedAddLayerNorm")
+    assert device.has_row("FusedAttention")
     assert not device.has_row("BatchNormalization")
     assert not device.has_row("")
 

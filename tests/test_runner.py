@@ -191,3 +191,38 @@ def test_add_layernorm_fusion_rules():
     assert f.nodes[0].attrs == {"axis": -1, "epsilon": 1e-6}
     for g in (build(b_shape=(8,)), build(extra_out=True), build(scale_init=False)):
         assert [n.op for n in fuse_add_layernorm(g).nodes] == ["Add", "LayerNormalization", "Add"]
+
+
+def test_fuse_attention_rules():
+    """The attention block becomes one FusedAttention(qkv) node carrying heads
+    and scale; it stays unfused when an intermediate is also a graph output
+    or when the head dimension is not 64."""
+    from attn_graph import attention_block
+    from nert_amd.runner import fuse_attention
+
+    f = fuse_attention(attention_block(2, 197, 12, scale=0.125))
+    assert [n.op for n in f.nodes] == ["FusedAttention"]
+    n = f.nodes[0]
+    assert n.inputs == ["qkv"] and n.outputs == ["attn_out"]
+    assert n.attrs == {"heads": 12, "scale": 0.125}
+    assert len(fuse_attention(attention_block(1, 1000, 2)).nodes) == 1
+    for g in (attention_block(2, 50, 3, scores_output=True), attention_block(2, 50, 3, head_dim=32)):
+        assert "FusedAttention" not in [n.op for n in fuse_attention(g).nodes]
+        assert len(fuse_attention(g).nodes) == len(g.nodes)
+
+
+def test_fuse_rows_on_vit():
+    """Two encoder layers: two attention blocks, eight MatMul chains (QKV,
+    projection and the two MLP products per layer) and four residual
+    Add + LayerNorm pairs fuse; without the attention fusion the QK^T chains
+    fuse as MatMul chains instead."""
+    from collections import Counter
+
+    from nert_amd import workloads
+    from nert_amd.runner import fuse_rows
+
+    g, _ = workloads.vit_b16(batch=2, layers=2)
+    ops = Counter(n.op for n in fuse_rows(g).nodes)
+    assert (ops["FusedAttention"], ops["FusedMatMul"], ops["FusedAddLayerNorm"], ops["Softmax"]) == (2, 8, 4, 0)
+    ops = Counter(n.op for n in fuse_rows(g, attention=False).nodes)
+    assert (ops["FusedAttention"], ops["FusedMatMul"], ops["Softmax"]) == (0, 10, 2)
