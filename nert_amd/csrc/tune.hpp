@@ -10,10 +10,11 @@
 // nert_amd/tuning/gfx950.tsv next to the library, or the file that
 // NERT_HIP_TUNE_TABLE names). A geometry the table lacks is timed on its
 // first eager call: every candidate that fits runs on a scratch output (one
-// warm-up and three timed launches each, HIP events on the caller's stream);
-// the four fastest are timed again (two interleaved rounds of five launches)
-// since the leaders are often closer than one pass's noise, and the fastest
-// is kept for the rest of the process. NERT_HIP_TUNE_RECORD=<file> appends
+// warm-up launch, then ten launches captured into a HIP graph and replayed
+// between HIP events on the caller's stream, as a replayed program runs
+// them); the four fastest are timed again (two interleaved rounds) since the
+// leaders are often closer than one pass's noise, and the fastest is kept
+// for the rest of the process. NERT_HIP_TUNE_RECORD=<file> appends
 // each such timed choice to <file> in the table's format. A first call
 // under stream capture cannot time anything and fixes the fallback instead,
 // as does NERT_HIP_CONV_TUNE=0 in the environment.
@@ -147,24 +148,56 @@ int ChooseConfig(const char* family, std::map<Key, int>& cache, std::mutex& mu, 
         try {
             Check(hipEventCreate(&start), "hipEventCreate");
             Check(hipEventCreate(&stop), "hipEventCreate");
+            // A candidate's time is measured as a replayed graph sees it:
+            // `reps` back-to-back launches captured into one HIP graph, one
+            // warm replay, then one replay between events. Timing eager
+            // launches instead would count the host's launch gaps, which on
+            // kernels of a few microseconds outweigh the kernels' own
+            // differences. (The candidate's eager launch before its first
+            // timing has grown every workspace it uses, so nothing allocates
+            // under capture; the launches queue no memsets.)
             auto time_us = [&](int i, int reps) {
-                Check(hipEventRecord(start, stream), "hipEventRecord");
-                for (int r = 0; r < reps; ++r) {
-                    launch(i, scratch);
+                Check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+                hipGraph_t graph = nullptr;
+                try {
+                    for (int r = 0; r < reps; ++r) {
+                        launch(i, scratch);
+                    }
+                } catch (...) {
+                    (void)hipStreamEndCapture(stream, &graph);
+                    if (graph != nullptr) {
+                        (void)hipGraphDestroy(graph);
+                    }
+                    throw;
                 }
-                Check(hipEventRecord(stop, stream), "hipEventRecord");
-                Check(hipEventSynchronize(stop), "hipEventSynchronize");
+                Check(hipStreamEndCapture(stream, &graph), "hipStreamEndCapture");
+                hipGraphExec_t exec = nullptr;
+                const hipError_t made = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+                (void)hipGraphDestroy(graph);
+                Check(made, "hipGraphInstantiate(tuning)");
                 float ms = 0.0f;
-                Check(hipEventElapsedTime(&ms, start, stop), "hipEventElapsedTime");
+                try {
+                    Check(hipGraphLaunch(exec, stream), "hipGraphLaunch");
+                    Check(hipEventRecord(start, stream), "hipEventRecord");
+                    Check(hipGraphLaunch(exec, stream), "hipGraphLaunch");
+                    Check(hipEventRecord(stop, stream), "hipEventRecord");
+                    Check(hipEventSynchronize(stop), "hipEventSynchronize");
+                    Check(hipEventElapsedTime(&ms, start, stop), "hipEventElapsedTime");
+                } catch (...) {
+                    (void)hipStreamSynchronize(stream);
+                    (void)hipGraphExecDestroy(exec);
+                    throw;
+                }
+                Check(hipGraphExecDestroy(exec), "hipGraphExecDestroy");
                 return ms * 1000.0f / static_cast<float>(reps);
             };
-            // First pass: one warm launch and three timed launches each.
+            // First pass: one warm eager launch, then a graph of ten launches.
             std::vector<std::pair<float, int>> first;
             for (int i = 0; i < count; ++i) {
                 if (!launch(i, scratch)) {
                     continue;
                 }
-                const float us = time_us(i, 3);
+                const float us = time_us(i, 10);
                 if (TuneLogEnabled()) {
                     std::fprintf(stderr, "nert_hip tune: candidate %d %.1f us\n", i, us);
                 }
@@ -172,13 +205,13 @@ int ChooseConfig(const char* family, std::map<Key, int>& cache, std::mutex& mu, 
             }
             // The leaders are often within a few percent of each other, about
             // the first pass's noise: re-time the best four in two interleaved
-            // rounds of five launches and keep each one's faster round.
+            // rounds of ten launches and keep each one's faster round.
             std::sort(first.begin(), first.end());
             const size_t finalists = std::min<size_t>(first.size(), 4);
             std::vector<float> best_us(finalists, -1.0f);
             for (int round = 0; round < 2 && finalists > 1; ++round) {
                 for (size_t f = 0; f < finalists; ++f) {
-                    const float us = time_us(first[f].second, 5);
+                    const float us = time_us(first[f].second, 10);
                     if (best_us[f] < 0.0f || us < best_us[f]) {
                         best_us[f] = us;
                     }
