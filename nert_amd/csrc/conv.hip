@@ -571,15 +571,31 @@ __global__ __launch_bounds__(256) void ConvSplitReduceQuadKernel(ConvArgs p, int
     const int plane_out = static_cast<int>(p.plane_out);
     for (uint32_t q = blockIdx.x * 256u + threadIdx.x; q < quads; q += gridDim.x * 256u) {
         const uint32_t i = q * 4u;
-        const nert_floatx4 sum = SumSlicesQuad(p.partial + i, per_split, splits);
+        // Output indices, bias and residual first, so their loads are in
+        // flight with the partials' loads.
+        int64_t yi[4];
+        float bias[4];
+        float res[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             uint32_t gc, pix;
             const uint32_t oc = DivMod(div_n, i + e, gc); // g * mg + m
             const uint32_t b = DivMod(div_plane, gc, pix);
-            const int64_t yi = (static_cast<int64_t>(b) * p.m + oc) * plane_out + pix;
-            const float bias = p.bias != nullptr ? p.bias[oc] : 0.f;
-            p.y[yi] = Finish(p, sum[e] + bias, yi);
+            yi[e] = (static_cast<int64_t>(b) * p.m + oc) * plane_out + pix;
+            bias[e] = p.bias != nullptr ? p.bias[oc] : 0.f;
+            res[e] = p.residual != nullptr ? p.residual[yi[e]] : 0.0f;
+        }
+        const nert_floatx4 sum = SumSlicesQuad(p.partial + i, per_split, splits);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float out = sum[e] + bias[e];
+            if (p.residual != nullptr) {
+                out = out + res[e];
+            }
+            if (p.relu) {
+                out = (0.0f < out) ? out : 0.0f; // std::max(0.0f, v)
+            }
+            p.y[yi[e]] = out;
         }
     }
 }
@@ -985,23 +1001,39 @@ __global__ __launch_bounds__(256) void ConvTailReduceQuadKernel(ConvArgs p, int 
             continue;
         }
         const uint32_t gc0 = tn * bn + 4 * c4;
-        const float* src = partial + static_cast<int64_t>(t) * pieces * per_tile + r * bn + 4 * c4;
-        const nert_floatx4 v = SumSlicesQuad(src, per_tile, pieces);
-        const float bias = p.bias != nullptr ? p.bias[gr] : 0.0f;
+        // Output indices, bias and residual first (clamped, always-valid
+        // addresses), so their loads are in flight with the pieces' loads.
+        int64_t yi[4];
+        bool ok[4];
+        float res[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const uint32_t gc = gc0 + e;
-            if (gc >= p.n_total) {
+            ok[e] = gc < p.n_total;
+            uint32_t pix;
+            const uint32_t b = DivMod(div_plane, ok[e] ? gc : 0u, pix);
+            yi[e] = (static_cast<int64_t>(b) * p.m + gr) * plane_out + pix;
+            res[e] = p.residual != nullptr ? p.residual[yi[e]] : 0.0f;
+        }
+        const float bias = p.bias != nullptr ? p.bias[gr] : 0.0f;
+        const float* src = partial + static_cast<int64_t>(t) * pieces * per_tile + r * bn + 4 * c4;
+        const nert_floatx4 v = SumSlicesQuad(src, per_tile, pieces);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (!ok[e]) {
                 break;
             }
-            uint32_t pix;
-            const uint32_t b = DivMod(div_plane, gc, pix);
-            const int64_t yi = (static_cast<int64_t>(b) * p.m + gr) * plane_out + pix;
             float out = v[e];
             if (p.bias != nullptr) {
                 out = out + bias;
             }
-            p.y[yi] = Finish(p, out, yi);
+            if (p.residual != nullptr) {
+                out = out + res[e];
+            }
+            if (p.relu) {
+                out = (0.0f < out) ? out : 0.0f; // std::max(0.0f, v)
+            }
+            p.y[yi[e]] = out;
         }
     }
 }
