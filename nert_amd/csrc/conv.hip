@@ -625,6 +625,8 @@ using ConvShapeS = TileShape<32, 128, 16, 1, 4>;  // 4 waves, 32x32 each, for M_
 // on the ResNet-18 bs32 shapes instead of 196 .. 208.
 using ConvShapeQ = TileShape<64, 64, 16, 2, 2>;  // 4 waves, 32x32 each
 using ConvShapeT = TileShape<32, 64, 32, 1, 2>;  // 2 waves, 32x32 each
+using ConvShapeQK = TileShape<64, 64, 32, 2, 2>; // ConvShapeQ with 32-deep K steps
+using ConvShapeMK = TileShape<64, 128, 32, 2, 2>; // 4 waves, 32x64 each, 32-deep K steps
 
 template <class Shape>
 int64_t ConvTiles(const ConvArgs& p) {
@@ -1460,8 +1462,9 @@ bool TryPointwiseDirect(const ConvArgs& p, hipStream_t stream) {
 }
 
 // Tap-major and gather kernels: 0-2 ConvShapeL, ConvShapeW, ConvShapeS;
-// 3: the direct 1x1 kernel; 4-5: ConvShapeQ, ConvShapeT.
-constexpr int kGatherCandidates = 6;
+// 3: the direct 1x1 kernel; 4-7: ConvShapeQ, ConvShapeT, ConvShapeQK,
+// ConvShapeMK.
+constexpr int kGatherCandidates = 8;
 
 bool LaunchGatherCandidate(int i, const ConvArgs& p, hipStream_t stream) {
     switch (i) {
@@ -1479,6 +1482,12 @@ bool LaunchGatherCandidate(int i, const ConvArgs& p, hipStream_t stream) {
         return true;
     case 5:
         LaunchConv<ConvShapeT>(p, stream);
+        return true;
+    case 6:
+        LaunchConv<ConvShapeQK>(p, stream);
+        return true;
+    case 7:
+        LaunchConv<ConvShapeMK>(p, stream);
         return true;
     default:
         return TryPointwiseDirect(p, stream);

@@ -330,6 +330,10 @@ constexpr int64_t kChunkK = 512;
 using ShapeL = TileShape<128, 128, 16, 2, 4>; // 8 waves, 64x32 per wave
 using ShapeM = TileShape<64, 128, 16, 2, 2>;  // 4 waves, 32x64 per wave
 using ShapeS = TileShape<32, 64, 32, 1, 2>;   // 2 waves, skinny M
+// The M and L tiles with 32-deep K steps: half the LDS-store/barrier phases
+// per K, twice the LDS.
+using ShapeMK = TileShape<64, 128, 32, 2, 2>;  // 4 waves, 32x64 per wave
+using ShapeLK = TileShape<128, 128, 32, 2, 4>; // 8 waves, 64x32 per wave
 
 template <class Shape>
 void LaunchShape(GemmArgs p, int64_t batches, int splits, hipStream_t stream) {
@@ -368,8 +372,8 @@ int64_t TileCount(const GemmArgs& p, int64_t batches) {
 
 namespace {
 
-// One configuration: tile shape (0 L, 1 M, 2 S) and split-K count (0: the
-// PlanSplits choice for that shape).
+// One configuration: tile shape (0 L, 1 M, 2 S, 3 MK, 4 LK) and split-K count
+// (0: the PlanSplits choice for that shape).
 void LaunchConfig(GemmArgs p, int64_t batches, int shape, int force_splits, hipStream_t stream) {
     int64_t tiles;
     int64_t min_k_tiles = 8;
@@ -378,6 +382,14 @@ void LaunchConfig(GemmArgs p, int64_t batches, int shape, int force_splits, hipS
         tiles = TileCount<ShapeL>(p, batches);
     } else if (shape == 1) {
         tiles = TileCount<ShapeM>(p, batches);
+    } else if (shape == 3) {
+        tiles = TileCount<ShapeMK>(p, batches);
+        min_k_tiles = 4;
+        bk = ShapeMK::kBK;
+    } else if (shape == 4) {
+        tiles = TileCount<ShapeLK>(p, batches);
+        min_k_tiles = 4;
+        bk = ShapeLK::kBK;
     } else {
         tiles = TileCount<ShapeS>(p, batches);
         min_k_tiles = 2;
@@ -385,9 +397,10 @@ void LaunchConfig(GemmArgs p, int64_t batches, int shape, int force_splits, hipS
     }
     const int64_t k_tiles = (p.k + bk - 1) / bk;
     // The 2- and 4-wave shapes keep about 1024 workgroups resident.
+    const bool eight_waves = shape == 0 || shape == 4;
     int splits = force_splits > 0
                      ? static_cast<int>(std::min<int64_t>(force_splits, std::max<int64_t>(k_tiles, 1)))
-                     : PlanSplits(tiles, k_tiles, shape == 0 ? kResidentBlocks : 2 * kResidentBlocks, min_k_tiles, 32);
+                     : PlanSplits(tiles, k_tiles, eight_waves ? kResidentBlocks : 2 * kResidentBlocks, min_k_tiles, 32);
     p.k_per_split = ((k_tiles + splits - 1) / splits) * bk;
     if (p.k == 0) {
         p.k_per_split = 0;
@@ -403,6 +416,12 @@ void LaunchConfig(GemmArgs p, int64_t batches, int shape, int force_splits, hipS
         break;
     case 1:
         LaunchShape<ShapeM>(p, batches, splits, stream);
+        break;
+    case 3:
+        LaunchShape<ShapeMK>(p, batches, splits, stream);
+        break;
+    case 4:
+        LaunchShape<ShapeLK>(p, batches, splits, stream);
         break;
     default:
         LaunchShape<ShapeS>(p, batches, splits, stream);
@@ -423,11 +442,24 @@ void LaunchConfig(GemmArgs p, int64_t batches, int shape, int force_splits, hipS
     }
 }
 
-// Candidates: shape i / 4 with split count {PlanSplits, 1, 2, 4}[i % 4].
+// Candidates: 0-11 shape i / 4 (L, M, S) with split count {PlanSplits, 1,
+// 2, 4}[i % 4]; 12 the skinny kernel; 13-20 shape 3 + (i - 13) / 4 (MK, LK)
+// with split count {...}[(i - 13) % 4].
 // Fallback (capture, tuning off): 8-wave 128x128 tiles for problems with at
 // least 1024 of them, 4-wave 64x128 below, 2-wave 32x64 for M <= 32.
 using GemmKey = std::array<int64_t, 10>;
 constexpr int kGemmSplits[4] = {0, 1, 2, 4};
+constexpr int kGemmCandidates = 21;
+constexpr int kSkinnyCandidate = 12;
+
+void LaunchTiled(const GemmArgs& p, int64_t batches, int i, hipStream_t stream) {
+    if (i < kSkinnyCandidate) {
+        LaunchConfig(p, batches, i / 4, kGemmSplits[i % 4], stream);
+    } else {
+        LaunchConfig(p, batches, 3 + (i - kSkinnyCandidate - 1) / 4, kGemmSplits[(i - kSkinnyCandidate - 1) % 4],
+                     stream);
+    }
+}
 
 } // namespace
 
@@ -446,42 +478,41 @@ void LaunchGemm(GemmArgs p, int64_t batches, hipStream_t stream) {
     // same product sum in the same order.
     const GemmKey key{p.m, p.n, p.k, batches, p.a_sk == 1, p.b_sn == 1, p.batch_rank, 0, 0, 0};
     const size_t y_bytes = static_cast<size_t>(batches * p.m * p.n) * sizeof(float);
-    // Candidates 0-11: tile shape x split count; 12: the skinny kernel.
     const bool skinny = SkinnyApplies(p, batches);
     // NERT_HIP_GEMM_CANDIDATE=i forces candidate i wherever it applies (tests
     // of each configuration use it).
     if (const char* forced = std::getenv("NERT_HIP_GEMM_CANDIDATE")) {
         const int i = std::atoi(forced);
-        if (i == 12 && skinny) {
+        if (i == kSkinnyCandidate && skinny) {
             LaunchSkinny(p, stream);
             return;
         }
-        if (i >= 0 && i < 12) {
-            LaunchConfig(p, batches, i / 4, kGemmSplits[i % 4], stream);
+        if (i >= 0 && i < kGemmCandidates && i != kSkinnyCandidate) {
+            LaunchTiled(p, batches, i, stream);
             return;
         }
     }
-    const int c = ChooseConfig("gemm", chosen, mu, key, y_bytes, stream, 13, 4 * fallback_shape, [&](int i, float* scratch) {
-        GemmArgs q = p;
-        q.y = scratch;
-        if (i == 12) {
-            if (!skinny) {
-                return false;
-            }
-            LaunchSkinny(q, stream);
-            return true;
-        }
-        LaunchConfig(q, batches, i / 4, kGemmSplits[i % 4], stream);
-        return true;
-    });
-    if (c == 12 && skinny) {
+    const int c = ChooseConfig("gemm", chosen, mu, key, y_bytes, stream, kGemmCandidates, 4 * fallback_shape,
+                               [&](int i, float* scratch) {
+                                   GemmArgs q = p;
+                                   q.y = scratch;
+                                   if (i == kSkinnyCandidate) {
+                                       if (!skinny) {
+                                           return false;
+                                       }
+                                       LaunchSkinny(q, stream);
+                                       return true;
+                                   }
+                                   LaunchTiled(q, batches, i, stream);
+                                   return true;
+                               });
+    if (c == kSkinnyCandidate && skinny) {
         LaunchSkinny(p, stream);
         return;
     }
     // (A cached skinny choice with operands that lost its alignment takes
     // the fallback tiles.)
-    const int tiled = c == 12 ? 4 * fallback_shape : c;
-    LaunchConfig(p, batches, tiled / 4, kGemmSplits[tiled % 4], stream);
+    LaunchTiled(p, batches, c == kSkinnyCandidate ? 4 * fallback_shape : c, stream);
 }
 
 } // namespace nert_hip

@@ -426,10 +426,11 @@ def _run_forced(cand, paths, attrs):
     ((3, 24, 9, 11), (40, 24, 1, 1), {"strides": [1, 2], "pads": [1, 0, 0, 1]}),
     ((2, 32, 8, 8), (48, 16, 1, 1), {"group": 2}),
 ])
-@pytest.mark.parametrize("cand", [100, 101, 102, 103, 104, 105])
+@pytest.mark.parametrize("cand", [100, 101, 102, 103, 104, 105, 106, 107])
 def test_conv_1x1_forced_configs(gpu, tmp_path, xs, ws, attrs, cand):
     """Every configuration of the other conv kernels, the direct 1x1 kernel
-    (103) and the small-tile shapes (104, 105) included, forced: matches the
+    (103), the small-tile shapes (104, 105) and the 32-deep K steps (106,
+    107) included, forced: matches the
     restatement, and the fused epilogue matches Conv + Add + Relu bit for
     bit."""
     x, w, b = randn(xs, seed=90), randn(ws, seed=91, scale=0.1), randn((ws[0],), seed=92)
@@ -459,7 +460,7 @@ GEMM_FORCED = [
 ]
 
 
-@pytest.mark.parametrize("candidate", list(range(13)))
+@pytest.mark.parametrize("candidate", list(range(21)))
 @pytest.mark.parametrize("op,shapes,attrs", GEMM_FORCED)
 def test_gemm_every_candidate(gpu, monkeypatch, candidate, op, shapes, attrs):
     """Each tile shape x split count and the skinny kernel, forced with
