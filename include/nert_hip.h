@@ -166,14 +166,16 @@ typedef struct nert_conv_desc {
  * Replaces Conv: src/kernels/conv.cpp:138-295, src/hip/conv.cu:159-338. */
 int nert_hip_conv_f32(const float* x, const float* w, const float* bias, float* y, const nert_conv_desc* d,
                       void* stream);
-/* The same convolution with an epilogue: y = relu?(conv + bias + residual),
- * residual (optional, NULL) laid out like y. Each step rounds as the separate
- * Conv, Add and Relu rows do, so the result is bit-identical to running them
- * one after another. No reference counterpart: the reference executor runs
- * those rows separately (src/executor.cpp:480-535); the runner in nert_amd
- * fuses them through the FusedConv row. */
+/* The same convolution with an epilogue: y = act(conv + bias + residual),
+ * residual (optional, NULL) laid out like y; act 0 is none, 1 Relu
+ * (std::max(0, v)), 2 SiLU (v * Sigmoid(v), the Sigmoid row's 1/(1+exp(-v))
+ * then the Mul row's product); other codes fail. Each step rounds as the
+ * separate Conv, Add, Relu / Sigmoid and Mul rows do, so the result is
+ * bit-identical to running them one after another. No reference counterpart:
+ * the reference executor runs those rows separately (src/executor.cpp:480-535);
+ * the runner in nert_amd fuses them through the FusedConv row. */
 int nert_hip_conv_fused_f32(const float* x, const float* w, const float* bias, const float* residual, float* y,
-                            const nert_conv_desc* d, int relu, void* stream);
+                            const nert_conv_desc* d, int act, void* stream);
 
 /* ---------------------------------------------------------- elementwise --- */
 

@@ -54,20 +54,30 @@ struct ConvArgs {
     int64_t k_per_split;
     float* partial; // [splits][group][M_g][N] when split
     // Optional epilogue (fused rows): y = act(acc + bias + residual), in that
-    // order, so the result equals Conv, then Add, then Relu bit for bit.
+    // order, so the result equals Conv, then Add, then the activation rows
+    // bit for bit.
     const float* residual; // same layout as y, or null
-    int32_t relu;
+    int32_t act;           // 0 none, 1 Relu, 2 SiLU (x * Sigmoid(x))
 };
 
-// std::max(0.0f, v): NaN maps to 0 like the reference Relu.
+// The fused activation, each step rounded as the separate rows round it:
+// Relu is std::max(0.0f, v) (NaN maps to 0 like the reference Relu); SiLU is
+// the Sigmoid row's 1 / (1 + exp(-v)) followed by the Mul row's product.
+__device__ __forceinline__ float Activate(int act, float v) {
+    if (act == 1) {
+        return (0.0f < v) ? v : 0.0f;
+    }
+    if (act == 2) {
+        return __fmul_rn(v, 1.0f / __fadd_rn(1.0f, expf(-v)));
+    }
+    return v;
+}
+
 __device__ __forceinline__ float Finish(const ConvArgs& p, float v, int64_t y_index) {
     if (p.residual != nullptr) {
         v = v + p.residual[y_index];
     }
-    if (p.relu) {
-        v = (0.0f < v) ? v : 0.0f;
-    }
-    return v;
+    return Activate(p.act, v);
 }
 
 // Gathers B(k, n) = X_col for one K tile. Thread t owns column nn = t % BN for
@@ -391,9 +401,7 @@ __device__ __forceinline__ void ConvEpilogue(const ConvArgs& p, const Accum<Shap
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 float out = value[v];
-                if (p.relu) {
-                    out = (0.0f < out) ? out : 0.0f; // std::max(0.0f, v)
-                }
+                out = Activate(p.act, out);
                 if (ok[v]) {
                     p.y[yi[v]] = out;
                 }
@@ -521,7 +529,7 @@ __global__ void ConvSplitReduceKernel(ConvArgs p, int splits, int vec) {
                 sum += *reinterpret_cast<const nert_floatx4*>(p.partial + s * per_split + i);
             }
             sum += bias;
-            if (p.residual != nullptr || p.relu) {
+            if (p.residual != nullptr || p.act != 0) {
                 for (int e = 0; e < 4; ++e) {
                     sum[e] = Finish(p, sum[e], yi + e);
                 }
@@ -592,9 +600,7 @@ __global__ __launch_bounds__(256) void ConvSplitReduceQuadKernel(ConvArgs p, int
             if (p.residual != nullptr) {
                 out = out + res[e];
             }
-            if (p.relu) {
-                out = (0.0f < out) ? out : 0.0f; // std::max(0.0f, v)
-            }
+            out = Activate(p.act, out);
             p.y[yi[e]] = out;
         }
     }
@@ -1032,9 +1038,7 @@ __global__ __launch_bounds__(256) void ConvTailReduceQuadKernel(ConvArgs p, int 
             if (p.residual != nullptr) {
                 out = out + res[e];
             }
-            if (p.relu) {
-                out = (0.0f < out) ? out : 0.0f; // std::max(0.0f, v)
-            }
+            out = Activate(p.act, out);
             p.y[yi[e]] = out;
         }
     }
@@ -1410,7 +1414,7 @@ __global__ __launch_bounds__(256) void PointwiseDirectKernel(ConvArgs p) {
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(m_ok ? a[q] : 0.0f, in ? bv[q] : 0.0f, acc, 0, 0, 0);
         }
     }
-    // Epilogue as in ConvEpilogue: bias, then residual, then Relu.
+    // Epilogue as in ConvEpilogue: bias, then residual, then the activation.
     const int64_t ybase = b * p.m * p.plane_out + opix;
     float value[16];
     int64_t yi[16];
@@ -1437,9 +1441,7 @@ __global__ __launch_bounds__(256) void PointwiseDirectKernel(ConvArgs p) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
         float out = value[v];
-        if (p.relu) {
-            out = (0.0f < out) ? out : 0.0f;
-        }
+        out = Activate(p.act, out);
         if (ok[v]) {
             p.y[yi[v]] = out;
         }
@@ -1706,9 +1708,7 @@ __global__ __launch_bounds__(512, 4) void PatchConvKernel(ConvArgs p, PatchGeom 
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     float out = value[v];
-                    if (p.relu) {
-                        out = (0.0f < out) ? out : 0.0f; // std::max(0.0f, v)
-                    }
+                    out = Activate(p.act, out);
                     if (ok[v]) {
                         yb[yi[v]] = out;
                     }
@@ -1969,9 +1969,7 @@ __global__ __launch_bounds__(512, 4) void StemQuadKernel(ConvArgs p, StemGeom sg
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     float out = value[v];
-                    if (p.relu) {
-                        out = (0.0f < out) ? out : 0.0f; // std::max(0.0f, v)
-                    }
+                    out = Activate(p.act, out);
                     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out), yr,
                                                           static_cast<int>(ok[v] ? static_cast<uint32_t>(yi[v]) * 4u
                                                                                  : kOutOfRange),
@@ -2094,26 +2092,23 @@ bool TryPatchConv(const ConvArgs& p, hipStream_t stream) {
     return launched;
 }
 
-// y = relu?(y + residual) in place: the fused pointwise convolution's
+// y = act(y + residual) in place: the fused pointwise convolution's
 // epilogue, run after the GEMM has written conv + bias (each step rounded
-// like the Add and Relu rows).
-__global__ void ResidualReluKernel(float* y, const float* residual, int relu, int64_t n) {
+// like the Add and activation rows).
+__global__ void ResidualActKernel(float* y, const float* residual, int act, int64_t n) {
     for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
          i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
         float v = y[i];
         if (residual != nullptr) {
             v = __fadd_rn(v, residual[i]);
         }
-        if (relu) {
-            v = (0.0f < v) ? v : 0.0f;
-        }
-        y[i] = v;
+        y[i] = Activate(act, v);
     }
 }
 
 // A 1x1, stride-1, unpadded, ungrouped convolution is Y[b] = W[M,C] * X[b][C,P]
 // with P = D*H*W: a batched GEMM whose B batches are the images. The fused
-// form (residual, Relu) runs the same GEMM and then ResidualReluKernel, so a
+// form (residual, activation) runs the same GEMM and then ResidualActKernel, so a
 // Conv and a FusedConv of one geometry sum in the same order.
 bool TryPointwise(const ConvArgs& p, hipStream_t stream) {
     const bool unit = p.k_d == 1 && p.k_h == 1 && p.k_w == 1 && p.s_d == 1 && p.s_h == 1 && p.s_w == 1 &&
@@ -2143,10 +2138,10 @@ bool TryPointwise(const ConvArgs& p, hipStream_t stream) {
     g.a_bs[0] = 0;
     g.b_bs[0] = p.c * p.plane_in;
     LaunchGemm(g, p.batch, stream);
-    if (p.residual != nullptr || p.relu) {
+    if (p.residual != nullptr || p.act != 0) {
         const int64_t n = p.batch * p.m * p.plane_out;
-        ResidualReluKernel<<<GridFor(n, 256, 16384), 256, 0, stream>>>(p.y, p.residual, p.relu, n);
-        CheckLaunch("ResidualReluKernel launch");
+        ResidualActKernel<<<GridFor(n, 256, 16384), 256, 0, stream>>>(p.y, p.residual, p.act, n);
+        CheckLaunch("ResidualActKernel launch");
     }
     return true;
 }
@@ -2155,7 +2150,7 @@ bool TryPointwise(const ConvArgs& p, hipStream_t stream) {
 } // namespace nert_hip
 
 extern "C" int nert_hip_conv_fused_f32(const float* x, const float* w, const float* bias, const float* residual,
-                                       float* y, const nert_conv_desc* d, int relu, void* stream) {
+                                       float* y, const nert_conv_desc* d, int act, void* stream) {
     return nert_hip::Guard([&] {
         nert_hip::ConvArgs p{};
         p.x = x;
@@ -2163,7 +2158,10 @@ extern "C" int nert_hip_conv_fused_f32(const float* x, const float* w, const flo
         p.bias = bias;
         p.y = y;
         p.residual = residual;
-        p.relu = relu != 0 ? 1 : 0;
+        if (act < 0 || act > 2) {
+            throw nert_hip::Error("conv: activation must be 0 (none), 1 (Relu) or 2 (SiLU)");
+        }
+        p.act = act;
         p.batch = d->batch;
         p.c = d->in_channels;
         p.m = d->out_channels;

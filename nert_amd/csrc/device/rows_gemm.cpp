@@ -386,9 +386,10 @@ int64_t WindowOutput(const std::string& context, int64_t in, int64_t kernel, int
 namespace {
 
 // The Conv row's work, shared with FusedConv: `residual` (or null) is added
-// and Relu applied in the kernel epilogue when the fused row asks for it.
+// and the activation (0 none, 1 Relu, 2 SiLU) applied in the kernel epilogue
+// when the fused row asks for them.
 void ConvCore(const Node& node, const std::string& context, const Views& inputs, bool has_bias,
-              const TensorView* residual, bool relu, const Views& outputs) {
+              const TensorView* residual, int act, const Views& outputs) {
     const TensorView& x = inputs[0];
     const TensorView& w = inputs[1];
     const TensorView& out = outputs[0];
@@ -496,7 +497,7 @@ void ConvCore(const Node& node, const std::string& context, const Views& inputs,
         res = static_cast<const float*>(residual->data);
     }
     CheckStatus(nert_hip_conv_fused_f32(static_cast<const float*>(x.data), static_cast<const float*>(w.data), bias, res,
-                                        static_cast<float*>(out.data), &d, relu ? 1 : 0, Stream()),
+                                        static_cast<float*>(out.data), &d, act, Stream()),
                 context);
     AfterRow(outputs, context);
 }
@@ -509,13 +510,15 @@ void Conv(const Node& node, const Views& inputs, const Views& outputs) {
     if (inputs.size() < 2 || inputs.size() > 3 || outputs.size() != 1) {
         throw InferenceException(context + ": expected two or three inputs and one output");
     }
-    ConvCore(node, context, inputs, inputs.size() == 3, nullptr, false, outputs);
+    ConvCore(node, context, inputs, inputs.size() == 3, nullptr, 0, outputs);
 }
 
 // Not a reference row: Y = activation(Conv(X, W, B) + Z), the contract of
 // the com.microsoft FusedConv contrib op (inputs X, W, optional B, optional
-// Z; attribute `activation`, here "Relu" or absent). The nert_amd runner
-// rewrites Conv -> [Add] -> [Relu] chains into it; every step rounds as the
+// Z; attribute `activation`, here "Relu", "Silu" or absent). "Silu" is this
+// layer's addition to that contract: Y * Sigmoid(Y), the Sigmoid -> Mul pair
+// of SiLU/Swish blocks. The nert_amd runner rewrites Conv -> [Add] -> [Relu]
+// and Conv -> Sigmoid -> Mul chains into it; every step rounds as the
 // separate rows do, so results are bit-identical to the unfused graph.
 void FusedConv(const Node& node, const Views& inputs, const Views& outputs) {
     const std::string context = "FusedConv (node '" + node.name + "')";
@@ -523,13 +526,18 @@ void FusedConv(const Node& node, const Views& inputs, const Views& outputs) {
         throw InferenceException(context + ": expected two to four inputs and one output");
     }
     const std::string activation = StringAttr(node, "activation", "", "FusedConv");
-    if (!activation.empty() && activation != "Relu") {
+    int act = 0;
+    if (activation == "Relu") {
+        act = 1;
+    } else if (activation == "Silu") {
+        act = 2;
+    } else if (!activation.empty()) {
         throw InferenceException(context + ": unsupported activation '" + activation + "'");
     }
     const bool has_bias = inputs.size() >= 3 && inputs[2].dtype != DataType::Unknown;
     const TensorView* z = inputs.size() == 4 && inputs[3].dtype != DataType::Unknown ? &inputs[3] : nullptr;
     Views conv_inputs(inputs.begin(), inputs.begin() + (has_bias ? 3 : 2));
-    ConvCore(node, context, conv_inputs, has_bias, z, activation == "Relu", outputs);
+    ConvCore(node, context, conv_inputs, has_bias, z, act, outputs);
 }
 
 } // namespace rows

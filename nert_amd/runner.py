@@ -124,15 +124,17 @@ def plan_arena(g: Graph, alias: dict[str, tuple[str, int]] | None = None) -> tup
 
 
 def fuse_conv_chains(g: Graph) -> Graph:
-    """Rewrites Conv -> [Add] -> [Relu] chains into single FusedConv nodes.
+    """Rewrites Conv -> [Add] -> [Relu | SiLU] chains into single FusedConv nodes.
 
     A chain fuses when each intermediate tensor has exactly one consumer and is
     not a graph output, and the Add sums the conv output with a tensor of the
-    same shape (no broadcasting). The fused node takes the place of the chain's
-    last node, where every operand (including the Add's other input) already
-    exists. The FusedConv row applies bias, summand and Relu in the kernel
-    epilogue in the unfused order, so the outputs are bit-identical; the
-    chain's intermediates are never written to memory.
+    same shape (no broadcasting). SiLU is the pair Sigmoid(t) -> Mul(t, s) (in
+    either operand order): t's only consumers are that Sigmoid and that Mul,
+    and s's only consumer is the Mul. The fused node takes the place of the
+    chain's last node, where every operand (including the Add's other input)
+    already exists. The FusedConv row applies bias, summand and activation in
+    the kernel epilogue in the unfused order, so the outputs are bit-identical;
+    the chain's intermediates are never written to memory.
     """
     consumers: dict[str, list[int]] = {}
     for idx, n in enumerate(g.nodes):
@@ -148,6 +150,25 @@ def fuse_conv_chains(g: Graph) -> Graph:
         if len(c) == 1 and g.nodes[c[0]].op == op:
             return c[0]
         return None
+
+    def silu(t: str) -> tuple[int, int] | None:
+        """(Sigmoid index, Mul index) when t feeds exactly a SiLU pair."""
+        if t in outputs:
+            return None
+        c = consumers.get(t, [])
+        if len(c) != 2:
+            return None
+        ops = {g.nodes[i].op: i for i in c}
+        if set(ops) != {"Sigmoid", "Mul"}:
+            return None
+        sig, mul = ops["Sigmoid"], ops["Mul"]
+        s_node, m_node = g.nodes[sig], g.nodes[mul]
+        if len(s_node.inputs) != 1 or len(s_node.outputs) != 1:
+            return None
+        s_out = s_node.outputs[0]
+        if sole(s_out, "Mul") != mul or sorted(m_node.inputs) != sorted([t, s_out]) or t == s_out:
+            return None
+        return sig, mul
 
     replace: dict[int, Node] = {}
     dropped: set[int] = set()
@@ -169,11 +190,17 @@ def fuse_conv_chains(g: Graph) -> Graph:
                 last = a
         activation = None
         r = sole(out, "Relu")
+        pair = silu(out)
         if r is not None and r not in dropped:
             activation = "Relu"
             dropped.add(r)
             out = g.nodes[r].outputs[0]
             last = r
+        elif pair is not None and not dropped.intersection(pair):
+            activation = "Silu"
+            dropped.update(pair)
+            out = g.nodes[pair[1]].outputs[0]
+            last = pair[1]
         if last == idx:
             continue
         inputs = [n.inputs[0], n.inputs[1], n.inputs[2] if len(n.inputs) > 2 else "", z]

@@ -270,6 +270,28 @@ def test_fused_conv_bit_identical(gpu, xs, ws, attrs, with_z):
             np.maximum(ref, 0).astype(F), what="FusedConv vs reference")
 
 
+@pytest.mark.parametrize("xs,ws,attrs", FUSED_CASES + [
+    ((2, 16, 40, 40), (32, 16, 3, 3), {"pads": [1, 1, 1, 1], "strides": [2, 2]}),  # detector stage
+])
+@pytest.mark.parametrize("with_z", [False, True])
+def test_fused_conv_silu_bit_identical(gpu, xs, ws, attrs, with_z):
+    """FusedConv(activation="Silu") == Conv row, [Add], Sigmoid row, Mul row,
+    bit for bit; and within the Conv tolerance of the reference rows."""
+    x, w, b = randn(xs, seed=44, scale=2.0), randn(ws, seed=45, scale=0.1), randn((ws[0],), seed=46)
+    out = _conv_out(xs, ws, attrs)
+    t = _hip("Conv", [x, w, b], out, attrs)
+    z = randn(t.shape, seed=47) if with_z else None
+    if with_z:
+        t = _hip("Add", [t, z], out)
+    want = _hip("Mul", [t, _hip("Sigmoid", [t], out)], out)
+    got = _hip("FusedConv", [x, w, b] + ([z] if with_z else []), out, dict(attrs, activation="Silu"))
+    assert np.array_equal(got, want)
+    r = restate.conv(x, w, b, **_restate_args(attrs)).astype(np.float64)
+    if with_z:
+        r = r + z
+    compare(got, (r / (1.0 + np.exp(-r))).astype(F), what="FusedConv Silu vs reference")
+
+
 @pytest.mark.parametrize("ashape,n,alpha,bias,gelu", [
     ((2, 197, 64), 96, None, True, False),     # projection + bias
     ((2, 197, 64), 96, None, True, True),      # fc1 + bias + Gelu

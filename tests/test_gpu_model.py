@@ -145,6 +145,27 @@ def test_fused_vit_program_is_bit_identical(gpu):
     assert np.array_equal(outs[0], outs[1])
 
 
+def test_fused_detector_program_is_bit_identical(gpu):
+    """The Conv -> Sigmoid -> Mul (SiLU) fusion changes no output bit: the
+    detector's sigmoid scores, top scores, boxes and classes (batch 1,
+    128x128) from the fused program equal the separate rows'."""
+    g, inputs = workloads.detector(batch=1, size=128, k=50, expose_scores=True)
+    outs = []
+    for fuse, views in ((False, False), (True, True)):
+        prog = Program(g, fuse=fuse, views=views)
+        try:
+            if fuse:
+                assert sum(1 for n in prog.graph.nodes if n.attrs.get("activation") == "Silu") == 7
+            prog.set_input("input", inputs["input"])
+            prog.run()
+            prog.check_errors()
+            outs.append([prog.output(t) for t in g.outputs])
+        finally:
+            prog.close()
+    for a, b in zip(*outs):
+        assert a.dtype == b.dtype and np.array_equal(a, b)
+
+
 def test_fused_attention_program_matches_separate_rows(gpu):
     """With the attention blocks fused (FusedAttention, one kernel for QK^T,
     scale, Softmax and PV), the ViT logits stay within the 2e-4 bar of the

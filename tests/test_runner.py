@@ -62,6 +62,51 @@ def test_fusion_rules():
     assert [n.op for n in fuse_conv_chains(_chain(broadcast=True)).nodes] == ["Conv", "Add", "Relu"]
 
 
+def _silu_chain(swap=False, sig_output=False, third_consumer=False, with_add=False):
+    g = Graph()
+    x = g.add_input("x", F, (1, 4, 6, 6))
+    w = g.add_initializer("w", np.ones((4, 4, 3, 3), F))
+    (c,) = g.add_node("Conv", [x, w], [("c", F, (1, 4, 6, 6))], {"pads": [1, 1, 1, 1]})
+    if with_add:
+        z = g.add_input("z", F, (1, 4, 6, 6))
+        (c,) = g.add_node("Add", [z, c], [("a", F, (1, 4, 6, 6))])
+    (s,) = g.add_node("Sigmoid", [c], [("s", F, (1, 4, 6, 6))])
+    (m,) = g.add_node("Mul", [s, c] if swap else [c, s], [("m", F, (1, 4, 6, 6))])
+    g.outputs = [m]
+    if sig_output:
+        g.outputs.append(s)
+    if third_consumer:
+        (e,) = g.add_node("Relu", [c], [("e", F, (1, 4, 6, 6))])
+        g.outputs.append(e)
+    return g
+
+
+def test_silu_fusion_rules():
+    for swap in (False, True):
+        f = fuse_conv_chains(_silu_chain(swap=swap))
+        assert [n.op for n in f.nodes] == ["FusedConv"]
+        assert f.nodes[0].attrs["activation"] == "Silu" and f.nodes[0].outputs == ["m"]
+        assert f.nodes[0].inputs == ["x", "w"]
+    f = fuse_conv_chains(_silu_chain(with_add=True))
+    assert [n.op for n in f.nodes] == ["FusedConv"] and f.nodes[0].inputs == ["x", "w", "", "z"]
+    _valid_order(f)
+    # the Sigmoid output is also a graph output, or the conv output has a
+    # third consumer: the pair stays separate rows
+    assert [n.op for n in fuse_conv_chains(_silu_chain(sig_output=True)).nodes] == ["Conv", "Sigmoid", "Mul"]
+    assert [n.op for n in fuse_conv_chains(_silu_chain(third_consumer=True)).nodes] == \
+        ["Conv", "Sigmoid", "Mul", "Relu"]
+
+
+def test_detector_fusion():
+    g, _ = workloads.detector(batch=1, size=128, k=50)
+    f = fuse_conv_chains(g)
+    silu = [n for n in f.nodes if n.op == "FusedConv" and n.attrs.get("activation") == "Silu"]
+    # five backbone stages and the two neck convolutions end in SiLU
+    assert len(silu) == 7
+    assert sum(1 for n in f.nodes if n.op == "Sigmoid") == 1  # the score head's
+    _valid_order(f)
+
+
 def test_arena_plan_reuses_memory():
     g, _ = workloads.resnet18(batch=2)
     offsets, size = plan_arena(fuse_conv_chains(g))
