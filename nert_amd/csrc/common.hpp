@@ -44,6 +44,15 @@ void* Workspace(int64_t bytes, hipStream_t stream, int slot = 0);
 // report data-dependent errors (out-of-range indices, integer division by
 // zero) back to the host.
 int32_t* ErrorFlags();
+// Tile counters for kernels whose workgroups finish a tile's split sum among
+// themselves (the last one to arrive reduces; conv.hip): kTileCounters words,
+// zeroed once at set-up, and every launch that uses them leaves them zero.
+// Null when `count` exceeds the capacity or NERT_HIP_CONV_FIXUP=0 (the
+// caller then runs its separate reduce kernel). Launches on one stream never
+// overlap; kernels on different streams that both use them race, as they do
+// on the workspaces.
+constexpr int64_t kTileCounters = 1 << 16;
+uint32_t* TileCounters(int64_t count);
 // True once the device, stream and error word are set up (nert_hip_init).
 bool RuntimeReady();
 // Set-up of the fixed scratch of nert_hip_topk_f32_noalloc (topk.hip), run by

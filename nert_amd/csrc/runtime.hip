@@ -30,6 +30,7 @@ struct Context {
     int64_t workspace_bytes[kWorkspaceSlots] = {};
     WorkspaceBook book;  // replaced workspaces stay alive while graph execs may use them
     int32_t* flags = nullptr;
+    uint32_t* tile_counters = nullptr;
 };
 
 Context& Ctx() {
@@ -60,6 +61,10 @@ void EnsureReady() {
     Check(hipStreamCreateWithFlags(&ctx.stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
     Check(hipMalloc(reinterpret_cast<void**>(&ctx.flags), 64), "hipMalloc(flags)");
     Check(hipMemsetAsync(ctx.flags, 0, 64, ctx.stream), "hipMemsetAsync(flags)");
+    Check(hipMalloc(reinterpret_cast<void**>(&ctx.tile_counters), kTileCounters * sizeof(uint32_t)),
+          "hipMalloc(tile counters)");
+    Check(hipMemsetAsync(ctx.tile_counters, 0, kTileCounters * sizeof(uint32_t), ctx.stream),
+          "hipMemsetAsync(tile counters)");
     Check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
     TopkScratchSetup();
     ctx.ready = true;
@@ -110,6 +115,15 @@ void* Workspace(int64_t bytes, hipStream_t stream, int slot) {
 int32_t* ErrorFlags() {
     EnsureReady();
     return Ctx().flags;
+}
+
+uint32_t* TileCounters(int64_t count) {
+    EnsureReady();
+    static const bool enabled = [] {
+        const char* v = std::getenv("NERT_HIP_CONV_FIXUP");
+        return v == nullptr || std::strcmp(v, "0") != 0;
+    }();
+    return enabled && count >= 0 && count <= kTileCounters ? Ctx().tile_counters : nullptr;
 }
 
 void GraphCreated() {

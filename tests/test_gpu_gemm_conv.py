@@ -401,8 +401,12 @@ def hip(op, ins, shape, attrs):
     run_node(op, dev, [out], attrs)
     return out.to_host()
 a = json.loads({attrs!r})
-np.save({out1!r}, hip("Conv", [x, w, b], z.shape, a))
+y = hip("Conv", [x, w, b], z.shape, a)
+np.save({out1!r}, y)
 np.save({out2!r}, hip("FusedConv", [x, w, b, z], z.shape, dict(a, activation="Relu")))
+# a third launch of the same geometry: split tiles finished in the kernel
+# leave their counters at zero for the next launch
+assert np.array_equal(hip("Conv", [x, w, b], z.shape, a), y), "second Conv launch differs"
 """
 
 
@@ -430,7 +434,32 @@ def test_conv_lds_patch_forced_configs(gpu, tmp_path, batch, hw, cand):
     assert np.array_equal(np.load(paths["out2"]), np.where(want > 0, want, np.float32(0)).astype(F))
 
 
-def _run_forced(cand, paths, attrs):
+@pytest.mark.parametrize("batch,hw", [(17, 32), (32, 28), (3, 9)])
+@pytest.mark.parametrize("cand", [2, 3, 11, 15, 16, 17, 18, 19, 20, 21, 22, 23, 25, 26, 28, 29, 31, 32])
+def test_conv_split_fixup_matches_reduce_kernels(gpu, tmp_path, batch, hw, cand):
+    """Split-K and tail-split configurations finish their split tiles inside
+    the conv kernel (the last workgroup of a tile to arrive adds the parts in
+    part order); the result equals, bit for bit, the same configuration
+    with the parts summed by the separate reduce kernels
+    (NERT_HIP_CONV_FIXUP=0), for Conv and for the fused epilogue. Where a
+    candidate does not fit the geometry, both runs take the fixed default
+    (NERT_HIP_CONV_TUNE=0) rather than a timed choice."""
+    x = randn((batch, 64, hw, hw), seed=84)
+    w = randn((64, 64, 3, 3), seed=85, scale=0.06)
+    b = randn((64,), seed=86, scale=0.1)
+    z = randn((batch, 64, hw, hw), seed=87)
+    outs = []
+    for fixup in (True, False):
+        paths = {k: str(tmp_path / f"{k}{int(fixup)}.npy") for k in ("x", "w", "b", "z", "out1", "out2")}
+        for k, v in (("x", x), ("w", w), ("b", b), ("z", z)):
+            np.save(paths[k], v)
+        _run_forced(cand, paths, {"pads": [1, 1, 1, 1]}, fixup=fixup, tune=False)
+        outs.append((np.load(paths["out1"]), np.load(paths["out2"])))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    compare(outs[0][0], restate.conv(x, w, b, None, None, [1, 1, 1, 1], 1, "NOTSET"), what=f"candidate {cand}")
+
+
+def _run_forced(cand, paths, attrs, fixup=True, tune=True):
     import json
     import os
     import subprocess
@@ -438,6 +467,10 @@ def _run_forced(cand, paths, attrs):
 
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     env = dict(os.environ, NERT_HIP_CONV_CANDIDATE=str(cand))
+    if not fixup:
+        env["NERT_HIP_CONV_FIXUP"] = "0"
+    if not tune:
+        env["NERT_HIP_CONV_TUNE"] = "0"
     subprocess.run([sys.executable, "-c", _FORCED.format(root=root, attrs=json.dumps(attrs), **paths)], env=env,
                    check=True, timeout=120)
 
