@@ -45,9 +45,10 @@ void* Workspace(int64_t bytes, hipStream_t stream, int slot = 0);
 // zero) back to the host.
 int32_t* ErrorFlags();
 // Tile counters for kernels whose workgroups finish a tile's split sum among
-// themselves (the last one to arrive reduces; conv.hip): kTileCounters words,
+// themselves (the last one to arrive reduces; FinishSplitTile in
+// mfma_tile.hpp, used by the conv and GEMM kernels): kTileCounters words,
 // zeroed once at set-up, and every launch that uses them leaves them zero.
-// Null when `count` exceeds the capacity or NERT_HIP_CONV_FIXUP=0 (the
+// Null when `count` exceeds the capacity or NERT_HIP_SPLIT_FIXUP=0 (the
 // caller then runs its separate reduce kernel). Launches on one stream never
 // overlap; kernels on different streams that both use them race, as they do
 // on the workspaces.
@@ -149,4 +150,5 @@ inline void CheckLaunch(const char* what) { Check(hipGetLastError(), what); }
 // Device-side vector types for the MFMA builtins.
 typedef float nert_floatx2 __attribute__((ext_vector_type(2)));
 typedef float nert_floatx4 __attribute__((ext_vector_type(4)));
+typedef unsigned int nert_uintx4 __attribute__((ext_vector_type(4)));
 typedef float nert_floatx16 __attribute__((ext_vector_type(16)));

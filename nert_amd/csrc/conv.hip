@@ -702,88 +702,6 @@ void LaunchConv(ConvArgs p, hipStream_t stream) {
 // B use the same pairing, so the sum over the block's eight channels is the
 // same convolution. Two barriers per block; the next block's global loads are
 // in flight during the current block's 9 x 4 MFMA steps.
-// Split tiles finished inside the kernel. Every workgroup that computes one
-// part of a tile's K sum stores its accumulators (slot `part` of the tile's
-// `parts` slots of BM * BN floats, register order, consecutive threads at
-// consecutive addresses) and counts itself in the tile's counter. The
-// workgroup that brings the count to `parts` resets it to zero (for the next
-// launch), adds the parts in part order (P0 + P1 + ..., the order of the
-// separate reduce kernels, so the sum is the same whichever workgroup
-// arrives last) and returns true to run the epilogue; the others return
-// false. No workgroup waits on another. `flag` is one int of LDS the
-// workgroup no longer reads.
-//
-// The slots are written and read with device-scope atomic stores and loads,
-// which are coherent across the XCDs' L2 caches by themselves; a store
-// completes (vmcnt) once it is performed at that scope, so waiting for the
-// stores before the barrier and the counter increment orders them without a
-// device-scope fence (whose L2 writeback and invalidation would hit every
-// workgroup of the XCD).
-template <class Shape>
-__device__ __forceinline__ bool FixupSplitTile(Accum<Shape>& acc, float* slots, uint32_t* counter, int part,
-                                               int parts, int* flag) {
-    constexpr int kThreads = Shape::kThreads;
-    constexpr int kPerTile = Shape::kBM * Shape::kBN;
-    const int tid = threadIdx.x;
-    auto at = [&](int q, int i, int j, int v) {
-        return slots + static_cast<int64_t>(q) * kPerTile + ((i * Shape::kSubN + j) * 16 + v) * kThreads + tid;
-    };
-#pragma unroll
-    for (int i = 0; i < Shape::kSubM; ++i) {
-#pragma unroll
-        for (int j = 0; j < Shape::kSubN; ++j) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                __hip_atomic_store(at(part, i, j, v), acc.c[i][j][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t before = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const bool last = before + 1 == static_cast<uint32_t>(parts);
-        if (last) {
-            __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        *flag = last ? 1 : 0;
-    }
-    __syncthreads();
-    if (*flag == 0) {
-        return false;
-    }
-    // Every part from the slots, this workgroup's own included (each thread
-    // reads back only what it stored), summed into the accumulators; the
-    // loads of four parts of a 32x32 block are in flight together.
-#pragma unroll
-    for (int i = 0; i < Shape::kSubM; ++i) {
-#pragma unroll
-        for (int j = 0; j < Shape::kSubN; ++j) {
-            for (int q0 = 0; q0 < parts; q0 += 4) {
-                float x[4][16];
-#pragma unroll
-                for (int dq = 0; dq < 4; ++dq) {
-                    const int q = min(q0 + dq, parts - 1);
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) {
-                        x[dq][v] = __hip_atomic_load(at(q, i, j, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    }
-                }
-#pragma unroll
-                for (int dq = 0; dq < 4; ++dq) {
-                    if (q0 + dq < parts) {
-#pragma unroll
-                        for (int v = 0; v < 16; ++v) {
-                            acc.c[i][j][v] = q0 + dq == 0 ? x[dq][v] : acc.c[i][j][v] + x[dq][v];
-                        }
-                    }
-                }
-            }
-        }
-    }
-    return true;
-}
-
 constexpr int kHaloBK = 8;               // channels per K step
 constexpr int kHaloCS = kHaloBK + 4;     // LDS floats per patch position (16-byte aligned rows)
 constexpr int kHaloMaxLds = 64 * 1024;   // dynamic LDS budget per workgroup
@@ -810,7 +728,7 @@ struct HaloGeom {
     // takes tiles_m / 8 channel tiles and every pixel tile, so it reads only
     // its eighth of the weights; set where the weights outweigh the input.
     int32_t xcd_by_channel;
-    // In-kernel finish of split tiles (FixupSplitTile), when non-null:
+    // In-kernel finish of split tiles (FinishSplitTile), when non-null:
     // counters[t] for tail tile t, or for tile g * tiles + tile under split-K,
     // whose parts go to split_slots[g * tiles + tile][split][BM * BN]; tail
     // pieces use tail_partial the same way. Null: the parts go to
@@ -1085,7 +1003,7 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
             parts = static_cast<int>(gridDim.z);
             slots = h.split_slots + t * parts * BM * BN;
         }
-        if (FixupSplitTile<Shape>(acc, slots, h.counters + t, part, parts, reinterpret_cast<int*>(smem))) {
+        if (FinishSplitTile<Shape, float>(acc, slots, h.counters + t, part, parts, reinterpret_cast<int*>(smem))) {
             ConvEpilogue<Shape>(p, acc, row0, col0, g, 0);
         }
         return;

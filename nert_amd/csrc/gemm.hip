@@ -5,8 +5,10 @@
 // (Gemm). Transposes are expressed as operand strides, so Gemm's four
 // (transA, transB) cases and MatMul's broadcast batches are the same code with
 // different loaders. Small problems that cannot fill 256 CUs are split along
-// K into a workspace and summed by a second kernel in a fixed order, so the
-// result does not depend on scheduling.
+// K; the parts of a tile are summed in a fixed order (in double, rounded
+// once) by the tile's last workgroup to finish, or by a second kernel when
+// the tile counters do not suffice, so the result does not depend on
+// scheduling.
 
 #include "gemm_engine.hpp"
 #include "mfma_tile.hpp"
@@ -166,6 +168,15 @@ __global__ __launch_bounds__(Shape::kThreads) void GemmKernel(GemmArgs p) {
     }
 
     const int64_t plane = p.m * p.n;
+    if (p.counters != nullptr) {
+        const int64_t t = batch * gridDim.x + tile;
+        float* slots = p.split_slots + t * gridDim.z * Shape::kBM * Shape::kBN;
+        if (FinishSplitTile<Shape, double>(acc, slots, p.counters + t, split, static_cast<int>(gridDim.z),
+                                           reinterpret_cast<int*>(lds))) {
+            GemmEpilogue<Shape>(p, acc, p.y + batch * plane, row0, col0, true);
+        }
+        return;
+    }
     if (p.partial != nullptr) {
         GemmEpilogue<Shape>(p, acc, p.partial + (static_cast<int64_t>(split) * gridDim.y + batch) * plane, row0, col0,
                             false);
@@ -339,6 +350,10 @@ template <class Shape>
 void LaunchShape(GemmArgs p, int64_t batches, int splits, hipStream_t stream) {
     const int64_t tiles = ((p.m + Shape::kBM - 1) / Shape::kBM) * ((p.n + Shape::kBN - 1) / Shape::kBN);
     dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(batches), static_cast<unsigned>(splits));
+    if (p.counters != nullptr) {
+        p.split_slots = static_cast<float*>(
+            Workspace(tiles * batches * splits * Shape::kBM * Shape::kBN * static_cast<int64_t>(sizeof(float)), stream));
+    }
     dim3 block(Shape::kThreads);
     const bool a_k = p.a_sk == 1;
     const bool b_n = p.b_sn == 1;
@@ -407,8 +422,16 @@ void LaunchConfig(GemmArgs p, int64_t batches, int shape, int force_splits, hipS
         splits = 1;
     }
     p.partial = nullptr;
+    p.counters = nullptr;
+    p.split_slots = nullptr;
     if (splits > 1) {
-        p.partial = static_cast<float*>(Workspace(static_cast<int64_t>(splits) * batches * p.m * p.n * 4, stream));
+        // Split tiles finish inside the kernel when the counters suffice,
+        // else in the reduce kernels below.
+        p.counters = TileCounters(tiles);
+        if (p.counters == nullptr) {
+            p.partial =
+                static_cast<float*>(Workspace(static_cast<int64_t>(splits) * batches * p.m * p.n * 4, stream));
+        }
     }
     switch (shape) {
     case 0:
@@ -427,7 +450,7 @@ void LaunchConfig(GemmArgs p, int64_t batches, int shape, int force_splits, hipS
         LaunchShape<ShapeS>(p, batches, splits, stream);
         break;
     }
-    if (splits > 1) {
+    if (splits > 1 && p.counters == nullptr) {
         const int vec = p.n % 4 == 0 ? 4 : 1;
         const int64_t total = batches * p.m * p.n;
         const int64_t work = total / vec;

@@ -23,7 +23,12 @@ struct GemmArgs {
     int64_t a_bs[4];
     int64_t b_bs[4];
     int64_t k_per_split; // set by LaunchGemm
-    float* partial;      // set by LaunchGemm
+    float* partial;      // set by LaunchGemm: split-K parts for the reduce kernels, or null
+    // Set by LaunchGemm instead of `partial` when the split tiles are
+    // finished inside the kernel (FinishSplitTile): per-tile counters and
+    // slots [batch * tiles + tile][split][BM * BN].
+    uint32_t* counters;
+    float* split_slots;
     // Optional activation after the bias (fused MatMul rows): act 1 is the
     // erf Gelu chain y -> y * (erf(y / act_div) + act_add) * act_mul.
     int act;

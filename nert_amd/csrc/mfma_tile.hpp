@@ -204,6 +204,105 @@ __device__ __forceinline__ void MainLoop(const ALoader& aload, const BLoader& bl
     }
 }
 
+// Split tiles finished inside the kernel. Every workgroup that computes one
+// part of a tile's K sum stores its accumulators (slot `part` of the tile's
+// `parts` slots of BM * BN floats, in register order: 16-byte pieces,
+// consecutive threads at consecutive addresses) and counts itself in the
+// tile's counter. The workgroup that brings the count to `parts` resets it
+// to zero (for the next launch), adds the parts in part order (P0 + P1 + ...,
+// in type Sum, rounded to float once: the order and precision of the
+// separate reduce kernels, so the sum is the same whichever workgroup arrives
+// last), leaves it in `acc` and returns true to run the epilogue; the others
+// return false. No workgroup waits on another. `flag` is one int of LDS the
+// workgroup no longer reads.
+//
+// The slots are stored and loaded with the sc1 cache policy, the device-scope
+// coherence bit the compiler itself puts on device-scope atomic loads and
+// stores: such an access is performed at a level shared by all XCDs, past
+// their separate L2 caches, and a store counts as complete (vmcnt) only once
+// it is. Waiting for the stores before the barrier and the counter increment
+// therefore orders them without a device-scope fence, whose L2 writeback and
+// invalidation would stall every workgroup of the XCD. The counter is a
+// device-scope atomic.
+template <class Shape, class Sum>
+__device__ __forceinline__ bool FinishSplitTile(Accum<Shape>& acc, float* slots, uint32_t* counter, int part,
+                                                int parts, int* flag) {
+    constexpr int kThreads = Shape::kThreads;
+    constexpr int kPerTile = Shape::kBM * Shape::kBN;
+    constexpr int kDeviceCoherent = 16; // cache policy: sc1
+    const int tid = threadIdx.x;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        slots, static_cast<short>(0), parts * kPerTile * static_cast<int>(sizeof(float)), 0x00020000);
+    // Byte offset of float4 v4 of block (i, j) in slot q.
+    auto at = [&](int q, int i, int j, int v4) {
+        return (q * kPerTile + (((i * Shape::kSubN + j) * 4 + v4) * kThreads + tid) * 4) * 4;
+    };
+#pragma unroll
+    for (int i = 0; i < Shape::kSubM; ++i) {
+#pragma unroll
+        for (int j = 0; j < Shape::kSubN; ++j) {
+#pragma unroll
+            for (int v4 = 0; v4 < 4; ++v4) {
+                const nert_floatx4 x{acc.c[i][j][4 * v4], acc.c[i][j][4 * v4 + 1], acc.c[i][j][4 * v4 + 2],
+                                     acc.c[i][j][4 * v4 + 3]};
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(nert_uintx4, x), r, at(part, i, j, v4), 0,
+                                                       kDeviceCoherent);
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t before = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = before + 1 == static_cast<uint32_t>(parts);
+        if (last) {
+            __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        *flag = last ? 1 : 0;
+    }
+    __syncthreads();
+    if (*flag == 0) {
+        return false;
+    }
+    // Every part from the slots, this workgroup's own included (each thread
+    // reads back only what it stored); the loads of four parts of a 32x32
+    // block are in flight together.
+#pragma unroll
+    for (int i = 0; i < Shape::kSubM; ++i) {
+#pragma unroll
+        for (int j = 0; j < Shape::kSubN; ++j) {
+            Sum sum[16];
+            for (int q0 = 0; q0 < parts; q0 += 4) {
+                nert_floatx4 x[4][4];
+#pragma unroll
+                for (int dq = 0; dq < 4; ++dq) {
+                    const int q = min(q0 + dq, parts - 1);
+#pragma unroll
+                    for (int v4 = 0; v4 < 4; ++v4) {
+                        x[dq][v4] = __builtin_bit_cast(
+                            nert_floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, at(q, i, j, v4), 0, kDeviceCoherent));
+                    }
+                }
+#pragma unroll
+                for (int dq = 0; dq < 4; ++dq) {
+                    if (q0 + dq < parts) {
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) {
+                            const Sum y = static_cast<Sum>(x[dq][v >> 2][v & 3]);
+                            sum[v] = q0 + dq == 0 ? y : sum[v] + y;
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                acc.c[i][j][v] = static_cast<float>(sum[v]);
+            }
+        }
+    }
+    return true;
+}
+
 // Visits every accumulator element with its tile-relative (row, col).
 template <class Shape, class F>
 __device__ __forceinline__ void ForEachAccum(const Accum<Shape>& acc, F&& fn) {

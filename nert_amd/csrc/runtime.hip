@@ -120,7 +120,7 @@ int32_t* ErrorFlags() {
 uint32_t* TileCounters(int64_t count) {
     EnsureReady();
     static const bool enabled = [] {
-        const char* v = std::getenv("NERT_HIP_CONV_FIXUP");
+        const char* v = std::getenv("NERT_HIP_SPLIT_FIXUP");
         return v == nullptr || std::strcmp(v, "0") != 0;
     }();
     return enabled && count >= 0 && count <= kTileCounters ? Ctx().tile_counters : nullptr;

@@ -441,7 +441,7 @@ def test_conv_split_fixup_matches_reduce_kernels(gpu, tmp_path, batch, hw, cand)
     the conv kernel (the last workgroup of a tile to arrive adds the parts in
     part order); the result equals, bit for bit, the same configuration
     with the parts summed by the separate reduce kernels
-    (NERT_HIP_CONV_FIXUP=0), for Conv and for the fused epilogue. Where a
+    (NERT_HIP_SPLIT_FIXUP=0), for Conv and for the fused epilogue. Where a
     candidate does not fit the geometry, both runs take the fixed default
     (NERT_HIP_CONV_TUNE=0) rather than a timed choice."""
     x = randn((batch, 64, hw, hw), seed=84)
@@ -468,7 +468,7 @@ def _run_forced(cand, paths, attrs, fixup=True, tune=True):
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     env = dict(os.environ, NERT_HIP_CONV_CANDIDATE=str(cand))
     if not fixup:
-        env["NERT_HIP_CONV_FIXUP"] = "0"
+        env["NERT_HIP_SPLIT_FIXUP"] = "0"
     if not tune:
         env["NERT_HIP_CONV_TUNE"] = "0"
     subprocess.run([sys.executable, "-c", _FORCED.format(root=root, attrs=json.dumps(attrs), **paths)], env=env,
@@ -513,6 +513,60 @@ GEMM_FORCED = [
     ("Gemm", [(37, 50), (37, 60)], {"transA": 1}),                  # A transposed
     ("Gemm", [(40, 1100), (1100, 24)], {}),                         # two-level accumulation (K > 1024)
 ]
+
+
+_GEMM_SPLIT = r"""
+import sys
+import numpy as np
+sys.path.insert(0, {root!r})
+from nert_amd.device import DeviceArray, run_node
+import os
+cases = {cases!r}
+outs = {{}}
+for ci, (op, shapes, attrs, out) in enumerate(cases):
+    xs = [np.random.default_rng(70 + ci * 4 + i).uniform(-1, 1, s).astype(np.float32) for i, s in enumerate(shapes)]
+    for cand in {cands!r}:
+        os.environ["NERT_HIP_GEMM_CANDIDATE"] = str(cand)
+        dev = [DeviceArray.from_host(a) for a in xs]
+        res = []
+        for rep in range(2):
+            y = DeviceArray(tuple(out), np.float32)
+            run_node(op, dev, [y], attrs)
+            res.append(y.to_host())
+        assert np.array_equal(res[0], res[1]), (ci, cand, "second launch differs")
+        outs[f"{{ci}}_{{cand}}"] = res[0]
+np.savez({path!r}, **outs)
+"""
+
+
+def test_gemm_split_fixup_matches_reduce_kernels(gpu, tmp_path):
+    """GEMM split-K tiles finished inside the kernel (parts summed in double
+    by the tile's last workgroup, in split order) equal, bit for bit, the
+    same configuration summed by the separate reduce kernels
+    (NERT_HIP_SPLIT_FIXUP=0): every split candidate, forced, on shapes with a
+    K remainder, a two-level K range and batches; two launches in a row."""
+    import os
+    import subprocess
+    import sys
+
+    cases = [("MatMul", [(3, 70, 333), (3, 333, 45)], {}, (3, 70, 45)),
+             ("Gemm", [(40, 1100), (1100, 24)], {}, (40, 24)),
+             ("Gemm", [(512, 512), (512, 512)], {"transB": 1}, (512, 512)),
+             ("MatMul", [(96, 200), (200, 80)], {}, (96, 80))]
+    cands = [i for i in range(21) if i != 12 and (i if i < 12 else i - 13) % 4 in (2, 3)]
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    got = []
+    for fixup in (True, False):
+        path = str(tmp_path / f"gemm{int(fixup)}.npz")
+        env = dict(os.environ)
+        if not fixup:
+            env["NERT_HIP_SPLIT_FIXUP"] = "0"
+        subprocess.run([sys.executable, "-c", _GEMM_SPLIT.format(root=root, cases=cases, cands=cands, path=path)],
+                       env=env, check=True, timeout=120)
+        got.append(np.load(path))
+    assert sorted(got[0].files) == sorted(got[1].files)
+    for k in got[0].files:
+        assert np.array_equal(got[0][k], got[1][k]), k
 
 
 @pytest.mark.parametrize("candidate", list(range(21)))
