@@ -58,6 +58,11 @@ struct ConvArgs {
     // bit for bit.
     const float* residual; // same layout as y, or null
     int32_t act;           // 0 none, 1 Relu, 2 SiLU (x * Sigmoid(x))
+    // Split tiles of the gather kernels finished inside the kernel
+    // (FinishSplitTile) instead of through `partial`: counters per
+    // [group][tile], slots [group * tiles + tile][split][BM * BN].
+    uint32_t* split_counters;
+    float* split_slots;
 };
 
 // The fused activation, each step rounded as the separate rows round it:
@@ -431,6 +436,14 @@ __global__ __launch_bounds__(Shape::kThreads) void ConvTapKernel(ConvArgs p) {
     TapBLoader<Shape::kBN, Shape::kBK, Shape::kThreads, Shape::kPitchB, KH, KW> bload;
     bload.init(p, col0, g);
     MainLoop<Shape>(aload, bload, k_begin, k_end, lds, acc);
+    if (p.split_counters != nullptr) {
+        const int64_t t = static_cast<int64_t>(g) * gridDim.x + tile;
+        if (!FinishSplitTile<Shape, float>(acc, p.split_slots + t * gridDim.z * Shape::kBM * Shape::kBN,
+                                           p.split_counters + t, split, static_cast<int>(gridDim.z),
+                                           reinterpret_cast<int*>(lds))) {
+            return;
+        }
+    }
     ConvEpilogue<Shape>(p, acc, row0, col0, g, split);
 }
 
@@ -483,7 +496,14 @@ __global__ __launch_bounds__(Shape::kThreads) void ConvKernel(ConvArgs p) {
         MainLoop<Shape>(aload, bload, k_full, k_end, lds, acc);
     }
 
-    if (p.partial != nullptr) {
+    if (p.split_counters != nullptr) {
+        const int64_t t = static_cast<int64_t>(g) * gridDim.x + tile;
+        if (!FinishSplitTile<Shape, float>(acc, p.split_slots + t * gridDim.z * Shape::kBM * Shape::kBN,
+                                           p.split_counters + t, split, static_cast<int>(gridDim.z),
+                                           reinterpret_cast<int*>(lds))) {
+            return;
+        }
+    } else if (p.partial != nullptr) {
         float* out = p.partial + (static_cast<int64_t>(split) * p.group + g) * p.mg * p.n_total;
         ForEachAccum<Shape>(acc, [&](int r, int c, float v) {
             const int64_t gr = row0 + r;
@@ -645,12 +665,20 @@ void LaunchConv(ConvArgs p, hipStream_t stream) {
     const int64_t tiles = ConvTiles<Shape>(p);
     const int splits = PlanSplits(tiles, k_tiles, kResidentBlocks, 8);
     p.k_per_split = ((k_tiles + splits - 1) / splits) * Shape::kBK;
-    p.partial = nullptr;
-    if (splits > 1) {
-        p.partial =
-            static_cast<float*>(Workspace(static_cast<int64_t>(splits) * p.group * p.mg * p.n_total * 4, stream));
-    }
     const int64_t tiles_mn = ((p.mg + Shape::kBM - 1) / Shape::kBM) * ((p.n_total + Shape::kBN - 1) / Shape::kBN);
+    p.partial = nullptr;
+    p.split_counters = nullptr;
+    p.split_slots = nullptr;
+    if (splits > 1) {
+        p.split_counters = TileCounters(tiles_mn * p.group);
+        if (p.split_counters != nullptr) {
+            p.split_slots = static_cast<float*>(Workspace(
+                tiles_mn * p.group * splits * Shape::kBM * Shape::kBN * static_cast<int64_t>(sizeof(float)), stream));
+        } else {
+            p.partial = static_cast<float*>(
+                Workspace(static_cast<int64_t>(splits) * p.group * p.mg * p.n_total * 4, stream));
+        }
+    }
     dim3 grid(static_cast<unsigned>(tiles_mn), static_cast<unsigned>(p.group), static_cast<unsigned>(splits));
     const bool tap_major = p.k_d == 1 && p.in_d == 1 && p.out_d == 1 && p.cg % Shape::kBK == 0 &&
                            p.batch * p.c * p.plane_in * 4 < (int64_t{1} << 31) &&
@@ -673,7 +701,7 @@ void LaunchConv(ConvArgs p, hipStream_t stream) {
         ConvKernel<Shape, 0, 0><<<grid, Shape::kThreads, 0, stream>>>(p);
     }
     CheckLaunch("ConvKernel launch");
-    if (splits > 1) {
+    if (splits > 1 && p.split_counters == nullptr) {
         LaunchSplitReduce(p, splits, stream);
     }
 }

@@ -459,6 +459,29 @@ def test_conv_split_fixup_matches_reduce_kernels(gpu, tmp_path, batch, hw, cand)
     compare(outs[0][0], restate.conv(x, w, b, None, None, [1, 1, 1, 1], 1, "NOTSET"), what=f"candidate {cand}")
 
 
+@pytest.mark.parametrize("xs,ws,attrs", [
+    ((2, 256, 14, 14), (512, 256, 1, 1), {"strides": [2, 2]}),                    # few tiles, long K
+    ((1, 120, 20, 20), (32, 60, 3, 3), {"pads": [1, 1, 1, 1], "group": 2}),       # grouped gather, long K
+])
+@pytest.mark.parametrize("cand", [100, 101, 102, 104, 105, 106, 107])
+def test_conv_gather_split_fixup_matches_reduce_kernels(gpu, tmp_path, xs, ws, attrs, cand):
+    """The gather / tap-major conv kernels' split-K tiles, finished inside the
+    kernel, equal the reduce-kernel sums bit for bit (Conv and the fused
+    epilogue), and the restatement within tolerance."""
+    x, w, b = randn(xs, seed=94), randn(ws, seed=95, scale=0.1), randn((ws[0],), seed=96)
+    z = randn(_conv_out(xs, ws, attrs), seed=97)
+    outs = []
+    for fixup in (True, False):
+        paths = {k: str(tmp_path / f"{k}{int(fixup)}.npy") for k in ("x", "w", "b", "z", "out1", "out2")}
+        for k, v in (("x", x), ("w", w), ("b", b), ("z", z)):
+            np.save(paths[k], v)
+        _run_forced(cand, paths, attrs, fixup=fixup, tune=False)
+        outs.append((np.load(paths["out1"]), np.load(paths["out2"])))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    compare(outs[0][0], restate.conv(x, w, b, attrs.get("strides"), None, attrs.get("pads"), attrs.get("group", 1),
+                                     "NOTSET"), what=f"candidate {cand}")
+
+
 def _run_forced(cand, paths, attrs, fixup=True, tune=True):
     import json
     import os
