@@ -276,8 +276,8 @@ def main() -> int:
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "Conv rows (implicit-GEMM conv kernels + split-K reduce; 17 of 20 carry the fused "
-                      "Add/Relu epilogue), 20 per step",
+            "kernel": "Conv rows (implicit-GEMM conv kernels, split tiles finished inside the kernel; 17 of 20 "
+                      "carry the fused Add/Relu epilogue), 20 per step",
             "achieved": round(achieved, 3),
             "peak": PEAK_FP32_MFMA_TFLOPS,
             "unit": "TFLOP/s",
