@@ -42,6 +42,11 @@ COMMON_FLAGS = [
     "-fPIC",
     f"--offload-arch={ARCH}",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs: otherwise, in kernels of 256 threads
+    # or fewer, the backend keeps them in AGPRs and copies all of them to
+    # VGPRs and back on every K-loop iteration (v_accvgpr_read/write, 16 per
+    # 32x32 block per iteration); with this form no kernel here gains a spill.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wall",
     "-Wno-unused-command-line-argument",
     "-Wno-unknown-warning-option",
@@ -87,7 +92,8 @@ def _compile(src: Path, force: bool, newest_header: float) -> Path:
 def build_device_layer(force: bool = False, jobs: int | None = None) -> Path:
     """Compiles every HIP/C++ source under nert_amd/csrc and links libnert_hip.so."""
     LIB.mkdir(parents=True, exist_ok=True)
-    newest_header = max((h.stat().st_mtime for h in _headers()), default=0.0)
+    # A change of the compile flags (this file) rebuilds every object too.
+    newest_header = max([h.stat().st_mtime for h in _headers()] + [Path(__file__).stat().st_mtime])
     sources = _sources()
     jobs = jobs or min(8, os.cpu_count() or 4)
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
