@@ -415,6 +415,9 @@ struct RowContigLoader {
 
     __device__ __forceinline__ void load(int64_t k0, Stage& s) const {
         const int tid = threadIdx.x;
+        // k0 * k_stride is wave-uniform (scalar); kk * k_stride + row depends
+        // on the thread only, so it stays out of the K loop.
+        const float* tile = base + k0 * k_stride;
 #pragma unroll
         for (int p = 0; p < kPer; ++p) {
             const int q = tid + p * THREADS;
@@ -425,7 +428,7 @@ struct RowContigLoader {
                 if (kQuads % THREADS != 0 && q >= kQuads) {
                     continue; // this thread owns no quad in this pass
                 }
-                s.v[p] = *reinterpret_cast<const nert_floatx4*>(base + k * k_stride + row);
+                s.v[p] = *reinterpret_cast<const nert_floatx4*>(tile + (kk * k_stride + row));
             } else {
                 const bool k_ok = q < kQuads && k < k_total;
                 const int64_t k_off = k_ok ? k * k_stride : 0;
