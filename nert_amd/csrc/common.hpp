@@ -147,6 +147,13 @@ inline void CheckLaunch(const char* what) { Check(hipGetLastError(), what); }
 
 } // namespace nert_hip
 
+// Sigmoid as the Sigmoid row and the fused SiLU epilogue both compute it:
+// 1 / (1 + exp(-x)) (src/kernels/sigmoid.cpp:52) with the hardware
+// reciprocal (v_rcp_f32, within 1 ulp) in place of an IEEE division, which
+// costs ten instructions; one definition, so the fused and separate rows
+// agree bit for bit.
+__device__ __forceinline__ float SigmoidF32(float x) { return __builtin_amdgcn_rcpf(__fadd_rn(1.0f, expf(-x))); }
+
 // Device-side vector types for the MFMA builtins.
 typedef float nert_floatx2 __attribute__((ext_vector_type(2)));
 typedef float nert_floatx4 __attribute__((ext_vector_type(4)));

@@ -67,13 +67,13 @@ struct ConvArgs {
 
 // The fused activation, each step rounded as the separate rows round it:
 // Relu is std::max(0.0f, v) (NaN maps to 0 like the reference Relu); SiLU is
-// the Sigmoid row's 1 / (1 + exp(-v)) followed by the Mul row's product.
+// the Sigmoid row's SigmoidF32(v) followed by the Mul row's product.
 __device__ __forceinline__ float Activate(int act, float v) {
     if (act == 1) {
         return (0.0f < v) ? v : 0.0f;
     }
     if (act == 2) {
-        return __fmul_rn(v, 1.0f / __fadd_rn(1.0f, expf(-v)));
+        return __fmul_rn(v, SigmoidF32(v));
     }
     return v;
 }
@@ -2095,6 +2095,136 @@ bool TryStemQuad(const ConvArgs& p, hipStream_t stream) {
     return true;
 }
 
+// ---- Tiny convolutions on the vector ALUs ------------------------------------
+//
+// A 2-D convolution with at most kDirectK taps x channels per group and at
+// most kDirectM output channels per group (the detector's stem: 3 channels,
+// 3x3, 16 outputs) does a few hundred multiply-adds per output pixel against
+// tens of bytes moved: HBM work, which the MFMA patch kernel (64 output
+// channels per tile) spends mostly on empty rows. Here one thread owns one
+// output pixel: it loads the pixel's K inputs once (buffer loads; padding
+// taps get an out-of-range offset and read 0) and runs M dot products of
+// length K in K order against weights every lane shares (wave-uniform
+// addresses, so scalar loads), then applies bias, residual and activation
+// as the other kernels do.
+constexpr int kDirectK = 32;
+constexpr int kDirectM = 32;
+
+struct DirectGeom {
+    FastDiv div_plane_out; // by OH * OW
+    FastDiv div_out_w;     // by OW
+};
+
+// KH, KW > 0: that filter size at compile time (the taps' offsets and
+// bounds checks unrolled); 0: any size up to kDirectK taps x channels.
+template <int KH, int KW>
+__global__ __launch_bounds__(256) void DirectSmallConvKernel(ConvArgs p, DirectGeom dg) {
+    // The group's weights, [m][k] rows padded to kDirectK floats, in LDS:
+    // every lane reads the same address (a broadcast), 16 bytes at a time.
+    __shared__ __attribute__((aligned(16))) float ws[kDirectM * kDirectK];
+    const int g = blockIdx.y;
+    const int kg = static_cast<int>(p.kg);
+    const int mg = static_cast<int>(p.mg);
+    const float* wg = p.w + static_cast<int64_t>(g) * mg * kg;
+    for (int e = threadIdx.x; e < kDirectM * kDirectK; e += 256) {
+        const int m = e / kDirectK;
+        const int k = e - m * kDirectK;
+        ws[e] = m < mg && k < kg ? wg[m * kg + k] : 0.0f;
+    }
+    __syncthreads();
+    const uint32_t n = blockIdx.x * 256u + threadIdx.x;
+    if (n >= static_cast<uint32_t>(p.n_total)) {
+        return;
+    }
+    uint32_t pix, ox;
+    const uint32_t b = DivMod(dg.div_plane_out, n, pix);
+    const int oy = static_cast<int>(DivMod(dg.div_out_w, pix, ox));
+    const int iy0 = oy * p.s_h - p.p_h;
+    const int ix0 = static_cast<int>(ox) * p.s_w - p.p_w;
+    const int kh_n = KH > 0 ? KH : p.k_h;
+    const int kw_n = KW > 0 ? KW : p.k_w;
+    const int plane_in = static_cast<int>(p.plane_in);
+    // Element offset of the pixel's window origin in channel 0 of its group
+    // (negative when the window starts in the padding; only in-image taps
+    // are loaded).
+    const int base = (static_cast<int>(b) * static_cast<int>(p.c) + g * static_cast<int>(p.cg)) * plane_in +
+                     iy0 * p.in_w + ix0;
+    const __amdgpu_buffer_rsrc_t xr = MakeRsrc(p.x, static_cast<uint32_t>(p.batch * p.c * p.plane_in * 4));
+    float x[kDirectK];
+#pragma unroll
+    for (int k = 0; k < kDirectK; ++k) {
+        x[k] = 0.0f;
+        if (k < kg) {
+            const int c = k / (kh_n * kw_n);
+            const int r = k - c * (kh_n * kw_n);
+            const int kh = r / kw_n;
+            const int kw = r - kh * kw_n;
+            const int ih = iy0 + kh * p.d_h;
+            const int iw = ix0 + kw * p.d_w;
+            const bool in = static_cast<unsigned>(ih) < static_cast<unsigned>(p.in_h) &&
+                            static_cast<unsigned>(iw) < static_cast<unsigned>(p.in_w);
+            const int off = base + c * plane_in + kh * p.d_h * p.in_w + kw * p.d_w;
+            x[k] = BufferLoad(xr, in ? static_cast<uint32_t>(off) * 4u : kOutOfRange, 0);
+        }
+    }
+    // Output element offset of channel 0 of the group at this pixel; plus
+    // m * OH * OW for channel m.
+    const int plane_out = static_cast<int>(p.plane_out);
+    const int ybase = (static_cast<int>(b) * static_cast<int>(p.m) + g * mg) * plane_out + static_cast<int>(pix);
+    // Four output channels at a time: four independent multiply-add chains.
+    for (int m0 = 0; m0 < mg; m0 += 4) {
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k4 = 0; k4 < kDirectK; k4 += 4) {
+            if (k4 < kg) {
+                nert_floatx4 w4[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    w4[j] = *reinterpret_cast<const nert_floatx4*>(ws + (m0 + j) * kDirectK + k4);
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (k4 + e < kg) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            acc[j] = fmaf(x[k4 + e], w4[j][e], acc[j]);
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int m = m0 + j;
+            if (m < mg) {
+                const int yi = ybase + m * plane_out;
+                const float v = p.bias != nullptr ? acc[j] + p.bias[g * mg + m] : acc[j];
+                p.y[yi] = Finish(p, v, yi);
+            }
+        }
+    }
+}
+
+// 32-bit element offsets: input and output under 2^31 bytes.
+bool DirectSmallApplies(const ConvArgs& p) {
+    return p.k_d == 1 && p.in_d == 1 && p.out_d == 1 && p.kg <= kDirectK && p.mg <= kDirectM &&
+           p.batch * p.c * p.plane_in * 4 < (int64_t{1} << 31) && p.batch * p.m * p.plane_out * 4 < (int64_t{1} << 31) &&
+           p.group <= 65535;
+}
+
+void LaunchDirectSmall(const ConvArgs& p, hipStream_t stream) {
+    DirectGeom dg{};
+    dg.div_plane_out = FastDiv::Make(static_cast<uint32_t>(p.plane_out));
+    dg.div_out_w = FastDiv::Make(static_cast<uint32_t>(p.out_w));
+    const dim3 grid(static_cast<unsigned>((p.n_total + 255) / 256), static_cast<unsigned>(p.group));
+    if (p.k_h == 3 && p.k_w == 3) {
+        DirectSmallConvKernel<3, 3><<<grid, 256, 0, stream>>>(p, dg);
+    } else {
+        DirectSmallConvKernel<0, 0><<<grid, 256, 0, stream>>>(p, dg);
+    }
+    CheckLaunch("DirectSmallConvKernel launch");
+}
+
 // True when the patch kernel applies: 2-D, few channels per group, filter
 // rows of up to 8 taps, and a workgroup's weights and two input patches fit
 // in 160 KiB of LDS.
@@ -2157,6 +2287,36 @@ bool TryPatchConv(const ConvArgs& p, hipStream_t stream) {
         CheckLaunch("PatchConvKernel launch");
     }
     return launched;
+}
+
+// Small-channel convolutions: the patch (or stem) kernel, or, where the
+// filter and output-channel counts are tiny, the direct VALU kernel -- the
+// per-geometry choice between the two (timed like the other families;
+// NERT_HIP_CONV_CANDIDATE=300 + i forces candidate i).
+bool LaunchSmallCandidate(int i, const ConvArgs& p, hipStream_t stream) {
+    if (i == 1) {
+        if (!DirectSmallApplies(p)) {
+            return false;
+        }
+        LaunchDirectSmall(p, stream);
+        return true;
+    }
+    return TryPatchConv(p, stream);
+}
+
+bool TrySmallChannelConv(const ConvArgs& p, hipStream_t stream) {
+    if (!DirectSmallApplies(p) || p.cg > 4) {
+        return TryPatchConv(p, stream);
+    }
+    if (const char* forced = std::getenv("NERT_HIP_CONV_CANDIDATE")) {
+        const int i = std::atoi(forced) - 300;
+        if ((i == 0 || i == 1) && LaunchSmallCandidate(i, p, stream)) {
+            return true;
+        }
+    }
+    static std::map<ConvKey, int> chosen;
+    const int c = ChooseConvConfig("small", chosen, p, stream, 2, 0, LaunchSmallCandidate);
+    return LaunchSmallCandidate(c, p, stream) || LaunchSmallCandidate(1, p, stream);
 }
 
 // y = act(y + residual) in place: the fused pointwise convolution's
@@ -2276,7 +2436,7 @@ extern "C" int nert_hip_conv_fused_f32(const float* x, const float* w, const flo
         if (nert_hip::TryPointwise(p, s)) {
             return;
         }
-        if (nert_hip::TryPatchConv(p, s)) {
+        if (nert_hip::TrySmallChannelConv(p, s)) {
             return;
         }
         if (nert_hip::TryHaloConv(p, s)) {

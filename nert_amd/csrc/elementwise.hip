@@ -38,7 +38,7 @@ __device__ __forceinline__ float UnaryF32(int op, float x, const UnaryParams& p)
     case NERT_UN_RELU:
         return RefMax(0.0f, x);
     case NERT_UN_SIGMOID:
-        return 1.0f / (1.0f + expf(-x));
+        return SigmoidF32(x);
     case NERT_UN_TANH:
         return tanhf(x);
     case NERT_UN_EXP:

@@ -377,6 +377,31 @@ def test_small_channel_conv(gpu, xs, ws, attrs):
     assert_parity("Conv", [x, w], [(_conv_out(xs, ws, attrs), F)], attrs)  # no bias
 
 
+@pytest.mark.parametrize("xs,ws,attrs", [
+    ((2, 3, 70, 50), (16, 3, 3, 3), {"pads": [1, 1, 1, 1], "strides": [2, 2]}),     # detector stem, ragged
+    ((2, 4, 20, 20), (8, 2, 3, 3), {"pads": [1, 1, 1, 1], "group": 2}),             # groups
+    ((2, 2, 17, 19), (32, 2, 4, 4), {"pads": [1, 2, 2, 1], "strides": [1, 2]}),     # K = 32, M = 32
+    ((1, 1, 9, 9), (5, 1, 3, 3), {"pads": [2, 2, 2, 2], "dilations": [2, 2]}),      # dilated, C = 1
+])
+@pytest.mark.parametrize("cand", [300, 301])
+def test_small_channel_conv_candidates(gpu, tmp_path, xs, ws, attrs, cand):
+    """Both small-channel candidates -- the MFMA patch kernel (300) and the
+    direct VALU kernel for tiny filters and channel counts (301) -- forced:
+    Conv within tolerance of the restatement, the fused epilogue equal to
+    Conv + Add + Relu bit for bit."""
+    x, w, b = randn(xs, seed=60), randn(ws, seed=61, scale=0.2), randn((ws[0],), seed=62)
+    z = randn(_conv_out(xs, ws, attrs), seed=63)
+    paths = {k: str(tmp_path / f"{k}.npy") for k in ("x", "w", "b", "z", "out1", "out2")}
+    for k, v in (("x", x), ("w", w), ("b", b), ("z", z)):
+        np.save(paths[k], v)
+    _run_forced(cand, paths, attrs, tune=False)
+    conv = np.load(paths["out1"])
+    compare(conv, restate.conv(x, w, b, attrs.get("strides"), attrs.get("dilations"), attrs.get("pads"),
+                               attrs.get("group", 1), "NOTSET"), what=f"candidate {cand}")
+    want = conv + z
+    assert np.array_equal(np.load(paths["out2"]), np.where(want > 0, want, np.float32(0)).astype(F))
+
+
 def test_small_channel_conv_nonfinite_inputs(gpu):
     """A padded (zero-weight) tap must not turn an inf input into NaN."""
     x = randn((1, 3, 40, 40), seed=53)
