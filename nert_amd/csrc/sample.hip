@@ -137,6 +137,55 @@ __global__ void ResizeNearestKernel(const T* __restrict__ x, T* __restrict__ y, 
     }
 }
 
+// Nearest, four consecutive outputs of the last axis per thread (its output
+// length a multiple of 4, fewer than 2^31 outputs, y 16-byte aligned): the
+// index decode and the outer axes' table lookups once per four outputs, one
+// 16-byte store. The same gathers as ResizeNearestKernel.
+__global__ void ResizeNearestQuadKernel(const float* __restrict__ x, float* __restrict__ y, ResizeArgs a,
+                                        ResizeTables t, uint32_t quads) {
+    const int last = a.rank - 1;
+    for (uint32_t q = blockIdx.x * blockDim.x + threadIdx.x; q < quads; q += gridDim.x * blockDim.x) {
+        uint32_t c_last;
+        uint32_t rem32 = DivMod(a.div[last], 4 * q, c_last);
+        int64_t off = 0;
+        for (int d = last - 1; d >= 0; --d) {
+            uint32_t c;
+            rem32 = DivMod(a.div[d], rem32, c);
+            off += t.lower[t.base[d] + c] * a.in_strides[d];
+        }
+        const int64_t* row = t.lower + t.base[last] + c_last;
+        nert_floatx4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] = x[off + row[e]];
+        }
+        *reinterpret_cast<nert_floatx4*>(y + 4 * static_cast<int64_t>(q)) = v;
+    }
+}
+
+// The same for a resize of the last two axes only (every outer axis keeps
+// its length at scale 1, where each coordinate transform and nearest mode
+// maps o to o): an output row's source row once, the plane offset from the
+// flattened outer index, four column lookups per thread.
+__global__ void ResizeNearestRowsQuadKernel(const float* __restrict__ x, float* __restrict__ y, ResizeArgs a,
+                                            ResizeTables t, uint32_t quads, FastDiv div_row_quads, FastDiv div_out_h,
+                                            int64_t in_plane, int64_t in_w) {
+    const int hd = a.rank - 2;
+    for (uint32_t q = blockIdx.x * blockDim.x + threadIdx.x; q < quads; q += gridDim.x * blockDim.x) {
+        uint32_t cq, oy;
+        const uint32_t row = DivMod(div_row_quads, q, cq);
+        const uint32_t plane = DivMod(div_out_h, row, oy);
+        const float* src = x + plane * in_plane + t.lower[t.base[hd] + oy] * in_w;
+        const int64_t* cols = t.lower + t.base[hd + 1] + 4 * cq;
+        nert_floatx4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] = src[cols[e]];
+        }
+        *reinterpret_cast<nert_floatx4*>(y + 4 * static_cast<int64_t>(q)) = v;
+    }
+}
+
 // Linear: the taps of every interpolating axis, in the reference's order
 // (each interpolating axis doubles the list, lower before upper,
 // src/kernels/resize.cpp:102-122), weights from the tables.
@@ -396,6 +445,26 @@ int nert_hip_resize(int dtype, const void* x, void* y, int rank, const int64_t* 
         if (dtype == NERT_F32 && linear) {
             ResizeLinearKernel<float><<<grid, 256, 0, s>>>(static_cast<const float*>(x), static_cast<float*>(y), a,
                                                            t, n);
+        } else if (dtype == NERT_F32 && a.small && rank >= 2 && out_dims[rank - 1] % 4 == 0 &&
+                   reinterpret_cast<uintptr_t>(y) % 16 == 0 && [&] {
+                       for (int d = 0; d + 2 < rank; ++d) {
+                           if (in_dims[d] != out_dims[d] || scales[d] != 1.0) {
+                               return false;
+                           }
+                       }
+                       return true;
+                   }()) {
+            const auto quads = static_cast<uint32_t>(n / 4);
+            ResizeNearestRowsQuadKernel<<<GridFor(quads, 256, 16384), 256, 0, s>>>(
+                static_cast<const float*>(x), static_cast<float*>(y), a, t, quads,
+                FastDiv::Make(static_cast<uint32_t>(out_dims[rank - 1] / 4)),
+                FastDiv::Make(static_cast<uint32_t>(out_dims[rank - 2])), in_dims[rank - 2] * in_dims[rank - 1],
+                in_dims[rank - 1]);
+        } else if (dtype == NERT_F32 && a.small && out_dims[rank - 1] % 4 == 0 &&
+                   reinterpret_cast<uintptr_t>(y) % 16 == 0) {
+            const auto quads = static_cast<uint32_t>(n / 4);
+            ResizeNearestQuadKernel<<<GridFor(quads, 256, 16384), 256, 0, s>>>(static_cast<const float*>(x),
+                                                                               static_cast<float*>(y), a, t, quads);
         } else if (dtype == NERT_F32) {
             ResizeNearestKernel<float><<<grid, 256, 0, s>>>(static_cast<const float*>(x), static_cast<float*>(y), a,
                                                             t, n);

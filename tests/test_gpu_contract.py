@@ -39,6 +39,9 @@ def test_resize_nearest(gpu, transform, nearest):
         assert_parity("Resize", [x, NONE, np.array(scales, F)], [(out, F)], attrs, **EXACT)
     sizes = np.array([2, 3, 5, 13], I)
     assert_parity("Resize", [x, NONE, NONE, sizes], [(tuple(sizes), F)], attrs, **EXACT)
+    # last output axis a multiple of 4: the four-outputs-per-thread kernel
+    for sizes in ([2, 3, 5, 12], [2, 3, 11, 4], [1, 3, 7, 20]):
+        assert_parity("Resize", [x, NONE, NONE, np.array(sizes, I)], [(tuple(sizes), F)], attrs, **EXACT)
     xi = rng(2).integers(-100, 100, (2, 3, 4, 5)).astype(I)
     assert_parity("Resize", [xi, NONE, np.array([1, 1, 2.5, 1.5], F)], [((2, 3, 10, 7), I)], attrs, **EXACT)
 
