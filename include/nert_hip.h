@@ -360,7 +360,7 @@ int nert_hip_topk_f32(const float* x, float* values, int64_t* indices, int64_t o
  * the long-row select state and candidates live in a fixed 4 MiB device
  * array that the library holds on each GPU until the process ends (set up
  * by nert_hip_init, which must have run). Rows longer than 4096 need about
- * 16 * rows * k + 1 KiB * rows bytes of it; larger requests fail with an
+ * 16 * rows * k + 3 KiB * rows bytes of it; larger requests fail with an
  * error and launch nothing. Every call on one GPU shares that GPU's array,
  * so calls that overlap in time on one GPU (two streams, two threads) race:
  * serialise them. The array keeps the last call's contents; each call

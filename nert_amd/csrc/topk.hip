@@ -12,10 +12,11 @@
 // (the detector's [8, 672000], K = 300) run a radix select over the key,
 // 8 bits per pass from the top, with many workgroups per row: each pass builds
 // a 256-bin histogram of the keys that still match the chosen prefix (one LDS
-// histogram per wave, so the waves do not contend for the same bins), and a
-// one-block-per-row kernel scans it in parallel and picks the bin holding the
-// K-th largest key. When that bin is needed whole the threshold is final and
-// later passes return at once. Keys >= threshold (exactly K per row) are
+// histogram per wave, so the waves do not contend for the same bins), and
+// every workgroup of the next pass (or of the collection) scans the previous
+// pass's histogram itself and picks the bin holding the K-th largest key, so
+// a pass is one launch. When that bin is needed whole the threshold is final
+// and later passes return at once. Keys >= threshold (exactly K per row) are
 // collected and ordered -- by rank (the count of larger keys, spread over
 // several workgroups per row) when K <= 1024, else in 4096-key LDS runs
 // merged by per-key binary search -- and written out.
@@ -115,25 +116,102 @@ struct SelectState {
     int32_t count; // collected keys
 };
 
-__global__ void InitSelectKernel(SelectState* st, uint32_t* hist, int64_t rows, int64_t k) {
+// Select state and histograms of the passes, per row: the state a pass
+// selects with goes to st[pass & 1] (written by the row's first workgroup of
+// the next pass), and pass p counts into hist[p % 3] while hist[(p + 1) % 3]
+// is cleared for pass p + 1 (nobody reads it during pass p).
+struct SelectBuffers {
+    SelectState* st[2];
+    uint32_t* hist[3];
+};
+
+__global__ void InitSelectKernel(SelectBuffers b, int64_t rows, int64_t k) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < rows * 256; i += stride) {
-        hist[i] = 0;
+        b.hist[0][i] = 0;
+        b.hist[1][i] = 0;
+        b.hist[2][i] = 0;
         if (i < rows) {
-            st[i].prefix = 0;
-            st[i].remaining = k;
-            st[i].done = 0;
-            st[i].count = 0;
+            b.st[0][i].prefix = 0;
+            b.st[0][i].remaining = k;
+            b.st[0][i].done = 0;
+            b.st[0][i].count = 0;
         }
     }
 }
 
+// The state after a pass: its histogram (256 digits) scanned from the top
+// digit down, the chosen digit the one whose inclusive count first reaches
+// `remaining`; when that digit's keys are all needed the threshold is final
+// (done). Run by all 256 threads of a workgroup (one digit each: in-wave
+// shuffles, then the four wave totals); every workgroup of the row gets the
+// same state from the same counts. The result is in `out` (LDS) after the
+// final barrier.
+__device__ void NextState(const SelectState& s, const uint32_t* rh, int pass, SelectState* out) {
+    __shared__ uint32_t totals[kThreads / 64];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const uint32_t count = rh[255 - t];
+    uint32_t incl = count;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(incl, off, 64);
+        if (lane >= off) {
+            incl += y;
+        }
+    }
+    if (lane == 63) {
+        totals[wave] = incl;
+    }
+    if (t == 0) {
+        *out = s;
+    }
+    __syncthreads();
+    for (int w = 0; w < wave; ++w) {
+        incl += totals[w];
+    }
+    const int64_t excl = static_cast<int64_t>(incl) - count;
+    if (!s.done && excl < s.remaining && static_cast<int64_t>(incl) >= s.remaining) {
+        SelectState ns = s;
+        ns.prefix |= static_cast<uint64_t>(255 - t) << (56 - 8 * pass);
+        ns.remaining = s.remaining - excl;
+        if (static_cast<int64_t>(count) == ns.remaining) {
+            ns.done = 1;
+        }
+        *out = ns;
+    }
+    __syncthreads();
+}
+
+// Pass `pass` over a chunk of a row: first the state to select with (pass
+// 0: the initial one; later passes: the previous pass's state advanced by
+// its histogram, NextState), then a 256-bin histogram of the keys that still
+// match the chosen prefix (one LDS histogram per wave, so the waves do not
+// contend for the same bins), added to the row's histogram for this pass.
+// The row's first workgroup also records the state and clears the next
+// pass's histogram. Once the threshold is final the pass returns at once.
 __global__ void __launch_bounds__(kThreads) HistKernel(const float* __restrict__ x, RowGeom g, int64_t chunk,
-                                                       int chunks, const SelectState* __restrict__ st,
-                                                       uint32_t* __restrict__ hist, int pass) {
+                                                       int chunks, SelectBuffers sb, int pass) {
     const int64_t row = blockIdx.x / chunks;
     const int c = blockIdx.x - static_cast<int>(row * chunks);
-    const SelectState s = st[row];
+    __shared__ SelectState cur;
+    if (pass == 0) {
+        if (threadIdx.x == 0) {
+            cur = sb.st[0][row];
+        }
+        __syncthreads();
+    } else {
+        const SelectState prev = sb.st[(pass - 1) & 1][row];
+        NextState(prev, sb.hist[(pass - 1) % 3] + row * 256, pass - 1, &cur);
+        if (c == 0) {
+            if (threadIdx.x == 0) {
+                sb.st[pass & 1][row] = cur;
+            }
+            sb.hist[(pass + 1) % 3][row * 256 + threadIdx.x] = 0;
+        }
+    }
+    const SelectState s = cur;
     if (s.done) {
         return;
     }
@@ -164,50 +242,22 @@ __global__ void __launch_bounds__(kThreads) HistKernel(const float* __restrict__
         v += h[w][threadIdx.x];
     }
     if (v != 0) {
-        atomicAdd(&hist[row * 256 + threadIdx.x], v);
+        atomicAdd(&sb.hist[pass % 3][row * 256 + threadIdx.x], v);
     }
 }
 
-// One 256-thread block per row: scan[j] = count of digit 255 - j, an
-// inclusive prefix sum, and the chosen digit is the one whose sum first
-// reaches `remaining`. Clears the row's histogram for the next pass.
-__global__ void __launch_bounds__(256) ScanKernel(SelectState* st, uint32_t* hist, int pass) {
-    const int64_t row = blockIdx.x;
-    const SelectState s = st[row];
-    if (s.done) {
-        return;
-    }
-    __shared__ uint32_t scan[256];
-    const int t = threadIdx.x;
-    uint32_t* rh = hist + row * 256;
-    const uint32_t count = rh[255 - t];
-    rh[255 - t] = 0;
-    scan[t] = count;
-    __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {
-        const uint32_t add = t >= off ? scan[t - off] : 0u;
-        __syncthreads();
-        scan[t] += add;
-        __syncthreads();
-    }
-    const int64_t incl = scan[t];
-    const int64_t excl = incl - count;
-    if (excl < s.remaining && incl >= s.remaining) {
-        SelectState ns = s;
-        ns.prefix |= static_cast<uint64_t>(255 - t) << (56 - 8 * pass);
-        ns.remaining = s.remaining - excl;
-        if (static_cast<int64_t>(count) == ns.remaining) {
-            ns.done = 1;
-        }
-        st[row] = ns;
-    }
-}
-
+// Keys >= the final threshold (the state after the last pass, advanced by
+// that pass's histogram here in every workgroup): exactly K per row.
 __global__ void __launch_bounds__(kThreads) CollectKernel(const float* __restrict__ x, RowGeom g, int64_t chunk,
-                                                          int chunks, SelectState* st, uint64_t* __restrict__ cand) {
+                                                          int chunks, SelectBuffers sb, int last_pass,
+                                                          uint64_t* __restrict__ cand) {
     const int64_t row = blockIdx.x / chunks;
     const int c = blockIdx.x - static_cast<int>(row * chunks);
-    const uint64_t threshold = st[row].prefix;
+    __shared__ SelectState fin;
+    NextState(sb.st[last_pass & 1][row], sb.hist[last_pass % 3] + row * 256, last_pass, &fin);
+    const uint64_t threshold = fin.prefix;
+    // The collected-key counter: st[0]'s count, zero since initialisation.
+    int32_t* count = &sb.st[0][row].count;
     const int64_t begin = c * chunk;
     int64_t end = begin + chunk;
     if (end > g.dim) {
@@ -217,7 +267,7 @@ __global__ void __launch_bounds__(kThreads) CollectKernel(const float* __restric
     for (int64_t i = begin + threadIdx.x; i < end; i += blockDim.x) {
         const uint64_t key = KeyOf(x[base + i * g.inner], i);
         if (key >= threshold) {
-            const int pos = atomicAdd(&st[row].count, 1);
+            const int pos = atomicAdd(count, 1);
             if (pos < g.k) {
                 cand[row * g.k + pos] = key;
             }
@@ -350,8 +400,8 @@ struct TopkLayout {
 
 TopkLayout LayoutFor(int64_t rows, int64_t k) {
     TopkLayout l{};
-    l.st_bytes = (rows * static_cast<int64_t>(sizeof(SelectState)) + 255) / 256 * 256;
-    l.hist_bytes = (rows * 256 * 4 + 255) / 256 * 256;
+    l.st_bytes = 2 * ((rows * static_cast<int64_t>(sizeof(SelectState)) + 255) / 256 * 256);
+    l.hist_bytes = 3 * ((rows * 256 * 4 + 255) / 256 * 256);
     l.cand_bytes = (rows * k * 8 + 255) / 256 * 256;
     return l;
 }
@@ -402,18 +452,22 @@ void TopkImpl(const float* x, float* values, int64_t* indices, int64_t outer, in
                     std::to_string(lay.total()) + " bytes of scratch; the fixed scratch holds " +
                     std::to_string(fixed_bytes));
     }
-    auto* st = reinterpret_cast<SelectState*>(ws);
-    auto* hist = reinterpret_cast<uint32_t*>(ws + st_bytes);
+    SelectBuffers sb{};
+    sb.st[0] = reinterpret_cast<SelectState*>(ws);
+    sb.st[1] = reinterpret_cast<SelectState*>(ws + st_bytes / 2);
+    for (int i = 0; i < 3; ++i) {
+        sb.hist[i] = reinterpret_cast<uint32_t*>(ws + st_bytes + i * (hist_bytes / 3));
+    }
     auto* cand = reinterpret_cast<uint64_t*>(ws + st_bytes + hist_bytes);
     auto* cand2 = reinterpret_cast<uint64_t*>(ws + st_bytes + hist_bytes + cand_bytes);
 
-    InitSelectKernel<<<GridFor(rows * 256, 256, 4096), 256, 0, s>>>(st, hist, rows, k);
+    InitSelectKernel<<<GridFor(rows * 256, 256, 4096), 256, 0, s>>>(sb, rows, k);
     const unsigned blocks = static_cast<unsigned>(rows * chunks);
-    for (int pass = 0; pass < 8; ++pass) {
-        HistKernel<<<blocks, kThreads, 0, s>>>(x, g, chunk, static_cast<int>(chunks), st, hist, pass);
-        ScanKernel<<<static_cast<unsigned>(rows), 256, 0, s>>>(st, hist, pass);
+    constexpr int kPasses = 8;
+    for (int pass = 0; pass < kPasses; ++pass) {
+        HistKernel<<<blocks, kThreads, 0, s>>>(x, g, chunk, static_cast<int>(chunks), sb, pass);
     }
-    CollectKernel<<<blocks, kThreads, 0, s>>>(x, g, chunk, static_cast<int>(chunks), st, cand);
+    CollectKernel<<<blocks, kThreads, 0, s>>>(x, g, chunk, static_cast<int>(chunks), sb, kPasses - 1, cand);
     if (k <= kRankMax) {
         const int parts = static_cast<int>((k + 63) / 64);
         RankSortKernel<<<static_cast<unsigned>(rows * parts), 256, 0, s>>>(cand, cand2, k, parts);

@@ -63,7 +63,7 @@ def test_noalloc_topk_small_rows(gpu):
 
 
 def test_noalloc_topk_rejects_oversized_request(gpu):
-    # 4096 rows of 8192 with k = 2048: 4096 * (16 * 2048 + 1024) bytes > 4 MiB.
+    # 4096 rows of 8192 with k = 2048: 4096 * (16 * 2048 + 3072) bytes > 4 MiB.
     x = np.zeros((4096, 8192), np.float32)
     _, _, err = _topk("nert_hip_topk_f32_noalloc", x, 2048)
     assert err is not None and "scratch" in err
