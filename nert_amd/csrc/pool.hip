@@ -201,6 +201,92 @@ bool TryMaxPoolTile(const PoolArgs& p, hipStream_t s) {
     return true;
 }
 
+// ---- 3x3 / stride 2 / pad 1 max pooling straight from registers -------------
+//
+// The ResNet stem pool. A lane owns one 16-byte column quad (input columns
+// 4k .. 4k+3, output columns 2k and 2k+1) of R consecutive output rows of one
+// plane: it loads its 2R+1 input rows' quads at once (all loads in flight
+// together, each input byte read once but for one shared row per R), takes
+// column 4k-1 from the lane to its left, reduces each input row to the two
+// outputs' 3-wide row maxima, then each output to the maximum of three row
+// maxima, and stores the two outputs as one 8-byte store. A wave holds
+// 64 / (W/4) planes' row runs side by side. Max semantics are those of the
+// tap loop above (start at -inf, take a tap only if it is strictly greater,
+// taps in row-major order, out-of-range taps skipped): the first maximal
+// tap in row-major order wins, which the row-then-column reduction keeps,
+// so the result is bit-identical, signed zeros and NaNs included.
+template <int R>
+__global__ __launch_bounds__(256) void MaxPool3x3S2Kernel(PoolArgs p, int32_t quads_row, int32_t groups_per_wave,
+                                                          int32_t chunks, int64_t groups) {
+    const float ninf = -__builtin_huge_valf();
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
+    const int gl = lane / quads_row;
+    const int k = lane - gl * quads_row;
+    const int64_t group = wave * groups_per_wave + gl;
+    const bool active = gl < groups_per_wave && group < groups;
+    const int64_t plane = active ? group / chunks : 0;
+    const int oh0 = static_cast<int>(group - plane * chunks) * R;
+    const float* xp = p.x + plane * p.in_h * p.in_w + 4 * k;
+    nert_floatx4 v[2 * R + 1];
+#pragma unroll
+    for (int j = 0; j < 2 * R + 1; ++j) {
+        const int ih = 2 * oh0 - 1 + j;
+        const bool in = active && static_cast<unsigned>(ih) < static_cast<unsigned>(p.in_h);
+        v[j] = in ? *reinterpret_cast<const nert_floatx4*>(xp + static_cast<int64_t>(ih) * p.in_w)
+                  : nert_floatx4{ninf, ninf, ninf, ninf};
+    }
+    auto max3 = [&](float a, float b, float c) {
+        float m = ninf;
+        m = a > m ? a : m;
+        m = b > m ? b : m;
+        m = c > m ? c : m;
+        return m;
+    };
+    float h0[2 * R + 1];
+    float h1[2 * R + 1];
+#pragma unroll
+    for (int j = 0; j < 2 * R + 1; ++j) {
+        const float up = __shfl_up(v[j][3], 1);
+        const float left = k == 0 ? ninf : up;
+        h0[j] = max3(left, v[j][0], v[j][1]);
+        h1[j] = max3(v[j][1], v[j][2], v[j][3]);
+    }
+    if (!active) {
+        return;
+    }
+    float* yp = p.y + plane * p.out_h * p.out_w + 2 * k;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int oh = oh0 + r;
+        if (oh < p.out_h) {
+            *reinterpret_cast<nert_floatx2*>(yp + static_cast<int64_t>(oh) * p.out_w) =
+                nert_floatx2{max3(h0[2 * r], h0[2 * r + 1], h0[2 * r + 2]), max3(h1[2 * r], h1[2 * r + 1], h1[2 * r + 2])};
+        }
+    }
+}
+
+bool TryMaxPool3x3S2(const PoolArgs& p, hipStream_t s) {
+    constexpr int kRows = 8;
+    if (p.k_h != 3 || p.k_w != 3 || p.s_h != 2 || p.s_w != 2 || p.d_h != 1 || p.d_w != 1 || p.p_h != 1 ||
+        p.p_w != 1 || p.in_w % 4 != 0 || p.in_w > 256 || p.out_w * 2 != p.in_w || p.out_h < 1 ||
+        (reinterpret_cast<uintptr_t>(p.x) & 15) != 0 || (reinterpret_cast<uintptr_t>(p.y) & 7) != 0) {
+        return false;
+    }
+    const int32_t quads_row = p.in_w / 4;
+    const int32_t groups_per_wave = 64 / quads_row;
+    const int32_t chunks = (p.out_h + kRows - 1) / kRows;
+    const int64_t groups = p.planes * chunks;
+    const int64_t waves = (groups + groups_per_wave - 1) / groups_per_wave;
+    const int64_t blocks = (waves + 3) / 4;
+    if (blocks > 0x7FFFFFFF) {
+        return false;
+    }
+    MaxPool3x3S2Kernel<kRows><<<static_cast<unsigned>(blocks), 256, 0, s>>>(p, quads_row, groups_per_wave, chunks,
+                                                                            groups);
+    return true;
+}
+
 // AveragePool, exactly as src/kernels/average_pool.cpp:196-223: a float sum
 // over the window clipped to the input, in row-major tap order, divided once
 // by either the clipped tap count or (count_include_pad) the window clipped to
@@ -347,7 +433,7 @@ int nert_hip_maxpool2d_f32(const float* x, float* y, const nert_pool_desc* d, vo
         if (total <= 0) {
             return;
         }
-        if (TryMaxPoolTile(p, StreamOr(stream))) {
+        if (TryMaxPool3x3S2(p, StreamOr(stream)) || TryMaxPoolTile(p, StreamOr(stream))) {
             // done
         } else if (total < (int64_t{1} << 31)) {
             MaxPool2dKernel<true><<<GridFor(total, 256, 16384), 256, 0, StreamOr(stream)>>>(p);

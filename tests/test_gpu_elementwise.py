@@ -4,7 +4,7 @@ and copy rows against the reference CpuDevice rows."""
 import numpy as np
 import pytest
 
-from rowcheck import assert_parity, assert_same_error, randn, rng
+from rowcheck import assert_parity, assert_same_error, randn, rng, run_hip, run_ref
 
 pytestmark = pytest.mark.gpu
 
@@ -232,6 +232,27 @@ def test_maxpool_nan_and_neg_inf(gpu):
     x = np.full((1, 1, 4, 4), np.nan, F)
     x[0, 0, 0, 0] = -np.inf
     assert_parity("MaxPool", [x], [((1, 1, 2, 2), F)], {"kernel_shape": [2, 2], "strides": [2, 2]})
+
+
+@pytest.mark.parametrize("xs", [(32, 64, 112, 112), (3, 5, 7, 8), (2, 3, 20, 256), (1, 7, 33, 4), (2, 2, 1, 12)])
+def test_maxpool_3x3_stride2_kernel(gpu, xs):
+    """The 3x3 / stride-2 / pad-1 pool (the ResNet stem pool; one lane per
+    column quad, rows reduced in registers), over whole and partial row runs,
+    one to 64 planes per wave, and a bottom padding row: bit-identical to the
+    reference, with signed zeros, NaNs and -inf sprinkled in."""
+    x = randn(xs, seed=31)
+    flat = x.reshape(-1)
+    pick = rng(32).random(flat.size)
+    flat[pick < 0.05] = 0.0
+    flat[(pick >= 0.05) & (pick < 0.1)] = -0.0
+    flat[(pick >= 0.1) & (pick < 0.12)] = np.nan
+    flat[(pick >= 0.12) & (pick < 0.13)] = -np.inf
+    attrs = {"kernel_shape": [3, 3], "strides": [2, 2], "pads": [1, 1, 1, 1]}
+    spec = [(_pool_out(xs, attrs), F)]
+    want, ref_err = run_ref("MaxPool", [x], spec, attrs)
+    got, hip_err = run_hip("MaxPool", [x], spec, attrs)
+    assert ref_err is None and hip_err is None, (ref_err, hip_err)
+    assert np.array_equal(got[0].view(np.uint32), want[0].view(np.uint32))
 
 
 @pytest.mark.parametrize("xs", [(32, 512, 7, 7), (8, 64, 112, 112), (2, 3, 5), (1, 4, 2, 3, 4), (3, 5),
