@@ -1828,9 +1828,25 @@ struct StemGeom {
     int32_t tiles_w, tiles_h;
     int32_t patch_floats;  // C_g * ph * pitch
     int32_t blocks;        // batch * tiles_h * tiles_w
+    int32_t whole;         // blocks taken whole; the rest as two halves each
+    int32_t units;         // whole + 2 * (blocks - whole)
     FastDiv div_plane;     // by ph * pitch
     FastDiv div_pitch;     // by pitch
 };
+
+// Work units: blocks below sg.whole are taken whole; each later block is two
+// units, its output rows 0-7 and 8-15, computed by the waves that own those
+// rows (the others skip it). The host sets whole to the blocks of the full
+// rounds of workgroups when the rest, halved, fits one round, so the last
+// partial round costs about half a block instead of a whole one.
+__device__ __forceinline__ int StemUnitBlock(const StemGeom& sg, int u, int& half) {
+    if (u < sg.whole) {
+        half = -1;
+        return u;
+    }
+    half = (u - sg.whole) & 1;
+    return sg.whole + ((u - sg.whole) >> 1);
+}
 
 __global__ __launch_bounds__(512, 4) void StemQuadKernel(ConvArgs p, StemGeom sg) {
     // Dynamic LDS: weights [kPatchM][wpitch], bias [kPatchM], two patches.
@@ -1915,11 +1931,13 @@ __global__ __launch_bounds__(512, 4) void StemQuadKernel(ConvArgs p, StemGeom sg
 
     float bias_r[16];
     bool bias_read = false;
-    int blk = blockIdx.x;
-    if (blk < sg.blocks) {
-        load_patch(blk, patches);
+    int unit = blockIdx.x;
+    int row_half = -1;
+    if (unit < sg.units) {
+        load_patch(StemUnitBlock(sg, unit, row_half), patches);
     }
-    for (int buf = 0; blk < sg.blocks; blk += gridDim.x, buf ^= 1) {
+    for (int buf = 0; unit < sg.units; unit += gridDim.x, buf ^= 1) {
+        const int blk = StemUnitBlock(sg, unit, row_half);
         float* const patch = patches + buf * sg.patch_floats;
         // This wave's copies of the current patch are complete; after the
         // barrier everyone's are, and nobody still reads the other buffer.
@@ -1948,9 +1966,16 @@ __global__ __launch_bounds__(512, 4) void StemQuadKernel(ConvArgs p, StemGeom sg
             }
             bias_read = true;
         }
-        const int next = blk + static_cast<int>(gridDim.x);
-        if (next < sg.blocks) {
-            load_patch(next, patches + (buf ^ 1) * sg.patch_floats);
+        const int next = unit + static_cast<int>(gridDim.x);
+        if (next < sg.units) {
+            int next_half;
+            load_patch(StemUnitBlock(sg, next, next_half), patches + (buf ^ 1) * sg.patch_floats);
+        }
+        // A half unit: only the waves owning its eight output rows work. Half
+        // units come only in a workgroup's last round, so the skipped waves'
+        // missing stores never meet the store-count wait above.
+        if (row_half >= 0 && (wave_n >> 1) != row_half) {
+            continue;
         }
         nert_floatx16 acc[2];
 #pragma unroll
@@ -2076,6 +2101,11 @@ bool TryStemQuad(const ConvArgs& p, hipStream_t stream) {
         return false;
     }
     sg.blocks = static_cast<int32_t>(blocks);
+    const int64_t per_slot = std::max<int64_t>(1, kResidentBlocks / (m_blocks * p.group));
+    const int64_t slots = std::min(blocks, per_slot);
+    const int64_t rest = blocks % slots;
+    sg.whole = static_cast<int32_t>(rest > 0 && 2 * rest <= slots ? blocks - rest : blocks);
+    sg.units = static_cast<int32_t>(sg.whole + 2 * (blocks - sg.whole));
     sg.div_plane = FastDiv::Make(static_cast<uint32_t>(sg.ph * sg.pitch));
     sg.div_pitch = FastDiv::Make(static_cast<uint32_t>(sg.pitch));
     static const bool allowed = hipFuncSetAttribute(reinterpret_cast<const void*>(&StemQuadKernel),
@@ -2087,9 +2117,7 @@ bool TryStemQuad(const ConvArgs& p, hipStream_t stream) {
             return false;
         }
     }
-    const int64_t per_slot = std::max<int64_t>(1, kResidentBlocks / (m_blocks * p.group));
-    const dim3 grid(static_cast<unsigned>(std::min(blocks, per_slot)), static_cast<unsigned>(m_blocks),
-                    static_cast<unsigned>(p.group));
+    const dim3 grid(static_cast<unsigned>(slots), static_cast<unsigned>(m_blocks), static_cast<unsigned>(p.group));
     StemQuadKernel<<<grid, 512, lds_bytes, stream>>>(p, sg);
     CheckLaunch("StemQuadKernel launch");
     return true;
