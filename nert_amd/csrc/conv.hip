@@ -1820,6 +1820,18 @@ bool LaunchPatch(const ConvArgs& p, const PatchGeom& pg, dim3 grid, size_t lds, 
 // input values are replaced by zero in registers (a 0 * inf would be NaN).
 constexpr int kStemTaps = 8;
 
+// Seven-tap filter rows (P7): padding each row to eight taps wastes one MFMA
+// step in eight. Instead filter rows r0 = 2q and r1 = 2q + 1 take seven
+// steps: r0's taps (0 | 4), (1 | 5), (2 | 6) (lanes 0-31 | lanes 32-63),
+// then (r0 tap 3 | r1 tap 3), then r1's three pairs; an odd last row takes
+// its three pairs and (tap 3 | zero). The weights are stored in that step
+// order, [pair][lane half][8 steps] per output channel, so a lane reads a
+// pair's steps as two 16-byte loads; the inputs come as an 8-byte read
+// (taps 0, 1 | 4, 5) and a 4-byte read (tap 2 | 6) per row and pixel column,
+// and one 4-byte read (tap 3 of r0 | of r1) per pair: 74 MFMA steps per
+// pixel column for the 3-channel 7x7 stem instead of 84.
+constexpr int kStemPairFloats = 16;
+
 struct StemGeom {
     int32_t rows;          // C_g * KH filter rows
     int32_t wpitch;        // LDS weight row pitch (rows * 8 + 4 floats)
@@ -1848,6 +1860,7 @@ __device__ __forceinline__ int StemUnitBlock(const StemGeom& sg, int u, int& hal
     return sg.whole + ((u - sg.whole) >> 1);
 }
 
+template <bool P7>
 __global__ __launch_bounds__(512, 4) void StemQuadKernel(ConvArgs p, StemGeom sg) {
     // Dynamic LDS: weights [kPatchM][wpitch], bias [kPatchM], two patches.
     extern __shared__ __attribute__((aligned(16))) float smem[];
@@ -1863,14 +1876,37 @@ __global__ __launch_bounds__(512, 4) void StemQuadKernel(ConvArgs p, StemGeom sg
     const int kh_n = p.k_h, kw_n = p.k_w;
     const int knat = cg * kh_n * kw_n;
 
-    // Weights, rows padded to 8 taps with zeros (zero rows past M_g).
+    // Weights, rows padded to 8 taps with zeros (zero rows past M_g), or in
+    // the seven-tap pair order.
     const float* wg = p.w + (static_cast<int64_t>(g) * p.mg + m0) * knat;
+    const int pairs = (sg.rows + 1) / 2;
     for (int m = wave; m < kPatchM; m += 8) {
         const bool ok = m0 + m < p.mg;
-        for (int k = lane; k < sg.rows * kStemTaps; k += 64) {
-            const int row = k >> 3;
-            const int t = k & 7;
-            ws[m * sg.wpitch + k] = ok && t < kw_n ? wg[static_cast<int64_t>(m) * knat + row * kw_n + t] : 0.0f;
+        if constexpr (P7) {
+            for (int k = lane; k < pairs * kStemPairFloats; k += 64) {
+                const int q = k >> 4;
+                const int hf = (k >> 3) & 1;
+                const int st = k & 7;
+                int row = 2 * q;
+                int t = -1;
+                if (st < 3) {
+                    t = st + 4 * hf;
+                } else if (st == 3) {
+                    row += hf;
+                    t = 3;
+                } else if (st < 7) {
+                    row += 1;
+                    t = st - 4 + 4 * hf;
+                }
+                ws[m * sg.wpitch + k] =
+                    ok && t >= 0 && row < sg.rows ? wg[static_cast<int64_t>(m) * knat + row * 7 + t] : 0.0f;
+            }
+        } else {
+            for (int k = lane; k < sg.rows * kStemTaps; k += 64) {
+                const int row = k >> 3;
+                const int t = k & 7;
+                ws[m * sg.wpitch + k] = ok && t < kw_n ? wg[static_cast<int64_t>(m) * knat + row * kw_n + t] : 0.0f;
+            }
         }
     }
     if (tid < kPatchM) {
@@ -1985,27 +2021,77 @@ __global__ __launch_bounds__(512, 4) void StemQuadKernel(ConvArgs p, StemGeom sg
                 acc[j][v] = 0.0f;
             }
         }
-        for (int c = 0; c < cg; ++c) {
-            const float* prow = patch + c * plane_patch;
-            const float* wr = wrow + c * kh_n * kStemTaps;
-            for (int kh = 0; kh < kh_n; ++kh) {
-                const nert_floatx4 a = *reinterpret_cast<const nert_floatx4*>(wr + kh * kStemTaps);
-                float bq[2][4];
+        if constexpr (P7) {
+            // Patch offset of filter row r (channel r / KH, row r % KH).
+            auto row_off = [&](int r) { return (r / kh_n) * plane_patch + (r % kh_n) * row_step; };
+            const float* wp = ws + (wave_m * 32 + col) * sg.wpitch + 8 * half;
+            for (int q = 0; q < pairs; ++q) {
+                const int r0 = 2 * q;
+                const bool two = r0 + 1 < sg.rows;
+                const int o0 = row_off(r0);
+                const int o1 = two ? row_off(r0 + 1) : o0;
+                const nert_floatx4 alo = *reinterpret_cast<const nert_floatx4*>(wp + q * kStemPairFloats);
+                const nert_floatx4 ahi = *reinterpret_cast<const nert_floatx4*>(wp + q * kStemPairFloats + 4);
+                float b[2][7];
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const float* src = prow + kh * row_step + boff[j];
-                    const nert_floatx2 lo = *reinterpret_cast<const nert_floatx2*>(src);
-                    const nert_floatx2 hi = *reinterpret_cast<const nert_floatx2*>(src + 2);
-                    bq[j][0] = zero_tap[0] ? 0.0f : lo[0];
-                    bq[j][1] = zero_tap[1] ? 0.0f : lo[1];
-                    bq[j][2] = zero_tap[2] ? 0.0f : hi[0];
-                    bq[j][3] = zero_tap[3] ? 0.0f : hi[1];
+                    const float* s0 = patch + o0 + boff[j];
+                    const float* s1 = patch + o1 + boff[j];
+                    const nert_floatx2 x01 = *reinterpret_cast<const nert_floatx2*>(s0);
+                    const float x2 = s0[2];
+                    // Tap 3 (column 2 ox + 3): row r0 in lanes 0-31, r1 in
+                    // lanes 32-63 (whose boff is 4 columns further on).
+                    const float x3 = patch[(half != 0 ? o1 : o0) + boff[j] - 4 * half + 3];
+                    const nert_floatx2 y01 = *reinterpret_cast<const nert_floatx2*>(s1);
+                    const float y2 = s1[2];
+                    b[j][0] = x01[0];
+                    b[j][1] = x01[1];
+                    b[j][2] = x2;
+                    b[j][3] = two || half == 0 ? x3 : 0.0f;
+                    b[j][4] = y01[0];
+                    b[j][5] = y01[1];
+                    b[j][6] = y2;
                 }
 #pragma unroll
-                for (int kk = 0; kk < 4; ++kk) {
+                for (int st = 0; st < 4; ++st) {
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
-                        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk], bq[j][kk], acc[j], 0, 0, 0);
+                        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(alo[st], b[j][st], acc[j], 0, 0, 0);
+                    }
+                }
+                if (two) {
+#pragma unroll
+                    for (int st = 0; st < 3; ++st) {
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) {
+                            acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(ahi[st], b[j][4 + st], acc[j], 0, 0, 0);
+                        }
+                    }
+                }
+            }
+        } else {
+            for (int c = 0; c < cg; ++c) {
+                const float* prow = patch + c * plane_patch;
+                const float* wr = wrow + c * kh_n * kStemTaps;
+                for (int kh = 0; kh < kh_n; ++kh) {
+                    const nert_floatx4 a = *reinterpret_cast<const nert_floatx4*>(wr + kh * kStemTaps);
+                    float bq[2][4];
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const float* src = prow + kh * row_step + boff[j];
+                        const nert_floatx2 lo = *reinterpret_cast<const nert_floatx2*>(src);
+                        const nert_floatx2 hi = *reinterpret_cast<const nert_floatx2*>(src + 2);
+                        bq[j][0] = zero_tap[0] ? 0.0f : lo[0];
+                        bq[j][1] = zero_tap[1] ? 0.0f : lo[1];
+                        bq[j][2] = zero_tap[2] ? 0.0f : hi[0];
+                        bq[j][3] = zero_tap[3] ? 0.0f : hi[1];
+                    }
+#pragma unroll
+                    for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) {
+                            acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk], bq[j][kk], acc[j], 0, 0, 0);
+                        }
                     }
                 }
             }
@@ -2080,8 +2166,9 @@ bool TryStemQuad(const ConvArgs& p, hipStream_t stream) {
         return false;
     }
     StemGeom sg{};
+    const bool p7 = p.k_w == 7;
     sg.rows = static_cast<int32_t>(p.cg) * p.k_h;
-    sg.wpitch = sg.rows * kStemTaps + 4;
+    sg.wpitch = p7 ? (sg.rows + 1) / 2 * kStemPairFloats + 4 : sg.rows * kStemTaps + 4;
     sg.ph = (kPatchTile - 1) * p.s_h + (p.k_h - 1) * p.d_h + 1;
     sg.pw = (kPatchTile - 1) * 2 + kStemTaps;
     sg.pitch = (sg.pw + 3) / 4 * 4;
@@ -2108,17 +2195,21 @@ bool TryStemQuad(const ConvArgs& p, hipStream_t stream) {
     sg.units = static_cast<int32_t>(sg.whole + 2 * (blocks - sg.whole));
     sg.div_plane = FastDiv::Make(static_cast<uint32_t>(sg.ph * sg.pitch));
     sg.div_pitch = FastDiv::Make(static_cast<uint32_t>(sg.pitch));
-    static const bool allowed = hipFuncSetAttribute(reinterpret_cast<const void*>(&StemQuadKernel),
-                                                    hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                    160 * 1024) == hipSuccess;
-    if (!allowed) {
+    auto* kernel = p7 ? &StemQuadKernel<true> : &StemQuadKernel<false>;
+    static const bool allowed7 = hipFuncSetAttribute(reinterpret_cast<const void*>(&StemQuadKernel<true>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     160 * 1024) == hipSuccess;
+    static const bool allowed8 = hipFuncSetAttribute(reinterpret_cast<const void*>(&StemQuadKernel<false>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     160 * 1024) == hipSuccess;
+    if (!(p7 ? allowed7 : allowed8)) {
         (void)hipGetLastError();
         if (lds_bytes > 64 * 1024) {
             return false;
         }
     }
     const dim3 grid(static_cast<unsigned>(slots), static_cast<unsigned>(m_blocks), static_cast<unsigned>(p.group));
-    StemQuadKernel<<<grid, 512, lds_bytes, stream>>>(p, sg);
+    kernel<<<grid, 512, lds_bytes, stream>>>(p, sg);
     CheckLaunch("StemQuadKernel launch");
     return true;
 }

@@ -370,6 +370,10 @@ def _restate_args(attrs):
     ((1, 2, 30, 30), (64, 2, 7, 7), {"pads": [2, 3, 1, 3], "dilations": [1, 2]}),   # 7x7, C=2, dilated
     ((2, 3, 40, 40), (24, 3, 3, 5), {"pads": [2, 2, 2, 2], "strides": [1, 2], "dilations": [2, 1]}),  # 5 taps
     ((1, 4, 36, 36), (32, 4, 4, 8), {"pads": [1, 3, 2, 4], "strides": [2, 2]}),     # 8 taps, C=4
+    # 7 taps: filter rows taken in pairs (an even count, an odd count, dilated rows)
+    ((2, 2, 40, 40), (32, 2, 7, 7), {"pads": [3, 3, 3, 3], "strides": [2, 2]}),     # 14 rows
+    ((2, 1, 33, 35), (40, 1, 5, 7), {"pads": [2, 3, 2, 3], "strides": [2, 2]}),     # 5 rows
+    ((1, 4, 30, 44), (48, 4, 3, 7), {"pads": [1, 3, 1, 3], "strides": [2, 2], "dilations": [2, 1]}),  # 12 rows
 ])
 def test_small_channel_conv(gpu, xs, ws, attrs):
     x, w, b = randn(xs, seed=50), randn(ws, seed=51), randn((ws[0],), seed=52)
