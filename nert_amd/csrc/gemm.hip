@@ -254,15 +254,18 @@ __global__ __launch_bounds__(256) void SplitReduceQuadKernel(GemmArgs p, int spl
 }
 
 // Skinny GEMM (M <= 32, K contiguous in both operands: the ResNet classifier
-// and Gemm with transB): one workgroup per 32 output columns; each of its 4
-// waves takes a quarter of K and runs MFMAs straight from 16-byte global loads
-// -- lane half h holds k = 8j + 4h .. 8j + 4h + 3 of its A row and B column,
-// so one load pair feeds four MFMA steps -- then the four partial 32x32
-// blocks are summed through LDS in wave order (deterministic) and the
-// epilogue is the engine's alpha * acc + beta * bias. One launch, no split-K
-// partials in memory.
-__global__ __launch_bounds__(256) void SkinnyGemmKernel(GemmArgs p, int64_t k_slice) {
-    __shared__ float part[3][64][17];
+// and Gemm with transB): one workgroup per 32 output columns; each of its 8
+// waves takes an eighth of K and runs MFMAs straight from 16-byte global
+// loads -- lane half h holds k = 8j + 4h .. 8j + 4h + 3 of its A row and B
+// column, so one load pair feeds four MFMA steps; with K up to 512 all of a
+// wave's loads are in flight at once -- then the eight partial 32x32 blocks
+// are summed through LDS in wave order (deterministic) and the epilogue is
+// the engine's alpha * acc + beta * bias. One launch, no split-K partials in
+// memory.
+constexpr int kSkinnyWaves = 8;
+
+__global__ __launch_bounds__(512) void SkinnyGemmKernel(GemmArgs p, int64_t k_slice) {
+    __shared__ float part[kSkinnyWaves - 1][64][17];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int half = lane >> 5;
@@ -279,7 +282,7 @@ __global__ __launch_bounds__(256) void SkinnyGemmKernel(GemmArgs p, int64_t k_sl
     for (int v = 0; v < 16; ++v) {
         acc[v] = 0.0f;
     }
-#pragma unroll 4
+#pragma unroll 8
     for (int64_t k = k_begin; k < k_end; k += 8) {
         nert_floatx4 a = *reinterpret_cast<const nert_floatx4*>(ap + k);
         nert_floatx4 b = *reinterpret_cast<const nert_floatx4*>(bp + k);
@@ -305,7 +308,7 @@ __global__ __launch_bounds__(256) void SkinnyGemmKernel(GemmArgs p, int64_t k_sl
         return;
     }
 #pragma unroll
-    for (int w = 0; w < 3; ++w) {
+    for (int w = 0; w < kSkinnyWaves - 1; ++w) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             acc[v] += part[w][lane][v];
@@ -327,8 +330,9 @@ bool SkinnyApplies(const GemmArgs& p, int64_t batches) {
 }
 
 void LaunchSkinny(const GemmArgs& p, hipStream_t stream) {
-    const int64_t k_slice = ((p.k + 31) / 32) * 8; // a multiple of 8, four slices cover K
-    SkinnyGemmKernel<<<static_cast<unsigned>((p.n + 31) / 32), 256, 0, stream>>>(p, k_slice);
+    // A multiple of 8; kSkinnyWaves slices cover K.
+    const int64_t k_slice = ((p.k + 8 * kSkinnyWaves - 1) / (8 * kSkinnyWaves)) * 8;
+    SkinnyGemmKernel<<<static_cast<unsigned>((p.n + 31) / 32), 64 * kSkinnyWaves, 0, stream>>>(p, k_slice);
     CheckLaunch("SkinnyGemmKernel launch");
 }
 
