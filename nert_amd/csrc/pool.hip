@@ -201,21 +201,23 @@ bool TryMaxPoolTile(const PoolArgs& p, hipStream_t s) {
     return true;
 }
 
-// ---- 3x3 / stride 2 / pad 1 max pooling straight from registers -------------
+// ---- 3x3 / stride 2 max pooling straight from registers ------------------------
 //
-// The ResNet stem pool. A lane owns one 16-byte column quad (input columns
-// 4k .. 4k+3, output columns 2k and 2k+1) of R consecutive output rows of one
-// plane: it loads its 2R+1 input rows' quads at once (all loads in flight
-// together, each input byte read once but for one shared row per R), takes
-// column 4k-1 from the lane to its left, reduces each input row to the two
-// outputs' 3-wide row maxima, then each output to the maximum of three row
-// maxima, and stores the two outputs as one 8-byte store. A wave holds
+// The ResNet stem pool (pad 1) and the unpadded 3x3/2 pool. A lane owns one
+// 16-byte column quad (input columns 4k .. 4k+3, output columns 2k and 2k+1)
+// of R consecutive output rows of one plane: it loads its 2R+1 input rows'
+// quads at once (all loads in flight together, each input byte read once but
+// for one shared row per R), takes column 4k-1 (pad 1) or 4k+4 (pad 0) from
+// the neighbouring lane, reduces each input row to the two outputs' 3-wide
+// row maxima, then each output to the maximum of three row maxima, and
+// stores the two outputs as one 8-byte store (4-byte stores where the row
+// length is odd or the second output is past the row). A wave holds
 // 64 / (W/4) planes' row runs side by side. Max semantics are those of the
 // tap loop above (start at -inf, take a tap only if it is strictly greater,
 // taps in row-major order, out-of-range taps skipped): the first maximal
 // tap in row-major order wins, which the row-then-column reduction keeps,
 // so the result is bit-identical, signed zeros and NaNs included.
-template <int R>
+template <int R, int PAD>
 __global__ __launch_bounds__(256) void MaxPool3x3S2Kernel(PoolArgs p, int32_t quads_row, int32_t groups_per_wave,
                                                           int32_t chunks, int64_t groups) {
     const float ninf = -__builtin_huge_valf();
@@ -231,7 +233,7 @@ __global__ __launch_bounds__(256) void MaxPool3x3S2Kernel(PoolArgs p, int32_t qu
     nert_floatx4 v[2 * R + 1];
 #pragma unroll
     for (int j = 0; j < 2 * R + 1; ++j) {
-        const int ih = 2 * oh0 - 1 + j;
+        const int ih = 2 * oh0 - PAD + j;
         const bool in = active && static_cast<unsigned>(ih) < static_cast<unsigned>(p.in_h);
         v[j] = in ? *reinterpret_cast<const nert_floatx4*>(xp + static_cast<int64_t>(ih) * p.in_w)
                   : nert_floatx4{ninf, ninf, ninf, ninf};
@@ -247,10 +249,17 @@ __global__ __launch_bounds__(256) void MaxPool3x3S2Kernel(PoolArgs p, int32_t qu
     float h1[2 * R + 1];
 #pragma unroll
     for (int j = 0; j < 2 * R + 1; ++j) {
-        const float up = __shfl_up(v[j][3], 1);
-        const float left = k == 0 ? ninf : up;
-        h0[j] = max3(left, v[j][0], v[j][1]);
-        h1[j] = max3(v[j][1], v[j][2], v[j][3]);
+        if constexpr (PAD == 1) {
+            const float up = __shfl_up(v[j][3], 1);
+            const float left = k == 0 ? ninf : up;
+            h0[j] = max3(left, v[j][0], v[j][1]);
+            h1[j] = max3(v[j][1], v[j][2], v[j][3]);
+        } else {
+            const float down = __shfl_down(v[j][0], 1);
+            const float right = k == quads_row - 1 ? ninf : down;
+            h0[j] = max3(v[j][0], v[j][1], v[j][2]);
+            h1[j] = max3(v[j][2], v[j][3], right);
+        }
     }
     if (!active) {
         return;
@@ -260,16 +269,32 @@ __global__ __launch_bounds__(256) void MaxPool3x3S2Kernel(PoolArgs p, int32_t qu
     for (int r = 0; r < R; ++r) {
         const int oh = oh0 + r;
         if (oh < p.out_h) {
-            *reinterpret_cast<nert_floatx2*>(yp + static_cast<int64_t>(oh) * p.out_w) =
-                nert_floatx2{max3(h0[2 * r], h0[2 * r + 1], h0[2 * r + 2]), max3(h1[2 * r], h1[2 * r + 1], h1[2 * r + 2])};
+            const float o0 = max3(h0[2 * r], h0[2 * r + 1], h0[2 * r + 2]);
+            const float o1 = max3(h1[2 * r], h1[2 * r + 1], h1[2 * r + 2]);
+            float* dst = yp + static_cast<int64_t>(oh) * p.out_w;
+            if (2 * k + 1 < p.out_w && p.out_w % 2 == 0) {
+                *reinterpret_cast<nert_floatx2*>(dst) = nert_floatx2{o0, o1};
+            } else {
+                if (2 * k < p.out_w) {
+                    dst[0] = o0;
+                }
+                if (2 * k + 1 < p.out_w) {
+                    dst[1] = o1;
+                }
+            }
         }
     }
 }
 
 bool TryMaxPool3x3S2(const PoolArgs& p, hipStream_t s) {
     constexpr int kRows = 8;
-    if (p.k_h != 3 || p.k_w != 3 || p.s_h != 2 || p.s_w != 2 || p.d_h != 1 || p.d_w != 1 || p.p_h != 1 ||
-        p.p_w != 1 || p.in_w % 4 != 0 || p.in_w > 256 || p.out_w * 2 != p.in_w || p.out_h < 1 ||
+    // Pad 1 on both axes: W = 2 OW (columns up to 2 OW read). Pad 0: OW =
+    // W / 2 - 1, or W / 2 with a right pad (whose tap is skipped). Odd OW
+    // stores its outputs one float at a time.
+    const bool pad1 = p.p_h == 1 && p.p_w == 1 && p.out_w * 2 == p.in_w;
+    const bool pad0 = p.p_h == 0 && p.p_w == 0 && (p.out_w == p.in_w / 2 - 1 || p.out_w == p.in_w / 2);
+    if (p.k_h != 3 || p.k_w != 3 || p.s_h != 2 || p.s_w != 2 || p.d_h != 1 || p.d_w != 1 || !(pad1 || pad0) ||
+        p.in_w % 4 != 0 || p.in_w > 256 || p.out_h < 1 || p.out_w < 1 ||
         (reinterpret_cast<uintptr_t>(p.x) & 15) != 0 || (reinterpret_cast<uintptr_t>(p.y) & 7) != 0) {
         return false;
     }
@@ -282,8 +307,13 @@ bool TryMaxPool3x3S2(const PoolArgs& p, hipStream_t s) {
     if (blocks > 0x7FFFFFFF) {
         return false;
     }
-    MaxPool3x3S2Kernel<kRows><<<static_cast<unsigned>(blocks), 256, 0, s>>>(p, quads_row, groups_per_wave, chunks,
-                                                                            groups);
+    if (pad1) {
+        MaxPool3x3S2Kernel<kRows, 1><<<static_cast<unsigned>(blocks), 256, 0, s>>>(p, quads_row, groups_per_wave,
+                                                                                   chunks, groups);
+    } else {
+        MaxPool3x3S2Kernel<kRows, 0><<<static_cast<unsigned>(blocks), 256, 0, s>>>(p, quads_row, groups_per_wave,
+                                                                                   chunks, groups);
+    }
     return true;
 }
 

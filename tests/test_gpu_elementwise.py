@@ -234,12 +234,18 @@ def test_maxpool_nan_and_neg_inf(gpu):
     assert_parity("MaxPool", [x], [((1, 1, 2, 2), F)], {"kernel_shape": [2, 2], "strides": [2, 2]})
 
 
-@pytest.mark.parametrize("xs", [(32, 64, 112, 112), (3, 5, 7, 8), (2, 3, 20, 256), (1, 7, 33, 4), (2, 2, 1, 12)])
-def test_maxpool_3x3_stride2_kernel(gpu, xs):
-    """The 3x3 / stride-2 / pad-1 pool (the ResNet stem pool; one lane per
-    column quad, rows reduced in registers), over whole and partial row runs,
-    one to 64 planes per wave, and a bottom padding row: bit-identical to the
-    reference, with signed zeros, NaNs and -inf sprinkled in."""
+@pytest.mark.parametrize("xs", [(32, 64, 112, 112), (3, 5, 7, 8), (2, 3, 20, 256), (1, 7, 33, 4), (2, 2, 1, 12),
+                                (8, 64, 112, 112), (2, 3, 9, 12)])
+@pytest.mark.parametrize("pad,ceil", [(1, 0), (0, 0), (0, 1)])
+def test_maxpool_3x3_stride2_kernel(gpu, xs, pad, ceil):
+    """The 3x3 / stride-2 pool from registers (one lane per column quad, rows
+    reduced in registers): pad 1 (the ResNet stem pool), pad 0 (odd and even
+    output widths; the reference's [8,64,112,112] fixture) and pad 0 in
+    ceil mode (a right and bottom padding tap), over whole and partial row
+    runs and one to 64 planes per wave: bit-identical to the reference, with
+    signed zeros, NaNs and -inf sprinkled in."""
+    if pad == 0 and xs[2] < 3:
+        pytest.skip("no 3x3 window fits without padding")
     x = randn(xs, seed=31)
     flat = x.reshape(-1)
     pick = rng(32).random(flat.size)
@@ -247,7 +253,7 @@ def test_maxpool_3x3_stride2_kernel(gpu, xs):
     flat[(pick >= 0.05) & (pick < 0.1)] = -0.0
     flat[(pick >= 0.1) & (pick < 0.12)] = np.nan
     flat[(pick >= 0.12) & (pick < 0.13)] = -np.inf
-    attrs = {"kernel_shape": [3, 3], "strides": [2, 2], "pads": [1, 1, 1, 1]}
+    attrs = {"kernel_shape": [3, 3], "strides": [2, 2], "pads": [pad] * 4, "ceil_mode": ceil}
     spec = [(_pool_out(xs, attrs), F)]
     want, ref_err = run_ref("MaxPool", [x], spec, attrs)
     got, hip_err = run_hip("MaxPool", [x], spec, attrs)
