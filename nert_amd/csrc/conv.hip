@@ -25,6 +25,7 @@
 #include <cstdlib>
 #include <map>
 #include <mutex>
+#include <type_traits>
 
 #include "gemm_engine.hpp"
 #include "tune.hpp"
@@ -1840,24 +1841,27 @@ struct StemGeom {
     int32_t tiles_w, tiles_h;
     int32_t patch_floats;  // C_g * ph * pitch
     int32_t blocks;        // batch * tiles_h * tiles_w
-    int32_t whole;         // blocks taken whole; the rest as two halves each
-    int32_t units;         // whole + 2 * (blocks - whole)
+    int32_t whole;         // blocks taken whole; the rest in `pieces` row strips each
+    int32_t pieces;        // 2 (rows 0-7, 8-15) or 4 (rows 4i .. 4i+3; seven-tap stems)
+    int32_t units;         // whole + pieces * (blocks - whole)
     FastDiv div_plane;     // by ph * pitch
     FastDiv div_pitch;     // by pitch
 };
 
-// Work units: blocks below sg.whole are taken whole; each later block is two
-// units, its output rows 0-7 and 8-15, computed by the waves that own those
-// rows (the others skip it). The host sets whole to the blocks of the full
-// rounds of workgroups when the rest, halved, fits one round, so the last
-// partial round costs about half a block instead of a whole one.
-__device__ __forceinline__ int StemUnitBlock(const StemGeom& sg, int u, int& half) {
+// Work units: blocks below sg.whole are taken whole; each later block is
+// sg.pieces units, strips of its output rows. A half (rows 0-7 or 8-15) is
+// computed by the four waves that own those rows; a quarter (4 rows, two
+// 32-pixel columns) by waves 0-3, one 32x32 output block each, so the four
+// SIMDs share it. The host sets whole to the blocks of the full rounds of
+// workgroups when the rest, cut, fits one round, so the last partial round
+// costs a half or a quarter of a block instead of a whole one.
+__device__ __forceinline__ int StemUnitBlock(const StemGeom& sg, int u, int& piece) {
     if (u < sg.whole) {
-        half = -1;
+        piece = -1;
         return u;
     }
-    half = (u - sg.whole) & 1;
-    return sg.whole + ((u - sg.whole) >> 1);
+    piece = (u - sg.whole) % sg.pieces;
+    return sg.whole + (u - sg.whole) / sg.pieces;
 }
 
 template <bool P7>
@@ -1950,12 +1954,6 @@ __global__ __launch_bounds__(512, 4) void StemQuadKernel(ConvArgs p, StemGeom sg
     const int wave_n = wave >> 1;
     const int half = lane >> 5;
     const int col = lane & 31;
-    int boff[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int n = wave_n * 64 + j * 32 + col;
-        boff[j] = (n / kPatchTile) * p.s_h * sg.pitch + (n % kPatchTile) * 2 + 4 * half;
-    }
     bool zero_tap[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
@@ -2007,11 +2005,31 @@ __global__ __launch_bounds__(512, 4) void StemQuadKernel(ConvArgs p, StemGeom sg
             int next_half;
             load_patch(StemUnitBlock(sg, next, next_half), patches + (buf ^ 1) * sg.patch_floats);
         }
-        // A half unit: only the waves owning its eight output rows work. Half
-        // units come only in a workgroup's last round, so the skipped waves'
-        // missing stores never meet the store-count wait above.
-        if (row_half >= 0 && (wave_n >> 1) != row_half) {
-            continue;
+        // A half or quarter unit: only the waves with a share of its rows
+        // work. Such units come only in a workgroup's last round, so the
+        // skipped waves' missing stores never meet the store-count wait above.
+        // wn: the 64-pixel strip (4 block rows) of this wave; j0, jn: its
+        // 32-pixel columns.
+        int wn = wave_n, j0 = 0, jn = 2;
+        if (row_half >= 0) {
+            if (sg.pieces == 2) {
+                if ((wave_n >> 1) != row_half) {
+                    continue;
+                }
+            } else {
+                if (wave >= 4) {
+                    continue;
+                }
+                wn = row_half;
+                j0 = wave >> 1;
+                jn = 1;
+            }
+        }
+        int boff[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int n = wn * 64 + (j0 + j) * 32 + col;
+            boff[j] = (n / kPatchTile) * p.s_h * sg.pitch + (n % kPatchTile) * 2 + 4 * half;
         }
         nert_floatx16 acc[2];
 #pragma unroll
@@ -2025,6 +2043,8 @@ __global__ __launch_bounds__(512, 4) void StemQuadKernel(ConvArgs p, StemGeom sg
             // Patch offset of filter row r (channel r / KH, row r % KH).
             auto row_off = [&](int r) { return (r / kh_n) * plane_patch + (r % kh_n) * row_step; };
             const float* wp = ws + (wave_m * 32 + col) * sg.wpitch + 8 * half;
+            auto pair_rows = [&](auto jn_c) {
+            constexpr int JN = decltype(jn_c)::value;
             for (int q = 0; q < pairs; ++q) {
                 const int r0 = 2 * q;
                 const bool two = r0 + 1 < sg.rows;
@@ -2032,9 +2052,9 @@ __global__ __launch_bounds__(512, 4) void StemQuadKernel(ConvArgs p, StemGeom sg
                 const int o1 = two ? row_off(r0 + 1) : o0;
                 const nert_floatx4 alo = *reinterpret_cast<const nert_floatx4*>(wp + q * kStemPairFloats);
                 const nert_floatx4 ahi = *reinterpret_cast<const nert_floatx4*>(wp + q * kStemPairFloats + 4);
-                float b[2][7];
+                float b[JN][7];
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                for (int j = 0; j < JN; ++j) {
                     const float* s0 = patch + o0 + boff[j];
                     const float* s1 = patch + o1 + boff[j];
                     const nert_floatx2 x01 = *reinterpret_cast<const nert_floatx2*>(s0);
@@ -2055,7 +2075,7 @@ __global__ __launch_bounds__(512, 4) void StemQuadKernel(ConvArgs p, StemGeom sg
 #pragma unroll
                 for (int st = 0; st < 4; ++st) {
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) {
+                    for (int j = 0; j < JN; ++j) {
                         acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(alo[st], b[j][st], acc[j], 0, 0, 0);
                     }
                 }
@@ -2063,11 +2083,17 @@ __global__ __launch_bounds__(512, 4) void StemQuadKernel(ConvArgs p, StemGeom sg
 #pragma unroll
                     for (int st = 0; st < 3; ++st) {
 #pragma unroll
-                        for (int j = 0; j < 2; ++j) {
+                        for (int j = 0; j < JN; ++j) {
                             acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(ahi[st], b[j][4 + st], acc[j], 0, 0, 0);
                         }
                     }
                 }
+            }
+            };
+            if (jn == 2) {
+                pair_rows(std::integral_constant<int, 2>{});
+            } else {
+                pair_rows(std::integral_constant<int, 1>{});
             }
         } else {
             for (int c = 0; c < cg; ++c) {
@@ -2114,7 +2140,10 @@ __global__ __launch_bounds__(512, 4) void StemQuadKernel(ConvArgs p, StemGeom sg
         const bool has_bias = p.bias != nullptr;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const int n = wave_n * 64 + j * 32 + col;
+            if (j >= jn) {
+                break;
+            }
+            const int n = wn * 64 + (j0 + j) * 32 + col;
             const int oy = ty0 + n / kPatchTile;
             const int ox = tx0 + n % kPatchTile;
             const bool pix_ok = oy < p.out_h && ox < p.out_w;
@@ -2191,8 +2220,10 @@ bool TryStemQuad(const ConvArgs& p, hipStream_t stream) {
     const int64_t per_slot = std::max<int64_t>(1, kResidentBlocks / (m_blocks * p.group));
     const int64_t slots = std::min(blocks, per_slot);
     const int64_t rest = blocks % slots;
-    sg.whole = static_cast<int32_t>(rest > 0 && 2 * rest <= slots ? blocks - rest : blocks);
-    sg.units = static_cast<int32_t>(sg.whole + 2 * (blocks - sg.whole));
+    // Quarters (seven-tap kernel only) when they fit the last round, else halves.
+    sg.pieces = p7 && 4 * rest <= slots ? 4 : 2;
+    sg.whole = static_cast<int32_t>(rest > 0 && sg.pieces * rest <= slots ? blocks - rest : blocks);
+    sg.units = static_cast<int32_t>(sg.whole + sg.pieces * (blocks - sg.whole));
     sg.div_plane = FastDiv::Make(static_cast<uint32_t>(sg.ph * sg.pitch));
     sg.div_pitch = FastDiv::Make(static_cast<uint32_t>(sg.pitch));
     auto* kernel = p7 ? &StemQuadKernel<true> : &StemQuadKernel<false>;

@@ -374,6 +374,8 @@ def _restate_args(attrs):
     ((2, 2, 40, 40), (32, 2, 7, 7), {"pads": [3, 3, 3, 3], "strides": [2, 2]}),     # 14 rows
     ((2, 1, 33, 35), (40, 1, 5, 7), {"pads": [2, 3, 2, 3], "strides": [2, 2]}),     # 5 rows
     ((1, 4, 30, 44), (48, 4, 3, 7), {"pads": [1, 3, 1, 3], "strides": [2, 2], "dilations": [2, 1]}),  # 12 rows
+    # 1029 pixel blocks on 512 workgroups: the last 5 blocks run as quarter blocks
+    ((21, 3, 224, 224), (64, 3, 7, 7), {"pads": [3, 3, 3, 3], "strides": [2, 2]}),
 ])
 def test_small_channel_conv(gpu, xs, ws, attrs):
     x, w, b = randn(xs, seed=50), randn(ws, seed=51), randn((ws[0],), seed=52)
