@@ -127,11 +127,13 @@ def test_dropin_end_to_end_bs32(resnet):
           f"{device_ms:.3f} ms per step ({32 / device_ms * 1e3:.0f} img/s)")
 
 
-def test_fused_vit_program_is_bit_identical(gpu):
+@pytest.mark.parametrize("batch", [1, 2])
+def test_fused_vit_program_is_bit_identical(gpu, batch):
     """The MatMul+scale+bias+Gelu fusion, the residual Add+LayerNorm fusion
     and the view aliasing change no output bit (ViT-B/16, two layers,
-    batch 2; the attention fusion, which is not bit-exact, left out)."""
-    g, inputs = workloads.vit_b16(batch=2, layers=2)
+    batch 1 and 2: 197 and 394 token rows; the attention fusion, which is
+    not bit-exact, left out)."""
+    g, inputs = workloads.vit_b16(batch=batch, layers=2)
     outs = []
     for fuse, views in ((False, False), (True, True)):
         prog = Program(g, fuse=fuse, views=views, attention=False)
@@ -141,7 +143,9 @@ def test_fused_vit_program_is_bit_identical(gpu):
         prog.close()
     fused = Program(g, attention=False).graph.nodes
     assert sum(1 for n in fused if n.op == "FusedMatMul") == 10
-    assert sum(1 for n in fused if n.op == "FusedAddLayerNorm") == 4
+    # At batch 1 the position-embedding Add has same-shape operands too, so
+    # the first LayerNorm fuses with it as well.
+    assert sum(1 for n in fused if n.op == "FusedAddLayerNorm") == (5 if batch == 1 else 4)
     assert np.array_equal(outs[0], outs[1])
 
 
