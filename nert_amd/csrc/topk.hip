@@ -35,7 +35,29 @@ struct RowGeom {
     int64_t dim;
     int64_t inner;
     int64_t k;
+    int32_t vec; // rows contiguous, 16-byte aligned, chunks of whole quads: 16-byte loads
 };
+
+// Calls visit(i, x[base + i * inner]) for i in [begin, end) of a row, one
+// element per thread per step, or (vec) one 16-byte quad per thread per step.
+template <class Visit>
+__device__ __forceinline__ void ForRowRange(const float* __restrict__ x, const RowGeom& g, int64_t base, int64_t begin,
+                                            int64_t end, Visit visit) {
+    if (g.vec) {
+        const nert_floatx4* q = reinterpret_cast<const nert_floatx4*>(x + base);
+        for (int64_t i = begin + 4 * threadIdx.x; i < end; i += 4 * blockDim.x) {
+            const nert_floatx4 v = q[i / 4];
+            visit(i, v[0]);
+            visit(i + 1, v[1]);
+            visit(i + 2, v[2]);
+            visit(i + 3, v[3]);
+        }
+    } else {
+        for (int64_t i = begin + threadIdx.x; i < end; i += blockDim.x) {
+            visit(i, x[base + i * g.inner]);
+        }
+    }
+}
 
 __device__ __forceinline__ int64_t RowBase(int64_t row, const RowGeom& g) {
     const int64_t o = row / g.inner;
@@ -228,14 +250,14 @@ __global__ void __launch_bounds__(kThreads) HistKernel(const float* __restrict__
         end = g.dim;
     }
     const int64_t base = RowBase(row, g);
-    for (int64_t i = begin + threadIdx.x; i < end; i += blockDim.x) {
-        const uint64_t key = KeyOf(x[base + i * g.inner], i);
+    ForRowRange(x, g, base, begin, end, [&](int64_t i, float v) {
+        const uint64_t key = KeyOf(v, i);
         // pass 0 has no prefix to match (a 64-bit shift would be undefined)
         const bool match = pass == 0 || (key >> (shift + 8)) == (s.prefix >> (shift + 8));
         if (match) {
             atomicAdd(&h[wave][(key >> shift) & 0xFF], 1u);
         }
-    }
+    });
     __syncthreads();
     uint32_t v = 0;
     for (int w = 0; w < kThreads / 64; ++w) {
@@ -264,15 +286,15 @@ __global__ void __launch_bounds__(kThreads) CollectKernel(const float* __restric
         end = g.dim;
     }
     const int64_t base = RowBase(row, g);
-    for (int64_t i = begin + threadIdx.x; i < end; i += blockDim.x) {
-        const uint64_t key = KeyOf(x[base + i * g.inner], i);
+    ForRowRange(x, g, base, begin, end, [&](int64_t i, float v) {
+        const uint64_t key = KeyOf(v, i);
         if (key >= threshold) {
             const int pos = atomicAdd(count, 1);
             if (pos < g.k) {
                 cand[row * g.k + pos] = key;
             }
         }
-    }
+    });
 }
 
 // Sorts runs of kRun candidates (descending) in LDS, in place.
@@ -418,7 +440,7 @@ void TopkImpl(const float* x, float* values, int64_t* indices, int64_t outer, in
         return;
     }
     hipStream_t s = StreamOr(stream);
-    const RowGeom g{dim, inner, k};
+    RowGeom g{dim, inner, k, 0};
     if (dim <= kSmallRow) {
         if (rows > 0x7FFFFFFF) {
             throw Error("topk: too many rows");
@@ -436,7 +458,12 @@ void TopkImpl(const float* x, float* values, int64_t* indices, int64_t outer, in
     if (chunks < 1) {
         chunks = 1;
     }
-    const int64_t chunk = (dim + chunks - 1) / chunks;
+    int64_t chunk = (dim + chunks - 1) / chunks;
+    // Contiguous, aligned rows of whole quads: chunks of whole quads too.
+    g.vec = inner == 1 && dim % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    if (g.vec) {
+        chunk = (chunk + 3) / 4 * 4;
+    }
     if (rows * chunks > 0x7FFFFFFF) {
         throw Error("topk: too many rows");
     }
