@@ -323,6 +323,14 @@ int nert_hip_cumsum(int dtype, const void* x, void* y, int64_t outer, int64_t di
 int nert_hip_copy_strided(int elem_size, const void* src, void* dst, int rank, const int64_t* dims,
                           const int64_t* src_strides, const int64_t* dst_strides, const int64_t* src_mods,
                           void* stream);
+
+/* Concatenates n_inputs (1..8) inputs along one axis in one launch: the
+ * output is `outer` rows of sum_i row_bytes[i] bytes, row r holding input
+ * i's row r (row_bytes[i] bytes at srcs[i] + r * row_bytes[i]) in input
+ * order. Inputs with row_bytes 0 may be NULL. Serves Concat
+ * (src/kernels/concat.cpp), one launch instead of one copy per input. */
+int nert_hip_concat_rows(int n_inputs, const void* const* srcs, const int64_t* row_bytes, void* dst, int64_t outer,
+                         void* stream);
 /* Pad of a dense tensor: out[c] = in[map(c - begins)] per axis, mode 0
  * constant (fill `fvalue` for float32, `ivalue` for int64), 1 reflect, 2 edge
  * (src/kernels/pad.cpp:43-96). */

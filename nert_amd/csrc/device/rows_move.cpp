@@ -166,6 +166,20 @@ NERT_HIP_ROW(Concat) {
     }
     const int64_t out_extent = expected[static_cast<size_t>(axis)];
     const int64_t esize = ElementSize(first.dtype);
+    if (inputs.size() <= 8) {
+        // One launch: output row r (of `outer`) is the inputs' rows r in order.
+        std::vector<const void*> srcs;
+        std::vector<int64_t> row_bytes;
+        for (const TensorView& view : inputs) {
+            srcs.push_back(view.data);
+            row_bytes.push_back(view.dims[static_cast<size_t>(axis)] * inner * esize);
+        }
+        CheckStatus(nert_hip_concat_rows(static_cast<int>(inputs.size()), srcs.data(), row_bytes.data(), out.data,
+                                         outer, Stream()),
+                    context);
+        AfterRow(outputs, context);
+        return;
+    }
     int64_t offset = 0;
     for (const TensorView& view : inputs) {
         const int64_t d = view.dims[static_cast<size_t>(axis)];

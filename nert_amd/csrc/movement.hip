@@ -310,12 +310,88 @@ bool TryTranspose(const CopyArgs& a, int elem_size, int64_t n, hipStream_t s) {
     return true;
 }
 
+// Concat in one launch: output row r is the inputs' rows r side by side.
+// blockIdx.y walks the rows, x the units (16, 4 or 1 bytes) of a row; a unit
+// finds its input by a scan over the (at most kConcatMax) input starts.
+constexpr int kConcatMax = 8;
+
+struct ConcatArgs {
+    const uint8_t* src[kConcatMax];
+    int64_t start[kConcatMax + 1]; // units of a row before input i; start[n] = row length
+    int32_t n;
+    int64_t outer;
+    uint8_t* dst;
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void ConcatRowsKernel(ConcatArgs a) {
+    const int64_t row_units = a.start[a.n];
+    for (int64_t row = blockIdx.y; row < a.outer; row += gridDim.y) {
+        T* d = reinterpret_cast<T*>(a.dst) + row * row_units;
+        for (int64_t j = blockIdx.x * 256 + threadIdx.x; j < row_units; j += static_cast<int64_t>(gridDim.x) * 256) {
+            int i = 0;
+            while (i + 1 < a.n && j >= a.start[i + 1]) {
+                ++i;
+            }
+            const int64_t len = a.start[i + 1] - a.start[i];
+            d[j] = reinterpret_cast<const T*>(a.src[i])[row * len + (j - a.start[i])];
+        }
+    }
+}
+
 } // namespace
 } // namespace nert_hip
 
 using namespace nert_hip;
 
 extern "C" {
+
+int nert_hip_concat_rows(int n_inputs, const void* const* srcs, const int64_t* row_bytes, void* dst, int64_t outer,
+                         void* stream) {
+    return Guard([&] {
+        if (n_inputs < 1 || n_inputs > kConcatMax) {
+            throw Error("concat_rows: 1 to " + std::to_string(kConcatMax) + " inputs");
+        }
+        int64_t total = 0;
+        uintptr_t align = reinterpret_cast<uintptr_t>(dst);
+        for (int i = 0; i < n_inputs; ++i) {
+            if (row_bytes[i] < 0) {
+                throw Error("concat_rows: negative row length");
+            }
+            total += row_bytes[i];
+            align |= static_cast<uintptr_t>(row_bytes[i]);
+            if (row_bytes[i] > 0) {
+                align |= reinterpret_cast<uintptr_t>(srcs[i]);
+            }
+        }
+        if (outer <= 0 || total == 0) {
+            return;
+        }
+        const int unit = (align & 15) == 0 ? 16 : ((align & 3) == 0 ? 4 : 1);
+        ConcatArgs a{};
+        a.n = n_inputs;
+        a.outer = outer;
+        a.dst = static_cast<uint8_t*>(dst);
+        for (int i = 0; i < n_inputs; ++i) {
+            a.src[i] = static_cast<const uint8_t*>(srcs[i]);
+            a.start[i + 1] = a.start[i] + row_bytes[i] / unit;
+        }
+        const int64_t row_units = total / unit;
+        const unsigned gy = static_cast<unsigned>(std::min<int64_t>(outer, 65535));
+        const int64_t want_x = (row_units + 255) / 256;
+        const unsigned gx = static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(want_x, 16384 / gy)));
+        hipStream_t s = StreamOr(stream);
+        const dim3 grid(gx, gy);
+        if (unit == 16) {
+            ConcatRowsKernel<uint4><<<grid, 256, 0, s>>>(a);
+        } else if (unit == 4) {
+            ConcatRowsKernel<uint32_t><<<grid, 256, 0, s>>>(a);
+        } else {
+            ConcatRowsKernel<uint8_t><<<grid, 256, 0, s>>>(a);
+        }
+        CheckLaunch("concat launch");
+    });
+}
 
 int nert_hip_copy_strided(int elem_size, const void* src, void* dst, int rank, const int64_t* dims,
                           const int64_t* src_strides, const int64_t* dst_strides, const int64_t* src_mods,

@@ -60,6 +60,9 @@ def test_transpose_errors(gpu):
     ([(2, 3), (2, 7)], -1),
     ([(5,), (0,), (3,)], 0),
     ([(1, 2, 3, 4)], 3),
+    ([(8, 64, 20, 20), (8, 128, 20, 20), (8, 32, 20, 20)], 1),  # detector neck: 16-byte units
+    ([(70000, 1), (70000, 2)], 1),                              # more rows than one grid column
+    ([(3, i + 1) for i in range(9)], 1),                        # nine inputs: one copy per input
 ])
 @pytest.mark.parametrize("dtype", [F, I, B])
 def test_concat(gpu, shapes, axis, dtype):
