@@ -27,6 +27,10 @@ Extra keys on the one JSON line:
                 input in, host logits out, 49 unfused rows launched one by
                 one), wall time per call; and the device time of those 49
                 unfused rows replayed as a HIP graph (no fusion, no views).
+  dropin_bs1    the reference's own full-model HIP gate
+                (tools/hip_model_check.cpp:57-88) on this device: ResNet-18 at
+                batch 1, Model construction ms, then Run 1 and Run 2 wall ms,
+                logits against the reference executor's committed fixture.
   cpu_baseline  the reference CpuDevice executor (oracle/_ref, one core) on
                 the first CPU_SAMPLE_BATCH images of the same input, timed in
                 this run; its logits re-check the GPU's.
@@ -183,6 +187,63 @@ def dropin_leg(g, x: np.ndarray, steps: int) -> dict:
     return result
 
 
+GATE_FIXTURE = ROOT / "tests" / "golden" / "models" / "resnet18_bs1.npz"
+
+
+def dropin_gate_bs1() -> dict:
+    """The reference's own full-model HIP gate (tools/hip_model_check.cpp:57-88)
+    on this device: ResNet-18 at batch 1, nert::Model(graph, dims,
+    nert::HipDevice()) construction timed, then Run 1 and Run 2 wall times,
+    and the logits against the reference executor's (committed fixture)."""
+    import ctypes as C
+
+    from nert_amd import workloads
+    from nert_amd.graph import to_onnx
+
+    lib_path = ROOT / "nert_amd" / "lib" / "libnert_seamrun.so"
+    if not lib_path.exists():
+        return {"checked": False, "reason": "libnert_seamrun.so not built"}
+    L = C.CDLL(str(lib_path))
+    L.nert_seam_gate.argtypes = [C.c_char_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_int64,
+                                 C.POINTER(C.c_double), C.POINTER(C.c_double), C.POINTER(C.c_double),
+                                 C.c_char_p, C.c_int]
+    g, inputs = workloads.resnet18(batch=1)
+    x = np.ascontiguousarray(inputs["input"])
+    out = np.zeros((1, 1000), np.float32)
+    construct, run1, run2 = C.c_double(), C.c_double(), C.c_double()
+    err = C.create_string_buffer(4096)
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "resnet18_bs1.onnx")
+        Path(path).write_bytes(to_onnx(g))
+        rc = L.nert_seam_gate(path.encode(), x.ctypes.data, x.size, out.ctypes.data, out.size, C.byref(construct),
+                              C.byref(run1), C.byref(run2), err, len(err))
+    if rc != 0:
+        raise RuntimeError(f"drop-in bs1 gate: {err.value.decode()}")
+    result = {
+        "path": "nert::LoadGraphFromFile -> nert::Model(graph, dims, nert::HipDevice()) -> Run x2 "
+                "(tools/hip_model_check.cpp:57-88)",
+        "batch": 1,
+        "nodes": len(g.nodes),
+        "construct_ms": round(construct.value, 3),
+        "run1_ms": round(run1.value, 3),
+        "run2_ms": round(run2.value, 3),
+        "run2_img_s": round(1e3 / run2.value, 1),
+        "published_mi300x_reference_hip_ms": {"construct": 80.3, "run1": 8.60, "run2": 6.85,
+                                              "source": "specs/2026-10-23-amd-devcloud/resnet-model.txt:1-3"},
+    }
+    sys.path.insert(0, str(ROOT / "tests" / "golden"))
+    import model_fixtures as fx
+
+    if GATE_FIXTURE.exists() and fx.matches("resnet18_bs1", g, inputs):
+        (want,) = fx.outputs("resnet18_bs1")
+        result["max_rel_err_vs_reference_fixture"] = max_rel_err(out, want)
+        result["reference_gate_max_ratio"] = float(
+            np.max(np.abs(out.astype(np.float64) - want) / (1e-3 * (1 + np.abs(want.astype(np.float64))))))
+    else:
+        result["max_rel_err_vs_reference_fixture"] = None
+    return result
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -294,6 +355,7 @@ def main() -> int:
         },
         "parity": parity,
         "dropin": None,
+        "dropin_bs1": None,
         "cpu_baseline": None,
     }
     ok = consistent and (not parity.get("checked") or parity["max_rel_err"] <= PARITY_RTOL)
@@ -305,6 +367,12 @@ def main() -> int:
             ok = ok and d["logits_max_rel_err_vs_replay"] <= PARITY_RTOL
         result["dropin"] = d
         log(f"drop-in: {d}")
+        log("drop-in gate: ResNet-18 bs1, construct + two Runs on HipDevice ...")
+        gate = dropin_gate_bs1()
+        result["dropin_bs1"] = gate
+        log(f"drop-in gate bs1: {gate}")
+        if gate.get("max_rel_err_vs_reference_fixture") is not None:
+            ok = ok and gate["max_rel_err_vs_reference_fixture"] <= PARITY_RTOL
     if not args.no_cpu:
         log(f"cpu baseline: reference CpuDevice on {CPU_SAMPLE_BATCH} images ...")
         result["cpu_baseline"] = cpu_baseline(g, x, logits)

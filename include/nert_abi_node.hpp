@@ -112,13 +112,15 @@ inline void CopyMessage(const std::string& message, char* err, int err_len) {
     err[n] = '\0';
 }
 
-// Runs one row from `device`'s table and maps the outcome to nert_status.
-inline int RunNode(const nert::Device& device, const char* op_type, const char* name, int64_t schema_version,
-                   const nert_attr_desc* attrs, int n_attrs, const nert_tensor_desc* inputs, int n_inputs,
-                   const nert_tensor_desc* outputs, int n_outputs, char* err, int err_len) {
+// Runs one row found by `find` (op type -> row, null when none) and maps the
+// outcome to nert_status.
+template <typename Find>
+inline int RunFoundRow(Find&& find, const char* op_type, const char* name, int64_t schema_version,
+                       const nert_attr_desc* attrs, int n_attrs, const nert_tensor_desc* inputs, int n_inputs,
+                       const nert_tensor_desc* outputs, int n_outputs, char* err, int err_len) {
     try {
         const nert::Node node = ToNode(op_type, name, schema_version, attrs, n_attrs, inputs, n_inputs, n_outputs);
-        const nert::KernelFn fn = device.kernels().find(node.op_type);
+        const nert::KernelFn fn = find(node.op_type);
         if (fn == nullptr) {
             CopyMessage("no kernel for op '" + node.op_type + "'", err, err_len);
             return NERT_NO_KERNEL;
@@ -133,6 +135,14 @@ inline int RunNode(const nert::Device& device, const char* op_type, const char* 
         CopyMessage(e.what(), err, err_len);
         return NERT_OTHER_ERROR;
     }
+}
+
+// Runs one row from `device`'s table (`device.kernels().find`).
+inline int RunNode(const nert::Device& device, const char* op_type, const char* name, int64_t schema_version,
+                   const nert_attr_desc* attrs, int n_attrs, const nert_tensor_desc* inputs, int n_inputs,
+                   const nert_tensor_desc* outputs, int n_outputs, char* err, int err_len) {
+    return RunFoundRow([&](const std::string& op) { return device.kernels().find(op); }, op_type, name,
+                       schema_version, attrs, n_attrs, inputs, n_inputs, outputs, n_outputs, err, err_len);
 }
 
 } // namespace nert_abi

@@ -74,7 +74,8 @@ int nert_hip_event_destroy(void* event);
  * copies) becomes one replayable graph; rows that must read device memory on
  * the host (control operands without a host shadow) cannot be captured and
  * fail the capture, while data-dependent error checks are deferred (see
- * nert_hip_take_error_flags; begin clears the error word first, eagerly).
+ * nert_hip_take_error_flags; begin clears the error word first, eagerly,
+ * keeping bits raised before the capture for the next take).
  * Workspaces (split-K partials, TopK state, ...) must reach their size before
  * capture: run the sequence once eagerly first. A later eager call may still
  * grow a workspace; while any graph exec is alive the replaced buffer is kept
@@ -91,7 +92,9 @@ int nert_hip_graph_destroy(void* graph_exec);
  * bit 1 = index out of range. Synchronises `stream`. While `stream` is being
  * captured into a graph it reports 0 without reading: the flag stays raised
  * and the first call after a replay reports it. A caller that replays graphs
- * holding such rows calls this after the replay to see their errors. */
+ * holding such rows calls this after the replay to see their errors. Bits
+ * that were raised when a capture began (eager rows before it) are reported
+ * by the next call too. */
 int nert_hip_take_error_flags(int32_t* flags_out, void* stream);
 
 /* Host shadows. nert_hip_memcpy_h2d keeps a host copy of every upload of at
@@ -109,7 +112,11 @@ int nert_hip_forget_host_shadow(const void* ptr, int64_t bytes);
 
 /* ---------------------------------------------------------- node level --- */
 
-/* Runs one row of the HIP table on device tensors. Returns a nert_status;
+/* Runs one row of the HIP table on device tensors: the 73 rows that
+ * nert::HipDevice().kernels().find answers for (the reference's op types), plus
+ * the fused rows that nert_amd's runner emits (FusedConv, FusedMatMul,
+ * FusedAddLayerNorm, FusedAttention; no counterpart in the reference, and not
+ * found through the seam). Returns a nert_status;
  * on error `err` receives the row's message ("<Op> (node '<name>'): ...",
  * the reference convention, e.g. src/kernels/gemm.cpp:60). The row's work is
  * queued on the layer stream; results are visible after the next blocking
@@ -118,7 +125,8 @@ int nert_hip_run_node(const char* op_type, const char* node_name, int64_t schema
                       const nert_attr_desc* attrs, int n_attrs, const nert_tensor_desc* inputs, int n_inputs,
                       const nert_tensor_desc* outputs, int n_outputs, char* err, int err_len);
 
-/* 1 when the HIP table has a row for op_type (KernelTable::find != null). */
+/* 1 when nert_hip_run_node has a row for op_type: KernelTable::find != null,
+ * or one of the four fused runner rows. */
 int nert_hip_has_row(const char* op_type);
 
 /* ------------------------------------------------------ GEMM on MFMA --- */

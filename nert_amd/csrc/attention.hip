@@ -107,20 +107,24 @@ __global__ __launch_bounds__(64, 2) void AttentionFlashKernel(AttnArgs a) {
     // + e % 4, dims c and 32 + c. Rows past the sequence read as 0.
     const uint32_t k_lane = static_cast<uint32_t>(c) * row_bytes + 16u * half;
     const uint32_t v_lane = static_cast<uint32_t>(4 * half) * row_bytes + 4u * c;
+    // The whole byte offset goes in the VGPR offset (soffset stays 0): the
+    // range check of a raw buffer load covers the VGPR offset and the
+    // instruction offset, not the scalar offset.
     const auto load = [&](int kb, nert_floatx4* kf, float* v0, float* v1) {
         const uint32_t blk = static_cast<uint32_t>(kb) * 32u * row_bytes;
+        const uint32_t kv = k_lane + blk;
+        const uint32_t vv = v_lane + blk;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             kf[j] = __builtin_bit_cast(nert_floatx4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                         kr, static_cast<int>(k_lane + 32u * j), static_cast<int>(blk), 0));
+                                                         kr, static_cast<int>(kv + 32u * j), 0, 0));
         }
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-            const uint32_t off = blk + static_cast<uint32_t>(8 * (e >> 2) + (e & 3)) * row_bytes;
-            v0[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vr, static_cast<int>(v_lane),
-                                                                                   static_cast<int>(off), 0));
-            v1[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vr, static_cast<int>(v_lane + 128u),
-                                                                                   static_cast<int>(off), 0));
+            const uint32_t off = vv + static_cast<uint32_t>(8 * (e >> 2) + (e & 3)) * row_bytes;
+            v0[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vr, static_cast<int>(off), 0, 0));
+            v1[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vr, static_cast<int>(off + 128u),
+                                                                                   0, 0));
         }
     };
     nert_floatx4 kf[8];
@@ -281,11 +285,13 @@ int nert_hip_attention_f32(const float* q, const float* k, const float* v, float
         }
         // Keys past the sequence must fall beyond a (batch, head) slice's last
         // row (the loads' range check reads them as 0): tokens at least a
-        // head's width apart, the slice under 2^32 bytes.
+        // head's width apart, and the byte offsets of the last key block's
+        // rows (up to 31 rows past the sequence) under 2^32, so no offset
+        // wraps back into the slice.
         if (in_strides[1] < head_dim) {
             throw Error("attention: token stride shorter than head_dim");
         }
-        if ((seq - 1) * in_strides[1] + head_dim >= (int64_t{1} << 30)) {
+        if ((seq + 32) * in_strides[1] + head_dim >= (int64_t{1} << 30)) {
             throw Error("attention: a (batch, head) slice spans 2^32 bytes or more");
         }
         // Largest element offsets must fit the kernel's 32-bit strides.

@@ -44,6 +44,9 @@ void* Workspace(int64_t bytes, hipStream_t stream, int slot = 0);
 // report data-dependent errors (out-of-range indices, integer division by
 // zero) back to the host.
 int32_t* ErrorFlags();
+// Bits read off the device word when a capture began (raised by eager rows
+// before it); the next nert_hip_take_error_flags reports and clears them.
+int32_t& PendingErrorFlags();
 // Tile counters for kernels whose workgroups finish a tile's split sum among
 // themselves (the last one to arrive reduces; FinishSplitTile in
 // mfma_tile.hpp, used by the conv and GEMM kernels): kTileCounters words,

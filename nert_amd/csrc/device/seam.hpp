@@ -143,7 +143,11 @@ void* Stream();
 
 } // namespace seam
 
-// Row lookup by op type (null when the op has no row).
+// Row lookup by op type (null when the op has no row): the reference's 73
+// op types, what the seam's KernelTable::find answers.
 nert::KernelFn FindRow(const std::string& op_type);
+// FindRow plus the runner's fused rows (FusedConv, FusedMatMul,
+// FusedAddLayerNorm, FusedAttention), for the node-level C entry points.
+nert::KernelFn FindRunnerRow(const std::string& op_type);
 
 } // namespace nert_hip

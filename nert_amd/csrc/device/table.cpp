@@ -2,7 +2,11 @@
 //
 // Exact op-type strings map to rows; unknown types resolve to null so the
 // executor rejects the node naming op and node (src/executor.cpp:485-488), as
-// with the CPU table (src/kernels/cpu_kernels.cpp:15-93).
+// with the CPU table (src/kernels/cpu_kernels.cpp:15-93). The seam's
+// KernelTable::find answers for exactly the reference's 73 op types
+// (src/hip/table.cpp:95-173); the fused rows that this library's own runner
+// emits (FusedConv, FusedMatMul, FusedAddLayerNorm, FusedAttention) are
+// reachable only through the node-level C entry points.
 
 #include "rows.hpp"
 #include "../../../include/nert_abi_node.hpp"
@@ -17,10 +21,6 @@ nert::KernelFn FindRow(const std::string& op_type) {
         {"Gemm", &Gemm},
         {"MatMul", &MatMul},
         {"Conv", &Conv},
-        {"FusedConv", &FusedConv},
-        {"FusedMatMul", &FusedMatMul},
-        {"FusedAddLayerNorm", &FusedAddLayerNorm},
-        {"FusedAttention", &FusedAttention},
         {"Relu", &Relu},
         {"Sigmoid", &Sigmoid},
         {"Tanh", &Tanh},
@@ -96,6 +96,18 @@ nert::KernelFn FindRow(const std::string& op_type) {
     return it == table.end() ? nullptr : it->second;
 }
 
+nert::KernelFn FindRunnerRow(const std::string& op_type) {
+    using namespace rows;
+    static const std::unordered_map<std::string, nert::KernelFn> fused = {
+        {"FusedConv", &FusedConv},
+        {"FusedMatMul", &FusedMatMul},
+        {"FusedAddLayerNorm", &FusedAddLayerNorm},
+        {"FusedAttention", &FusedAttention},
+    };
+    const auto it = fused.find(op_type);
+    return it == fused.end() ? FindRow(op_type) : it->second;
+}
+
 } // namespace nert_hip
 
 extern "C" {
@@ -104,9 +116,9 @@ int nert_hip_run_node(const char* op_type, const char* node_name, int64_t schema
                       int n_attrs, const nert_tensor_desc* inputs, int n_inputs, const nert_tensor_desc* outputs,
                       int n_outputs, char* err, int err_len) {
     try {
-        const nert::Device& device = nert::HipDevice();
-        return nert_abi::RunNode(device, op_type, node_name, schema_version, attrs, n_attrs, inputs, n_inputs, outputs,
-                                 n_outputs, err, err_len);
+        (void)nert::HipDevice(); // device set-up; throws when no GPU is usable
+        return nert_abi::RunFoundRow(&nert_hip::FindRunnerRow, op_type, node_name, schema_version, attrs, n_attrs,
+                                     inputs, n_inputs, outputs, n_outputs, err, err_len);
     } catch (const std::exception& e) {
         nert_abi::CopyMessage(e.what(), err, err_len);
         return NERT_OTHER_ERROR;
@@ -114,7 +126,7 @@ int nert_hip_run_node(const char* op_type, const char* node_name, int64_t schema
 }
 
 int nert_hip_has_row(const char* op_type) {
-    return nert_hip::FindRow(op_type != nullptr ? op_type : "") != nullptr ? 1 : 0;
+    return nert_hip::FindRunnerRow(op_type != nullptr ? op_type : "") != nullptr ? 1 : 0;
 }
 
 } // extern "C"

@@ -588,13 +588,16 @@ int nert_hip_take_error_flags(int32_t* flags_out, void* stream) {
             *flags_out = 0;
             return;
         }
-        Check(hipMemcpyAsync(flags_out, flags, sizeof(int32_t), hipMemcpyDeviceToHost, s), "hipMemcpyAsync(flags)");
+        int32_t raised = 0;
+        Check(hipMemcpyAsync(&raised, flags, sizeof(int32_t), hipMemcpyDeviceToHost, s), "hipMemcpyAsync(flags)");
         Check(hipStreamSynchronize(s), "hipStreamSynchronize");
-        if (*flags_out != 0) {
+        if (raised != 0) {
             const int32_t zero = 0;
             Check(hipMemcpyAsync(flags, &zero, sizeof(int32_t), hipMemcpyHostToDevice, s), "hipMemcpyAsync(flags)");
             Check(hipStreamSynchronize(s), "hipStreamSynchronize");
         }
+        *flags_out = raised | PendingErrorFlags();
+        PendingErrorFlags() = 0;
     });
 }
 

@@ -117,6 +117,11 @@ int32_t* ErrorFlags() {
     return Ctx().flags;
 }
 
+int32_t& PendingErrorFlags() {
+    static int32_t pending = 0;
+    return pending;
+}
+
 uint32_t* TileCounters(int64_t count) {
     EnsureReady();
     static const bool enabled = [] {
@@ -528,8 +533,15 @@ int nert_hip_capture_begin(void) {
     return Guard([&] {
         // The graph's deferred checks report through the error word: start
         // it cleared (eagerly, before the capture; no memset node is
-        // recorded into the graph).
+        // recorded into the graph). Bits that eager rows raised before the
+        // capture are kept in the host-side pending mask, so the next
+        // nert_hip_take_error_flags still reports them.
         hipStream_t s = nert_hip::DefaultStream();
+        int32_t raised = 0;
+        nert_hip::Check(hipMemcpyAsync(&raised, nert_hip::ErrorFlags(), sizeof(raised), hipMemcpyDeviceToHost, s),
+                        "hipMemcpyAsync(flags)");
+        nert_hip::Check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        nert_hip::PendingErrorFlags() |= raised;
         const int32_t zero = 0;
         nert_hip::Check(hipMemcpyAsync(nert_hip::ErrorFlags(), &zero, sizeof(zero), hipMemcpyHostToDevice, s),
                         "hipMemcpyAsync(flags)");

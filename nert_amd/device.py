@@ -70,6 +70,7 @@ def lib() -> C.CDLL:
     L.nert_hip_graph_launch.argtypes = [vp, vp]
     L.nert_hip_graph_destroy.argtypes = [vp]
     L.nert_hip_take_error_flags.argtypes = [C.POINTER(C.c_int32), vp]
+    L.nert_hip_gather.argtypes = [i32, vp, vp, vp, i64, i64, i64, i64, vp]
     L.nert_hip_attention_f32.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, C.POINTER(C.c_int64),
                                          C.POINTER(C.c_int64), C.c_float, vp]
     _lib = L

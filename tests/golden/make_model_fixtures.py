@@ -13,9 +13,13 @@ generator from a wrong kernel.
 
 Cases:
   resnet18_bs32  configs[2] at full size: logits [32,1000]           (~45 s)
+  resnet18_bs1   configs[2]'s network at batch 1, the reference's own
+                 full-model gate batch (tools/hip_model_check.cpp)   (~3 s)
   vit_bs2        configs[3] with all 12 layers at batch 2: logits [2,1000]
                  (the reference's naive MatMul makes batch 16 a half-hour
                  run; batch 2 exercises every layer)                 (~4 min)
+  vit_bs16       configs[3] at full size: logits [16,1000], all 16 images
+                                                                     (~30 min)
   detector_bs8   configs[4] at full size: top scores [8,300], boxes
                  [8,300,4], classes [8,300] int64                    (~20 s)
 """
@@ -41,7 +45,9 @@ from model_fixtures import DIR as OUT, fingerprint  # noqa: E402
 
 CASES = {
     "resnet18_bs32": lambda: workloads.resnet18(batch=32),
+    "resnet18_bs1": lambda: workloads.resnet18(batch=1),
     "vit_bs2": lambda: workloads.vit_b16(batch=2, layers=12),
+    "vit_bs16": lambda: workloads.vit_b16(batch=16, layers=12),
     "detector_bs8": lambda: workloads.detector(batch=8),
 }
 

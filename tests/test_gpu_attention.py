@@ -72,17 +72,14 @@ def test_fused_attention_matches_reference_rows(gpu, batch, seq, heads, scale, s
     compare(eager, want, what=f"attention {batch}x{seq}x{heads}")
 
 
-def test_attention_entry_point_with_head_major_strides(gpu):
-    """nert_hip_attention_f32 on separate Q, K, V tensors in [B, H, S, D]
-    layout, written to a [B, H, S, D] output (strides other than the packed
-    projection's), against MatMul / Mul / Softmax / MatMul on the reference."""
-    b, h, s, d = 3, 3, 70, 64
-    rng = np.random.default_rng(5)
-    q, k, v = (rng.standard_normal((b, h, s, d)).astype(np.float32) for _ in range(3))
+def _head_major_reference(q, k, v, scale: float) -> np.ndarray:
+    """MatMul(Q, K^T), Mul, Softmax, MatMul(P, V) on the reference executor
+    for [B, H, S, D] tensors."""
+    b, h, s, d = q.shape
     g = graph.Graph()
     for n in ("q", "k", "v"):
         g.add_input(n, np.float32, (b, h, s, d))
-    g.add_initializer("scale", np.array(0.2, np.float32))
+    g.add_initializer("scale", np.array(scale, np.float32))
     kt = g.add_node("Transpose", ["k"], [("kt", np.float32, (b, h, d, s))], {"perm": [0, 1, 3, 2]})[0]
     sc = g.add_node("MatMul", ["q", kt], [("s", np.float32, (b, h, s, s))])[0]
     sc = g.add_node("Mul", [sc, "scale"], [("ss", np.float32, (b, h, s, s))])[0]
@@ -90,6 +87,17 @@ def test_attention_entry_point_with_head_major_strides(gpu):
     o = g.add_node("MatMul", [p, "v"], [("o", np.float32, (b, h, s, d))])[0]
     g.outputs.append(o)
     (want,) = _reference(g, [q, k, v], [(b, h, s, d)])
+    return want
+
+
+def test_attention_entry_point_with_head_major_strides(gpu):
+    """nert_hip_attention_f32 on separate Q, K, V tensors in [B, H, S, D]
+    layout, written to a [B, H, S, D] output (strides other than the packed
+    projection's), against MatMul / Mul / Softmax / MatMul on the reference."""
+    b, h, s, d = 3, 3, 70, 64
+    rng = np.random.default_rng(5)
+    q, k, v = (rng.standard_normal((b, h, s, d)).astype(np.float32) for _ in range(3))
+    want = _head_major_reference(q, k, v, 0.2)
     dq, dk, dv = (DeviceArray.from_host(t) for t in (q, k, v))
     out = DeviceArray.from_host(np.zeros((b, h, s, d), np.float32))
     strides = (C.c_int64 * 3)(h * s * d, d, s * d)
@@ -97,6 +105,43 @@ def test_attention_entry_point_with_head_major_strides(gpu):
           "attention")
     synchronize()
     compare(out.to_host(), want, what="head-major attention")
+    for t in (dq, dk, dv, out):
+        t.close()
+
+
+@pytest.mark.parametrize("seq", [1, 33, 197])
+def test_attention_reads_no_key_past_the_sequence(gpu, seq):
+    """Each (batch, head) slice of K and V sits in a larger buffer whose rows
+    after the sequence hold NaN, +inf and -inf (inside the allocation, so a
+    read of them cannot fault). The last key block's rows past the sequence
+    must not be read: the output stays finite and matches the reference rows
+    on the unpadded tensors."""
+    b, h, d, spare = 2, 3, 64, 40
+    print(f"case seq={seq}", flush=True)
+    rng = np.random.default_rng(seq + 17)
+    q, k, v = (rng.standard_normal((b, h, seq, d)).astype(np.float32) for _ in range(3))
+    want = _head_major_reference(q, k, v, 0.125)
+
+    def poisoned(t: np.ndarray) -> np.ndarray:
+        full = np.empty((b, h, seq + spare, d), np.float32)
+        full[:, :, :seq] = t
+        full[:, :, seq::3] = np.nan
+        full[:, :, seq + 1::3] = np.inf
+        full[:, :, seq + 2::3] = -np.inf
+        return full
+
+    # One stride set serves Q, K and V, so Q sits in the same padded layout
+    # (its rows past the sequence are never read either).
+    dq, dk, dv = (DeviceArray.from_host(poisoned(t)) for t in (q, k, v))
+    out = DeviceArray.from_host(np.zeros((b, h, seq, d), np.float32))
+    in_strides = (C.c_int64 * 3)(h * (seq + spare) * d, d, (seq + spare) * d)
+    out_strides = (C.c_int64 * 3)(h * seq * d, d, seq * d)
+    check(lib().nert_hip_attention_f32(dq.ptr, dk.ptr, dv.ptr, out.ptr, b, h, seq, d, in_strides, out_strides,
+                                       0.125, None), "attention")
+    synchronize()
+    got = out.to_host()
+    assert np.isfinite(got).all(), "a key row past the sequence reached the output"
+    compare(got, want, what=f"attention over poisoned padding, seq {seq}")
     for t in (dq, dk, dv, out):
         t.close()
 

@@ -41,6 +41,14 @@ def test_unary_int64(gpu, op):
     assert_parity(op, [x], [(x.shape, I)])
 
 
+def test_sign_int64_extremes(gpu):
+    """Sign over the whole int64 range, INT64_MIN included: the reference's
+    cross-device release contract (test/release_kernels_test.cpp:41-46)."""
+    x = np.array([np.iinfo(I).min, -1, 0, 1, np.iinfo(I).max], I)
+    got = assert_parity("Sign", [x], [(x.shape, I)])
+    assert np.array_equal(got[0], np.array([-1, -1, 0, 1, 1], I))
+
+
 def test_elu_alpha(gpu):
     x = randn((1000,), seed=4)
     assert_parity("Elu", [x], [(x.shape, F)], {"alpha": 0.3})

@@ -8,11 +8,13 @@ executor on CpuDevice (oracle/_ref):
 Logits must agree within |d| <= 2e-4 * (1 + |ref|) (north_star: rel 2e-4
 end-to-end on logits). At the full batch of 32, per-image independence is
 the size-independent property: images 0-1 of the batch-32 run must match the
-oracle's batch-2 run of the same two images.
+oracle's batch-2 run of the same two images; the drop-in's batch-32 logits are
+also compared, all 32 images, with the reference executor's batch-32 fixture.
 """
 
 import ctypes as C
 import os
+import sys
 import tempfile
 from pathlib import Path
 
@@ -23,6 +25,9 @@ from nert_amd import abi, graph, workloads
 from nert_amd.runner import Program
 from oracle import ref
 from rowcheck import compare
+
+sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
+import model_fixtures as fixtures  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -107,6 +112,11 @@ def test_dropin_end_to_end_bs32(resnet):
     _dropin_run(lg, x, runs=1)  # first run: per-geometry kernel choices, allocator warm-up
     got, secs, _ = _dropin_run(lg, x, runs=5)
     compare(got[:2], want, rtol=RTOL, atol=RTOL, what="drop-in bs32 logits, images 0-1")
+    # All 32 images against the reference executor's own bs32 run (the
+    # committed fixture, written by tests/golden/make_model_fixtures.py).
+    assert fixtures.matches("resnet18_bs32", g, {"input": x}), "fixture made from another graph or input"
+    (want32,) = fixtures.outputs("resnet18_bs32")
+    compare(got, want32, rtol=RTOL, atol=RTOL, what="drop-in bs32 logits, all 32 images vs the reference executor")
     prog = Program(g)
     prog.set_input("input", x)
     prog.capture()
@@ -217,3 +227,29 @@ def test_fused_program_is_bit_identical(gpu):
         outs.append(prog.output(g.outputs[0]))
         prog.close()
     assert np.array_equal(outs[0], outs[1])
+
+
+def test_reference_model_gate_bs1(gpu, tmp_path):
+    """The reference's full-model HIP gate (tools/hip_model_check.cpp:57-88)
+    through the seam: ResNet-18 at batch 1, nert::Model on HipDevice() built,
+    then Run twice; run 2's logits against the reference executor's batch-1
+    fixture within rel 2e-4 (the gate's own bar is 1e-3 * (1 + |ref|))."""
+    g, inputs = workloads.resnet18(batch=1)
+    assert fixtures.matches("resnet18_bs1", g, inputs), "fixture made from another graph or input"
+    (want,) = fixtures.outputs("resnet18_bs1")
+    L = C.CDLL(str(ROOT / "nert_amd" / "lib" / "libnert_seamrun.so"))
+    L.nert_seam_gate.argtypes = [C.c_char_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_int64,
+                                 C.POINTER(C.c_double), C.POINTER(C.c_double), C.POINTER(C.c_double),
+                                 C.c_char_p, C.c_int]
+    path = str(tmp_path / "resnet18_bs1.onnx")
+    Path(path).write_bytes(graph.to_onnx(g))
+    x = np.ascontiguousarray(inputs["input"])
+    out = np.zeros((1, 1000), np.float32)
+    times = [C.c_double() for _ in range(3)]
+    err = C.create_string_buffer(4096)
+    rc = L.nert_seam_gate(path.encode(), x.ctypes.data, x.size, out.ctypes.data, out.size,
+                          *(C.byref(t) for t in times), err, len(err))
+    assert rc == abi.OK, err.value.decode()
+    compare(out, want, rtol=RTOL, atol=RTOL, what="gate logits, ResNet-18 bs1")
+    print(f"\nResNet-18 bs1 gate on HipDevice: construct {times[0].value:.1f} ms, run 1 {times[1].value:.2f} ms, "
+          f"run 2 {times[2].value:.2f} ms")

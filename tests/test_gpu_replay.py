@@ -10,7 +10,7 @@ host checks run again on the new values (no stale shadow)."""
 import numpy as np
 import pytest
 
-from nert_amd.device import NertError
+from nert_amd.device import DeviceArray, NertError, check, lib
 from nert_amd.graph import Graph
 from nert_amd.runner import Program
 
@@ -51,6 +51,35 @@ def test_replayed_gather_reports_out_of_range(gpu):
         assert np.array_equal(prog.output("z"), DATA[[9, 0, 4]])
     finally:
         prog.close()
+
+
+def test_error_raised_before_capture_is_still_reported(gpu):
+    """nert_hip_capture_begin clears the device error word before a capture.
+    A bit that earlier work raised without a check (here the kernel-level
+    Gather entry point with an out-of-range index, which only raises the bit)
+    must survive into the next check_errors, and be cleared by that report.
+    The captured program has no row that checks the word eagerly."""
+    data = DeviceArray.from_host(DATA)
+    idx = DeviceArray.from_host(np.array([1, 12], I))
+    out = DeviceArray.from_host(np.zeros((2, 4), F))
+    g = Graph()
+    x = g.add_input("x", F, (3,))
+    g.outputs.append(g.add_node("Relu", [x], [("y", F, (3,))], name="relu")[0])
+    prog = Program(g)
+    try:
+        check(lib().nert_hip_gather(4, data.ptr, idx.ptr, out.ptr, 1, 10, 2, 4, None), "gather")
+        prog.set_input("x", np.array([-1, 0, 2], F))
+        prog.capture()                                  # clears the device word before capturing
+        with pytest.raises(NertError, match="index out of range"):
+            prog.check_errors()
+        prog.check_errors()                             # reported once
+        prog.replay()
+        prog.check_errors()
+        assert np.array_equal(prog.output("y"), np.array([0, 0, 2], F))
+    finally:
+        prog.close()
+        for t in (data, idx, out):
+            t.close()
 
 
 def _div_graph():

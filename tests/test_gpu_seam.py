@@ -26,6 +26,7 @@ import numpy as np
 import pytest
 
 from nert_amd import abi, graph
+from nert_amd.device import has_row
 from nert_amd.graph import Graph
 from oracle import ref
 from test_library import REFERENCE_ROWS
@@ -90,7 +91,11 @@ def test_device_names_itself(gpu):
 
 
 def test_every_reference_row_resolves_through_find(gpu):
-    ops = REFERENCE_ROWS + ["BatchNormalization", "NoSuchOp", ""]
+    # The runner's fused rows are not reference op types: find answers null
+    # for them, as both reference tables do (src/kernels/cpu_kernels.cpp:15-93,
+    # src/hip/table.cpp:95-173).
+    fused = ["FusedConv", "FusedMatMul", "FusedAddLayerNorm", "FusedAttention"]
+    ops = REFERENCE_ROWS + fused + ["BatchNormalization", "NoSuchOp", ""]
     arr = (C.c_char_p * len(ops))(*[o.encode() for o in ops])
     found = (C.c_int * len(ops))()
     cpu = (C.c_int * len(ops))()
@@ -98,6 +103,8 @@ def test_every_reference_row_resolves_through_find(gpu):
     for i, op in enumerate(ops):
         assert found[i] == cpu[i], f"{op!r}: HipDevice find {found[i]} vs CpuDevice find {cpu[i]}"
     assert sum(found) == 73
+    assert all(found[ops.index(op)] == 0 for op in fused)
+    assert all(has_row(op) for op in fused), "the node-level entry point serves the fused rows"
 
 
 def test_allocator_and_transfer_contract(gpu):
