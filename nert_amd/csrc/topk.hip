@@ -9,17 +9,27 @@
 // exactly the reference's order and there are no ties left.
 //
 // Rows of up to kSmallRow elements sort in one workgroup's LDS. Longer rows
-// (the detector's [8, 672000], K = 300) run a radix select over the key,
-// 8 bits per pass from the top, with many workgroups per row: each pass builds
-// a 256-bin histogram of the keys that still match the chosen prefix (one LDS
-// histogram per wave, so the waves do not contend for the same bins), and
-// every workgroup of the next pass (or of the collection) scans the previous
-// pass's histogram itself and picks the bin holding the K-th largest key, so
-// a pass is one launch. When that bin is needed whole the threshold is final
-// and later passes return at once. Keys >= threshold (exactly K per row) are
-// collected and ordered -- by rank (the count of larger keys, spread over
-// several workgroups per row) when K <= 1024, else in 4096-key LDS runs
-// merged by per-key binary search -- and written out.
+// with K <= 1024 (the detector's [8, 672000], K = 300) take two launches
+// and read the row twice:
+//   1. HistTopKernel: many workgroups per row count the top 12 bits of the
+//      orderable value into an LDS histogram, added into the row's 4096-bin
+//      histogram (and a 64-bin summary of it) in a zero-kept workspace.
+//   2. CollectTopKernel: every workgroup finds the bin holding the K-th
+//      largest value from the summary and that bin's 64 counts (two wave
+//      scans), then keeps its chunk's keys above that bin ("sure": fewer
+//      than K per row) and in it ("maybe", up to a per-row capacity), staged
+//      in LDS and appended with one reservation per workgroup. The row's last
+//      workgroup to finish then completes the row: it histograms the next 12
+//      bits of the maybe keys in LDS, picks the bin of the remaining rank,
+//      moves the keys above it to the result and selects among the keys tied
+//      on all 24 bits by rank (or, past an LDS capacity, by a radix select
+//      over their remaining 40 key bits); the K keys are ranked (all keys are
+//      unique) and written out, and the row's histograms and counters are
+//      cleared for the next call. When the maybe keys overflowed their list
+//      it reads the row again instead.
+// Longer rows with K > 1024 run a radix select over the whole key, 8 bits per
+// pass, then sort the K collected keys in 4096-key LDS runs merged by per-key
+// binary search.
 
 #include "common.hpp"
 #include "../../include/nert_hip.h"
@@ -65,19 +75,24 @@ __device__ __forceinline__ int64_t RowBase(int64_t row, const RowGeom& g) {
     return o * g.dim * g.inner + n;
 }
 
-__device__ __forceinline__ uint64_t KeyOf(float v, int64_t index) {
+// Float bits -> unsigned integer with the float order: -0.0 folded onto
+// +0.0, every NaN above +inf.
+__device__ __forceinline__ uint32_t OrdOf(float v) {
     uint32_t b = __float_as_uint(v);
     if ((b & 0x7FFFFFFFu) == 0) {
         b = 0; // -0.0 == +0.0
     }
-    uint32_t ord;
     if ((b & 0x7FFFFFFFu) > 0x7F800000u) {
-        ord = 0xFFFFFFFFu; // NaN: above +inf
-    } else {
-        ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+        return 0xFFFFFFFFu; // NaN: above +inf
     }
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ uint64_t MakeKey(uint32_t ord, int64_t index) {
     return (static_cast<uint64_t>(ord) << 32) | static_cast<uint64_t>(0xFFFFFFFFu - static_cast<uint32_t>(index));
 }
+
+__device__ __forceinline__ uint64_t KeyOf(float v, int64_t index) { return MakeKey(OrdOf(v), index); }
 
 __device__ __forceinline__ int64_t IndexOf(uint64_t key) {
     return static_cast<int64_t>(0xFFFFFFFFu - static_cast<uint32_t>(key & 0xFFFFFFFFu));
@@ -126,6 +141,567 @@ __global__ void __launch_bounds__(kThreads) SmallRowKernel(const float* __restri
     BitonicDesc(s, n_pow2);
     for (int t = threadIdx.x; t < g.k; t += blockDim.x) {
         WriteOut(x, values, indices, row, t, s[t], g);
+    }
+}
+
+// ---- long rows, K <= kFastMaxK: one read of the row -----------------------
+
+constexpr int kFastMaxK = 1024;
+constexpr int kFT = 1024;            // threads per workgroup of the two kernels
+constexpr int kBins = 4096;          // 12-bit digits
+constexpr int kWgCand = 1024;        // candidate keys a chunk workgroup keeps
+constexpr int kBatch = 16;           // candidate keys per merging thread held in registers
+constexpr int kTieCap = 2048;        // keys tied on 24 bits that the merge ranks in LDS
+constexpr int kChunkQuads = 6;       // 16-byte loads per thread and chunk (all issued up front)
+constexpr int kChunkMax = kFT * 4 * kChunkQuads;
+constexpr int kMergeKeys = kFT * kBatch; // candidates per row the merge aims for
+constexpr int64_t kFastMaxRows = 4096;
+
+// A chunk of a row, loaded up front: up to kChunkQuads 16-byte loads per
+// thread (contiguous aligned rows) or 4 * kChunkQuads scalar loads (strided
+// rows); element e of the thread has row index Index(e), valid while < end.
+struct ChunkRegs {
+    float v[4 * kChunkQuads];
+    int64_t begin;
+    int64_t end;
+    int32_t vec;
+    __device__ __forceinline__ int64_t Index(int e) const {
+        return vec ? begin + 4 * (threadIdx.x + (e >> 2) * kFT) + (e & 3)
+                   : begin + threadIdx.x + static_cast<int64_t>(e) * kFT;
+    }
+    __device__ __forceinline__ void Load(const float* __restrict__ x, const RowGeom& g, int64_t base, int64_t b,
+                                         int64_t e) {
+        begin = b;
+        end = e;
+        vec = g.vec;
+        if (vec) {
+            const nert_floatx4* q = reinterpret_cast<const nert_floatx4*>(x + base);
+#pragma unroll
+            for (int j = 0; j < kChunkQuads; ++j) {
+                const int64_t i = begin + 4 * (threadIdx.x + j * kFT);
+                const nert_floatx4 t = i < end ? q[i / 4] : nert_floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+                v[4 * j] = t[0];
+                v[4 * j + 1] = t[1];
+                v[4 * j + 2] = t[2];
+                v[4 * j + 3] = t[3];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4 * kChunkQuads; ++j) {
+                const int64_t i = begin + threadIdx.x + static_cast<int64_t>(j) * kFT;
+                v[j] = i < end ? x[base + i * g.inner] : 0.0f;
+            }
+        }
+    }
+};
+
+// The bin holding the `need`-th largest key among `nbins` LDS counts (bin
+// nbins - 1 highest), counting from the top; *above = keys in higher bins.
+// Run by a whole workgroup of kFT threads; contains barriers. The counts
+// must reach `need`.
+__device__ __forceinline__ uint32_t BlockTopSelect(const uint32_t* h, int nbins, uint32_t need, uint32_t* above) {
+    __shared__ uint32_t wave_sum[kFT / 64];
+    __shared__ uint32_t res_bin;
+    __shared__ uint32_t res_above;
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int per = nbins >= kFT ? nbins / kFT : 1;
+    const bool active = per * t < nbins;
+    uint32_t local = 0;
+    if (active) {
+        for (int j = 0; j < per; ++j) {
+            local += h[nbins - 1 - per * t - j];
+        }
+    }
+    uint32_t incl = local;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(incl, off, 64);
+        if (lane >= off) {
+            incl += y;
+        }
+    }
+    if (lane == 63) {
+        wave_sum[wave] = incl;
+    }
+    if (t == 0) {
+        res_bin = 0;
+        res_above = 0;
+    }
+    __syncthreads();
+    for (int w = 0; w < wave; ++w) {
+        incl += wave_sum[w];
+    }
+    const uint32_t excl = incl - local;
+    if (active && excl < need && incl >= need) {
+        uint32_t cum = excl;
+        for (int j = 0; j < per; ++j) {
+            const int b = nbins - 1 - per * t - j;
+            const uint32_t c = h[b];
+            if (cum + c >= need) {
+                res_bin = static_cast<uint32_t>(b);
+                res_above = cum;
+                break;
+            }
+            cum += c;
+        }
+    }
+    __syncthreads();
+    const uint32_t bin = res_bin;
+    *above = res_above;
+    __syncthreads(); // the next call may overwrite the results
+    return bin;
+}
+
+// Block-wide maximum of `hi` and minimum of `lo` (kFT threads; barriers).
+__device__ __forceinline__ void BlockRange(uint32_t hi, uint32_t lo, uint32_t* top, uint32_t* bottom) {
+    __shared__ uint32_t range[2];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t h2 = __shfl_xor(hi, off, 64);
+        const uint32_t l2 = __shfl_xor(lo, off, 64);
+        hi = h2 > hi ? h2 : hi;
+        lo = l2 < lo ? l2 : lo;
+    }
+    if (threadIdx.x == 0) {
+        range[0] = 0;
+        range[1] = 0xFFFFFFFFu;
+    }
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) {
+        atomicMax(&range[0], hi);
+        atomicMin(&range[1], lo);
+    }
+    __syncthreads();
+    *top = range[0];
+    *bottom = range[1];
+    __syncthreads(); // the next call may overwrite the results
+}
+
+// The threshold of a set of keys for rank `need`, on a window of 24 key
+// bits fitted to the set's orderable values, which lie in [bottom, top]:
+// every key shares the key bits above bit L + 24, where L = 20 + s and s is
+// how far the highest bit in which top and bottom differ lies above bit 11
+// (0 if it does not). The top 12 window bits of the keys give bin t1 (with
+// `above1` keys above it), the next 12 bits of the keys in t1 give bin t2;
+// returns L and sets *floor = (top's bits above the window) << 24 | t1 << 12
+// | t2, so that (key >> L) > *floor holds for fewer than `need` keys and
+// (key >> L) >= *floor for at least `need`. A window fitted to the values
+// spreads them over the bins (few LDS adds to one address), however narrow
+// their range. `visit(f)` calls f(key, valid) for each thread's share of
+// the set, the same in every call; `h` is kBins words of LDS. Run by the
+// whole workgroup; contains barriers.
+template <typename Visit>
+__device__ __forceinline__ int ThresholdInRange(uint32_t* h, uint32_t need, Visit visit, uint32_t top, uint32_t bottom,
+                                                uint64_t* floor) {
+    const uint32_t diff = top ^ bottom;
+    const int width = diff == 0 ? 0 : 32 - __clz(static_cast<int>(diff));
+    const int L = 20 + (width > 12 ? width - 12 : 0);
+    for (int b = threadIdx.x; b < kBins; b += kFT) {
+        h[b] = 0;
+    }
+    __syncthreads();
+    visit([&](uint64_t key, bool valid) {
+        if (valid) {
+            atomicAdd(&h[static_cast<uint32_t>(key >> (L + 12)) & 0xFFF], 1u);
+        }
+    });
+    __syncthreads();
+    uint32_t above1 = 0;
+    const uint32_t t1 = BlockTopSelect(h, kBins, need, &above1);
+    for (int b = threadIdx.x; b < kBins; b += kFT) {
+        h[b] = 0;
+    }
+    __syncthreads();
+    visit([&](uint64_t key, bool valid) {
+        if (valid && (static_cast<uint32_t>(key >> (L + 12)) & 0xFFF) == t1) {
+            atomicAdd(&h[static_cast<uint32_t>(key >> L) & 0xFFF], 1u);
+        }
+    });
+    __syncthreads();
+    uint32_t above2 = 0;
+    const uint32_t t2 = BlockTopSelect(h, kBins, need - above1, &above2);
+    // top's bits above the window (none when the window reaches the top bit;
+    // a 64-bit shift would be undefined).
+    const uint64_t common = L + 24 < 64 ? (static_cast<uint64_t>(top) << 32) >> (L + 24) : 0;
+    *floor = (common << 24) | (static_cast<uint64_t>(t1) << 12) | t2;
+    return L;
+}
+
+// The range of the orderable values a visit covers, block-wide.
+template <typename Visit>
+__device__ __forceinline__ void VisitRange(Visit visit, uint32_t* top, uint32_t* bottom) {
+    uint32_t hi = 0;
+    uint32_t lo = 0xFFFFFFFFu;
+    visit([&](uint64_t key, bool valid) {
+        const uint32_t ord = static_cast<uint32_t>(key >> 32);
+        hi = valid && ord > hi ? ord : hi;
+        lo = valid && ord < lo ? ord : lo;
+    });
+    BlockRange(hi, lo, top, bottom);
+}
+
+// Per chunk workgroup: how many candidates it found (may exceed kWgCand)
+// and bounds on their orderable values: the chunk's largest, and a value no
+// larger than the smallest candidate's.
+struct ChunkStats {
+    uint32_t count;
+    uint32_t top;
+    uint32_t bottom;
+    uint32_t pad;
+};
+
+// Read of the row, one workgroup per chunk: the chunk's candidates for the
+// row's K largest -- every key at or above the chunk's own threshold for rank
+// K (all of them when the chunk has at most K keys), which holds the chunk's
+// K largest -- written in thread order to the workgroup's slots (the first
+// kWgCand), with the chunk's stats.
+__global__ void __launch_bounds__(kFT) ChunkTopKernel(const float* __restrict__ x, RowGeom g, int64_t chunk,
+                                                      int chunks, uint64_t* cand, ChunkStats* stats) {
+    const int64_t row = blockIdx.x / chunks;
+    const int c = blockIdx.x - static_cast<int>(row * chunks);
+    const uint32_t k = static_cast<uint32_t>(g.k);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    ChunkRegs r;
+    const int64_t begin = c * chunk;
+    const int64_t end = begin + chunk < g.dim ? begin + chunk : g.dim;
+    r.Load(x, g, RowBase(row, g), begin, end);
+    __shared__ uint32_t h[kBins];
+    __shared__ uint32_t wave_sum[kFT / 64];
+    // Keys are formed where they are used (the values stay in registers).
+    const auto visit = [&](auto f) {
+#pragma unroll
+        for (int e = 0; e < 4 * kChunkQuads; ++e) {
+            f(KeyOf(r.v[e], r.Index(e)), r.Index(e) < r.end);
+        }
+    };
+    uint32_t top = 0;
+    uint32_t bottom = 0;
+    VisitRange(visit, &top, &bottom);
+    // A chunk of at most K keys passes them all (floor 0 at L = 0). Every
+    // candidate's orderable value is at least the floor's.
+    uint64_t floor = 0;
+    int L = 0;
+    if (end - begin > static_cast<int64_t>(k)) {
+        L = ThresholdInRange(h, k, visit, top, bottom, &floor);
+        bottom = static_cast<uint32_t>((floor << L) >> 32);
+    }
+    // Candidates of this thread (bit e of `pass` for element e), then their
+    // places: a block-wide exclusive sum over threads.
+    uint32_t pass = 0;
+#pragma unroll
+    for (int e = 0; e < 4 * kChunkQuads; ++e) {
+        if (r.Index(e) < r.end && (KeyOf(r.v[e], r.Index(e)) >> L) >= floor) {
+            pass |= 1u << e;
+        }
+    }
+    const uint32_t mine = static_cast<uint32_t>(__popc(pass));
+    uint32_t incl = mine;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(incl, off, 64);
+        if (lane >= off) {
+            incl += y;
+        }
+    }
+    if (lane == 63) {
+        wave_sum[wave] = incl;
+    }
+    __syncthreads();
+    uint32_t at = incl - mine;
+    uint32_t total = 0;
+    for (int w = 0; w < kFT / 64; ++w) {
+        at += w < wave ? wave_sum[w] : 0;
+        total += wave_sum[w];
+    }
+    uint64_t* slots = cand + static_cast<int64_t>(blockIdx.x) * kWgCand;
+#pragma unroll
+    for (int e = 0; e < 4 * kChunkQuads; ++e) {
+        if ((pass >> e) & 1u) {
+            if (at < kWgCand) {
+                slots[at] = KeyOf(r.v[e], r.Index(e));
+            }
+            ++at;
+        }
+    }
+    if (tid == 0) {
+        stats[blockIdx.x] = ChunkStats{total, top, bottom, 0};
+    }
+}
+
+// The value of a result key: rebuilt from its orderable bits, except for
+// zeros (-0.0 was folded onto +0.0) and NaNs, which are read back.
+__device__ __forceinline__ float ValueOf(const float* x, const RowGeom& g, int64_t row, uint64_t key) {
+    const uint32_t ord = static_cast<uint32_t>(key >> 32);
+    if (ord == 0x80000000u || ord == 0xFFFFFFFFu) {
+        return x[RowBase(row, g) + IndexOf(key) * g.inner];
+    }
+    return __uint_as_float((ord & 0x80000000u) ? (ord & 0x7FFFFFFFu) : ~ord);
+}
+
+// One workgroup per row: the row's K largest among its chunks' candidates
+// (or, when a chunk had more candidates than slots, among all of the row's
+// keys, read again). The 24-bit threshold of the candidates for rank K
+// splits them: keys above it are in the result, keys on it (tied on 24 bits)
+// are ranked among themselves in LDS, or radix-selected over their remaining
+// 40 key bits past kTieCap. The K keys are then ranked (all keys are unique)
+// and written out.
+__global__ void __launch_bounds__(kFT) MergeTopKernel(const float* __restrict__ x, float* values, int64_t* indices,
+                                                      RowGeom g, int chunks, const uint64_t* __restrict__ cand,
+                                                      const ChunkStats* __restrict__ stats) {
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const uint32_t k = static_cast<uint32_t>(g.k);
+    const int64_t wg0 = row * chunks;
+    __shared__ uint32_t h[kBins];
+    __shared__ __attribute__((aligned(16))) uint64_t fin[kFastMaxK];
+    __shared__ uint64_t ties[kTieCap];
+    __shared__ uint32_t rank_s[kFastMaxK];
+    __shared__ uint32_t off_s[kFT];
+    __shared__ uint32_t wave_sum[kFT / 64];
+    __shared__ uint32_t total_s;
+    __shared__ uint32_t fits_s;
+    __shared__ uint32_t overflow_s;
+    __shared__ uint32_t n_fin;
+    __shared__ uint32_t n_ties;
+    // Chunk c's candidates go to threads c * T .. c * T + T - 1, kBatch
+    // slots each: the chunk's stats and every slot are loaded at once (slots
+    // past the chunk's count are read but not used).
+    const int T = kFT / chunks;
+    const int group = tid / T;
+    const int member_slot = tid - group * T;
+    const bool member = group < chunks;
+    ChunkStats cs{0, 0, 0xFFFFFFFFu, 0};
+    if (member) {
+        cs = stats[wg0 + group];
+    }
+    uint64_t kv[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+        const int slot = member_slot + T * j;
+        kv[j] = member && slot < kWgCand ? cand[(wg0 + group) * kWgCand + slot] : 0;
+    }
+    if (tid == 0) {
+        fits_s = 1;
+        overflow_s = 0;
+        n_fin = 0;
+        n_ties = 0;
+    }
+    for (uint32_t i = tid; i < k; i += kFT) {
+        fin[i] = uint64_t{0xFFFFFFFFu}; // a key of index 0: every index read back stays in the row
+        rank_s[i] = 0;
+    }
+    __syncthreads();
+    if (member && (cs.count > static_cast<uint32_t>(kWgCand) || cs.count > static_cast<uint32_t>(T * kBatch))) {
+        fits_s = 0;
+    }
+    if (member && cs.count > static_cast<uint32_t>(kWgCand)) {
+        overflow_s = 1;
+    }
+    __syncthreads();
+    const bool in_regs = fits_s != 0;
+    const bool from_cand = overflow_s == 0;
+    uint32_t total = 0;
+    if (!in_regs && from_cand) {
+        // More candidates than the groups' registers hold: offsets of the
+        // chunks' candidates in chunk order, for streaming them in batches.
+        const uint32_t nc = tid < chunks ? stats[wg0 + tid].count : 0;
+        uint32_t incl = nc;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint32_t y = __shfl_up(incl, off, 64);
+            if (lane >= off) {
+                incl += y;
+            }
+        }
+        if (lane == 63) {
+            wave_sum[wave] = incl;
+        }
+        __syncthreads();
+        uint32_t before = 0;
+        uint32_t all = 0;
+        for (int w = 0; w < kFT / 64; ++w) {
+            before += w < wave ? wave_sum[w] : 0;
+            all += wave_sum[w];
+        }
+        off_s[tid] = before + incl - nc;
+        if (tid == 0) {
+            total_s = all;
+        }
+        __syncthreads();
+        total = total_s;
+    }
+    // Candidate i (in chunk order) sits in the slots of the last chunk whose
+    // offset is <= i.
+    const auto owner = [&](uint32_t i) {
+        int lo = 0;
+        int hi = chunks - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (off_s[mid] <= i) {
+                lo = mid;
+            } else {
+                hi = mid - 1;
+            }
+        }
+        return lo;
+    };
+    const uint32_t held = member ? (cs.count < static_cast<uint32_t>(kWgCand) ? cs.count : kWgCand) : 0;
+    const int64_t base = RowBase(row, g);
+    // The candidates: in the groups' registers; else streamed in batches;
+    // or the whole row when a chunk had more than its slots hold.
+    const auto source = [&](auto f) {
+        if (in_regs) {
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                f(kv[j], static_cast<uint32_t>(member_slot + T * j) < held);
+            }
+        } else if (from_cand) {
+            // (kv is free here: the registers path is not taken.)
+            for (uint32_t b0 = 0; b0 < total; b0 += kMergeKeys) {
+#pragma unroll
+                for (int j = 0; j < kBatch; ++j) {
+                    const uint32_t i = b0 + tid + j * kFT;
+                    kv[j] = 0;
+                    if (i < total) {
+                        const int w = owner(i);
+                        kv[j] = cand[(wg0 + w) * kWgCand + (i - off_s[w])];
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < kBatch; ++j) {
+                    f(kv[j], b0 + tid + j * kFT < total);
+                }
+            }
+        } else {
+            for (int64_t i0 = 0; i0 < g.dim; i0 += kFT) {
+                const int64_t i = i0 + tid;
+                const bool ok = i < g.dim;
+                f(ok ? KeyOf(x[base + i * g.inner], i) : 0, ok);
+            }
+        }
+    };
+    uint32_t range_top = 0;
+    uint32_t range_bottom = 0;
+    if (in_regs) {
+        BlockRange(cs.top, cs.bottom, &range_top, &range_bottom);
+    } else {
+        VisitRange(source, &range_top, &range_bottom);
+    }
+    uint64_t top = 0;
+    const int L = ThresholdInRange(h, k, source, range_top, range_bottom, &top);
+    source([&](uint64_t key, bool valid) {
+        if (!valid) {
+            return;
+        }
+        if ((key >> L) > top) {
+            const uint32_t p = atomicAdd(&n_fin, 1u);
+            if (p < k) {
+                fin[p] = key;
+            }
+        } else if ((key >> L) == top) {
+            const uint32_t p = atomicAdd(&n_ties, 1u);
+            if (p < kTieCap) {
+                ties[p] = key;
+            }
+        }
+    });
+    __syncthreads();
+    const uint32_t fin0 = n_fin < k ? n_fin : k; // keys above the floor
+    const uint32_t need = k - fin0;
+    const uint32_t nt = n_ties;
+    if (nt <= static_cast<uint32_t>(kTieCap)) {
+        // A tied key's place among the ties is the count of larger ones
+        // (keys are unique); the `need` largest join the result.
+        for (uint32_t i = tid; i < nt; i += kFT) {
+            const uint64_t key = ties[i];
+            uint32_t rank = 0;
+            for (uint32_t j = 0; j < nt; ++j) {
+                rank += ties[j] > key ? 1u : 0u;
+            }
+            if (rank < need) {
+                fin[fin0 + rank] = key;
+            }
+        }
+    } else {
+        // Radix select over the tied keys' remaining L bits, 8 per pass from
+        // the top (the last pass's digit may also hold bits fixed already,
+        // equal in every key it counts), then take the tied keys at or above
+        // the result.
+        uint64_t prefix = top << L;
+        uint64_t mask = ~((uint64_t{1} << L) - 1);
+        uint32_t remaining = need;
+        for (int shift = L - 8;; shift -= 8) {
+            const int sh = shift > 0 ? shift : 0;
+            for (int b = tid; b < 256; b += kFT) {
+                h[b] = 0;
+            }
+            __syncthreads();
+            source([&](uint64_t key, bool valid) {
+                if (valid && (key & mask) == prefix) {
+                    atomicAdd(&h[static_cast<uint32_t>(key >> sh) & 0xFF], 1u);
+                }
+            });
+            __syncthreads();
+            uint32_t ab = 0;
+            const uint32_t d = BlockTopSelect(h, 256, remaining, &ab);
+            remaining -= ab;
+            prefix = (prefix & ~(0xFFull << sh)) | (static_cast<uint64_t>(d) << sh);
+            mask |= 0xFFull << sh;
+            if (sh == 0) {
+                break;
+            }
+        }
+        source([&](uint64_t key, bool valid) {
+            if (valid && (key >> L) == top && key >= prefix) {
+                const uint32_t p = atomicAdd(&n_fin, 1u);
+                if (p < k) {
+                    fin[p] = key;
+                }
+            }
+        });
+    }
+    __syncthreads();
+    // Ranks: `per` threads count the larger keys of one result key each,
+    // over slices of four-key (two 16-byte LDS reads) steps; slots past K
+    // hold the smallest key, never larger.
+    for (uint32_t i = k + tid; i < (k + 3) / 4 * 4; i += kFT) {
+        fin[i] = 0;
+    }
+    __syncthreads();
+    const uint32_t quads = (k + 3) / 4;
+    const uint32_t per = k < static_cast<uint32_t>(kFT) ? static_cast<uint32_t>(kFT) / k : 1u;
+    const uint32_t slice = (quads + per - 1) / per;
+    const ulonglong2* fin2 = reinterpret_cast<const ulonglong2*>(fin);
+    for (uint32_t t = tid; t < k * per; t += kFT) {
+        const uint32_t i = t / per;
+        const uint32_t part = t - i * per;
+        const uint64_t key = fin[i];
+        const uint32_t q1 = (part + 1) * slice < quads ? (part + 1) * slice : quads;
+        uint32_t larger = 0;
+#pragma unroll 4
+        for (uint32_t q = part * slice; q < q1; ++q) {
+            const ulonglong2 a = fin2[2 * q];
+            const ulonglong2 b = fin2[2 * q + 1];
+            larger += (a.x > key ? 1u : 0u) + (a.y > key ? 1u : 0u) + (b.x > key ? 1u : 0u) + (b.y > key ? 1u : 0u);
+        }
+        if (larger != 0) {
+            atomicAdd(&rank_s[i], larger);
+        }
+    }
+    __syncthreads();
+    const int64_t o = row / g.inner;
+    const int64_t n = row - o * g.inner;
+    for (uint32_t i = tid; i < k; i += kFT) {
+        const uint64_t key = fin[i];
+        const int64_t dst = (o * g.k + rank_s[i]) * g.inner + n;
+        values[dst] = ValueOf(x, g, row, key);
+        indices[dst] = IndexOf(key);
     }
 }
 
@@ -428,6 +1004,52 @@ TopkLayout LayoutFor(int64_t rows, int64_t k) {
     return l;
 }
 
+// Byte sizes of the K <= kFastMaxK path's buffers (256-byte aligned pieces):
+// the part kept zero between calls, then the two key lists.
+// Long rows with K <= kFastMaxK: chunk candidates, then the per-row merge
+// (two launches, one read of the row).
+void FastTopk(const float* x, float* values, int64_t* indices, int64_t rows, RowGeom g, hipStream_t s, uint8_t* fixed,
+              int64_t fixed_bytes) {
+    // About 256 workgroups over all rows; chunks of at most kChunkMax keys
+    // and at least 4096, and (where the chunk limit allows) few enough per
+    // row that their candidates, about K each, fit the merge's registers.
+    int64_t chunks = (256 + rows - 1) / rows;
+    const int64_t min_chunks = (g.dim + kChunkMax - 1) / kChunkMax;
+    const int64_t max_chunks = (g.dim + 4095) / 4096;
+    const int64_t merge_chunks = kMergeKeys / (g.k + 16);
+    chunks = chunks > merge_chunks ? merge_chunks : chunks;
+    chunks = chunks > max_chunks ? max_chunks : chunks;
+    chunks = chunks < min_chunks ? min_chunks : chunks;
+    chunks = chunks < 1 ? 1 : chunks;
+    int64_t chunk = (g.dim + chunks - 1) / chunks;
+    g.vec = g.inner == 1 && g.dim % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    if (g.vec) {
+        chunk = (chunk + 3) / 4 * 4;
+    }
+    chunks = (g.dim + chunk - 1) / chunk; // every chunk non-empty
+    if (chunk > kChunkMax || chunks > kFT || rows * chunks > 0x7FFFFFFF) {
+        throw Error("topk: chunking out of range");
+    }
+    const auto up = [](int64_t b) { return (b + 255) / 256 * 256; };
+    const int64_t cand_bytes = up(rows * chunks * kWgCand * 8);
+    const int64_t need = cand_bytes + up(rows * chunks * static_cast<int64_t>(sizeof(ChunkStats)));
+    uint8_t* ws = fixed;
+    if (fixed == nullptr) {
+        ws = static_cast<uint8_t*>(Workspace(need, s));
+    } else if (need > fixed_bytes) {
+        throw Error("topk_noalloc: " + std::to_string(rows) + " rows x k = " + std::to_string(g.k) + " need " +
+                    std::to_string(need) + " bytes of scratch; the fixed scratch holds " +
+                    std::to_string(fixed_bytes));
+    }
+    auto* cand = reinterpret_cast<uint64_t*>(ws);
+    auto* stats = reinterpret_cast<ChunkStats*>(ws + cand_bytes);
+    ChunkTopKernel<<<static_cast<unsigned>(rows * chunks), kFT, 0, s>>>(x, g, chunk, static_cast<int>(chunks), cand,
+                                                                          stats);
+    MergeTopKernel<<<static_cast<unsigned>(rows), kFT, 0, s>>>(x, values, indices, g, static_cast<int>(chunks), cand,
+                                                               stats);
+    CheckLaunch("topk launch");
+}
+
 // The TopK launch sequence. `fixed` is the caller's scratch (fixed_bytes
 // long) or null, in which case the layer's grow-only workspace is used.
 void TopkImpl(const float* x, float* values, int64_t* indices, int64_t outer, int64_t dim, int64_t inner, int64_t k,
@@ -447,6 +1069,10 @@ void TopkImpl(const float* x, float* values, int64_t* indices, int64_t outer, in
         }
         SmallRowKernel<<<static_cast<unsigned>(rows), kThreads, 0, s>>>(x, values, indices, g, PowTwoAtLeast(dim));
         CheckLaunch("topk small-row launch");
+        return;
+    }
+    if (k <= kFastMaxK && rows <= kFastMaxRows) {
+        FastTopk(x, values, indices, rows, g, s, fixed, fixed_bytes);
         return;
     }
     // Long rows: about 2048 workgroups over all rows, >= 4096 keys each.

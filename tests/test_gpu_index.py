@@ -219,6 +219,29 @@ def test_topk_long_rows(gpu):
     _topk_case(z, 64)                                   # -0.0 ties with +0.0
 
 
+def test_topk_long_row_select_paths(gpu):
+    """Long rows with K <= 1024 select in two reads of the row plus a
+    per-row finish; each of the finish's ways is exercised:
+    the threshold bin's keys from the collected list or (past its capacity)
+    from the row again, and the keys tied on 24 bits ranked in LDS or (past
+    its capacity) radix-selected."""
+    r = rng(31)
+    _topk_case(randn((3, 50000), seed=32), 1)                        # K = 1
+    _topk_case(randn((2, 70000), seed=33), 1024)                     # the largest K of this path
+    spread = (1.0 + r.random((4, 100000)) * 0.125).astype(F)         # one 12-bit bin: the row reread, ranked ties
+    _topk_case(spread, 300)
+    same = np.full((2, 10000), 2.5, F)                               # one value: listed, radix-selected ties
+    _topk_case(same, 100)
+    inf = randn((2, 30000), seed=34)
+    inf[0, ::1000] = np.inf
+    inf[1, 5::777] = np.inf
+    inf[1, 7] = -np.inf
+    _topk_case(inf, 40)                                              # +inf ties, the top bin
+    few = np.zeros((2, 40000), F)
+    few[:, 123] = 1.0
+    _topk_case(few, 300)                                             # one key above the threshold bin
+
+
 def test_topk_errors(gpu):
     x = randn((3, 5))
     assert_same_error("TopK", [x, np.array(6, I)], [((3, 6), F), ((3, 6), I)])
