@@ -5,10 +5,10 @@ reference executor on CpuDevice (oracle/_ref) on the same seeded inputs.
 The reference's naive loops make the full ViT (562 GFLOP) a half-hour CPU
 run, so the full-size configs are pinned against fixtures the reference
 executor wrote in the build container (tests/golden/make_model_fixtures.py):
-ResNet-18 logits for all 32 images, the 12-layer ViT's logits at batch 2, and
-the detector's top scores, boxes and classes at batch 8. One ViT encoder
-layer and the detector at batch 2 also run live against the reference here;
-the 12-layer batch-16 ViT is further checked against its own batch-2 run.
+ResNet-18 logits for all 32 images, the 12-layer ViT's logits at batch 2 and
+at its configured batch 16 (all 16 images), and the detector's top scores,
+boxes and classes at batch 8. One ViT encoder layer and the detector at batch
+2 also run live against the reference here.
 TopK indices must be bit-exact: the reference TopK row is run on the GPU's
 own score tensor and must select the same indices and values."""
 
@@ -162,6 +162,19 @@ def test_vit_12_layers_matches_reference_fixture(gpu):
     (want,) = _fixture_for("vit_bs2", g, inputs)
     (got,) = _gpu_run(g, inputs, capture=True)
     compare(got, want, rtol=RTOL, atol=RTOL, what="ViT-B/16 12-layer bs2 logits")
+
+
+def test_vit_bs16_matches_reference_fixture(gpu):
+    """configs[3] at its own batch: all 16 images' logits against the
+    reference executor's batch-16 run (the fixture), eager and replayed,
+    within rel 2e-4. The batch-16 program takes other GEMM tile and split
+    choices than batch 2, so this pins the summation order the benchmark
+    geometry actually uses."""
+    g, inputs = workloads.vit_b16(batch=16, layers=12)
+    (want,) = _fixture_for("vit_bs16", g, inputs)
+    for capture in (False, True):
+        (got,) = _gpu_run(g, inputs, capture)
+        compare(got, want, rtol=RTOL, atol=RTOL, what=f"ViT-B/16 bs16 logits (capture={capture})")
 
 
 def test_detector_bs8_matches_reference_fixture(gpu):
