@@ -2487,6 +2487,106 @@ __global__ void ResidualActKernel(float* y, const float* residual, int act, int6
 // with P = D*H*W: a batched GEMM whose B batches are the images. The fused
 // form (residual, activation) runs the same GEMM and then ResidualActKernel, so a
 // Conv and a FusedConv of one geometry sum in the same order.
+// ---- Non-overlapping patches (stride = kernel, no padding): a GEMM -----------
+//
+// A conv whose windows tile the input exactly (the ViT patch embedding:
+// 16 x 16 windows at stride 16) reads every input element once, so it is a
+// plain GEMM once each image's patches are laid out as rows:
+//     P[b][p][k] = X[b][c][oh * KH + kh][ow * KW + kw],
+//     p = oh * OW + ow,  k = (c * KH + kh) * KW + kw,
+// and Y = W (M x K, the ONNX weight as it is) * P^T + bias over all images'
+// patches at once (B K-contiguous), the output written back per image in
+// NCHW (the engine's grouped output layout; the batched form with W
+// broadcast when the pixels per image are not whole quads).
+// PatchRowsKernel builds P: the OW patch rows of one band of KH input rows
+// (b, oh) are a contiguous run of OW * K floats, written by a few
+// workgroups, kPatchQuadsPerBlock floats x 4 each, one 16-byte load and
+// store per thread and step; the loads are runs of KW floats of X.
+constexpr int32_t kPatchQuadsPerBlock = 1024;
+__global__ __launch_bounds__(256) void PatchRowsKernel(const float* __restrict__ x, float* __restrict__ out,
+                                                       int32_t c, int32_t kh, int32_t kw, int32_t out_h,
+                                                       int32_t out_w, int32_t in_h, int32_t in_w, int32_t parts) {
+    const int64_t band = blockIdx.x / parts; // b * out_h + oh
+    const int32_t part = static_cast<int32_t>(blockIdx.x - band * parts);
+    const int64_t b = band / out_h;
+    const int32_t oh = static_cast<int32_t>(band - b * out_h);
+    const int32_t k_total = c * kh * kw;
+    const int32_t quads = out_w * k_total / 4;
+    const float* xb = x + (b * c * in_h + static_cast<int64_t>(oh) * kh) * in_w;
+    nert_floatx4* dst = reinterpret_cast<nert_floatx4*>(out + band * out_w * static_cast<int64_t>(k_total));
+    const int32_t end = min(quads, (part + 1) * kPatchQuadsPerBlock);
+    for (int32_t q = part * kPatchQuadsPerBlock + threadIdx.x; q < end; q += 256) {
+        const int32_t e = 4 * q;
+        const int32_t ow = e / k_total;
+        const int32_t k = e - ow * k_total;
+        const int32_t q_kw = k % kw;
+        const int32_t t = k / kw; // c * KH + kh
+        const int32_t r = t % kh;
+        const int32_t ch = t / kh;
+        const float* src = xb + (static_cast<int64_t>(ch) * in_h + r) * in_w + ow * kw + q_kw;
+        dst[q] = *reinterpret_cast<const nert_floatx4*>(src);
+    }
+}
+
+bool TryPatchGemm(const ConvArgs& p, hipStream_t stream) {
+    const bool tiles_exactly = p.k_d == 1 && p.in_d == 1 && p.out_d == 1 && p.group == 1 && p.s_h == p.k_h &&
+                               p.s_w == p.k_w && p.d_h == 1 && p.d_w == 1 && p.p_h == 0 && p.p_w == 0 &&
+                               p.in_h == p.out_h * p.k_h && p.in_w == p.out_w * p.k_w && p.k_h * p.k_w > 1;
+    // Four-float moves: KW and the row length multiples of 4, X 16-byte aligned.
+    const bool quads = p.k_w % 4 == 0 && p.in_w % 4 == 0 && (reinterpret_cast<uintptr_t>(p.x) & 15) == 0;
+    if (!tiles_exactly || !quads || p.batch > 65535 || p.batch * p.out_h * p.out_w * p.c >= (int64_t{1} << 31) ||
+        p.out_w * p.c * p.k_h * p.k_w >= (int64_t{1} << 31)) {
+        return false;
+    }
+    const int64_t k_total = p.c * p.k_h * p.k_w;
+    // Slot 1: the patch rows stay alive across the GEMM, which may take slot
+    // 0 for split-K partial sums.
+    auto* rows = static_cast<float*>(Workspace(p.batch * p.plane_out * k_total * static_cast<int64_t>(sizeof(float)),
+                                               stream, 1));
+    const int64_t band_quads = p.out_w * k_total / 4;
+    const int64_t parts = (band_quads + kPatchQuadsPerBlock - 1) / kPatchQuadsPerBlock;
+    PatchRowsKernel<<<static_cast<unsigned>(p.batch * p.out_h * parts), 256, 0, stream>>>(
+        p.x, rows, static_cast<int32_t>(p.c), p.k_h, p.k_w, p.out_h, p.out_w, p.in_h, p.in_w,
+        static_cast<int32_t>(parts));
+    CheckLaunch("PatchRowsKernel launch");
+    GemmArgs g{};
+    g.a = p.w;
+    g.b = rows;
+    g.y = p.y;
+    g.m = p.m;
+    g.k = k_total;
+    g.a_sm = k_total;
+    g.a_sk = 1;
+    g.b_sk = 1;
+    g.b_sn = k_total;
+    g.alpha = 1.0f;
+    g.beta = 1.0f;
+    g.has_bias = p.bias != nullptr ? 1 : 0;
+    g.bias = p.bias;
+    g.bias_sm = 1;
+    g.bias_sn = 0;
+    if (p.plane_out % 4 == 0 && p.n_total < (int64_t{1} << 31)) {
+        // One GEMM over every image's patches (N = batch x pixels, no
+        // per-image column tiles half empty), written back per image in NCHW.
+        g.n = p.n_total;
+        g.y_group = p.plane_out;
+        LaunchGemm(g, 1, stream);
+    } else {
+        g.n = p.plane_out;
+        g.batch_rank = 1;
+        g.bdims[0] = p.batch;
+        g.a_bs[0] = 0;
+        g.b_bs[0] = p.plane_out * k_total;
+        LaunchGemm(g, p.batch, stream);
+    }
+    if (p.residual != nullptr || p.act != 0) {
+        const int64_t n = p.batch * p.m * p.plane_out;
+        ResidualActKernel<<<GridFor(n, 256, 16384), 256, 0, stream>>>(p.y, p.residual, p.act, n);
+        CheckLaunch("ResidualActKernel launch");
+    }
+    return true;
+}
+
 bool TryPointwise(const ConvArgs& p, hipStream_t stream) {
     const bool unit = p.k_d == 1 && p.k_h == 1 && p.k_w == 1 && p.s_d == 1 && p.s_h == 1 && p.s_w == 1 &&
                       p.p_d == 0 && p.p_h == 0 && p.p_w == 0 && p.group == 1 && p.plane_in == p.plane_out;
@@ -2584,6 +2684,9 @@ extern "C" int nert_hip_conv_fused_f32(const float* x, const float* w, const flo
         }
         hipStream_t s = nert_hip::StreamOr(stream);
         if (nert_hip::TryPointwise(p, s)) {
+            return;
+        }
+        if (nert_hip::TryPatchGemm(p, s)) {
             return;
         }
         if (nert_hip::TrySmallChannelConv(p, s)) {

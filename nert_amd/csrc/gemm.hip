@@ -81,15 +81,20 @@ __device__ __forceinline__ void GemmEpilogue(const GemmArgs& p, const Accum<Shap
     const int wave_m = wave % Shape::kWavesM;
     const int wave_n = wave / Shape::kWavesM;
     const int half = lane >> 5;
+    // Finished outputs follow the output layout (GemmOutIndex); raw partial
+    // sums stay dense [m][n].
+    const bool grouped = finish && p.y_group > 0;
+    const int64_t row_stride = grouped ? p.y_group : p.n;
 #pragma unroll
     for (int j = 0; j < Shape::kSubN; ++j) {
         const int64_t gc = col0 + wave_n * Shape::kWaveN + 32 * j + (lane & 31);
         const bool col_ok = gc < p.n;
         const int64_t cc = col_ok ? gc : 0;
+        const int64_t col_base = grouped ? GemmOutIndex(p, 0, cc) : cc;
 #pragma unroll
         for (int i = 0; i < Shape::kSubM; ++i) {
             const int64_t r0 = row0 + wave_m * Shape::kWaveM + 32 * i + 4 * half;
-            float* base = out + r0 * p.n + cc;
+            float* base = out + r0 * row_stride + col_base;
             float value[16];
             bool ok[16];
 #pragma unroll
@@ -106,7 +111,7 @@ __device__ __forceinline__ void GemmEpilogue(const GemmArgs& p, const Accum<Shap
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 if (ok[v]) {
-                    base[(8 * (v >> 2) + (v & 3)) * p.n] = value[v];
+                    base[(8 * (v >> 2) + (v & 3)) * row_stride] = value[v];
                 }
             }
         }
@@ -203,7 +208,7 @@ __global__ void SplitReduceKernel(GemmArgs p, int splits, int64_t batches, int v
             for (int s = 1; s < splits; ++s) {
                 sum += p.partial[s * total + i + v];
             }
-            p.y[i + v] = FinishGemm(p, static_cast<float>(sum), r, c + v);
+            p.y[(i - e) + GemmOutIndex(p, r, c + v)] = FinishGemm(p, static_cast<float>(sum), r, c + v);
         }
     }
 }
@@ -249,7 +254,9 @@ __global__ __launch_bounds__(256) void SplitReduceQuadKernel(GemmArgs p, int spl
         for (int e = 0; e < 4; ++e) {
             out[e] = FinishGemm(p, static_cast<float>(sum[e]), r, 4 * cq + e);
         }
-        *reinterpret_cast<nert_floatx4*>(p.y + i) = out;
+        // Four columns of one output group (groups are whole quads).
+        const int64_t at = p.y_group > 0 ? GemmOutIndex(p, r, 4 * static_cast<int64_t>(cq)) : i;
+        *reinterpret_cast<nert_floatx4*>(p.y + at) = out;
     }
 }
 
@@ -324,7 +331,7 @@ __global__ __launch_bounds__(512) void SkinnyGemmKernel(GemmArgs p, int64_t k_sl
 }
 
 bool SkinnyApplies(const GemmArgs& p, int64_t batches) {
-    return batches == 1 && p.m <= 32 && p.a_sk == 1 && p.b_sk == 1 && p.k % 8 == 0 && p.a_sm % 4 == 0 &&
+    return batches == 1 && p.y_group == 0 && p.m <= 32 && p.a_sk == 1 && p.b_sk == 1 && p.k % 8 == 0 && p.a_sm % 4 == 0 &&
            p.b_sn % 4 == 0 && (reinterpret_cast<uintptr_t>(p.a) & 15) == 0 &&
            (reinterpret_cast<uintptr_t>(p.b) & 15) == 0 && p.k > 0 && (p.n + 31) / 32 < (int64_t{1} << 31);
 }
@@ -497,6 +504,9 @@ void LaunchGemm(GemmArgs p, int64_t batches, hipStream_t stream) {
     // Operand strides must make one of each pair unit (contiguous tensors).
     if (!(p.a_sk == 1 || p.a_sm == 1) || !(p.b_sn == 1 || p.b_sk == 1)) {
         throw Error("gemm: operands must be contiguous in one index");
+    }
+    if (p.y_group > 0 && (batches != 1 || p.y_group % 4 != 0 || p.n % p.y_group != 0)) {
+        throw Error("gemm: grouped output needs one batch and groups of whole quads dividing n");
     }
     const int fallback_shape = p.m <= 32 ? 2 : (TileCount<ShapeL>(p, batches) < 1024 ? 1 : 0);
     static std::mutex mu;

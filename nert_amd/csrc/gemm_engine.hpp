@@ -33,7 +33,21 @@ struct GemmArgs {
     // erf Gelu chain y -> y * (erf(y / act_div) + act_add) * act_mul.
     int act;
     float act_div, act_add, act_mul;
+    // Output layout (one batch only): 0, Y(m, n) at y[m * n_total + n]; G > 0
+    // (a multiple of 4 dividing n), the columns form groups of G stored as
+    // [n / G][m][n % G], e.g. a conv's NCHW output when n runs over (image,
+    // pixel) and G is the pixels per image.
+    int64_t y_group;
 };
+
+// Offset of output (r, c) under the layout above.
+__device__ __forceinline__ int64_t GemmOutIndex(const GemmArgs& p, int64_t r, int64_t c) {
+    if (p.y_group > 0) {
+        const int64_t g = c / p.y_group;
+        return (g * p.m + r) * p.y_group + (c - g * p.y_group);
+    }
+    return r * p.n + c;
+}
 
 void LaunchGemm(GemmArgs p, int64_t batches, hipStream_t stream);
 

@@ -134,6 +134,10 @@ CONV_CASES = [
     ((1, 2, 5, 6, 7), (3, 2, 2, 3, 3), {"pads": [1, 0, 1, 1, 1, 1]}),  # 3-D
     ((1, 8, 10, 10), (8, 1, 3, 3), {"group": 8, "pads": [1, 1, 1, 1]}),  # depthwise
     ((4, 64, 14, 14), (128, 64, 3, 3), {"pads": [1, 1, 1, 1], "strides": [2, 2]}),
+    # windows that tile the input exactly run as a GEMM over patch columns
+    ((2, 3, 32, 32), (48, 3, 16, 16), {"strides": [16, 16]}),    # the ViT patch embedding, small
+    ((3, 5, 12, 20), (7, 5, 2, 4), {"strides": [2, 4]}),        # non-square windows, odd channels
+    ((1, 4, 9, 9), (6, 4, 3, 3), {"strides": [3, 3]}),          # KW not a multiple of 4: the gather kernel
 ]
 
 
@@ -191,6 +195,16 @@ def test_conv_lds_patch_repeatable(gpu):
 
 # --- BASELINE.json configs at full size -----------------------------------
 
+def test_vit_patch_embedding_full_size(gpu):
+    """configs[3]'s patch embedding at full size: [16,3,224,224] * [768,3,16,16]
+    at stride 16, as patch columns and one batched GEMM, against the
+    restatement."""
+    xs, ws, attrs = (16, 3, 224, 224), (768, 3, 16, 16), {"strides": [16, 16]}
+    x, w, b = randn(xs, seed=70), randn(ws, seed=71, scale=0.02), randn((768,), seed=72, scale=0.02)
+    got = _hip("Conv", [x, w, b], _conv_out(xs, ws, attrs), attrs)
+    compare(got, restate.conv(x, w, b, [16, 16], None, None, 1, "NOTSET"), what="ViT patch embedding")
+
+
 def test_config0_conv_3x3(gpu):
     """X[1,64,56,56], W[64,64,3,3], B[64], pad 1 -> [1,64,56,56]."""
     x = randn((1, 64, 56, 56), seed=0)
@@ -244,6 +258,7 @@ FUSED_CASES = [
     ((24, 3, 224, 224), (64, 3, 7, 7), {"pads": [3, 3, 3, 3], "strides": [2, 2]}),  # stem, 2-3 blocks per workgroup
     ((2, 32, 9, 9), (48, 32, 1, 1), {}),                                            # pointwise shape
     ((1, 64, 20, 20), (64, 16, 3, 3), {"pads": [1, 1, 1, 1], "group": 4}),          # groups
+    ((2, 3, 64, 64), (40, 3, 8, 8), {"strides": [8, 8]}),                           # patch columns + GEMM
 ]
 
 
