@@ -20,7 +20,8 @@
 // memory-bound), LayerNorm/InstanceNorm two-pass double statistics
 // (layer_normalization.cpp:134-159, instance_normalization.cpp:80-103),
 // ArgMax's sequential first/last-maximum rule (arg_max.cpp:41-57) and
-// CumSum's sequential scan (cum_sum.cpp:40-70).
+// CumSum's sequential scan (cum_sum.cpp:40-70), and a block scan per row
+// when the scan axis is contiguous.
 
 #include "common.hpp"
 #include "../../include/nert_hip.h"
@@ -1002,6 +1003,66 @@ __global__ void CumSumKernel(const T* __restrict__ x, T* __restrict__ y, int64_t
     }
 }
 
+// Contiguous scan axis (inner == 1): one workgroup per row scans it in
+// chunks of 1024 positions, four consecutive positions per thread: each
+// thread's running sum over its four, a block-wide exclusive scan of the
+// thread totals (wave shuffles, then the four wave totals), plus the carry of
+// the chunks before. Sums in Acc (double for float rows, like the sequential
+// kernel; the association differs only inside double precision).
+template <typename T, typename Acc>
+__global__ __launch_bounds__(256) void CumSumRowsKernel(const T* __restrict__ x, T* __restrict__ y, int64_t dim,
+                                                        int exclusive, int reverse) {
+    constexpr int kPer = 4;
+    __shared__ Acc wave_total[4];
+    const int64_t row = blockIdx.x;
+    const T* xr = x + row * dim;
+    T* yr = y + row * dim;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    Acc carry = Acc{};
+    for (int64_t base = 0; base < dim; base += 256 * kPer) {
+        Acc v[kPer];
+        Acc total = Acc{};
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) {
+            const int64_t pos = base + threadIdx.x * kPer + e; // position in scan order
+            v[e] = pos < dim ? static_cast<Acc>(xr[reverse ? dim - 1 - pos : pos]) : Acc{};
+            total += v[e];
+        }
+        Acc incl = total;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const Acc up = __shfl_up(incl, off, 64);
+            if (lane >= off) {
+                incl += up;
+            }
+        }
+        if (lane == 63) {
+            wave_total[wave] = incl;
+        }
+        __syncthreads();
+        Acc before = carry + (incl - total);
+        Acc block_total = Acc{};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            before += w < wave ? wave_total[w] : Acc{};
+            block_total += wave_total[w];
+        }
+        __syncthreads(); // wave_total is rewritten by the next chunk
+        Acc run = before;
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) {
+            const int64_t pos = base + threadIdx.x * kPer + e;
+            const Acc out = exclusive ? run : run + v[e];
+            run += v[e];
+            if (pos < dim) {
+                yr[reverse ? dim - 1 - pos : pos] = static_cast<T>(out);
+            }
+        }
+        carry += block_total;
+    }
+}
+
 unsigned RowBlocks(int64_t rows) {
     const int64_t b = (rows + 3) / 4;
     if (b > 0x7FFFFFFF) {
@@ -1241,6 +1302,17 @@ int nert_hip_cumsum(int dtype, const void* x, void* y, int64_t outer, int64_t di
             return;
         }
         hipStream_t s = StreamOr(stream);
+        if (inner == 1 && dim >= 64 && outer <= 0x7FFFFFFF) {
+            if (dtype == NERT_F32) {
+                CumSumRowsKernel<float, double><<<static_cast<unsigned>(outer), 256, 0, s>>>(
+                    static_cast<const float*>(x), static_cast<float*>(y), dim, exclusive, reverse);
+            } else {
+                CumSumRowsKernel<int64_t, int64_t><<<static_cast<unsigned>(outer), 256, 0, s>>>(
+                    static_cast<const int64_t*>(x), static_cast<int64_t*>(y), dim, exclusive, reverse);
+            }
+            CheckLaunch("cumsum launch");
+            return;
+        }
         if (dtype == NERT_F32) {
             CumSumKernel<float, double><<<GridFor(outer * inner, 256, 8192), 256, 0, s>>>(
                 static_cast<const float*>(x), static_cast<float*>(y), outer, dim, inner, exclusive, reverse);

@@ -1,5 +1,5 @@
-"""Op-level measurement cases: the reference's published op-bench fixtures
-(olibartfast/nert bench/runtime/main.cpp:331-674, the twelve quoted with
+"""Op-level measurement cases: all 49 of the reference's op-bench fixtures
+(olibartfast/nert bench/runtime/main.cpp:331-674; twelve of them quoted with
 MI300X figures), BASELINE.json configs[0] and configs[1](a)(b)(c), and the
 bandwidth-bound rows at the shapes configs[2] and configs[3] run them.
 
@@ -23,7 +23,7 @@ import numpy as np
 from .graph import Graph
 from .workloads import Rng
 
-F32, I64 = np.float32, np.int64
+F32, I64, BOOL = np.float32, np.int64, np.bool_
 
 
 @dataclass
@@ -38,6 +38,7 @@ class OpCase:
     initializers: dict = field(default_factory=dict)
     mi300x_ms: float | None = None
     source: str = ""
+    order: list[str] | None = None  # node input order, when inputs and initializers interleave
 
     def graph(self) -> Graph:
         g = Graph()
@@ -45,7 +46,7 @@ class OpCase:
             g.add_input(n, dtype, shape)
         for n, v in self.initializers.items():
             g.add_initializer(n, v)
-        names = [s[0] for s in self.inputs_spec] + list(self.initializers)
+        names = self.order or [s[0] for s in self.inputs_spec] + list(self.initializers)
         outs = g.add_node(self.op, names, [(n, d, s) for n, s, d in self.outputs_spec], self.attrs, name=self.name)
         g.outputs.extend(outs)
         return g
@@ -61,6 +62,29 @@ def _u(lo, hi):
 
 def _nrm(std):
     return lambda rng, shape: rng.normal(shape, 0.0, std)
+
+
+def _signed(lo, hi):
+    """|v| ~ U(lo, hi) with a random sign (the Div fixture's divisor)."""
+    def make(rng, shape):
+        mag = rng.uniform(shape, lo, hi)
+        return np.where(rng.uniform(shape, 0.0, 1.0) < 0.5, -mag, mag)
+    return make
+
+
+def _bool(rng, shape):
+    return rng.uniform(shape, 0.0, 1.0) < 0.5
+
+
+def _with_nans(lo, hi):
+    """U(lo, hi) with a NaN at element 17 and a negative NaN at 9001 (the
+    IsNaN fixture)."""
+    def make(rng, shape):
+        x = rng.uniform(shape, lo, hi).astype(F32)
+        x.reshape(-1)[17] = np.nan
+        x.reshape(-1)[9001] = -np.float32(np.nan)
+        return x
+    return make
 
 
 def _bytes(*shapes_dtypes) -> float:
@@ -109,6 +133,82 @@ def _cases() -> list[OpCase]:
     c.append(OpCase("argmax_1024x1024", "ArgMax", [("x", (1024, 1024), F32, _u(-3, 3))], [("y", (1024, 1), I64)],
                     "hbm", _bytes(((1024, 1024), F32), ((1024, 1), I64)), {"axis": 1}, mi300x_ms=0.27,
                     source=f"{src}:578-586"))
+    # --- the rest of the reference's op-bench fixtures (no published MI300X figure) ---
+    c.append(OpCase("tanh_4m", "Tanh", [("x", (K_BIG,), F32, _u(-6, 6))], [("y", (K_BIG,), F32)], "hbm",
+                    _bytes(((K_BIG,), F32), ((K_BIG,), F32)), source=f"{src}:347-355"))
+    for op in ("Mul", "Sub"):
+        c.append(OpCase(f"{op.lower()}_2048x2048", op,
+                        [("a", (2048, 2048), F32, _u(-3, 3)), ("b", (2048,), F32, _u(-3, 3))],
+                        [("y", (2048, 2048), F32)], "hbm",
+                        _bytes(((2048, 2048), F32), ((2048,), F32), ((2048, 2048), F32)), source=f"{src}:356-365"))
+    c.append(OpCase("div_4m", "Div", [("a", (K_BIG,), F32, _u(-3, 3)), ("b", (K_BIG,), F32, _signed(0.5, 2.0))],
+                    [("y", (K_BIG,), F32)], "hbm", _bytes(((K_BIG,), F32), ((K_BIG,), F32), ((K_BIG,), F32)),
+                    source=f"{src}:366-381"))
+    c.append(OpCase("averagepool_8x64x112x112", "AveragePool", [("x", (8, 64, 112, 112), F32, _u(-3, 3))],
+                    [("y", (8, 64, 55, 55), F32)], "hbm", _bytes(((8, 64, 112, 112), F32), ((8, 64, 55, 55), F32)),
+                    {"kernel_shape": [3, 3], "strides": [2, 2]}, source=f"{src}:382-392"))
+    c.append(OpCase("reshape_2x3x4", "Reshape", [("x", (2, 3, 4), F32, _u(-1, 1))], [("y", (6, 4), F32)], "hbm",
+                    _bytes(((2, 3, 4), F32), ((6, 4), F32)), {}, {"shape": np.array([6, 4], I64)},
+                    source=f"{src}:402-410"))
+    for op, lo, hi in (("Sin", -6, 6), ("Cos", -6, 6), ("Exp", -6, 3), ("Elu", -6, 6), ("Log", 0.1, 6),
+                       ("Floor", -6, 6), ("Abs", -6, 6), ("Neg", -6, 6), ("Sqrt", 0, 16)):
+        c.append(OpCase(f"{op.lower()}_1m", op, [("x", (K_NEW,), F32, _u(lo, hi))], [("y", (K_NEW,), F32)], "hbm",
+                        _bytes(((K_NEW,), F32), ((K_NEW,), F32)), source=f"{src}:429-441"))
+    c.append(OpCase("isnan_1m", "IsNaN", [("x", (K_NEW,), F32, _with_nans(-3, 3))], [("y", (K_NEW,), BOOL)],
+                    "hbm", _bytes(((K_NEW,), F32), ((K_NEW,), BOOL)), source=f"{src}:442-453"))
+    for op in ("Greater", "Less", "GreaterOrEqual", "LessOrEqual"):
+        c.append(OpCase(f"{op.lower()}_1024x1024", op,
+                        [("a", (1024, 1024), F32, _u(-3, 3)), ("b", (1024,), F32, _u(-3, 3))],
+                        [("y", (1024, 1024), BOOL)], "hbm",
+                        _bytes(((1024, 1024), F32), ((1024,), F32), ((1024, 1024), BOOL)), source=f"{src}:454-463"))
+    for op in ("And", "Or"):
+        c.append(OpCase(f"{op.lower()}_1024x1024", op,
+                        [("a", (1024, 1024), BOOL, _bool), ("b", (1024,), BOOL, _bool)],
+                        [("y", (1024, 1024), BOOL)], "hbm",
+                        _bytes(((1024, 1024), BOOL), ((1024,), BOOL), ((1024, 1024), BOOL)), source=f"{src}:464-473"))
+    c.append(OpCase("not_1m", "Not", [("x", (K_NEW,), BOOL, _bool)], [("y", (K_NEW,), BOOL)], "hbm",
+                    _bytes(((K_NEW,), BOOL), ((K_NEW,), BOOL)), source=f"{src}:474-482"))
+    c.append(OpCase("pow_1024x1024", "Pow", [("a", (1024, 1024), F32, _u(0.5, 2)), ("b", (1024,), F32, _u(-1, 1))],
+                    [("y", (1024, 1024), F32)], "hbm",
+                    _bytes(((1024, 1024), F32), ((1024,), F32), ((1024, 1024), F32)), source=f"{src}:483-491"))
+    for op in ("Max", "Min"):
+        c.append(OpCase(f"{op.lower()}_1024x1024_fold3", op,
+                        [("a", (1024, 1024), F32, _u(-3, 3)), ("b", (1024,), F32, _u(-3, 3)),
+                         ("c", (1,), F32, _u(-3, 3))],
+                        [("y", (1024, 1024), F32)], "hbm",
+                        _bytes(((1024, 1024), F32), ((1024,), F32), ((1,), F32), ((1024, 1024), F32)),
+                        source=f"{src}:493-502"))
+    c.append(OpCase("clip_1m", "Clip", [("x", (K_NEW,), F32, _u(-5, 5))], [("y", (K_NEW,), F32)], "hbm",
+                    _bytes(((K_NEW,), F32), ((K_NEW,), F32)), {},
+                    {"min": np.array([0.0], F32), "max": np.array([1.0], F32)}, source=f"{src}:503-512"))
+    c.append(OpCase("identity_1m", "Identity", [("x", (K_NEW,), F32, _u(-3, 3))], [("y", (K_NEW,), F32)], "hbm",
+                    _bytes(((K_NEW,), F32), ((K_NEW,), F32)), source=f"{src}:513-520"))
+    c.append(OpCase("squeeze_1x1024x1", "Squeeze", [("x", (1, 1024, 1), F32, _u(-3, 3))], [("y", (1024,), F32)],
+                    "hbm", _bytes(((1, 1024, 1), F32), ((1024,), F32)), source=f"{src}:522-529"))
+    c.append(OpCase("tile_1024x1", "Tile", [("x", (1024, 1), F32, _u(-3, 3))], [("y", (2048, 3), F32)], "hbm",
+                    _bytes(((1024, 1), F32), ((2048, 3), F32)), {}, {"repeats": np.array([2, 3], I64)},
+                    source=f"{src}:531-538"))
+    c.append(OpCase("range_1m", "Range", [], [("y", (K_NEW,), F32)], "hbm", _bytes(((K_NEW,), F32)), {},
+                    {"start": np.array([0.0], F32), "limit": np.array([float(K_NEW)], F32),
+                     "delta": np.array([1.0], F32)}, source=f"{src}:540-547"))
+    c.append(OpCase("eyelike_1024x1024", "EyeLike", [("x", (1024, 1024), F32, _u(-1, 1))],
+                    [("y", (1024, 1024), F32)], "hbm", _bytes(((1024, 1024), F32)), source=f"{src}:549-556"))
+    c.append(OpCase("pad_1024x1024", "Pad", [("x", (1024, 1024), F32, _u(-3, 3))], [("y", (1026, 1026), F32)],
+                    "hbm", _bytes(((1024, 1024), F32), ((1026, 1026), F32)), {},
+                    {"pads": np.array([1, 1, 1, 1], I64)}, source=f"{src}:558-566"))
+    for op in ("ReduceSum", "ReduceL2"):
+        c.append(OpCase(f"{op.lower()}_1024x1024", op, [("x", (1024, 1024), F32, _u(-3, 3))],
+                        [("y", (1024, 1), F32)], "hbm", _bytes(((1024, 1024), F32), ((1024, 1), F32)), {},
+                        {"axes": np.array([1], I64)}, source=f"{src}:568-577"))
+    c.append(OpCase("cumsum_1024x1024", "CumSum", [("x", (1024, 1024), F32, _u(-3, 3))],
+                    [("y", (1024, 1024), F32)], "hbm", _bytes(((1024, 1024), F32), ((1024, 1024), F32)), {},
+                    {"axis": np.array([1], I64)}, source=f"{src}:588-597"))
+    c.append(OpCase("scatternd_1024x1024", "ScatterND",
+                    [("x", (1024, 1024), F32, _u(-3, 3)), ("updates", (1024, 1024), F32, _u(-3, 3))],
+                    [("y", (1024, 1024), F32)], "hbm",
+                    _bytes(((1024, 1024), F32), ((1024, 1), I64), ((1024, 1024), F32), ((1024, 1024), F32)), {},
+                    {"indices": np.arange(1024, dtype=I64).reshape(1024, 1)}, source=f"{src}:598-612",
+                    order=["x", "indices", "updates"]))
     # --- BASELINE.json configs[0] and configs[1] ---
     c.append(OpCase("cfg0_conv_1x64x56x56", "Conv",
                     [("x", (1, 64, 56, 56), F32, _nrm(1.0)), ("w", (64, 64, 3, 3), F32, _nrm(np.sqrt(2 / 576))),

@@ -162,3 +162,10 @@ def test_cumsum(gpu, exclusive, reverse):
         assert_parity("CumSum", [x, np.array(axis, I)], [(x.shape, F)], {"exclusive": exclusive, "reverse": reverse})
     xi = rng(20).integers(-9, 9, (4, 6)).astype(I)
     assert_parity("CumSum", [xi, np.array([1], I)], [(xi.shape, I)], {"exclusive": exclusive, "reverse": reverse})
+    # Contiguous scan axes take the block scan per row: one chunk, several
+    # chunks with a ragged last one, and int64 rows (exact).
+    for shape in ((5, 300), (3, 2500)):
+        xr = randn(shape, seed=21)
+        assert_parity("CumSum", [xr, np.array(-1, I)], [(shape, F)], {"exclusive": exclusive, "reverse": reverse})
+    xl = rng(22).integers(-2**40, 2**40, (2, 3000)).astype(I)
+    assert_parity("CumSum", [xl, np.array(1, I)], [(xl.shape, I)], {"exclusive": exclusive, "reverse": reverse})
