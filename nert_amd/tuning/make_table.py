@@ -26,7 +26,7 @@ HERE = Path(__file__).resolve().parent
 ROOT = HERE.parent.parent
 
 WORKLOADS = [
-    ("resnet18", {"batch": 32}), ("resnet18", {"batch": 2}),
+    ("resnet18", {"batch": 32}), ("resnet18", {"batch": 2}), ("resnet18", {"batch": 1}),
     ("vit_b16", {"batch": 16}), ("vit_b16", {"batch": 2, "layers": 1}),
     ("detector", {"batch": 8}), ("detector", {"batch": 2}),
 ]
