@@ -7,8 +7,11 @@ BASELINE.json: BN folded, [32,3,224,224] -> [32,1000]) through the gfx950
 HipDevice rows, with weights and the input already resident in HBM. The
 runner (nert_amd.runner.Program) first fuses each Conv -> [Add] -> [Relu]
 chain into one FusedConv row (bias, residual and Relu in the conv epilogue,
-bit-identical outputs) and turns the Flatten into a view, leaving 23 of the
-49 rows; they are captured once into a HIP graph and replayed. K replays are
+bit-identical outputs), pairs each stage's 3x3/2 conv with its 1x1/2
+downsampling shortcut (one launch computes both; the shortcut's sums run in
+another order, within the parity bar) and turns the Flatten into a view,
+leaving 20 of the 49 rows; they are captured once into a HIP graph and
+replayed. K replays are
 timed with HIP events on the layer stream, bracketed by stream syncs. The
 step's logits must match the reference executor's (the committed fixture
 tests/golden/models/resnet18_bs32.npz, all 32 images, and the live
@@ -332,13 +335,15 @@ def main() -> int:
             "nodes": len(g.nodes),
             "rows_after_fusion": len(pg.nodes),
             "gflop_per_step": round(g.flops() / 1e9, 3),
-            "launch": "nert_amd runner: HIP graph replay after Conv->Add->Relu fusion (bit-identical outputs) "
-                      "and view aliasing; the drop-in seam path is reported under 'dropin'",
+            "launch": "nert_amd runner: HIP graph replay after Conv->Add->Relu fusion (bit-identical outputs), "
+                      "each stage's 3x3/2 conv paired with its 1x1/2 shortcut in one launch, and view aliasing; "
+                      "the drop-in seam path is reported under 'dropin'",
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "Conv rows (implicit-GEMM conv kernels, split tiles finished inside the kernel; 17 of 20 "
-                      "carry the fused Add/Relu epilogue), 20 per step",
+            "kernel": f"Conv rows (implicit-GEMM conv kernels, split tiles finished inside the kernel; fused "
+                      f"Add/Relu epilogues; 3 rows also compute their stage's 1x1 shortcut), {len(conv_idx)} per "
+                      f"step for the 20 convolutions",
             "achieved": round(achieved, 3),
             "peak": PEAK_FP32_MFMA_TFLOPS,
             "unit": "TFLOP/s",
@@ -488,10 +493,16 @@ def measured_traffic() -> dict | None:
 
 
 def conv_row_flops(g, idx: int) -> int:
+    """2 * MACs of a Conv or FusedConv row; a paired FusedConv (six inputs,
+    two outputs) also counts its 1x1 convolution."""
     n = g.nodes[idx]
     w = g.tensors[n.inputs[1]][1]
     y = g.tensors[n.outputs[0]][1]
-    return 2 * int(np.prod(y)) * int(np.prod(w[1:]))
+    flops = 2 * int(np.prod(y)) * int(np.prod(w[1:]))
+    if n.op == "FusedConv" and len(n.inputs) == 6 and len(n.outputs) == 2:
+        w2 = g.tensors[n.inputs[4]][1]
+        flops += 2 * int(np.prod(g.tensors[n.outputs[1]][1])) * int(np.prod(w2[1:]))
+    return flops
 
 
 if __name__ == "__main__":

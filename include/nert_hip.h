@@ -184,6 +184,21 @@ int nert_hip_conv_f32(const float* x, const float* w, const float* bias, float* 
  * the runner in nert_amd fuses them through the FusedConv row. */
 int nert_hip_conv_fused_f32(const float* x, const float* w, const float* bias, const float* residual, float* y,
                             const nert_conv_desc* d, int act, void* stream);
+/* Two convolutions of one input in one launch: y = act(conv3x3(x, w) + bias
+ * + residual) as nert_hip_conv_fused_f32 computes it, and y2 = conv1x1(x, w2)
+ * + bias2 at the same stride with pad 0 (w2 [M][C]; bias2 optional, NULL).
+ * `d` describes the 3x3 convolution, which must have pad 1, dilation 1 and
+ * group 1; y2 has y's shape. The 1x1 reads exactly the 3x3's centre-tap
+ * inputs (a ResNet block's first conv and its downsampling shortcut), so it
+ * shares the 3x3's staged input. y is bit-identical to
+ * nert_hip_conv_fused_f32 with the same kernel configuration; y2 differs
+ * from nert_hip_conv_f32 of the 1x1 only in the order of its fp32 additions.
+ * No reference counterpart: the reference runs the two Conv rows separately
+ * (src/executor.cpp:480-535); nert_amd's runner pairs them through the
+ * FusedConv row (six inputs, two outputs). */
+int nert_hip_conv_pair_f32(const float* x, const float* w, const float* bias, const float* residual, float* y,
+                           const float* w2, const float* bias2, float* y2, const nert_conv_desc* d, int act,
+                           void* stream);
 
 /* ---------------------------------------------------------- elementwise --- */
 

@@ -765,11 +765,36 @@ struct HaloGeom {
     uint32_t* counters;
     float* split_slots;
     int32_t tiles;
+    // Paired 1x1 convolution (HaloConvKernel<..., true>): Y2 = X (*) W2 + B2
+    // at the same stride, pad 0, which reads exactly the centre tap's inputs
+    // (the 3x3 conv has pad 1 and dilation 1). W2 is [M][C]; each lane loads
+    // its own MFMA operands of a channel block straight into registers (no
+    // LDS, so the paired launch keeps the plain launch's occupancy). Split
+    // parts of Y2 go to split_slots2 / tail_partial2 the way the main
+    // output's go to the fields above, under the same tile counter
+    // (FinishSplitTilePair).
+    const float* w2;
+    const float* bias2;
+    float* y2;
+    float* split_slots2;
+    float* tail_partial2;
 };
+
+// The epilogue arguments of a paired 1x1 output: its own output and bias,
+// no summand, no activation.
+__device__ __forceinline__ ConvArgs PairArgs(const ConvArgs& p, const HaloGeom& h) {
+    ConvArgs q = p;
+    q.y = h.y2;
+    q.bias = h.bias2;
+    q.residual = nullptr;
+    q.act = 0;
+    q.partial = nullptr;
+    return q;
+}
 
 // Register budget: 128 VGPRs (four waves per SIMD, two workgroups per CU),
 // except with four patch positions per thread, where that would spill.
-template <class Shape, int KH, int KW, int NPOS>
+template <class Shape, int KH, int KW, int NPOS, bool PAIR = false>
 __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKernel(ConvArgs p, HaloGeom h) {
     constexpr int BM = Shape::kBM;
     constexpr int BN = Shape::kBN;
@@ -782,6 +807,7 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
     constexpr int kQuadsRow = kTaps * BK / 4;                      // 16-byte weight loads per row and block
     constexpr int kAQuads = (BM * kQuadsRow + THREADS - 1) / THREADS; // weight loads per thread
     static_assert(BK % 8 == 0 && (kTaps * BK) % 4 == 0, "weight rows must split into 16-byte loads");
+    constexpr int kCentre = (KH / 2) * KW + KW / 2; // the tap a paired 1x1 shares
     extern __shared__ __attribute__((aligned(16))) float smem[];
     float* const as = smem;
     float* const bs = smem + BM * kAPitch;
@@ -871,6 +897,16 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
         avoff[j] = e < BM * kQuadsRow && m < p.mg ? static_cast<uint32_t>(((g * p.mg + m) * p.kg + k0) * 4)
                                                   : kOutOfRange;
     }
+    const __amdgpu_buffer_rsrc_t w2r = MakeRsrc(PAIR ? h.w2 : p.w, static_cast<uint32_t>(p.m * p.cg * 4));
+    // Paired 1x1 operands: lane l of sub-block i takes row l % 32 and, for
+    // channel group g of a block, channels 8 g + 4 (l / 32) .. + 3 -- the
+    // A-fragment layout of the main weights, read from W2 [m][c] directly.
+    uint32_t a2off[PAIR ? Shape::kSubM : 1];
+#pragma unroll
+    for (int i = 0; i < (PAIR ? Shape::kSubM : 0); ++i) {
+        const int64_t m = row0 + wave_m * Shape::kWaveM + 32 * i + (lane & 31);
+        a2off[i] = m < p.mg ? static_cast<uint32_t>((m * p.cg + half * 4) * 4) : kOutOfRange;
+    }
 
     // MFMA operand bases: A row of this lane, B patch position of the window
     // origin of each of the wave's pixel columns.
@@ -896,6 +932,8 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
 
     float bv[NPOS][BK];
     nert_floatx4 av[kAQuads];
+    nert_floatx4 a2n[PAIR ? Shape::kSubM : 1][KG];
+    nert_floatx4 a2v[PAIR ? Shape::kSubM : 1][KG];
     auto load = [&](int cb) {
         const uint32_t c_off = static_cast<uint32_t>(cb * BK) * plane_bytes;
 #pragma unroll
@@ -910,6 +948,15 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
         for (int j = 0; j < kAQuads; ++j) {
             av[j] = __builtin_bit_cast(nert_floatx4, __builtin_amdgcn_raw_buffer_load_b128(
                                                          wr, static_cast<int>(avoff[j]), static_cast<int>(w_off), 0));
+        }
+#pragma unroll
+        for (int i = 0; i < (PAIR ? Shape::kSubM : 0); ++i) {
+#pragma unroll
+            for (int g = 0; g < KG; ++g) {
+                a2n[i][g] = __builtin_bit_cast(nert_floatx4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                 w2r, static_cast<int>(a2off[i]),
+                                                                 static_cast<int>((cb * BK + 8 * g) * 4), 0));
+            }
         }
     };
     auto store = [&]() {
@@ -939,10 +986,21 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
                 }
             }
         }
+#pragma unroll
+        for (int i = 0; i < (PAIR ? Shape::kSubM : 0); ++i) {
+#pragma unroll
+            for (int g = 0; g < KG; ++g) {
+                a2v[i][g] = a2n[i][g];
+            }
+        }
     };
 
     Accum<Shape> acc;
     acc.zero();
+    Accum<Shape> acc2;
+    if constexpr (PAIR) {
+        acc2.zero();
+    }
     if (cb_begin < cb_end) {
         load(cb_begin);
     }
@@ -1013,6 +1071,25 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
                     }
                 }
             }
+            if constexpr (PAIR) {
+                if (t == kCentre) {
+                    // The paired 1x1 conv reads the centre tap's inputs.
+#pragma unroll
+                    for (int g = 0; g < KG; ++g) {
+#pragma unroll
+                        for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+                            for (int i = 0; i < Shape::kSubM; ++i) {
+#pragma unroll
+                                for (int j = 0; j < Shape::kSubN; ++j) {
+                                    acc2.c[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a2v[i][g][kk], b[j][g][kk],
+                                                                                         acc2.c[i][j], 0, 0, 0);
+                                }
+                            }
+                        }
+                    }
+                }
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
         __syncthreads();
@@ -1032,7 +1109,15 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
             parts = static_cast<int>(gridDim.z);
             slots = h.split_slots + t * parts * BM * BN;
         }
-        if (FinishSplitTile<Shape, float>(acc, slots, h.counters + t, part, parts, reinterpret_cast<int*>(smem))) {
+        if constexpr (PAIR) {
+            float* slots2 = piece >= 0 ? h.tail_partial2 + t * parts * BM * BN : h.split_slots2 + t * parts * BM * BN;
+            if (FinishSplitTilePair<Shape, float>(acc, slots, acc2, slots2, h.counters + t, part, parts,
+                                                  reinterpret_cast<int*>(smem))) {
+                ConvEpilogue<Shape>(p, acc, row0, col0, g, 0);
+                ConvEpilogue<Shape>(PairArgs(p, h), acc2, row0, col0, g, 0);
+            }
+        } else if (FinishSplitTile<Shape, float>(acc, slots, h.counters + t, part, parts,
+                                                 reinterpret_cast<int*>(smem))) {
             ConvEpilogue<Shape>(p, acc, row0, col0, g, 0);
         }
         return;
@@ -1043,6 +1128,10 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
         return;
     }
     ConvEpilogue<Shape>(p, acc, row0, col0, g, split);
+    if constexpr (PAIR) {
+        // Paired launches are never split without the in-kernel finish.
+        ConvEpilogue<Shape>(PairArgs(p, h), acc2, row0, col0, g, 0);
+    }
 }
 
 // Sums each tail tile's pieces in piece order (deterministic) and applies the
@@ -1147,8 +1236,24 @@ using HaloShapeQ16 = TileShape<64, 64, 16, 2, 2>;
 using HaloShapeN16 = TileShape<32, 128, 16, 1, 4>;
 
 template <class Shape, int NPOS>
-void LaunchHalo(const ConvArgs& p, const HaloGeom& h, dim3 grid, size_t lds, hipStream_t stream) {
-    HaloConvKernel<Shape, 3, 3, NPOS><<<grid, Shape::kThreads, lds, stream>>>(p, h);
+void LaunchHaloPos(const ConvArgs& p, const HaloGeom& h, dim3 grid, size_t lds, hipStream_t stream) {
+    if (h.w2 != nullptr) {
+        HaloConvKernel<Shape, 3, 3, NPOS, true><<<grid, Shape::kThreads, lds, stream>>>(p, h);
+    } else {
+        HaloConvKernel<Shape, 3, 3, NPOS><<<grid, Shape::kThreads, lds, stream>>>(p, h);
+    }
+}
+
+template <class Shape>
+void LaunchHalo(const ConvArgs& p, const HaloGeom& h, dim3 grid, size_t lds, int64_t per_thread,
+                hipStream_t stream) {
+    if (per_thread == 1) {
+        LaunchHaloPos<Shape, 1>(p, h, grid, lds, stream);
+    } else if (per_thread == 2) {
+        LaunchHaloPos<Shape, 2>(p, h, grid, lds, stream);
+    } else {
+        LaunchHaloPos<Shape, 4>(p, h, grid, lds, stream);
+    }
 }
 
 // Shapes with 16-channel K steps need more than the 64 KiB default of
@@ -1165,6 +1270,12 @@ bool AllowHaloLds() {
         ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(&HaloConvKernel<Shape, 3, 3, 2>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, kHaloMaxLds16) == hipSuccess;
         ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(&HaloConvKernel<Shape, 3, 3, 4>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kHaloMaxLds16) == hipSuccess;
+        ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(&HaloConvKernel<Shape, 3, 3, 1, true>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kHaloMaxLds16) == hipSuccess;
+        ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(&HaloConvKernel<Shape, 3, 3, 2, true>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kHaloMaxLds16) == hipSuccess;
+        ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(&HaloConvKernel<Shape, 3, 3, 4, true>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, kHaloMaxLds16) == hipSuccess;
         if (!ok) {
             (void)hipGetLastError();
@@ -1193,8 +1304,16 @@ inline int BalancedSplits(int64_t tiles, int blocks) {
     return best;
 }
 
+// The paired 1x1 output of a launch (HaloGeom::w2): null for a plain conv.
+struct HaloPair {
+    const float* w2;
+    const float* bias2;
+    float* y2;
+};
+
 template <class Shape>
-bool TryHaloShape(ConvArgs p, hipStream_t stream, int force_splits, bool tail = false) {
+bool TryHaloShape(ConvArgs p, hipStream_t stream, int force_splits, bool tail = false,
+                  const HaloPair* pair = nullptr) {
     constexpr int kTaps = 9;
     HaloGeom h{};
     h.pw = (p.out_w - 1) * p.s_w + 2 * p.d_w + 1;
@@ -1210,6 +1329,14 @@ bool TryHaloShape(ConvArgs p, hipStream_t stream, int force_splits, bool tail = 
         return false;
     }
     const int64_t lds = (static_cast<int64_t>(Shape::kBM) * (kTaps * BK + 4) + positions * (BK + 4)) * 4;
+    if (pair != nullptr) {
+        if (p.group != 1) {
+            return false;
+        }
+        h.w2 = pair->w2;
+        h.bias2 = pair->bias2;
+        h.y2 = pair->y2;
+    }
     if (lds > (BK > 8 ? kHaloMaxLds16 : kHaloMaxLds) || (lds > kHaloMaxLds && !AllowHaloLds<Shape>())) {
         return false;
     }
@@ -1249,19 +1376,20 @@ bool TryHaloShape(ConvArgs p, hipStream_t stream, int force_splits, bool tail = 
         h.n_full = static_cast<int32_t>(n_full);
         h.blocks_per_split = h.blocks;
         const int64_t per_tile = static_cast<int64_t>(Shape::kBM) * Shape::kBN;
-        h.tail_partial = static_cast<float*>(
-            Workspace(rest * h.tail_pieces * per_tile * static_cast<int64_t>(sizeof(float)), stream));
+        const int64_t outputs = pair != nullptr ? 2 : 1;
         h.counters = TileCounters(rest);
+        if (pair != nullptr && h.counters == nullptr) {
+            return false;
+        }
+        h.tail_partial = static_cast<float*>(
+            Workspace(outputs * rest * h.tail_pieces * per_tile * static_cast<int64_t>(sizeof(float)), stream));
+        if (pair != nullptr) {
+            h.tail_partial2 = h.tail_partial + rest * h.tail_pieces * per_tile;
+        }
         p.k_per_split = 0;
         p.partial = nullptr;
         const dim3 grid(static_cast<unsigned>(n_full + rest * h.tail_pieces), 1, 1);
-        if (per_thread == 1) {
-            LaunchHalo<Shape, 1>(p, h, grid, static_cast<size_t>(lds), stream);
-        } else if (per_thread == 2) {
-            LaunchHalo<Shape, 2>(p, h, grid, static_cast<size_t>(lds), stream);
-        } else {
-            LaunchHalo<Shape, 4>(p, h, grid, static_cast<size_t>(lds), stream);
-        }
+        LaunchHalo<Shape>(p, h, grid, static_cast<size_t>(lds), per_thread, stream);
         CheckLaunch("HaloConvKernel launch");
         if (h.counters != nullptr) {
             return true;
@@ -1288,11 +1416,19 @@ bool TryHaloShape(ConvArgs p, hipStream_t stream, int force_splits, bool tail = 
     p.k_per_split = 0;
     p.partial = nullptr;
     if (splits > 1) {
+        const int64_t outputs = pair != nullptr ? 2 : 1;
         h.counters = TileCounters(tiles * p.group);
+        if (pair != nullptr && h.counters == nullptr) {
+            return false;
+        }
         if (h.counters != nullptr) {
             h.tiles = static_cast<int32_t>(tiles);
-            h.split_slots = static_cast<float*>(Workspace(
-                tiles * p.group * splits * Shape::kBM * Shape::kBN * static_cast<int64_t>(sizeof(float)), stream));
+            const int64_t slot_floats = tiles * p.group * splits * Shape::kBM * Shape::kBN;
+            h.split_slots = static_cast<float*>(
+                Workspace(outputs * slot_floats * static_cast<int64_t>(sizeof(float)), stream));
+            if (pair != nullptr) {
+                h.split_slots2 = h.split_slots + slot_floats;
+            }
         } else {
             p.partial = static_cast<float*>(
                 Workspace(static_cast<int64_t>(splits) * p.group * p.mg * p.n_total * 4, stream));
@@ -1300,13 +1436,7 @@ bool TryHaloShape(ConvArgs p, hipStream_t stream, int force_splits, bool tail = 
     }
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(p.group), static_cast<unsigned>(splits));
     h.xcd_by_channel = ((p.mg + Shape::kBM - 1) / Shape::kBM) % 8 == 0 && p.m * p.kg > p.batch * p.c * p.plane_in;
-    if (per_thread == 1) {
-        LaunchHalo<Shape, 1>(p, h, grid, static_cast<size_t>(lds), stream);
-    } else if (per_thread == 2) {
-        LaunchHalo<Shape, 2>(p, h, grid, static_cast<size_t>(lds), stream);
-    } else {
-        LaunchHalo<Shape, 4>(p, h, grid, static_cast<size_t>(lds), stream);
-    }
+    LaunchHalo<Shape>(p, h, grid, static_cast<size_t>(lds), per_thread, stream);
     CheckLaunch("HaloConvKernel launch");
     if (splits > 1 && h.counters == nullptr) {
         LaunchSplitReduce(p, splits, stream);
@@ -1354,53 +1484,55 @@ int ChooseConvConfig(const char* family, std::map<ConvKey, int>& cache, const Co
 constexpr int kHaloCandidates = 33;
 
 template <class Shape>
-bool TryHalo16(const ConvArgs& p, hipStream_t stream, int v) {
-    return v == 0 ? TryHaloShape<Shape>(p, stream, 0)
-                  : (v == 1 ? TryHaloShape<Shape>(p, stream, 0, true) : TryHaloShape<Shape>(p, stream, -1));
+bool TryHalo16(const ConvArgs& p, hipStream_t stream, int v, const HaloPair* pair) {
+    return v == 0   ? TryHaloShape<Shape>(p, stream, 0, false, pair)
+           : v == 1 ? TryHaloShape<Shape>(p, stream, 0, true, pair)
+                    : TryHaloShape<Shape>(p, stream, -1, false, pair);
 }
 
-bool LaunchHaloCandidate(int i, const ConvArgs& p, hipStream_t stream) {
+bool LaunchHaloCandidate(int i, const ConvArgs& p, hipStream_t stream, const HaloPair* pair = nullptr) {
     static constexpr int kSplits[4] = {0, 1, 2, 4};
     if (i >= 24) {
         const int s16 = (i - 24) / 3;
         const int v = (i - 24) % 3;
-        return s16 == 0 ? TryHalo16<HaloShapeM16>(p, stream, v)
-                        : (s16 == 1 ? TryHalo16<HaloShapeQ16>(p, stream, v) : TryHalo16<HaloShapeN16>(p, stream, v));
+        return s16 == 0   ? TryHalo16<HaloShapeM16>(p, stream, v, pair)
+               : s16 == 1 ? TryHalo16<HaloShapeQ16>(p, stream, v, pair)
+                          : TryHalo16<HaloShapeN16>(p, stream, v, pair);
     }
     if (i >= 20) {
         switch (i - 20) {
         case 0:
-            return p.mg <= 64 && TryHaloShape<HaloShapeW>(p, stream, -1);
+            return p.mg <= 64 && TryHaloShape<HaloShapeW>(p, stream, -1, false, pair);
         case 1:
-            return TryHaloShape<HaloShapeM>(p, stream, -1);
+            return TryHaloShape<HaloShapeM>(p, stream, -1, false, pair);
         case 2:
-            return TryHaloShape<HaloShapeQ>(p, stream, -1);
+            return TryHaloShape<HaloShapeQ>(p, stream, -1, false, pair);
         default:
-            return TryHaloShape<HaloShapeN>(p, stream, -1);
+            return TryHaloShape<HaloShapeN>(p, stream, -1, false, pair);
         }
     }
     if (i >= 16) {
         switch (i - 16) {
         case 0:
-            return p.mg <= 64 && TryHaloShape<HaloShapeW>(p, stream, 0, true);
+            return p.mg <= 64 && TryHaloShape<HaloShapeW>(p, stream, 0, true, pair);
         case 1:
-            return TryHaloShape<HaloShapeM>(p, stream, 0, true);
+            return TryHaloShape<HaloShapeM>(p, stream, 0, true, pair);
         case 2:
-            return TryHaloShape<HaloShapeQ>(p, stream, 0, true);
+            return TryHaloShape<HaloShapeQ>(p, stream, 0, true, pair);
         default:
-            return TryHaloShape<HaloShapeN>(p, stream, 0, true);
+            return TryHaloShape<HaloShapeN>(p, stream, 0, true, pair);
         }
     }
     const int splits = kSplits[i % 4];
     switch (i / 4) {
     case 0:
-        return p.mg <= 64 && TryHaloShape<HaloShapeW>(p, stream, splits);
+        return p.mg <= 64 && TryHaloShape<HaloShapeW>(p, stream, splits, false, pair);
     case 1:
-        return TryHaloShape<HaloShapeM>(p, stream, splits);
+        return TryHaloShape<HaloShapeM>(p, stream, splits, false, pair);
     case 2:
-        return TryHaloShape<HaloShapeQ>(p, stream, splits);
+        return TryHaloShape<HaloShapeQ>(p, stream, splits, false, pair);
     default:
-        return TryHaloShape<HaloShapeN>(p, stream, splits);
+        return TryHaloShape<HaloShapeN>(p, stream, splits, false, pair);
     }
 }
 
@@ -1419,10 +1551,40 @@ bool TryHaloConv(const ConvArgs& p, hipStream_t stream) {
             return true;
         }
     }
-    const int c = ChooseConvConfig("conv3x3", chosen, p, stream, kHaloCandidates, fallback, LaunchHaloCandidate);
+    const int c = ChooseConvConfig("conv3x3", chosen, p, stream, kHaloCandidates, fallback,
+                                   [](int i, const ConvArgs& q, hipStream_t st) { return LaunchHaloCandidate(i, q, st); });
     // Whether a candidate fits depends on the geometry alone, so a cached
     // choice fits; the default is tried next only as a safeguard.
     return LaunchHaloCandidate(c, p, stream) || LaunchHaloCandidate(fallback, p, stream);
+}
+
+// A 3x3 convolution (pad 1, dilation 1, group 1) and the 1x1 convolution of
+// the same input at the same stride with pad 0 -- a ResNet block's first conv
+// and its downsampling shortcut -- in one launch of the halo kernel: the 1x1
+// reads exactly the inputs of the 3x3's centre tap, so it adds one tap's
+// MFMAs per channel block to the 3x3 and no loads beyond its weights. The
+// 1x1 output has the 3x3's M and output shape, its own bias, no summand and
+// no activation. Its sums run over the same channel blocks and split parts
+// as the 3x3's, so they differ from a separate 1x1 launch only in the order
+// of the additions. Per-geometry choice under its own family ("conv3x3pair",
+// keyed by the 3x3 geometry). False when the pair does not fit the halo
+// kernel; the caller then runs the two convolutions separately.
+bool TryHaloPair(const ConvArgs& p, const HaloPair& pair, hipStream_t stream) {
+    if (!HaloApplies(p) || p.group != 1 || p.d_h != 1 || p.d_w != 1 || p.p_h != 1 || p.p_w != 1 ||
+        reinterpret_cast<uintptr_t>(pair.w2) % 16 != 0) {
+        return false;
+    }
+    static std::map<ConvKey, int> chosen;
+    auto launch = [&pair](int i, const ConvArgs& q, hipStream_t st) { return LaunchHaloCandidate(i, q, st, &pair); };
+    if (const char* forced = std::getenv("NERT_HIP_CONV_CANDIDATE")) {
+        const int i = std::atoi(forced);
+        if (i >= 0 && i < kHaloCandidates && launch(i, p, stream)) {
+            return true;
+        }
+    }
+    const int fallback = p.mg <= 64 ? 0 : 4;
+    const int c = ChooseConvConfig("conv3x3pair", chosen, p, stream, kHaloCandidates, fallback, launch);
+    return launch(c, p, stream) || launch(fallback, p, stream);
 }
 
 // ---- 1x1 convolutions with a short K, straight from memory --------------------
@@ -2626,76 +2788,119 @@ bool TryPointwise(const ConvArgs& p, hipStream_t stream) {
 } // namespace
 } // namespace nert_hip
 
+namespace nert_hip {
+
+// The kernel arguments of one convolution from the C-ABI descriptor; throws
+// on an invalid group, activation or reduction length.
+ConvArgs MakeConvArgs(const float* x, const float* w, const float* bias, const float* residual, float* y,
+                      const nert_conv_desc* d, int act) {
+    ConvArgs p{};
+    p.x = x;
+    p.w = w;
+    p.bias = bias;
+    p.y = y;
+    p.residual = residual;
+    if (act < 0 || act > 2) {
+        throw Error("conv: activation must be 0 (none), 1 (Relu) or 2 (SiLU)");
+    }
+    p.act = act;
+    p.batch = d->batch;
+    p.c = d->in_channels;
+    p.m = d->out_channels;
+    p.group = d->group;
+    if (p.group <= 0 || p.c % p.group != 0 || p.m % p.group != 0) {
+        throw Error("conv: invalid group");
+    }
+    if (p.group > 65535) {
+        throw Error("conv: more than 65535 groups");
+    }
+    p.cg = p.c / p.group;
+    p.mg = p.m / p.group;
+    p.in_d = static_cast<int32_t>(d->in[0]);
+    p.in_h = static_cast<int32_t>(d->in[1]);
+    p.in_w = static_cast<int32_t>(d->in[2]);
+    p.k_d = static_cast<int32_t>(d->kernel[0]);
+    p.k_h = static_cast<int32_t>(d->kernel[1]);
+    p.k_w = static_cast<int32_t>(d->kernel[2]);
+    p.out_d = static_cast<int32_t>(d->out[0]);
+    p.out_h = static_cast<int32_t>(d->out[1]);
+    p.out_w = static_cast<int32_t>(d->out[2]);
+    p.s_d = static_cast<int32_t>(d->stride[0]);
+    p.s_h = static_cast<int32_t>(d->stride[1]);
+    p.s_w = static_cast<int32_t>(d->stride[2]);
+    p.d_d = static_cast<int32_t>(d->dilation[0]);
+    p.d_h = static_cast<int32_t>(d->dilation[1]);
+    p.d_w = static_cast<int32_t>(d->dilation[2]);
+    p.p_d = static_cast<int32_t>(d->pad[0]);
+    p.p_h = static_cast<int32_t>(d->pad[1]);
+    p.p_w = static_cast<int32_t>(d->pad[2]);
+    p.kg = p.cg * p.k_d * p.k_h * p.k_w;
+    p.plane_out = static_cast<int64_t>(p.out_d) * p.out_h * p.out_w;
+    p.plane_in = static_cast<int64_t>(p.in_d) * p.in_h * p.in_w;
+    p.n_total = p.batch * p.plane_out;
+    if (p.kg >= (int64_t{1} << 31) || p.plane_in * p.cg >= (int64_t{1} << 40)) {
+        throw Error("conv: reduction length exceeds 2^31");
+    }
+    p.div_kvol = FastDiv::Make(static_cast<uint32_t>(p.k_d * p.k_h * p.k_w));
+    p.div_khw = FastDiv::Make(static_cast<uint32_t>(p.k_h * p.k_w));
+    p.div_kw = FastDiv::Make(static_cast<uint32_t>(p.k_w));
+    return p;
+}
+
+// Runs one convolution on the fastest kernel that applies.
+void RunConv(const ConvArgs& p, hipStream_t s) {
+    if (p.n_total == 0 || p.mg == 0) {
+        return;
+    }
+    if (TryPointwise(p, s) || TryPatchGemm(p, s) || TrySmallChannelConv(p, s) || TryHaloConv(p, s)) {
+        return;
+    }
+    LaunchGatherConv(p, s);
+}
+
+} // namespace nert_hip
+
 extern "C" int nert_hip_conv_fused_f32(const float* x, const float* w, const float* bias, const float* residual,
                                        float* y, const nert_conv_desc* d, int act, void* stream) {
     return nert_hip::Guard([&] {
-        nert_hip::ConvArgs p{};
-        p.x = x;
-        p.w = w;
-        p.bias = bias;
-        p.y = y;
-        p.residual = residual;
-        if (act < 0 || act > 2) {
-            throw nert_hip::Error("conv: activation must be 0 (none), 1 (Relu) or 2 (SiLU)");
+        nert_hip::RunConv(nert_hip::MakeConvArgs(x, w, bias, residual, y, d, act), nert_hip::StreamOr(stream));
+    });
+}
+
+extern "C" int nert_hip_conv_pair_f32(const float* x, const float* w, const float* bias, const float* residual,
+                                      float* y, const float* w2, const float* bias2, float* y2,
+                                      const nert_conv_desc* d, int act, void* stream) {
+    return nert_hip::Guard([&] {
+        const nert_hip::ConvArgs p = nert_hip::MakeConvArgs(x, w, bias, residual, y, d, act);
+        // The 1x1 convolution: same input, stride and output shape, kernel
+        // 1, pad 0, dilation 1.
+        nert_conv_desc d2 = *d;
+        for (int i = 0; i < 3; ++i) {
+            d2.kernel[i] = 1;
+            d2.pad[i] = 0;
+            d2.dilation[i] = 1;
         }
-        p.act = act;
-        p.batch = d->batch;
-        p.c = d->in_channels;
-        p.m = d->out_channels;
-        p.group = d->group;
-        if (p.group <= 0 || p.c % p.group != 0 || p.m % p.group != 0) {
-            throw nert_hip::Error("conv: invalid group");
+        const nert_hip::ConvArgs p2 = nert_hip::MakeConvArgs(x, w2, bias2, nullptr, y2, &d2, 0);
+        if (p.group != 1 || p.k_d != 1 || p.k_h != 3 || p.k_w != 3 || p.p_h != 1 || p.p_w != 1 || p.d_h != 1 ||
+            p.d_w != 1) {
+            throw nert_hip::Error("conv pair: the first convolution must be 3x3 with pad 1, dilation 1, group 1");
         }
-        if (p.group > 65535) {
-            throw nert_hip::Error("conv: more than 65535 groups");
+        for (int i = 0; i < 3; ++i) {
+            const int64_t in = d->in[i];
+            const int64_t expect = (in - 1) / d->stride[i] + 1;
+            if (d->out[i] != expect) {
+                throw nert_hip::Error("conv pair: the output shape is not that of both convolutions");
+            }
         }
-        p.cg = p.c / p.group;
-        p.mg = p.m / p.group;
-        p.in_d = static_cast<int32_t>(d->in[0]);
-        p.in_h = static_cast<int32_t>(d->in[1]);
-        p.in_w = static_cast<int32_t>(d->in[2]);
-        p.k_d = static_cast<int32_t>(d->kernel[0]);
-        p.k_h = static_cast<int32_t>(d->kernel[1]);
-        p.k_w = static_cast<int32_t>(d->kernel[2]);
-        p.out_d = static_cast<int32_t>(d->out[0]);
-        p.out_h = static_cast<int32_t>(d->out[1]);
-        p.out_w = static_cast<int32_t>(d->out[2]);
-        p.s_d = static_cast<int32_t>(d->stride[0]);
-        p.s_h = static_cast<int32_t>(d->stride[1]);
-        p.s_w = static_cast<int32_t>(d->stride[2]);
-        p.d_d = static_cast<int32_t>(d->dilation[0]);
-        p.d_h = static_cast<int32_t>(d->dilation[1]);
-        p.d_w = static_cast<int32_t>(d->dilation[2]);
-        p.p_d = static_cast<int32_t>(d->pad[0]);
-        p.p_h = static_cast<int32_t>(d->pad[1]);
-        p.p_w = static_cast<int32_t>(d->pad[2]);
-        p.kg = p.cg * p.k_d * p.k_h * p.k_w;
-        p.plane_out = static_cast<int64_t>(p.out_d) * p.out_h * p.out_w;
-        p.plane_in = static_cast<int64_t>(p.in_d) * p.in_h * p.in_w;
-        p.n_total = p.batch * p.plane_out;
-        if (p.kg >= (int64_t{1} << 31) || p.plane_in * p.cg >= (int64_t{1} << 40)) {
-            throw nert_hip::Error("conv: reduction length exceeds 2^31");
-        }
-        p.div_kvol = nert_hip::FastDiv::Make(static_cast<uint32_t>(p.k_d * p.k_h * p.k_w));
-        p.div_khw = nert_hip::FastDiv::Make(static_cast<uint32_t>(p.k_h * p.k_w));
-        p.div_kw = nert_hip::FastDiv::Make(static_cast<uint32_t>(p.k_w));
         if (p.n_total == 0 || p.mg == 0) {
             return;
         }
         hipStream_t s = nert_hip::StreamOr(stream);
-        if (nert_hip::TryPointwise(p, s)) {
+        if (nert_hip::TryHaloPair(p, nert_hip::HaloPair{w2, bias2, y2}, s)) {
             return;
         }
-        if (nert_hip::TryPatchGemm(p, s)) {
-            return;
-        }
-        if (nert_hip::TrySmallChannelConv(p, s)) {
-            return;
-        }
-        if (nert_hip::TryHaloConv(p, s)) {
-            return;
-        }
-        nert_hip::LaunchGatherConv(p, s);
+        nert_hip::RunConv(p, s);
+        nert_hip::RunConv(p2, s);
     });
 }
 

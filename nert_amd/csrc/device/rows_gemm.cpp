@@ -388,8 +388,15 @@ namespace {
 // The Conv row's work, shared with FusedConv: `residual` (or null) is added
 // and the activation (0 none, 1 Relu, 2 SiLU) applied in the kernel epilogue
 // when the fused row asks for them.
-void ConvCore(const Node& node, const std::string& context, const Views& inputs, bool has_bias,
-              const TensorView* residual, int act, const Views& outputs) {
+struct ConvCall {
+    nert_conv_desc d;
+    const float* bias;
+    const float* residual;
+};
+
+// The checks of the Conv row and the kernel descriptor of its convolution.
+ConvCall CheckConv(const Node& node, const std::string& context, const Views& inputs, bool has_bias,
+                   const TensorView* residual, const Views& outputs) {
     const TensorView& x = inputs[0];
     const TensorView& w = inputs[1];
     const TensorView& out = outputs[0];
@@ -496,8 +503,69 @@ void ConvCore(const Node& node, const std::string& context, const Views& inputs,
         }
         res = static_cast<const float*>(residual->data);
     }
-    CheckStatus(nert_hip_conv_fused_f32(static_cast<const float*>(x.data), static_cast<const float*>(w.data), bias, res,
-                                        static_cast<float*>(out.data), &d, act, Stream()),
+    return ConvCall{d, bias, res};
+}
+
+void ConvCore(const Node& node, const std::string& context, const Views& inputs, bool has_bias,
+              const TensorView* residual, int act, const Views& outputs) {
+    const ConvCall c = CheckConv(node, context, inputs, has_bias, residual, outputs);
+    CheckStatus(nert_hip_conv_fused_f32(static_cast<const float*>(inputs[0].data),
+                                        static_cast<const float*>(inputs[1].data), c.bias, c.residual,
+                                        static_cast<float*>(outputs[0].data), &c.d, act, Stream()),
+                context);
+    AfterRow(outputs, context);
+}
+
+int ActivationCode(const Node& node, const std::string& context) {
+    const std::string activation = StringAttr(node, "activation", "", "FusedConv");
+    if (activation == "Relu") {
+        return 1;
+    }
+    if (activation == "Silu") {
+        return 2;
+    }
+    if (!activation.empty()) {
+        throw InferenceException(context + ": unsupported activation '" + activation + "'");
+    }
+    return 0;
+}
+
+// FusedConv with a paired 1x1 convolution: inputs X, W, B, Z, W2, B2 (B, Z
+// and B2 may be omitted), outputs Y and Y2.
+void FusedConvPair(const Node& node, const std::string& context, const Views& inputs, const Views& outputs) {
+    const int act = ActivationCode(node, context);
+    const bool has_bias = inputs[2].dtype != DataType::Unknown;
+    const TensorView* z = inputs[3].dtype != DataType::Unknown ? &inputs[3] : nullptr;
+    Views main_inputs(inputs.begin(), inputs.begin() + (has_bias ? 3 : 2));
+    const ConvCall c = CheckConv(node, context, main_inputs, has_bias, z, Views{outputs[0]});
+    const TensorView& w2 = inputs[4];
+    const TensorView& b2 = inputs[5];
+    const TensorView& y2 = outputs[1];
+    const nert_conv_desc& d = c.d;
+    const bool pad1 = d.kernel[0] == 1 && d.kernel[1] == 3 && d.kernel[2] == 3 && d.pad[1] == 1 && d.pad[2] == 1 &&
+                      d.dilation[1] == 1 && d.dilation[2] == 1 && d.group == 1;
+    if (!pad1) {
+        throw InferenceException(context + ": a paired conv needs a 3x3 first conv with pad 1, dilation 1, group 1");
+    }
+    const std::vector<int64_t> w2_dims = {d.out_channels, d.in_channels, 1, 1};
+    if (w2.dtype != DataType::Float32 || w2.dims != w2_dims) {
+        throw InferenceException(context + ": the paired weight must be float32 [M, C, 1, 1]");
+    }
+    const bool has_b2 = b2.dtype != DataType::Unknown;
+    if (has_b2 && (b2.dtype != DataType::Float32 || b2.dims != std::vector<int64_t>{d.out_channels})) {
+        throw InferenceException(context + ": the paired bias must be float32 [M]");
+    }
+    if (y2.dtype != DataType::Float32 || y2.dims != outputs[0].dims) {
+        throw InferenceException(context + ": the paired output must be float32 with the first output's shape");
+    }
+    if (w2.data == nullptr || y2.data == nullptr || (has_b2 && b2.data == nullptr)) {
+        throw InferenceException(context + ": null buffer");
+    }
+    CheckStatus(nert_hip_conv_pair_f32(static_cast<const float*>(inputs[0].data),
+                                       static_cast<const float*>(inputs[1].data), c.bias, c.residual,
+                                       static_cast<float*>(outputs[0].data), static_cast<const float*>(w2.data),
+                                       has_b2 ? static_cast<const float*>(b2.data) : nullptr,
+                                       static_cast<float*>(y2.data), &d, act, Stream()),
                 context);
     AfterRow(outputs, context);
 }
@@ -520,20 +588,22 @@ void Conv(const Node& node, const Views& inputs, const Views& outputs) {
 // of SiLU/Swish blocks. The nert_amd runner rewrites Conv -> [Add] -> [Relu]
 // and Conv -> Sigmoid -> Mul chains into it; every step rounds as the
 // separate rows do, so results are bit-identical to the unfused graph.
+//
+// With six inputs (X, W, B, Z, W2, B2; B, Z and B2 may be omitted) and two
+// outputs it also computes Y2 = Conv(X, W2, B2) for a 1x1 W2 at the node's
+// strides with pad 0, which the runner pairs with a 3x3 pad-1 conv of the
+// same input (a ResNet block's downsampling shortcut): one launch for both
+// (nert_hip_conv_pair_f32).
 void FusedConv(const Node& node, const Views& inputs, const Views& outputs) {
     const std::string context = "FusedConv (node '" + node.name + "')";
+    if (inputs.size() == 6 && outputs.size() == 2) {
+        FusedConvPair(node, context, inputs, outputs);
+        return;
+    }
     if (inputs.size() < 2 || inputs.size() > 4 || outputs.size() != 1) {
         throw InferenceException(context + ": expected two to four inputs and one output");
     }
-    const std::string activation = StringAttr(node, "activation", "", "FusedConv");
-    int act = 0;
-    if (activation == "Relu") {
-        act = 1;
-    } else if (activation == "Silu") {
-        act = 2;
-    } else if (!activation.empty()) {
-        throw InferenceException(context + ": unsupported activation '" + activation + "'");
-    }
+    const int act = ActivationCode(node, context);
     const bool has_bias = inputs.size() >= 3 && inputs[2].dtype != DataType::Unknown;
     const TensorView* z = inputs.size() == 4 && inputs[3].dtype != DataType::Unknown ? &inputs[3] : nullptr;
     Views conv_inputs(inputs.begin(), inputs.begin() + (has_bias ? 3 : 2));

@@ -224,19 +224,26 @@ __device__ __forceinline__ void MainLoop(const ALoader& aload, const BLoader& bl
 // therefore orders them without a device-scope fence, whose L2 writeback and
 // invalidation would stall every workgroup of the XCD. The counter is a
 // device-scope atomic.
-template <class Shape, class Sum>
-__device__ __forceinline__ bool FinishSplitTile(Accum<Shape>& acc, float* slots, uint32_t* counter, int part,
-                                                int parts, int* flag) {
-    constexpr int kThreads = Shape::kThreads;
-    constexpr int kPerTile = Shape::kBM * Shape::kBN;
-    constexpr int kDeviceCoherent = 16; // cache policy: sc1
-    const int tid = threadIdx.x;
-    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-        slots, static_cast<short>(0), parts * kPerTile * static_cast<int>(sizeof(float)), 0x00020000);
-    // Byte offset of float4 v4 of block (i, j) in slot q.
-    auto at = [&](int q, int i, int j, int v4) {
-        return (q * kPerTile + (((i * Shape::kSubN + j) * 4 + v4) * kThreads + tid) * 4) * 4;
-    };
+namespace split_detail {
+
+constexpr int kDeviceCoherent = 16; // cache policy: sc1
+
+template <class Shape>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t SlotRsrc(float* slots, int parts) {
+    return __builtin_amdgcn_make_buffer_rsrc(slots, static_cast<short>(0),
+                                             parts * Shape::kBM * Shape::kBN * static_cast<int>(sizeof(float)),
+                                             0x00020000);
+}
+
+// Byte offset of float4 v4 of block (i, j) in slot q, for this thread.
+template <class Shape>
+__device__ __forceinline__ int SlotAt(int q, int i, int j, int v4) {
+    return (q * Shape::kBM * Shape::kBN + (((i * Shape::kSubN + j) * 4 + v4) * Shape::kThreads + threadIdx.x) * 4) *
+           4;
+}
+
+template <class Shape>
+__device__ __forceinline__ void StorePart(const Accum<Shape>& acc, __amdgpu_buffer_rsrc_t r, int part) {
 #pragma unroll
     for (int i = 0; i < Shape::kSubM; ++i) {
 #pragma unroll
@@ -245,14 +252,19 @@ __device__ __forceinline__ bool FinishSplitTile(Accum<Shape>& acc, float* slots,
             for (int v4 = 0; v4 < 4; ++v4) {
                 const nert_floatx4 x{acc.c[i][j][4 * v4], acc.c[i][j][4 * v4 + 1], acc.c[i][j][4 * v4 + 2],
                                      acc.c[i][j][4 * v4 + 3]};
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(nert_uintx4, x), r, at(part, i, j, v4), 0,
-                                                       kDeviceCoherent);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(nert_uintx4, x), r,
+                                                       SlotAt<Shape>(part, i, j, v4), 0, kDeviceCoherent);
             }
         }
     }
+}
+
+// After this workgroup's part stores: waits for them, counts the workgroup
+// in, and returns (to every thread) whether it was the last of `parts`.
+__device__ __forceinline__ bool ArriveLast(uint32_t* counter, int parts, int* flag) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (tid == 0) {
+    if (threadIdx.x == 0) {
         const uint32_t before = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const bool last = before + 1 == static_cast<uint32_t>(parts);
         if (last) {
@@ -261,12 +273,14 @@ __device__ __forceinline__ bool FinishSplitTile(Accum<Shape>& acc, float* slots,
         *flag = last ? 1 : 0;
     }
     __syncthreads();
-    if (*flag == 0) {
-        return false;
-    }
-    // Every part from the slots, this workgroup's own included (each thread
-    // reads back only what it stored); the loads of four parts of a 32x32
-    // block are in flight together.
+    return *flag != 0;
+}
+
+// Every part from the slots, this workgroup's own included (each thread
+// reads back only what it stored); the loads of four parts of a 32x32 block
+// are in flight together. Sums in part order in type Sum, rounded once.
+template <class Shape, class Sum>
+__device__ __forceinline__ void SumParts(Accum<Shape>& acc, __amdgpu_buffer_rsrc_t r, int parts) {
 #pragma unroll
     for (int i = 0; i < Shape::kSubM; ++i) {
 #pragma unroll
@@ -279,8 +293,9 @@ __device__ __forceinline__ bool FinishSplitTile(Accum<Shape>& acc, float* slots,
                     const int q = min(q0 + dq, parts - 1);
 #pragma unroll
                     for (int v4 = 0; v4 < 4; ++v4) {
-                        x[dq][v4] = __builtin_bit_cast(
-                            nert_floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, at(q, i, j, v4), 0, kDeviceCoherent));
+                        x[dq][v4] = __builtin_bit_cast(nert_floatx4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                         r, SlotAt<Shape>(q, i, j, v4), 0,
+                                                                         kDeviceCoherent));
                     }
                 }
 #pragma unroll
@@ -300,6 +315,38 @@ __device__ __forceinline__ bool FinishSplitTile(Accum<Shape>& acc, float* slots,
             }
         }
     }
+}
+
+} // namespace split_detail
+
+template <class Shape, class Sum>
+__device__ __forceinline__ bool FinishSplitTile(Accum<Shape>& acc, float* slots, uint32_t* counter, int part,
+                                                int parts, int* flag) {
+    const __amdgpu_buffer_rsrc_t r = split_detail::SlotRsrc<Shape>(slots, parts);
+    split_detail::StorePart<Shape>(acc, r, part);
+    if (!split_detail::ArriveLast(counter, parts, flag)) {
+        return false;
+    }
+    split_detail::SumParts<Shape, Sum>(acc, r, parts);
+    return true;
+}
+
+// The same for two accumulators of one tile (a conv and its paired 1x1):
+// both parts are stored before the one arrival, so a single counter serves
+// both and the last workgroup sums both.
+template <class Shape, class Sum>
+__device__ __forceinline__ bool FinishSplitTilePair(Accum<Shape>& acc, float* slots, Accum<Shape>& acc2,
+                                                    float* slots2, uint32_t* counter, int part, int parts,
+                                                    int* flag) {
+    const __amdgpu_buffer_rsrc_t r = split_detail::SlotRsrc<Shape>(slots, parts);
+    const __amdgpu_buffer_rsrc_t r2 = split_detail::SlotRsrc<Shape>(slots2, parts);
+    split_detail::StorePart<Shape>(acc, r, part);
+    split_detail::StorePart<Shape>(acc2, r2, part);
+    if (!split_detail::ArriveLast(counter, parts, flag)) {
+        return false;
+    }
+    split_detail::SumParts<Shape, Sum>(acc, r, parts);
+    split_detail::SumParts<Shape, Sum>(acc2, r2, parts);
     return true;
 }
 

@@ -216,6 +216,72 @@ def fuse_conv_chains(g: Graph) -> Graph:
     return Graph(nodes=nodes, initializers=g.initializers, inputs=g.inputs, outputs=g.outputs, tensors=g.tensors)
 
 
+def _conv_geometry(g: Graph, n: Node) -> tuple[tuple[int, ...], list[int], list[int], list[int], int] | None:
+    """(weight shape, strides, pads, dilations, group) of a 2-D Conv or
+    FusedConv node with an initializer weight and explicit padding."""
+    if n.op not in ("Conv", "FusedConv") or len(n.inputs) < 2 or n.inputs[1] not in g.initializers:
+        return None
+    w = g.initializers[n.inputs[1]]
+    if w.ndim != 4 or w.dtype != np.float32 or n.attrs.get("auto_pad", "NOTSET") != "NOTSET":
+        return None
+    strides = [int(v) for v in n.attrs.get("strides", [1, 1])]
+    pads = [int(v) for v in n.attrs.get("pads", [0, 0, 0, 0])]
+    dilations = [int(v) for v in n.attrs.get("dilations", [1, 1])]
+    return tuple(w.shape), strides, pads, dilations, int(n.attrs.get("group", 1))
+
+
+def pair_downsample_convs(g: Graph) -> Graph:
+    """Pairs a 3x3 convolution (pad 1, dilation 1, group 1; a Conv or a
+    FusedConv) with a 1x1 Conv (pad 0, bias optional) of the same input,
+    stride and output channels -- a ResNet block's first conv and its
+    downsampling shortcut -- into one FusedConv node with six inputs
+    (X, W, B, Z, W2, B2) and two outputs, which nert_hip_conv_pair_f32 runs in
+    one launch (the 1x1 reads the 3x3's centre-tap inputs). The 3x3 output
+    keeps its bits; the 1x1 output differs from the separate Conv row only in
+    the order of its fp32 additions. The pair sits at the later of the two
+    nodes' positions, which is taken only when no node in between reads the
+    earlier node's output.
+    """
+    consumers: dict[str, list[int]] = {}
+    for idx, n in enumerate(g.nodes):
+        for t in n.inputs:
+            if t:
+                consumers.setdefault(t, []).append(idx)
+    replace: dict[int, Node] = {}
+    dropped: set[int] = set()
+    for idx, n in enumerate(g.nodes):
+        geo = _conv_geometry(g, n)
+        if idx in dropped or idx in replace or geo is None or len(n.outputs) != 1 or len(n.inputs) > 4:
+            continue
+        ws, strides, pads, dil, group = geo
+        if ws[2:] != (3, 3) or pads != [1, 1, 1, 1] or dil != [1, 1] or group != 1:
+            continue
+        for c in consumers.get(n.inputs[0], []):
+            d = g.nodes[c]
+            if c == idx or c in dropped or c in replace or d.op != "Conv" or len(d.outputs) != 1:
+                continue
+            dgeo = _conv_geometry(g, d)
+            if dgeo is None or dgeo[0] != (ws[0], ws[1], 1, 1) or dgeo[1] != strides or any(dgeo[2]) or \
+                    dgeo[3] != [1, 1] or dgeo[4] != 1:
+                continue
+            b2 = d.inputs[2] if len(d.inputs) > 2 else ""
+            if b2 and b2 not in g.initializers:
+                continue
+            lo, hi = sorted((idx, c))
+            early_out = g.nodes[lo].outputs[0]
+            if any(lo < k < hi for k in consumers.get(early_out, [])):
+                continue
+            if g.tensors[d.outputs[0]][1] != g.tensors[n.outputs[0]][1]:
+                continue
+            ins = list(n.inputs) + [""] * (4 - len(n.inputs))
+            attrs = {k: v for k, v in n.attrs.items() if k in ("strides", "pads", "dilations", "group", "activation")}
+            replace[hi] = Node("FusedConv", ins + [d.inputs[1], b2], [n.outputs[0], d.outputs[0]], attrs, n.name)
+            dropped.add(lo)
+            break
+    nodes = [replace.get(i, nd) for i, nd in enumerate(g.nodes) if i not in dropped]
+    return Graph(nodes=nodes, initializers=g.initializers, inputs=g.inputs, outputs=g.outputs, tensors=g.tensors)
+
+
 def _scalar(g: Graph, name: str) -> float | None:
     """The value of a float32 scalar initializer (shape () or (1,)), else None."""
     v = g.initializers.get(name)
@@ -525,20 +591,24 @@ class _PackedNode:
         self.err = C.create_string_buffer(1024)
 
 
-def fuse_rows(g: Graph, attention: bool = True) -> Graph:
-    """The runner's fusions in order: Conv chains, attention blocks (when
-    `attention`; the only fusion whose outputs are not bit-identical to the
-    separate rows), MatMul chains, residual Add + LayerNorm."""
+def fuse_rows(g: Graph, attention: bool = True, pairs: bool = True) -> Graph:
+    """The runner's fusions in order: Conv chains, 3x3 convs paired with
+    their 1x1 downsampling shortcuts (when `pairs`), attention blocks (when
+    `attention`), MatMul chains, residual Add + LayerNorm. All but the pairs'
+    1x1 outputs and the attention blocks are bit-identical to the separate
+    rows; those two sum in another order, within the rows' tolerance."""
     g = fuse_conv_chains(g)
+    if pairs:
+        g = pair_downsample_convs(g)
     if attention:
         g = fuse_attention(g)
     return fuse_add_layernorm(fuse_matmul_chains(g))
 
 
 class Program:
-    def __init__(self, g: Graph, fuse: bool = True, views: bool = True, attention: bool = True):
+    def __init__(self, g: Graph, fuse: bool = True, views: bool = True, attention: bool = True, pairs: bool = True):
         if fuse:
-            g = fuse_rows(g, attention)
+            g = fuse_rows(g, attention, pairs)
         self.alias: dict[str, tuple[str, int]] = {}
         if views:
             g, self.alias = alias_views(g)

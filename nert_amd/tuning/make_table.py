@@ -42,10 +42,11 @@ def _round() -> None:
     for name, kwargs in WORKLOADS:
         g, inputs = getattr(workloads, name)(**kwargs)
         # Fused and unfused Conv/MatMul rows share their geometry keys; the
-        # attention fusion removes the QK^T and PV products, which the
-        # unfused rows (the seam's executor) still run.
-        for attention in (True, False):
-            prog = Program(g, attention=attention)
+        # attention fusion removes the QK^T and PV products and the conv
+        # pairing the separate 3x3/2 and 1x1/2 launches, which the unfused
+        # rows (the seam's executor) still run.
+        for fused in (True, False):
+            prog = Program(g, attention=fused, pairs=fused)
             for n in g.inputs:
                 prog.set_input(n, inputs[n])
             prog.run()

@@ -480,6 +480,113 @@ def test_conv_lds_patch_forced_configs(gpu, tmp_path, batch, hw, cand):
     assert np.array_equal(np.load(paths["out2"]), np.where(want > 0, want, np.float32(0)).astype(F))
 
 
+_PAIR = """
+import json, sys
+import numpy as np
+sys.path.insert(0, {root!r})
+from nert_amd.device import DeviceArray, run_node
+x, w, b, z, w2, b2 = (np.load(p) for p in {ins!r})
+a = dict(json.loads({attrs!r}), activation="Relu")
+dev = lambda v: DeviceArray.from_host(v)
+def pair(zz, bb2):
+    y, y2 = DeviceArray(z.shape, np.float32), DeviceArray(z.shape, np.float32)
+    run_node("FusedConv", [dev(x), dev(w), dev(b), None if zz is None else dev(zz), dev(w2),
+                           None if bb2 is None else dev(bb2)], [y, y2], a)
+    return y.to_host(), y2.to_host()
+y, y2 = pair(None, b2)
+single = DeviceArray(z.shape, np.float32)
+run_node("FusedConv", [dev(x), dev(w), dev(b)], [single], a)
+yz, y2z = pair(z, None)
+single_z = DeviceArray(z.shape, np.float32)
+run_node("FusedConv", [dev(x), dev(w), dev(b), dev(z)], [single_z], a)
+again = pair(None, b2)
+np.savez({out!r}, y=y, y2=y2, single=single.to_host(), yz=yz, y2z=y2z, single_z=single_z.to_host(),
+         again_y=again[0], again_y2=again[1])
+"""
+
+
+@pytest.mark.parametrize("xs,m", [((2, 64, 56, 56), 128), ((2, 128, 28, 28), 256), ((2, 256, 14, 14), 512),
+                                  ((3, 32, 15, 13), 32), ((2, 64, 16, 16), 64)])
+@pytest.mark.parametrize("cand", [None, 1, 5, 9, 13, 16, 17, 18, 19, 20, 21, 22, 23, 24, 25, 27, 28, 30, 31])
+def test_conv_pair_matches_separate_rows(gpu, tmp_path, xs, m, cand):
+    """A 3x3 pad-1 conv paired with the 1x1 shortcut conv of its input at the
+    same stride (six-input FusedConv, one launch of the halo kernel): the 3x3
+    output equals the single FusedConv row bit for bit under the same forced
+    configuration (None: the tuned choice, then only within the tolerance),
+    the 1x1 output matches the restatement of the 1x1 conv with and without
+    its bias, the summand path is applied to the 3x3 output only, and a
+    second launch is bit-identical (split counters reset)."""
+    import json
+    import os
+    import subprocess
+    import sys
+
+    stride = 1 if xs[2] == 16 else 2
+    attrs = {"pads": [1, 1, 1, 1], "strides": [stride, stride]}
+    x = randn(xs, seed=130)
+    w = randn((m, xs[1], 3, 3), seed=131, scale=0.05)
+    b = randn((m,), seed=132, scale=0.1)
+    w2 = randn((m, xs[1], 1, 1), seed=133, scale=0.1)
+    b2 = randn((m,), seed=134, scale=0.1)
+    z = randn(_conv_out(xs, w.shape, attrs), seed=135)
+    ins = []
+    for k, v in (("x", x), ("w", w), ("b", b), ("z", z), ("w2", w2), ("b2", b2)):
+        ins.append(str(tmp_path / f"{k}.npy"))
+        np.save(ins[-1], v)
+    out = str(tmp_path / "out.npz")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ)
+    if cand is not None:
+        # A candidate that does not fit the geometry falls back to the fixed
+        # default (not a table or timed choice, which the paired family makes
+        # apart from the single conv).
+        env["NERT_HIP_CONV_CANDIDATE"] = str(cand)
+        env["NERT_HIP_CONV_TUNE"] = "0"
+        env["NERT_HIP_TUNE_TABLE"] = os.devnull
+    subprocess.run([sys.executable, "-c", _PAIR.format(root=root, ins=ins, attrs=json.dumps(attrs), out=out)],
+                   env=env, check=True, timeout=120)
+    r = np.load(out)
+    conv = restate.conv(x, w, b, attrs["strides"], None, attrs["pads"], 1, "NOTSET")
+    relu = lambda v: np.where(v > 0, v, np.float32(0)).astype(F)
+    want2 = restate.conv(x, w2, b2, attrs["strides"], None, [0, 0, 0, 0], 1, "NOTSET")
+    compare(r["y2"], want2, what=f"paired 1x1, candidate {cand}")
+    compare(r["y2z"], restate.conv(x, w2, None, attrs["strides"], None, [0, 0, 0, 0], 1, "NOTSET"),
+            what=f"paired 1x1 without bias, candidate {cand}")
+    if cand is not None:
+        assert np.array_equal(r["y"], r["single"]) and np.array_equal(r["yz"], r["single_z"])
+    compare(r["y"], relu(conv), what=f"paired 3x3, candidate {cand}")
+    compare(r["yz"], relu((conv.astype(np.float64) + z).astype(F)), rtol=2e-4, atol=2e-4,
+            what=f"paired 3x3 with summand, candidate {cand}")
+    assert np.array_equal(r["again_y"], r["y"]) and np.array_equal(r["again_y2"], r["y2"])
+
+
+def test_conv_pair_rejects_bad_operands(gpu):
+    """The paired FusedConv row checks the 1x1 operands before launching and
+    names the node in its message."""
+    from nert_amd.device import NertError
+
+    x = DeviceArray.from_host(randn((1, 8, 8, 8), seed=1))
+    w = DeviceArray.from_host(randn((16, 8, 3, 3), seed=2))
+    w2 = DeviceArray.from_host(randn((16, 8, 1, 1), seed=4))
+    y = DeviceArray((1, 16, 4, 4), F)
+    y2 = DeviceArray((1, 16, 4, 4), F)
+    attrs = {"pads": [1, 1, 1, 1], "strides": [2, 2]}
+    cases = [
+        ([x, w, None, None, DeviceArray.from_host(randn((16, 8, 3, 3), seed=3)), None], [y, y2], attrs,
+         "the paired weight must be float32 [M, C, 1, 1]"),
+        ([x, w, None, None, w2, None], [y, DeviceArray((1, 16, 3, 3), F)], attrs,
+         "the paired output must be float32 with the first output's shape"),
+        ([x, w, None, None, w2, DeviceArray.from_host(randn((8,), seed=5))], [y, y2], attrs,
+         "the paired bias must be float32 [M]"),
+        ([x, w, None, None, w2, None], [y, y2], dict(attrs, dilations=[2, 2], pads=[2, 2, 2, 2]),
+         "a paired conv needs a 3x3 first conv with pad 1, dilation 1, group 1"),
+    ]
+    for ins, outs, a, msg in cases:
+        with pytest.raises(NertError) as err:
+            run_node("FusedConv", ins, outs, a, name="p")
+        assert "FusedConv (node 'p'): " + msg in str(err.value), str(err.value)
+
+
 @pytest.mark.parametrize("batch,hw", [(17, 32), (32, 28), (3, 9)])
 @pytest.mark.parametrize("cand", [2, 3, 11, 15, 16, 17, 18, 19, 20, 21, 22, 23, 25, 26, 28, 29, 31, 32])
 def test_conv_split_fixup_matches_reduce_kernels(gpu, tmp_path, batch, hw, cand):

@@ -217,16 +217,22 @@ def test_fused_attention_program_matches_separate_rows(gpu):
 
 
 def test_fused_program_is_bit_identical(gpu):
-    """The runner's Conv+Add+Relu fusion changes no output bit (batch 2)."""
+    """The runner's Conv+Add+Relu fusion changes no output bit (batch 2);
+    pairing each stage's 3x3/2 conv with its 1x1/2 shortcut in one launch
+    changes only the order of the shortcut's additions, so the logits stay
+    within the end-to-end bar of the unpaired program's."""
     g, inputs = workloads.resnet18(batch=2)
     outs = []
-    for fuse in (False, True):
-        prog = Program(g, fuse=fuse)
+    for fuse, pairs in ((False, False), (True, False), (True, True)):
+        prog = Program(g, fuse=fuse, pairs=pairs)
+        if pairs:
+            assert sum(1 for n in prog.graph.nodes if len(n.outputs) == 2 and n.op == "FusedConv") == 3
         prog.set_input("input", inputs["input"])
         prog.run()
         outs.append(prog.output(g.outputs[0]))
         prog.close()
     assert np.array_equal(outs[0], outs[1])
+    compare(outs[2], outs[1], rtol=2e-4, atol=2e-4, what="paired vs unpaired program")
 
 
 def test_reference_model_gate_bs1(gpu, tmp_path):

@@ -4,7 +4,7 @@ import numpy as np
 
 from nert_amd import workloads
 from nert_amd.graph import Graph
-from nert_amd.runner import fuse_conv_chains, plan_arena
+from nert_amd.runner import fuse_conv_chains, pair_downsample_convs, plan_arena
 
 F = np.float32
 
@@ -30,6 +30,48 @@ def test_resnet18_fusion():
     assert all(n.attrs.get("activation") == "Relu" for n in f.nodes if n.op == "FusedConv")
     _valid_order(f)
     assert f.outputs == g.outputs
+
+
+def test_resnet18_downsample_pairs():
+    """Each stage's first 3x3/2 conv and its 1x1/2 shortcut become one
+    six-input, two-output FusedConv at the later node's position."""
+    g, _ = workloads.resnet18(batch=2)
+    f = pair_downsample_convs(fuse_conv_chains(g))
+    pairs = [n for n in f.nodes if n.op == "FusedConv" and len(n.outputs) == 2]
+    assert len(pairs) == 3 and sum(1 for n in f.nodes if n.op == "Conv") == 0
+    for n in pairs:
+        x, w, b, z, w2, b2 = n.inputs
+        assert z == "" and g.initializers[w].shape[2:] == (3, 3) and g.initializers[w2].shape[2:] == (1, 1)
+        assert g.initializers[w2].shape[:2] == g.initializers[w].shape[:2] and b2 in g.initializers
+        assert n.attrs["strides"] == [2, 2] and n.attrs["pads"] == [1, 1, 1, 1] and n.attrs["activation"] == "Relu"
+        assert g.tensors[n.outputs[0]][1] == g.tensors[n.outputs[1]][1]
+    _valid_order(f)
+    assert len(f.nodes) == len(fuse_conv_chains(g).nodes) - 3
+
+
+def _pair_graph(pads2=(0, 0, 0, 0), stride2=(2, 2), m2=8, between=False):
+    g = Graph()
+    x = g.add_input("x", F, (1, 4, 8, 8))
+    w = g.add_initializer("w", np.ones((8, 4, 3, 3), F))
+    w2 = g.add_initializer("w2", np.ones((m2, 4, 1, 1), F))
+    oh = (8 + pads2[0] + pads2[2] - 1) // stride2[0] + 1
+    (d,) = g.add_node("Conv", [x, w2], [("d", F, (1, m2, oh, oh))], {"strides": list(stride2), "pads": list(pads2)})
+    if between:
+        (e,) = g.add_node("Relu", [d], [("e", F, (1, m2, oh, oh))])
+    (c,) = g.add_node("Conv", [x, w], [("c", F, (1, 8, 4, 4))], {"strides": [2, 2], "pads": [1, 1, 1, 1]})
+    g.outputs = [c, d] + ([e] if between else [])
+    return g
+
+
+def test_downsample_pair_rules():
+    f = pair_downsample_convs(_pair_graph())
+    assert [n.op for n in f.nodes] == ["FusedConv"] and f.nodes[0].outputs == ["c", "d"]
+    assert f.nodes[0].inputs == ["x", "w", "", "", "w2", ""]
+    _valid_order(f)
+    # a padded or differently strided 1x1, other output channels, or a reader
+    # of the earlier output between the two: no pair
+    for kw in ({"pads2": (1, 1, 1, 1)}, {"stride2": (1, 1)}, {"m2": 4}, {"between": True}):
+        assert all(n.op != "FusedConv" for n in pair_downsample_convs(_pair_graph(**kw)).nodes), kw
 
 
 def _chain(extra_consumer=False, output_mid=False, broadcast=False):
