@@ -277,41 +277,50 @@ __device__ __forceinline__ bool ArriveLast(uint32_t* counter, int parts, int* fl
 }
 
 // Every part from the slots, this workgroup's own included (each thread
-// reads back only what it stored); the loads of four parts of a 32x32 block
-// are in flight together. Sums in part order in type Sum, rounded once.
+// reads back only what it stored), summed in part order in type Sum and
+// rounded once. A float sum takes a 32x32 block at a time, the loads of four
+// parts of it (64 floats) in flight together. A double sum would need twice
+// the registers for that, which would set the register budget (and so the
+// occupancy) of the GEMM kernels around it, so it takes four consecutive
+// floats at a time (still four parts' loads in flight). Both add the parts
+// of an element in the same order.
 template <class Shape, class Sum>
 __device__ __forceinline__ void SumParts(Accum<Shape>& acc, __amdgpu_buffer_rsrc_t r, int parts) {
+    constexpr int kQuads = sizeof(Sum) > sizeof(float) ? 1 : 4; // float4 pieces per part per round
 #pragma unroll
     for (int i = 0; i < Shape::kSubM; ++i) {
 #pragma unroll
         for (int j = 0; j < Shape::kSubN; ++j) {
-            Sum sum[16];
-            for (int q0 = 0; q0 < parts; q0 += 4) {
-                nert_floatx4 x[4][4];
 #pragma unroll
-                for (int dq = 0; dq < 4; ++dq) {
-                    const int q = min(q0 + dq, parts - 1);
+            for (int v0 = 0; v0 < 4; v0 += kQuads) {
+                Sum sum[4 * kQuads];
+                for (int q0 = 0; q0 < parts; q0 += 4) {
+                    nert_floatx4 x[4][kQuads];
 #pragma unroll
-                    for (int v4 = 0; v4 < 4; ++v4) {
-                        x[dq][v4] = __builtin_bit_cast(nert_floatx4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                                         r, SlotAt<Shape>(q, i, j, v4), 0,
-                                                                         kDeviceCoherent));
+                    for (int dq = 0; dq < 4; ++dq) {
+                        const int q = min(q0 + dq, parts - 1);
+#pragma unroll
+                        for (int v = 0; v < kQuads; ++v) {
+                            x[dq][v] = __builtin_bit_cast(nert_floatx4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                            r, SlotAt<Shape>(q, i, j, v0 + v), 0,
+                                                                            kDeviceCoherent));
+                        }
                     }
-                }
 #pragma unroll
-                for (int dq = 0; dq < 4; ++dq) {
-                    if (q0 + dq < parts) {
+                    for (int dq = 0; dq < 4; ++dq) {
+                        if (q0 + dq < parts) {
 #pragma unroll
-                        for (int v = 0; v < 16; ++v) {
-                            const Sum y = static_cast<Sum>(x[dq][v >> 2][v & 3]);
-                            sum[v] = q0 + dq == 0 ? y : sum[v] + y;
+                            for (int e = 0; e < 4 * kQuads; ++e) {
+                                const Sum y = static_cast<Sum>(x[dq][e >> 2][e & 3]);
+                                sum[e] = q0 + dq == 0 ? y : sum[e] + y;
+                            }
                         }
                     }
                 }
-            }
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                acc.c[i][j][v] = static_cast<float>(sum[v]);
+                for (int e = 0; e < 4 * kQuads; ++e) {
+                    acc.c[i][j][4 * v0 + e] = static_cast<float>(sum[e]);
+                }
             }
         }
     }
