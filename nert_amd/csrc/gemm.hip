@@ -151,11 +151,17 @@ __global__ __launch_bounds__(Shape::kThreads) void GemmKernel(GemmArgs p) {
 
     Accum<Shape> acc;
     acc.zero();
-    // Interior tiles with 16-byte aligned rows take unchecked float4 loads for
-    // every full K tile; edge tiles and the K remainder use the checked form.
+    // Tiles with 16-byte aligned rows take unchecked float4 loads for every
+    // full K tile; the K remainder uses the checked form. So do edge tiles
+    // whose missing rows (or columns) the unchecked loaders can stand in for
+    // with valid ones -- any count along a K-contiguous operand, whole quads
+    // along a row-contiguous one: those rows only reach outputs that are never
+    // stored, and the stored outputs sum the same products in the same order.
     const bool a_vec = (A_KCONTIG ? p.a_sm : p.a_sk) % 4 == 0 && ((reinterpret_cast<uintptr_t>(a) & 15) == 0);
     const bool b_vec = (B_NCONTIG ? p.b_sk : p.b_sn) % 4 == 0 && ((reinterpret_cast<uintptr_t>(b) & 15) == 0);
-    const bool interior = a_vec && b_vec && row0 + Shape::kBM <= p.m && col0 + Shape::kBN <= p.n;
+    const bool a_rows = row0 + Shape::kBM <= p.m || A_KCONTIG || p.m % 4 == 0;
+    const bool b_cols = col0 + Shape::kBN <= p.n || !B_NCONTIG || p.n % 4 == 0;
+    const bool interior = a_vec && b_vec && a_rows && b_cols;
     const int64_t k_full = interior ? k_begin + (k_end - k_begin) / Shape::kBK * Shape::kBK : k_begin;
     if (k_full > k_begin) {
         const auto aload = MakeOperand<Shape::kBM, Shape::kBK, Shape::kThreads, Shape::kPitchA, A_KCONTIG, false>(

@@ -421,7 +421,10 @@ struct KContigLoader {
                 if (kQuads % THREADS != 0 && q >= kQuads) {
                     continue; // this thread owns no quad in this pass
                 }
-                const nert_floatx4 val = *reinterpret_cast<const nert_floatx4*>(base + row * row_stride + k);
+                // Rows past the operand (an edge tile) read its last row:
+                // they only feed output rows that are never stored.
+                const int64_t r = row < rows_left ? row : rows_left - 1;
+                const nert_floatx4 val = *reinterpret_cast<const nert_floatx4*>(base + r * row_stride + k);
                 s.v[p][0] = val[0];
                 s.v[p][1] = val[1];
                 s.v[p][2] = val[2];
@@ -484,7 +487,11 @@ struct RowContigLoader {
                 if (kQuads % THREADS != 0 && q >= kQuads) {
                     continue; // this thread owns no quad in this pass
                 }
-                s.v[p] = *reinterpret_cast<const nert_floatx4*>(tile + (kk * k_stride + row));
+                // Quads past the operand (an edge tile whose valid rows are
+                // whole quads) read quad 0: they only feed outputs that are
+                // never stored.
+                const int r = row < rows_left ? row : 0;
+                s.v[p] = *reinterpret_cast<const nert_floatx4*>(tile + (kk * k_stride + r));
             } else {
                 const bool k_ok = q < kQuads && k < k_total;
                 const int64_t k_off = k_ok ? k * k_stride : 0;
