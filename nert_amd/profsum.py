@@ -230,9 +230,9 @@ def cmd_ops(a) -> None:
                            _case_bytes(a.write, "WRITE_SIZE", a.write_scale, len(cases))))
     head = ("| case | reference fixture | kernels per launch | kernel-only µs (rocprof) | achieved | % of peak |"
             + (" HBM MB per launch (counters) | algorithmic MB |" if traffic else "")
-            + " MI300X reference HIP µs | speed-up |")
+            + " MI300X reference HIP µs | speed-up | reference CPU row ms (1 core) | parity |")
     print(head)
-    print("|---|---|---|---:|---:|---:|" + ("---:|---:|" if traffic else "") + "---:|---:|")
+    print("|---|---|---|---:|---:|---:|" + ("---:|---:|" if traffic else "") + "---:|---:|---:|---|")
     for k, ((s, p, reps), c) in enumerate(zip(runs, cases)):
         last = rows[s + (reps - 20) * p: s + reps * p]
         us = sum(r["us"] for r in last) / 20
@@ -251,6 +251,13 @@ def cmd_ops(a) -> None:
             line += f" {(fb + wb) / 1e6:.2f} | {'' if alg is None else f'{alg / 1e6:.2f}'} |"
         line += (f" {'' if ref is None else f'{ref * 1e3:.0f}'} |"
                  f" {'' if ref is None else f'{ref * 1e3 / us:.0f}x'} |")
+        cpu = c.get("cpu_baseline")
+        if cpu:
+            exact = "bit-exact" if cpu["float_max_ratio_to_1e-4_bar"] == 0 else \
+                f"{cpu['float_max_ratio_to_1e-4_bar']:.2f} of the 1e-4 bar"
+            line += f" {cpu['ms']:.3f} | {'ok' if cpu['parity_ok'] else 'FAIL'} ({exact}) |"
+        else:
+            line += " | |"
         print(line)
 
 
