@@ -12,10 +12,11 @@
 // first eager call: every candidate that fits runs on a scratch output (one
 // warm-up launch, then ten launches captured into a HIP graph and replayed
 // between HIP events on the caller's stream, as a replayed program runs
-// them); the four fastest are timed again (two interleaved rounds) since the
+// them); the four fastest are timed again (three interleaved rounds) since the
 // leaders are often closer than one pass's noise, and the fastest is kept
 // for the rest of the process. NERT_HIP_TUNE_RECORD=<file> appends
-// each such timed choice to <file> in the table's format. A first call
+// each such timed choice to <file> in the table's format, with the
+// finalists' times after a '#'. A first call
 // under stream capture cannot time anything and fixes the fallback instead,
 // as does NERT_HIP_CONV_TUNE=0 in the environment.
 //
@@ -103,7 +104,10 @@ inline const std::unordered_map<std::string, int>& TuneTable() {
     return table;
 }
 
-inline void RecordChoice(const std::string& table_key, int choice) {
+// Appends "<key> <choice> # <candidate>:<us> ..." (the finalists' re-timed
+// microseconds after the '#', which table readers skip).
+inline void RecordChoice(const std::string& table_key, int choice,
+                         const std::vector<std::pair<int, float>>& finalists) {
     const char* path = std::getenv("NERT_HIP_TUNE_RECORD");
     if (path == nullptr || *path == 0) {
         return;
@@ -111,7 +115,11 @@ inline void RecordChoice(const std::string& table_key, int choice) {
     static std::mutex mu;
     std::lock_guard<std::mutex> lock(mu);
     if (FILE* f = std::fopen(path, "a")) {
-        std::fprintf(f, "%s %d\n", table_key.c_str(), choice);
+        std::fprintf(f, "%s %d #", table_key.c_str(), choice);
+        for (const auto& c : finalists) {
+            std::fprintf(f, " %d:%.3f", c.first, c.second);
+        }
+        std::fprintf(f, "\n");
         std::fclose(f);
     }
 }
@@ -138,6 +146,7 @@ int ChooseConfig(const char* family, std::map<Key, int>& cache, std::mutex& mu, 
     }
     int best = fallback;
     bool timed = false;
+    std::vector<std::pair<int, float>> finalist_us;
     hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
     Check(hipStreamIsCapturing(stream, &capture), "hipStreamIsCapturing");
     if (TuningEnabled() && capture == hipStreamCaptureStatusNone && count > 1 && scratch_bytes > 0) {
@@ -204,18 +213,22 @@ int ChooseConfig(const char* family, std::map<Key, int>& cache, std::mutex& mu, 
                 first.emplace_back(us, i);
             }
             // The leaders are often within a few percent of each other, about
-            // the first pass's noise: re-time the best four in two interleaved
-            // rounds of ten launches and keep each one's faster round.
+            // the first pass's noise: re-time the best four in three
+            // interleaved rounds of ten launches and keep each one's fastest
+            // round.
             std::sort(first.begin(), first.end());
             const size_t finalists = std::min<size_t>(first.size(), 4);
             std::vector<float> best_us(finalists, -1.0f);
-            for (int round = 0; round < 2 && finalists > 1; ++round) {
+            for (int round = 0; round < 3 && finalists > 1; ++round) {
                 for (size_t f = 0; f < finalists; ++f) {
                     const float us = time_us(first[f].second, 10);
                     if (best_us[f] < 0.0f || us < best_us[f]) {
                         best_us[f] = us;
                     }
                 }
+            }
+            for (size_t f = 0; f < finalists; ++f) {
+                finalist_us.emplace_back(first[f].second, finalists > 1 ? best_us[f] : first[f].first);
             }
             if (!first.empty()) {
                 best = first[0].second;
@@ -243,7 +256,7 @@ int ChooseConfig(const char* family, std::map<Key, int>& cache, std::mutex& mu, 
         std::fprintf(stderr, "nert_hip tune: chose %d of %d for %s\n", best, count, table_key.c_str());
     }
     if (timed) {
-        RecordChoice(table_key, best);
+        RecordChoice(table_key, best, finalist_us);
     }
     cache.emplace(key, best);
     return best;

@@ -7,9 +7,13 @@ processes (nert_amd/csrc/tune.hpp reads it).
 Each round is a fresh process that ignores the current table and times
 every candidate of every geometry the seeded workloads reach (the
 BASELINE.json configs, the batch sizes the parity tests use, and the
-op-level cases), recording its choices (NERT_HIP_TUNE_RECORD). Per
-geometry the table keeps the choice most rounds made (ties: the earliest
-round). Needs the GPU.
+op-level cases), recording its choice and its finalists' re-timed
+microseconds (NERT_HIP_TUNE_RECORD). Per geometry the table keeps the
+finalist with the lowest mean time over the rounds that timed it, among
+those timed in at least half of the rounds (fallback: the choice most rounds
+made, ties to the earliest round): the leaders are often within the noise
+of one round, and one round's winner is a coin flip between them. Needs the
+GPU.
 """
 
 from __future__ import annotations
@@ -65,7 +69,7 @@ def _round() -> None:
 
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--rounds", type=int, default=3)
+    ap.add_argument("--rounds", type=int, default=5)
     ap.add_argument("--out", default=str(HERE / "gfx950.tsv"))
     ap.add_argument("--_round", action="store_true", help=argparse.SUPPRESS)
     a = ap.parse_args(argv)
@@ -73,6 +77,7 @@ def main(argv: list[str] | None = None) -> int:
         _round()
         return 0
     votes: dict[str, list[int]] = collections.defaultdict(list)
+    times: dict[str, dict[int, list[float]]] = collections.defaultdict(lambda: collections.defaultdict(list))
     with tempfile.TemporaryDirectory() as tmp:
         for r in range(a.rounds):
             rec = os.path.join(tmp, f"round{r}.tsv")
@@ -80,15 +85,24 @@ def main(argv: list[str] | None = None) -> int:
             subprocess.run([sys.executable, "-m", "nert_amd.tuning.make_table", "--_round"], cwd=ROOT, env=env,
                            check=True)
             for line in Path(rec).read_text().splitlines():
-                key, choice = line.rsplit(" ", 1)
+                entry, _, finalists = line.partition("#")
+                key, choice = entry.strip().rsplit(" ", 1)
                 votes[key].append(int(choice))
+                for item in finalists.split():
+                    cand, us = item.split(":")
+                    times[key][int(cand)].append(float(us))
     lines = ["# Per-geometry kernel choices for gfx950 (MI355X): <family> <candidates> <geometry key> <choice>.",
-             f"# Written by `python3 -m nert_amd.tuning.make_table --rounds {a.rounds}`: the choice most of "
-             f"{a.rounds} timing rounds made.", ""]
+             f"# Written by `python3 -m nert_amd.tuning.make_table --rounds {a.rounds}`: per geometry the "
+             f"finalist with the lowest mean time over {a.rounds} timing rounds.", ""]
     for key in sorted(votes):
-        counts = collections.Counter(votes[key])
-        top = max(counts.values())
-        choice = next(c for c in votes[key] if counts[c] == top)
+        rounds = len(votes[key])
+        timed = {c: sum(t) / len(t) for c, t in times[key].items() if 2 * len(t) >= rounds}
+        if timed:
+            choice = min(timed, key=lambda c: (timed[c], c))
+        else:
+            counts = collections.Counter(votes[key])
+            top = max(counts.values())
+            choice = next(c for c in votes[key] if counts[c] == top)
         lines.append(f"{key} {choice}")
     Path(a.out).write_text("\n".join(lines) + "\n")
     print(f"wrote {len(votes)} geometries to {a.out}", flush=True)
