@@ -388,14 +388,16 @@ int nert_hip_topk_f32(const float* x, float* values, int64_t* indices, int64_t o
  * it is for callers that cannot allocate device memory -- work being
  * captured into a HIP graph, tight serving loops, harnesses that forbid
  * hipMalloc. Same arguments, results and errors as nert_hip_topk_f32, but
- * the long-row select state and candidates live in a fixed 4 MiB device
- * array that the library holds on each GPU until the process ends (set up
- * by nert_hip_init, which must have run). Rows longer than 4096 need about
- * 16 * rows * k + 3 KiB * rows bytes of it; larger requests fail with an
- * error and launch nothing. Every call on one GPU shares that GPU's array,
- * so calls that overlap in time on one GPU (two streams, two threads) race:
- * serialise them. The array keeps the last call's contents; each call
- * clears what it needs with a kernel (no memset node). */
+ * the long-row counters, select state and candidates live in a fixed 4 MiB
+ * device array that the library holds on each GPU until the process ends
+ * (set up by nert_hip_init, which must have run). Rows longer than 4096
+ * need about 16 * rows * k + 3 KiB * rows bytes of it; larger requests fail
+ * with an error and launch nothing. Every call on one GPU shares that GPU's
+ * array, so calls that overlap in time on one GPU (two streams, two
+ * threads) race: serialise them. The array keeps the last call's contents;
+ * its per-row counters are zeroed once at set-up and every call leaves them
+ * zero, and each call clears the rest of what it needs with a kernel (no
+ * memset node). */
 int nert_hip_topk_f32_noalloc(const float* x, float* values, int64_t* indices, int64_t outer, int64_t dim,
                               int64_t inner, int64_t k, void* stream);
 /* Range: y[i] = start + i * delta, float32 rounded after the product and

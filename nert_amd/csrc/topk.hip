@@ -9,24 +9,19 @@
 // exactly the reference's order and there are no ties left.
 //
 // Rows of up to kSmallRow elements sort in one workgroup's LDS. Longer rows
-// with K <= 1024 (the detector's [8, 672000], K = 300) take two launches
-// and read the row twice:
-//   1. HistTopKernel: many workgroups per row count the top 12 bits of the
-//      orderable value into an LDS histogram, added into the row's 4096-bin
-//      histogram (and a 64-bin summary of it) in a zero-kept workspace.
-//   2. CollectTopKernel: every workgroup finds the bin holding the K-th
-//      largest value from the summary and that bin's 64 counts (two wave
-//      scans), then keeps its chunk's keys above that bin ("sure": fewer
-//      than K per row) and in it ("maybe", up to a per-row capacity), staged
-//      in LDS and appended with one reservation per workgroup. The row's last
-//      workgroup to finish then completes the row: it histograms the next 12
-//      bits of the maybe keys in LDS, picks the bin of the remaining rank,
-//      moves the keys above it to the result and selects among the keys tied
-//      on all 24 bits by rank (or, past an LDS capacity, by a radix select
-//      over their remaining 40 key bits); the K keys are ranked (all keys are
-//      unique) and written out, and the row's histograms and counters are
-//      cleared for the next call. When the maybe keys overflowed their list
-//      it reads the row again instead.
+// with K <= 1024 (the detector's [8, 672000], K = 300) read the row once, in
+// chunks of up to 24576 keys, one workgroup each (ChunkTop): a chunk keeps
+// every key at or above its own threshold for rank K (a 24-bit window fitted
+// to the chunk's value range), which holds the chunk's K largest, so the
+// row's K largest are among the chunks' candidates. The row's last chunk
+// workgroup to finish (a zero-kept counter per row) then merges them
+// (MergeTop): the candidates' own threshold for rank K splits them into keys
+// in the result and keys tied on the threshold's 24 bits, ranked among
+// themselves in LDS (or radix-selected past an LDS capacity); the K keys are
+// ranked (all keys are unique) and written out. When a chunk had more
+// candidates than its slots hold, the merge reads the row again. Without the
+// counters (NERT_HIP_SPLIT_FIXUP=0) the merge is a second launch, one
+// workgroup per row.
 // Longer rows with K > 1024 run a radix select over the whole key, 8 bits per
 // pass, then sort the K collected keys in 4096-key LDS runs merged by per-key
 // binary search.
@@ -352,15 +347,38 @@ struct ChunkStats {
     uint32_t pad;
 };
 
-// Read of the row, one workgroup per chunk: the chunk's candidates for the
-// row's K largest -- every key at or above the chunk's own threshold for rank
-// K (all of them when the chunk has at most K keys), which holds the chunk's
-// K largest -- written in thread order to the workgroup's slots (the first
-// kWgCand), with the chunk's stats.
-__global__ void __launch_bounds__(kFT) ChunkTopKernel(const float* __restrict__ x, RowGeom g, int64_t chunk,
-                                                      int chunks, uint64_t* cand, ChunkStats* stats) {
-    const int64_t row = blockIdx.x / chunks;
-    const int c = blockIdx.x - static_cast<int>(row * chunks);
+// Candidates and stats are written and read at device scope (sc1): the
+// workgroup that merges a row may run on another XCD, with its own L2, in
+// the same launch as the workgroups that wrote them.
+__device__ __forceinline__ void StoreShared(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t LoadShared(const uint64_t* p) {
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void StoreStats(ChunkStats* p, const ChunkStats& v) {
+    uint32_t* w = &p->count;
+    __hip_atomic_store(w, v.count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(w + 1, v.top, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(w + 2, v.bottom, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ ChunkStats LoadStats(const ChunkStats* p) {
+    uint32_t* w = const_cast<uint32_t*>(&p->count);
+    return ChunkStats{__hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                      __hip_atomic_load(w + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                      __hip_atomic_load(w + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), 0};
+}
+
+// Read of the row, one workgroup per chunk (workgroup wg = row * chunks +
+// c): the chunk's candidates for the row's K largest -- every key at or
+// above the chunk's own threshold for rank K (all of them when the chunk has
+// at most K keys), which holds the chunk's K largest -- written in thread
+// order to the workgroup's slots (the first kWgCand), with the chunk's
+// stats.
+__device__ __forceinline__ void ChunkTop(const float* __restrict__ x, const RowGeom& g, int64_t chunk, int chunks,
+                                         uint64_t* cand, ChunkStats* stats, int wg) {
+    const int64_t row = wg / chunks;
+    const int c = wg - static_cast<int>(row * chunks);
     const uint32_t k = static_cast<uint32_t>(g.k);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -371,22 +389,58 @@ __global__ void __launch_bounds__(kFT) ChunkTopKernel(const float* __restrict__ 
     r.Load(x, g, RowBase(row, g), begin, end);
     __shared__ uint32_t h[kBins];
     __shared__ uint32_t wave_sum[kFT / 64];
-    // Keys are formed where they are used (the values stay in registers).
+    // The elements' orderable values, formed once (0 past the chunk's end:
+    // no value maps to 0, -inf maps to 0x007FFFFF), and the low key word of
+    // element e, (0xFFFFFFFF - index), as the thread's first element's minus
+    // a constant: every visit then costs 32-bit operations only.
+    uint32_t ord[4 * kChunkQuads];
+#pragma unroll
+    for (int e = 0; e < 4 * kChunkQuads; ++e) {
+        ord[e] = r.Index(e) < r.end ? OrdOf(r.v[e]) : 0u;
+    }
+    const uint32_t low0 = 0xFFFFFFFFu - static_cast<uint32_t>(r.Index(0));
+    const auto low = [&](int e) {
+        return low0 - static_cast<uint32_t>(r.vec ? 4 * (e >> 2) * kFT + (e & 3) : e * kFT);
+    };
     const auto visit = [&](auto f) {
 #pragma unroll
         for (int e = 0; e < 4 * kChunkQuads; ++e) {
-            f(KeyOf(r.v[e], r.Index(e)), r.Index(e) < r.end);
+            f((static_cast<uint64_t>(ord[e]) << 32) | low(e), ord[e] != 0u);
         }
     };
+    // Bounds of the chunk's K-th largest value: at most the chunk's largest;
+    // at least the smallest of the threads' own largest values when at
+    // least K threads hold keys (those are that many distinct keys), else
+    // at least the chunk's smallest. The threshold histograms count only
+    // the keys within the bounds, so their window is fitted to the top of
+    // the chunk rather than to its whole range.
+    uint32_t hi = 0;
+    uint32_t lo = 0xFFFFFFFFu;
+    visit([&](uint64_t key, bool valid) {
+        const uint32_t ord = static_cast<uint32_t>(key >> 32);
+        hi = valid && ord > hi ? ord : hi;
+        lo = valid && ord < lo ? ord : lo;
+    });
+    const int64_t n = end - begin;
+    const int64_t holders = g.vec ? (n + 3) / 4 : n; // threads with a key: this many, up to kFT
+    if (holders >= static_cast<int64_t>(k)) {
+        lo = r.Index(0) < r.end ? hi : 0xFFFFFFFFu;
+    }
     uint32_t top = 0;
     uint32_t bottom = 0;
-    VisitRange(visit, &top, &bottom);
+    BlockRange(hi, lo, &top, &bottom);
     // A chunk of at most K keys passes them all (floor 0 at L = 0). Every
     // candidate's orderable value is at least the floor's.
     uint64_t floor = 0;
     int L = 0;
-    if (end - begin > static_cast<int64_t>(k)) {
-        L = ThresholdInRange(h, k, visit, top, bottom, &floor);
+    if (n > static_cast<int64_t>(k)) {
+        const uint32_t low = bottom;
+        L = ThresholdInRange(
+            h, k,
+            [&](auto f) {
+                visit([&](uint64_t key, bool valid) { f(key, valid && static_cast<uint32_t>(key >> 32) >= low); });
+            },
+            top, bottom, &floor);
         bottom = static_cast<uint32_t>((floor << L) >> 32);
     }
     // Candidates of this thread (bit e of `pass` for element e), then their
@@ -394,7 +448,8 @@ __global__ void __launch_bounds__(kFT) ChunkTopKernel(const float* __restrict__ 
     uint32_t pass = 0;
 #pragma unroll
     for (int e = 0; e < 4 * kChunkQuads; ++e) {
-        if (r.Index(e) < r.end && (KeyOf(r.v[e], r.Index(e)) >> L) >= floor) {
+        const uint64_t key = (static_cast<uint64_t>(ord[e]) << 32) | low(e);
+        if (ord[e] != 0u && (key >> L) >= floor) {
             pass |= 1u << e;
         }
     }
@@ -417,18 +472,18 @@ __global__ void __launch_bounds__(kFT) ChunkTopKernel(const float* __restrict__ 
         at += w < wave ? wave_sum[w] : 0;
         total += wave_sum[w];
     }
-    uint64_t* slots = cand + static_cast<int64_t>(blockIdx.x) * kWgCand;
+    uint64_t* slots = cand + static_cast<int64_t>(wg) * kWgCand;
 #pragma unroll
     for (int e = 0; e < 4 * kChunkQuads; ++e) {
         if ((pass >> e) & 1u) {
             if (at < kWgCand) {
-                slots[at] = KeyOf(r.v[e], r.Index(e));
+                StoreShared(slots + at, (static_cast<uint64_t>(ord[e]) << 32) | low(e));
             }
             ++at;
         }
     }
     if (tid == 0) {
-        stats[blockIdx.x] = ChunkStats{total, top, bottom, 0};
+        StoreStats(stats + wg, ChunkStats{total, top, bottom, 0});
     }
 }
 
@@ -449,10 +504,9 @@ __device__ __forceinline__ float ValueOf(const float* x, const RowGeom& g, int64
 // are ranked among themselves in LDS, or radix-selected over their remaining
 // 40 key bits past kTieCap. The K keys are then ranked (all keys are unique)
 // and written out.
-__global__ void __launch_bounds__(kFT) MergeTopKernel(const float* __restrict__ x, float* values, int64_t* indices,
-                                                      RowGeom g, int chunks, const uint64_t* __restrict__ cand,
-                                                      const ChunkStats* __restrict__ stats) {
-    const int64_t row = blockIdx.x;
+__device__ __forceinline__ void MergeTop(const float* __restrict__ x, float* values, int64_t* indices,
+                                         const RowGeom& g, int chunks, const uint64_t* cand, const ChunkStats* stats,
+                                         int64_t row) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -478,13 +532,13 @@ __global__ void __launch_bounds__(kFT) MergeTopKernel(const float* __restrict__ 
     const bool member = group < chunks;
     ChunkStats cs{0, 0, 0xFFFFFFFFu, 0};
     if (member) {
-        cs = stats[wg0 + group];
+        cs = LoadStats(stats + wg0 + group);
     }
     uint64_t kv[kBatch];
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
         const int slot = member_slot + T * j;
-        kv[j] = member && slot < kWgCand ? cand[(wg0 + group) * kWgCand + slot] : 0;
+        kv[j] = member && slot < kWgCand ? LoadShared(cand + (wg0 + group) * kWgCand + slot) : 0;
     }
     if (tid == 0) {
         fits_s = 1;
@@ -510,7 +564,7 @@ __global__ void __launch_bounds__(kFT) MergeTopKernel(const float* __restrict__ 
     if (!in_regs && from_cand) {
         // More candidates than the groups' registers hold: offsets of the
         // chunks' candidates in chunk order, for streaming them in batches.
-        const uint32_t nc = tid < chunks ? stats[wg0 + tid].count : 0;
+        const uint32_t nc = tid < chunks ? LoadStats(stats + wg0 + tid).count : 0;
         uint32_t incl = nc;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
@@ -570,7 +624,7 @@ __global__ void __launch_bounds__(kFT) MergeTopKernel(const float* __restrict__ 
                     kv[j] = 0;
                     if (i < total) {
                         const int w = owner(i);
-                        kv[j] = cand[(wg0 + w) * kWgCand + (i - off_s[w])];
+                        kv[j] = LoadShared(cand + (wg0 + w) * kWgCand + (i - off_s[w]));
                     }
                 }
 #pragma unroll
@@ -703,6 +757,49 @@ __global__ void __launch_bounds__(kFT) MergeTopKernel(const float* __restrict__ 
         values[dst] = ValueOf(x, g, row, key);
         indices[dst] = IndexOf(key);
     }
+}
+
+// After a chunk's candidate and stats stores: waits for them, counts the
+// workgroup in on its row's counter, and returns (to every thread) whether
+// it was the row's last chunk; the last one leaves the counter zero.
+__device__ __forceinline__ bool ArriveLastChunk(uint32_t* counter, int chunks, int* flag) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t before = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = before + 1 == static_cast<uint32_t>(chunks);
+        if (last) {
+            __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        *flag = last ? 1 : 0;
+    }
+    __syncthreads();
+    return *flag != 0;
+}
+
+// One launch: every chunk workgroup finds its candidates; the row's last to
+// finish merges the row (counters[row] zero before and after).
+__global__ void __launch_bounds__(kFT) ChunkMergeTopKernel(const float* __restrict__ x, float* values,
+                                                           int64_t* indices, RowGeom g, int64_t chunk, int chunks,
+                                                           uint64_t* cand, ChunkStats* stats, uint32_t* counters) {
+    ChunkTop(x, g, chunk, chunks, cand, stats, static_cast<int>(blockIdx.x));
+    __shared__ int last;
+    const int64_t row = blockIdx.x / chunks;
+    if (ArriveLastChunk(counters + row, chunks, &last)) {
+        MergeTop(x, values, indices, g, chunks, cand, stats, row);
+    }
+}
+
+// The same as two launches (no counters): chunks, then one workgroup per row.
+__global__ void __launch_bounds__(kFT) ChunkTopKernel(const float* __restrict__ x, RowGeom g, int64_t chunk,
+                                                      int chunks, uint64_t* cand, ChunkStats* stats) {
+    ChunkTop(x, g, chunk, chunks, cand, stats, static_cast<int>(blockIdx.x));
+}
+
+__global__ void __launch_bounds__(kFT) MergeTopKernel(const float* __restrict__ x, float* values, int64_t* indices,
+                                                      RowGeom g, int chunks, const uint64_t* cand,
+                                                      const ChunkStats* stats) {
+    MergeTop(x, values, indices, g, chunks, cand, stats, blockIdx.x);
 }
 
 // ---- long rows: radix select ----------------------------------------------
@@ -985,6 +1082,7 @@ int PowTwoAtLeast(int64_t n) {
 // names a host-side stand-in, never the device memory: the device address
 // comes from hipGetSymbolAddress (TopkScratchSetup), once per device.
 constexpr int64_t kNoAllocScratchBytes = 4 << 20;
+constexpr int64_t kRowCounterBytes = kFastMaxRows * 4; // zero-kept, at the start of the scratch
 constexpr int kMaxDevices = 64;
 __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 uint8_t* g_scratch_ptr[kMaxDevices] = {};
@@ -1004,12 +1102,11 @@ TopkLayout LayoutFor(int64_t rows, int64_t k) {
     return l;
 }
 
-// Byte sizes of the K <= kFastMaxK path's buffers (256-byte aligned pieces):
-// the part kept zero between calls, then the two key lists.
-// Long rows with K <= kFastMaxK: chunk candidates, then the per-row merge
-// (two launches, one read of the row).
+// Long rows with K <= kFastMaxK: chunk candidates and the per-row merge,
+// one read of the row. `counters` (one zero-kept word per row) or null for
+// two launches.
 void FastTopk(const float* x, float* values, int64_t* indices, int64_t rows, RowGeom g, hipStream_t s, uint8_t* fixed,
-              int64_t fixed_bytes) {
+              int64_t fixed_bytes, uint32_t* counters) {
     // About 256 workgroups over all rows; chunks of at most kChunkMax keys
     // and at least 4096, and (where the chunk limit allows) few enough per
     // row that their candidates, about K each, fit the merge's registers.
@@ -1043,15 +1140,21 @@ void FastTopk(const float* x, float* values, int64_t* indices, int64_t rows, Row
     }
     auto* cand = reinterpret_cast<uint64_t*>(ws);
     auto* stats = reinterpret_cast<ChunkStats*>(ws + cand_bytes);
-    ChunkTopKernel<<<static_cast<unsigned>(rows * chunks), kFT, 0, s>>>(x, g, chunk, static_cast<int>(chunks), cand,
-                                                                          stats);
-    MergeTopKernel<<<static_cast<unsigned>(rows), kFT, 0, s>>>(x, values, indices, g, static_cast<int>(chunks), cand,
-                                                               stats);
+    if (counters != nullptr) {
+        ChunkMergeTopKernel<<<static_cast<unsigned>(rows * chunks), kFT, 0, s>>>(
+            x, values, indices, g, chunk, static_cast<int>(chunks), cand, stats, counters);
+    } else {
+        ChunkTopKernel<<<static_cast<unsigned>(rows * chunks), kFT, 0, s>>>(x, g, chunk, static_cast<int>(chunks),
+                                                                              cand, stats);
+        MergeTopKernel<<<static_cast<unsigned>(rows), kFT, 0, s>>>(x, values, indices, g, static_cast<int>(chunks),
+                                                                   cand, stats);
+    }
     CheckLaunch("topk launch");
 }
 
 // The TopK launch sequence. `fixed` is the caller's scratch (fixed_bytes
-// long) or null, in which case the layer's grow-only workspace is used.
+// long, its first kRowCounterBytes the zero-kept row counters) or null, in
+// which case the layer's grow-only workspace and tile counters are used.
 void TopkImpl(const float* x, float* values, int64_t* indices, int64_t outer, int64_t dim, int64_t inner, int64_t k,
               void* stream, uint8_t* fixed, int64_t fixed_bytes) {
     if (k <= 0 || k > dim || dim > 0xFFFFFFFFll) {
@@ -1071,8 +1174,17 @@ void TopkImpl(const float* x, float* values, int64_t* indices, int64_t outer, in
         CheckLaunch("topk small-row launch");
         return;
     }
+    uint32_t* counters = nullptr;
+    if (fixed != nullptr) {
+        counters = reinterpret_cast<uint32_t*>(fixed);
+        fixed += kRowCounterBytes;
+        fixed_bytes -= kRowCounterBytes;
+    }
     if (k <= kFastMaxK && rows <= kFastMaxRows) {
-        FastTopk(x, values, indices, rows, g, s, fixed, fixed_bytes);
+        if (counters == nullptr) {
+            counters = TileCounters(rows);
+        }
+        FastTopk(x, values, indices, rows, g, s, fixed, fixed_bytes, counters);
         return;
     }
     // Long rows: about 2048 workgroups over all rows, >= 4096 keys each.
@@ -1156,6 +1268,9 @@ void TopkScratchSetup() {
     }
     void* ptr = nullptr;
     Check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(topk scratch)");
+    // The row counters start at zero; every launch that uses them leaves
+    // them zero.
+    Check(hipMemset(ptr, 0, kRowCounterBytes), "hipMemset(topk scratch counters)");
     g_scratch_ptr[dev] = static_cast<uint8_t*>(ptr);
 }
 

@@ -220,11 +220,11 @@ def test_topk_long_rows(gpu):
 
 
 def test_topk_long_row_select_paths(gpu):
-    """Long rows with K <= 1024 select in two reads of the row plus a
-    per-row finish; each of the finish's ways is exercised:
-    the threshold bin's keys from the collected list or (past its capacity)
-    from the row again, and the keys tied on 24 bits ranked in LDS or (past
-    its capacity) radix-selected."""
+    """Long rows with K <= 1024 read the row once in chunks, and the row's
+    last chunk workgroup merges the chunks' candidates; each of the merge's
+    ways is exercised: the candidates from the chunks' lists or (past a
+    list's capacity) from the row again, and the keys tied on 24 bits ranked
+    in LDS or (past its capacity) radix-selected."""
     r = rng(31)
     _topk_case(randn((3, 50000), seed=32), 1)                        # K = 1
     _topk_case(randn((2, 70000), seed=33), 1024)                     # the largest K of this path
@@ -240,6 +240,71 @@ def test_topk_long_row_select_paths(gpu):
     few = np.zeros((2, 40000), F)
     few[:, 123] = 1.0
     _topk_case(few, 300)                                             # one key above the threshold bin
+
+
+_TWO_LAUNCH = """
+import ctypes as C, sys
+import numpy as np
+sys.path.insert(0, {root!r})
+from nert_amd import device
+from nert_amd.device import DeviceArray
+device.init()
+L = device.lib()
+L.nert_hip_topk_f32.argtypes = [C.c_void_p] * 3 + [C.c_int64] * 4 + [C.c_void_p]
+out = {{}}
+for name, (rows, dim, k, seed) in {cases!r}.items():
+    x = np.load({path!r} + name + ".npy")
+    dx = DeviceArray.from_host(x)
+    v = DeviceArray((rows, k), np.float32)
+    i = DeviceArray((rows, k), np.int64)
+    assert L.nert_hip_topk_f32(dx.ptr, v.ptr, i.ptr, rows, dim, 1, k, None) == 0, device.last_error()
+    device.synchronize()
+    out[name + "_v"] = v.to_host()
+    out[name + "_i"] = i.to_host()
+np.savez({path!r} + "out.npz", **out)
+"""
+
+
+def test_topk_merge_in_chunk_launch_matches_two_launches(gpu, tmp_path):
+    """The fused path (the row's last chunk workgroup merges, per-row
+    counters) against the two-launch path (NERT_HIP_SPLIT_FIXUP=0, a merge
+    launch of one workgroup per row) in a fresh process: bit-identical
+    values and indices, twice in a row on the fused side (the counters are
+    left zero)."""
+    import ctypes as C
+    import os
+    import subprocess
+    import sys
+
+    from nert_amd import device
+    from nert_amd.device import DeviceArray
+
+    cases = {"det": (8, 672000, 300, 41), "ties": (5, 100000, 64, 42), "one": (3, 50000, 1, 43)}
+    path = str(tmp_path) + os.sep
+    xs = {}
+    for name, (rows, dim, k, seed) in cases.items():
+        r = rng(seed)
+        x = r.random((rows, dim), dtype=np.float32)
+        if name == "ties":
+            x = r.integers(0, 20, (rows, dim)).astype(F)
+        xs[name] = x
+        np.save(path + name + ".npy", x)
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, NERT_HIP_SPLIT_FIXUP="0")
+    subprocess.run([sys.executable, "-c", _TWO_LAUNCH.format(root=root, cases=cases, path=path)], env=env,
+                   check=True, timeout=120)
+    want = np.load(path + "out.npz")
+    L = device.lib()
+    L.nert_hip_topk_f32.argtypes = [C.c_void_p] * 3 + [C.c_int64] * 4 + [C.c_void_p]
+    for _ in range(2):
+        for name, (rows, dim, k, _seed) in cases.items():
+            dx = DeviceArray.from_host(xs[name])
+            v = DeviceArray((rows, k), np.float32)
+            i = DeviceArray((rows, k), np.int64)
+            assert L.nert_hip_topk_f32(dx.ptr, v.ptr, i.ptr, rows, dim, 1, k, None) == 0, device.last_error()
+            device.synchronize()
+            assert np.array_equal(v.to_host(), want[name + "_v"]), name
+            assert np.array_equal(i.to_host(), want[name + "_i"]), name
 
 
 def test_topk_errors(gpu):
