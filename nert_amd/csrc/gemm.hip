@@ -362,6 +362,9 @@ using ShapeS = TileShape<32, 64, 32, 1, 2>;   // 2 waves, skinny M
 // per K, twice the LDS.
 using ShapeMK = TileShape<64, 128, 32, 2, 2>;  // 4 waves, 32x64 per wave
 using ShapeLK = TileShape<128, 128, 32, 2, 4>; // 8 waves, 64x32 per wave
+// 4 waves of 32x32 for products a few hundred 64x128 tiles cover unevenly
+// (N = 768 next to M ~ 3000: 294 such tiles on 256 CUs, 600 of these).
+using ShapeQ = TileShape<64, 64, 32, 2, 2>;
 
 template <class Shape>
 void LaunchShape(GemmArgs p, int64_t batches, int splits, hipStream_t stream) {
@@ -404,7 +407,7 @@ int64_t TileCount(const GemmArgs& p, int64_t batches) {
 
 namespace {
 
-// One configuration: tile shape (0 L, 1 M, 2 S, 3 MK, 4 LK) and split-K count
+// One configuration: tile shape (0 L, 1 M, 2 S, 3 MK, 4 LK, 5 Q) and split-K count
 // (0: the PlanSplits choice for that shape).
 void LaunchConfig(GemmArgs p, int64_t batches, int shape, int force_splits, hipStream_t stream) {
     int64_t tiles;
@@ -422,6 +425,10 @@ void LaunchConfig(GemmArgs p, int64_t batches, int shape, int force_splits, hipS
         tiles = TileCount<ShapeLK>(p, batches);
         min_k_tiles = 4;
         bk = ShapeLK::kBK;
+    } else if (shape == 5) {
+        tiles = TileCount<ShapeQ>(p, batches);
+        min_k_tiles = 4;
+        bk = ShapeQ::kBK;
     } else {
         tiles = TileCount<ShapeS>(p, batches);
         min_k_tiles = 2;
@@ -463,6 +470,9 @@ void LaunchConfig(GemmArgs p, int64_t batches, int shape, int force_splits, hipS
     case 4:
         LaunchShape<ShapeLK>(p, batches, splits, stream);
         break;
+    case 5:
+        LaunchShape<ShapeQ>(p, batches, splits, stream);
+        break;
     default:
         LaunchShape<ShapeS>(p, batches, splits, stream);
         break;
@@ -483,13 +493,13 @@ void LaunchConfig(GemmArgs p, int64_t batches, int shape, int force_splits, hipS
 }
 
 // Candidates: 0-11 shape i / 4 (L, M, S) with split count {PlanSplits, 1,
-// 2, 4}[i % 4]; 12 the skinny kernel; 13-20 shape 3 + (i - 13) / 4 (MK, LK)
-// with split count {...}[(i - 13) % 4].
+// 2, 4}[i % 4]; 12 the skinny kernel; 13-24 shape 3 + (i - 13) / 4 (MK, LK,
+// Q) with split count {...}[(i - 13) % 4].
 // Fallback (capture, tuning off): 8-wave 128x128 tiles for problems with at
 // least 1024 of them, 4-wave 64x128 below, 2-wave 32x64 for M <= 32.
 using GemmKey = std::array<int64_t, 10>;
 constexpr int kGemmSplits[4] = {0, 1, 2, 4};
-constexpr int kGemmCandidates = 21;
+constexpr int kGemmCandidates = 25;
 constexpr int kSkinnyCandidate = 12;
 
 void LaunchTiled(const GemmArgs& p, int64_t batches, int i, hipStream_t stream) {

@@ -729,7 +729,7 @@ def test_gemm_split_fixup_matches_reduce_kernels(gpu, tmp_path):
              ("Gemm", [(40, 1100), (1100, 24)], {}, (40, 24)),
              ("Gemm", [(512, 512), (512, 512)], {"transB": 1}, (512, 512)),
              ("MatMul", [(96, 200), (200, 80)], {}, (96, 80))]
-    cands = [i for i in range(21) if i != 12 and (i if i < 12 else i - 13) % 4 in (2, 3)]
+    cands = [i for i in range(25) if i != 12 and (i if i < 12 else i - 13) % 4 in (2, 3)]
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     got = []
     for fixup in (True, False):
@@ -745,7 +745,7 @@ def test_gemm_split_fixup_matches_reduce_kernels(gpu, tmp_path):
         assert np.array_equal(got[0][k], got[1][k]), k
 
 
-@pytest.mark.parametrize("candidate", list(range(21)))
+@pytest.mark.parametrize("candidate", list(range(25)))
 @pytest.mark.parametrize("op,shapes,attrs", GEMM_FORCED)
 def test_gemm_every_candidate(gpu, monkeypatch, candidate, op, shapes, attrs):
     """Each tile shape x split count and the skinny kernel, forced with
