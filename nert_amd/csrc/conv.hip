@@ -2658,8 +2658,10 @@ __global__ void ResidualActKernel(float* y, const float* residual, int act, int6
 //     p = oh * OW + ow,  k = (c * KH + kh) * KW + kw,
 // and Y = W (M x K, the ONNX weight as it is) * P^T + bias over all images'
 // patches at once (B K-contiguous), the output written back per image in
-// NCHW (the engine's grouped output layout; the batched form with W
-// broadcast when the pixels per image are not whole quads).
+// NCHW (the engine's grouped output layout). The GEMM's B loader reads P
+// from X in place (GemmArgs::PatchB): a run of 4 k is 4 consecutive input
+// columns. When the pixels per image are not whole quads, the batched form
+// with W broadcast runs over P built first by PatchRowsKernel.
 // PatchRowsKernel builds P: the OW patch rows of one band of KH input rows
 // (b, oh) are a contiguous run of OW * K floats, written by a few
 // workgroups, kPatchQuadsPerBlock floats x 4 each, one 16-byte load and
@@ -2701,19 +2703,8 @@ bool TryPatchGemm(const ConvArgs& p, hipStream_t stream) {
         return false;
     }
     const int64_t k_total = p.c * p.k_h * p.k_w;
-    // Slot 1: the patch rows stay alive across the GEMM, which may take slot
-    // 0 for split-K partial sums.
-    auto* rows = static_cast<float*>(Workspace(p.batch * p.plane_out * k_total * static_cast<int64_t>(sizeof(float)),
-                                               stream, 1));
-    const int64_t band_quads = p.out_w * k_total / 4;
-    const int64_t parts = (band_quads + kPatchQuadsPerBlock - 1) / kPatchQuadsPerBlock;
-    PatchRowsKernel<<<static_cast<unsigned>(p.batch * p.out_h * parts), 256, 0, stream>>>(
-        p.x, rows, static_cast<int32_t>(p.c), p.k_h, p.k_w, p.out_h, p.out_w, p.in_h, p.in_w,
-        static_cast<int32_t>(parts));
-    CheckLaunch("PatchRowsKernel launch");
     GemmArgs g{};
     g.a = p.w;
-    g.b = rows;
     g.y = p.y;
     g.m = p.m;
     g.k = k_total;
@@ -2727,13 +2718,40 @@ bool TryPatchGemm(const ConvArgs& p, hipStream_t stream) {
     g.bias = p.bias;
     g.bias_sm = 1;
     g.bias_sn = 0;
-    if (p.plane_out % 4 == 0 && p.n_total < (int64_t{1} << 31)) {
+    if (p.plane_out % 4 == 0 && p.n_total < (int64_t{1} << 31) &&
+        p.batch * p.c * p.plane_in < (int64_t{1} << 31)) {
         // One GEMM over every image's patches (N = batch x pixels, no
-        // per-image column tiles half empty), written back per image in NCHW.
+        // per-image column tiles half empty), B read from X in place, written
+        // back per image in NCHW.
+        g.b = p.x;
+        g.patch = GemmArgs::PatchB{p.x,
+                                   static_cast<int32_t>(p.c),
+                                   p.k_h,
+                                   p.k_w,
+                                   p.in_h,
+                                   p.in_w,
+                                   p.out_h,
+                                   p.out_w,
+                                   FastDiv::Make(static_cast<uint32_t>(p.k_h * p.k_w)),
+                                   FastDiv::Make(static_cast<uint32_t>(p.k_w)),
+                                   FastDiv::Make(static_cast<uint32_t>(p.plane_out)),
+                                   FastDiv::Make(static_cast<uint32_t>(p.out_w))};
         g.n = p.n_total;
         g.y_group = p.plane_out;
         LaunchGemm(g, 1, stream);
     } else {
+        // Images whose pixels are not whole quads: the patch rows first
+        // (workspace slot 1, alive across the GEMM, which may take slot 0 for
+        // split-K partial sums), then one GEMM per image.
+        auto* rows = static_cast<float*>(
+            Workspace(p.batch * p.plane_out * k_total * static_cast<int64_t>(sizeof(float)), stream, 1));
+        const int64_t band_quads = p.out_w * k_total / 4;
+        const int64_t parts = (band_quads + kPatchQuadsPerBlock - 1) / kPatchQuadsPerBlock;
+        PatchRowsKernel<<<static_cast<unsigned>(p.batch * p.out_h * parts), 256, 0, stream>>>(
+            p.x, rows, static_cast<int32_t>(p.c), p.k_h, p.k_w, p.out_h, p.out_w, p.in_h, p.in_w,
+            static_cast<int32_t>(parts));
+        CheckLaunch("PatchRowsKernel launch");
+        g.b = rows;
         g.n = p.plane_out;
         g.batch_rank = 1;
         g.bdims[0] = p.batch;

@@ -46,6 +46,78 @@ __device__ __forceinline__ auto MakeOperand(const float* base, int64_t row0, int
     }
 }
 
+// B of a patch convolution read in place (GemmArgs::PatchB): each thread
+// loads runs of 4 consecutive k of one column n, i.e. 4 consecutive input
+// columns of one input row, into the k-major LDS tile the way the
+// K-contiguous loader does. The x offsets of the thread's columns at k = 0
+// are fixed for the whole K walk; a k's offset is c * H * W + r * W + q.
+template <int ROWS, int BK, int THREADS, int PITCH, bool CHECKED>
+struct PatchLoader {
+    using Rows = KContigLoader<ROWS, BK, THREADS, PITCH, CHECKED>;
+    static constexpr int kQuads = Rows::kQuads;
+    static constexpr int kPer = Rows::kPer;
+    using Stage = typename Rows::Stage;
+    const GemmArgs::PatchB* v;
+    uint32_t col_off[kPer];
+    bool col_ok[kPer];
+    uint32_t k_total;
+
+    __device__ __forceinline__ void init(const GemmArgs::PatchB& pv, int64_t col0, int64_t n_total, int64_t k_tot) {
+        v = &pv;
+        k_total = static_cast<uint32_t>(k_tot);
+#pragma unroll
+        for (int p = 0; p < kPer; ++p) {
+            const int q = threadIdx.x + p * THREADS;
+            const int64_t n = col0 + q / (BK / 4);
+            col_ok[p] = q < kQuads && n < n_total;
+            // Columns past the operand (an edge tile) read its last column:
+            // they only feed outputs that are never stored.
+            const uint32_t nn = static_cast<uint32_t>(n < n_total ? n : n_total - 1);
+            uint32_t rem;
+            const uint32_t img = DivMod(pv.div_plane, nn, rem);
+            uint32_t ow;
+            const uint32_t oh = DivMod(pv.div_ow, rem, ow);
+            col_off[p] = ((img * static_cast<uint32_t>(pv.c) * static_cast<uint32_t>(pv.in_h) +
+                           oh * static_cast<uint32_t>(pv.kh)) *
+                              static_cast<uint32_t>(pv.in_w) +
+                          ow * static_cast<uint32_t>(pv.kw));
+        }
+    }
+    __device__ __forceinline__ uint32_t KOff(uint32_t k) const {
+        uint32_t rem;
+        const uint32_t c = DivMod(v->div_khkw, k, rem);
+        uint32_t q;
+        const uint32_t r = DivMod(v->div_kw, rem, q);
+        return (c * static_cast<uint32_t>(v->in_h) + r) * static_cast<uint32_t>(v->in_w) + q;
+    }
+    __device__ __forceinline__ void load(int64_t k0, Stage& s) const {
+        const int tid = threadIdx.x;
+#pragma unroll
+        for (int p = 0; p < kPer; ++p) {
+            const int q = tid + p * THREADS;
+            const uint32_t k = static_cast<uint32_t>(k0) + static_cast<uint32_t>((q % (BK / 4)) * 4);
+            if constexpr (!CHECKED) {
+                if (kQuads % THREADS != 0 && q >= kQuads) {
+                    continue; // this thread owns no quad in this pass
+                }
+                const nert_floatx4 val = *reinterpret_cast<const nert_floatx4*>(v->x + col_off[p] + KOff(k));
+                s.v[p][0] = val[0];
+                s.v[p][1] = val[1];
+                s.v[p][2] = val[2];
+                s.v[p][3] = val[3];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bool ok = col_ok[p] && k + e < k_total;
+                    const float x = v->x[ok ? col_off[p] + KOff(k + e) : 0];
+                    s.v[p][e] = ok ? x : 0.f;
+                }
+            }
+        }
+    }
+    __device__ __forceinline__ void store(const Stage& s, float* lds) const { Rows{}.store(s, lds); }
+};
+
 // The epilogue of every GEMM kernel: alpha * acc, plus beta * bias, then the
 // optional Gelu chain, each operation rounded on its own (no contraction),
 // so a fused MatMul -> Mul -> Add -> Div/Erf/Add/Mul/Mul row reproduces the
@@ -118,7 +190,7 @@ __device__ __forceinline__ void GemmEpilogue(const GemmArgs& p, const Accum<Shap
     }
 }
 
-template <class Shape, bool A_KCONTIG, bool B_NCONTIG, int FLUSH>
+template <class Shape, bool A_KCONTIG, bool B_NCONTIG, int FLUSH, bool B_PATCH = false>
 __global__ __launch_bounds__(Shape::kThreads) void GemmKernel(GemmArgs p) {
     __shared__ __attribute__((aligned(16))) float lds[2 * (Shape::kLdsA + Shape::kLdsB)];
     const int64_t tiles_m = (p.m + Shape::kBM - 1) / Shape::kBM;
@@ -158,7 +230,8 @@ __global__ __launch_bounds__(Shape::kThreads) void GemmKernel(GemmArgs p) {
     // along a row-contiguous one: those rows only reach outputs that are never
     // stored, and the stored outputs sum the same products in the same order.
     const bool a_vec = (A_KCONTIG ? p.a_sm : p.a_sk) % 4 == 0 && ((reinterpret_cast<uintptr_t>(a) & 15) == 0);
-    const bool b_vec = (B_NCONTIG ? p.b_sk : p.b_sn) % 4 == 0 && ((reinterpret_cast<uintptr_t>(b) & 15) == 0);
+    const bool b_vec =
+        B_PATCH || ((B_NCONTIG ? p.b_sk : p.b_sn) % 4 == 0 && ((reinterpret_cast<uintptr_t>(b) & 15) == 0));
     const bool a_rows = row0 + Shape::kBM <= p.m || A_KCONTIG || p.m % 4 == 0;
     const bool b_cols = col0 + Shape::kBN <= p.n || !B_NCONTIG || p.n % 4 == 0;
     const bool interior = a_vec && b_vec && a_rows && b_cols;
@@ -166,16 +239,28 @@ __global__ __launch_bounds__(Shape::kThreads) void GemmKernel(GemmArgs p) {
     if (k_full > k_begin) {
         const auto aload = MakeOperand<Shape::kBM, Shape::kBK, Shape::kThreads, Shape::kPitchA, A_KCONTIG, false>(
             a, row0, p.a_sm, p.a_sk, p.m, k_full);
-        const auto bload = MakeOperand<Shape::kBN, Shape::kBK, Shape::kThreads, Shape::kPitchB, !B_NCONTIG, false>(
-            b, col0, p.b_sn, p.b_sk, p.n, k_full);
-        MainLoop<Shape, FLUSH>(aload, bload, k_begin, k_full, lds, acc);
+        if constexpr (B_PATCH) {
+            PatchLoader<Shape::kBN, Shape::kBK, Shape::kThreads, Shape::kPitchB, false> bload;
+            bload.init(p.patch, col0, p.n, k_full);
+            MainLoop<Shape, FLUSH>(aload, bload, k_begin, k_full, lds, acc);
+        } else {
+            const auto bload = MakeOperand<Shape::kBN, Shape::kBK, Shape::kThreads, Shape::kPitchB, !B_NCONTIG, false>(
+                b, col0, p.b_sn, p.b_sk, p.n, k_full);
+            MainLoop<Shape, FLUSH>(aload, bload, k_begin, k_full, lds, acc);
+        }
     }
     if (k_full < k_end) {
         const auto aload = MakeOperand<Shape::kBM, Shape::kBK, Shape::kThreads, Shape::kPitchA, A_KCONTIG, true>(
             a, row0, p.a_sm, p.a_sk, p.m, k_end);
-        const auto bload = MakeOperand<Shape::kBN, Shape::kBK, Shape::kThreads, Shape::kPitchB, !B_NCONTIG, true>(
-            b, col0, p.b_sn, p.b_sk, p.n, k_end);
-        MainLoop<Shape, FLUSH>(aload, bload, k_full, k_end, lds, acc);
+        if constexpr (B_PATCH) {
+            PatchLoader<Shape::kBN, Shape::kBK, Shape::kThreads, Shape::kPitchB, true> bload;
+            bload.init(p.patch, col0, p.n, k_end);
+            MainLoop<Shape, FLUSH>(aload, bload, k_full, k_end, lds, acc);
+        } else {
+            const auto bload = MakeOperand<Shape::kBN, Shape::kBK, Shape::kThreads, Shape::kPitchB, !B_NCONTIG, true>(
+                b, col0, p.b_sn, p.b_sk, p.n, k_end);
+            MainLoop<Shape, FLUSH>(aload, bload, k_full, k_end, lds, acc);
+        }
     }
 
     const int64_t plane = p.m * p.n;
@@ -337,7 +422,7 @@ __global__ __launch_bounds__(512) void SkinnyGemmKernel(GemmArgs p, int64_t k_sl
 }
 
 bool SkinnyApplies(const GemmArgs& p, int64_t batches) {
-    return batches == 1 && p.y_group == 0 && p.m <= 32 && p.a_sk == 1 && p.b_sk == 1 && p.k % 8 == 0 && p.a_sm % 4 == 0 &&
+    return batches == 1 && p.patch.x == nullptr && p.y_group == 0 && p.m <= 32 && p.a_sk == 1 && p.b_sk == 1 && p.k % 8 == 0 && p.a_sm % 4 == 0 &&
            p.b_sn % 4 == 0 && (reinterpret_cast<uintptr_t>(p.a) & 15) == 0 &&
            (reinterpret_cast<uintptr_t>(p.b) & 15) == 0 && p.k > 0 && (p.n + 31) / 32 < (int64_t{1} << 31);
 }
@@ -382,7 +467,11 @@ void LaunchShape(GemmArgs p, int64_t batches, int splits, hipStream_t stream) {
     // costs occupancy).
     const bool two_level = p.k_per_split > kTwoLevelK;
     constexpr int kFlush = kChunkK / Shape::kBK;
-    if (a_k && b_n) {
+    if (p.patch.x != nullptr) {
+        // (A K-contiguous, one batch: LaunchGemm checks.)
+        two_level ? GemmKernel<Shape, true, false, kFlush, true><<<grid, block, 0, stream>>>(p)
+                  : GemmKernel<Shape, true, false, 0, true><<<grid, block, 0, stream>>>(p);
+    } else if (a_k && b_n) {
         two_level ? GemmKernel<Shape, true, true, kFlush><<<grid, block, 0, stream>>>(p)
                   : GemmKernel<Shape, true, true, 0><<<grid, block, 0, stream>>>(p);
     } else if (a_k) {
@@ -524,12 +613,16 @@ void LaunchGemm(GemmArgs p, int64_t batches, hipStream_t stream) {
     if (p.y_group > 0 && (batches != 1 || p.y_group % 4 != 0 || p.n % p.y_group != 0)) {
         throw Error("gemm: grouped output needs one batch and groups of whole quads dividing n");
     }
+    if (p.patch.x != nullptr && (batches != 1 || p.a_sk != 1 || p.patch.kw % 4 != 0 ||
+                                 (reinterpret_cast<uintptr_t>(p.patch.x) & 15) != 0)) {
+        throw Error("gemm: an in-place patch operand needs one batch, A K-contiguous and 16-byte runs");
+    }
     const int fallback_shape = p.m <= 32 ? 2 : (TileCount<ShapeL>(p, batches) < 1024 ? 1 : 0);
     static std::mutex mu;
     static std::map<GemmKey, int> chosen;
     // The key leaves the epilogue out: a fused and an unfused call of the
     // same product sum in the same order.
-    const GemmKey key{p.m, p.n, p.k, batches, p.a_sk == 1, p.b_sn == 1, p.batch_rank, 0, 0, 0};
+    const GemmKey key{p.m, p.n, p.k, batches, p.a_sk == 1, p.b_sn == 1, p.batch_rank, p.patch.x != nullptr, 0, 0};
     const size_t y_bytes = static_cast<size_t>(batches * p.m * p.n) * sizeof(float);
     const bool skinny = SkinnyApplies(p, batches);
     // NERT_HIP_GEMM_CANDIDATE=i forces candidate i wherever it applies (tests

@@ -38,6 +38,19 @@ struct GemmArgs {
     // [n / G][m][n % G], e.g. a conv's NCHW output when n runs over (image,
     // pixel) and G is the pixels per image.
     int64_t y_group;
+    // B read in place from the input of a convolution whose windows tile it
+    // exactly (stride = kernel, no padding) when patch.x is set (one batch,
+    // A K-contiguous): B(k, n) = x[img][c][oh * kh + r][ow * kw + q] for
+    // n = (img * out_h + oh) * out_w + ow and k = (c * kh + r) * kw + q, with
+    // kw a multiple of 4 and x 16-byte aligned (runs of 4 k are 16 bytes).
+    struct PatchB {
+        const float* x;
+        int32_t c, kh, kw, in_h, in_w, out_h, out_w;
+        FastDiv div_khkw;  // by kh * kw
+        FastDiv div_kw;    // by kw
+        FastDiv div_plane; // by out_h * out_w
+        FastDiv div_ow;    // by out_w
+    } patch;
 };
 
 // Offset of output (r, c) under the layout above.

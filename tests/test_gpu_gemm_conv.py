@@ -759,3 +759,19 @@ def test_gemm_every_candidate(gpu, monkeypatch, candidate, op, shapes, attrs):
         n = shapes[1][0] if attrs.get("transB") else shapes[1][1]
         out = (m, n)
     assert_parity(op, xs, [(out, F)], attrs)
+
+
+@pytest.mark.parametrize("candidate", list(range(25)))
+@pytest.mark.parametrize("xs,ws,strides", [
+    ((3, 5, 16, 16), (6, 5, 4, 4), [4, 4]),    # K = 80: a checked K tail; 48 pixels: edge tiles
+    ((2, 3, 64, 64), (40, 3, 16, 8), [16, 8]),  # non-square windows, 64 pixels
+])
+def test_patch_conv_every_gemm_candidate(gpu, monkeypatch, candidate, xs, ws, strides):
+    """A convolution whose windows tile its input runs as one GEMM whose B
+    loader reads the patches from X in place; under every GEMM candidate
+    (tile shapes, split counts) forced with NERT_HIP_GEMM_CANDIDATE, against
+    the reference row."""
+    monkeypatch.setenv("NERT_HIP_GEMM_CANDIDATE", str(candidate))
+    x, w, b = uniform(xs, seed=80), uniform(ws, seed=81), uniform((ws[0],), seed=82)
+    attrs = {"strides": strides}
+    assert_parity("Conv", [x, w, b], [(_conv_out(xs, ws, attrs), F)], attrs)
