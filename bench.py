@@ -336,7 +336,8 @@ def main() -> int:
             "rows_after_fusion": len(pg.nodes),
             "gflop_per_step": round(g.flops() / 1e9, 3),
             "launch": "nert_amd runner: HIP graph replay after Conv->Add->Relu fusion (bit-identical outputs), "
-                      "each stage's 3x3/2 conv paired with its 1x1/2 shortcut in one launch, and view aliasing; "
+                      "each stage's 3x3/2 conv paired with its 1x1/2 shortcut in one launch, the 3x3 weights packed once "
+                      "into the halo kernel's LDS order, and view aliasing; "
                       "the drop-in seam path is reported under 'dropin'",
         },
         "roofline": {
@@ -493,13 +494,14 @@ def measured_traffic() -> dict | None:
 
 
 def conv_row_flops(g, idx: int) -> int:
-    """2 * MACs of a Conv or FusedConv row; a paired FusedConv (six inputs,
-    two outputs) also counts its 1x1 convolution."""
+    """2 * MACs of a Conv or FusedConv row; a paired FusedConv (W2 as its
+    fifth input, two outputs) also counts its 1x1 convolution. (A seventh
+    input, the packed copy of W, adds no work.)"""
     n = g.nodes[idx]
     w = g.tensors[n.inputs[1]][1]
     y = g.tensors[n.outputs[0]][1]
     flops = 2 * int(np.prod(y)) * int(np.prod(w[1:]))
-    if n.op == "FusedConv" and len(n.inputs) == 6 and len(n.outputs) == 2:
+    if n.op == "FusedConv" and len(n.inputs) >= 6 and n.inputs[4] and len(n.outputs) == 2:
         w2 = g.tensors[n.inputs[4]][1]
         flops += 2 * int(np.prod(g.tensors[n.outputs[1]][1])) * int(np.prod(w2[1:]))
     return flops

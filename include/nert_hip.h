@@ -199,6 +199,20 @@ int nert_hip_conv_fused_f32(const float* x, const float* w, const float* bias, c
 int nert_hip_conv_pair_f32(const float* x, const float* w, const float* bias, const float* residual, float* y,
                            const float* w2, const float* bias2, float* y2, const nert_conv_desc* d, int act,
                            void* stream);
+/* nert_hip_conv_fused_f32 (w2 NULL) or nert_hip_conv_pair_f32 (w2 set) with
+ * the weights also given in the order the 3x3 LDS-patch kernel stores them,
+ * for weights that stay fixed across calls (a model's initializers, packed
+ * once): w_packed[m][b][t][j] = w[m][8 b + j][t] for output channel m,
+ * channel block b < C/group/8, tap t < KD*KH*KW (row-major over the
+ * kernel's axes) and j < 8; C/group must be a multiple of 8. That kernel
+ * copies the packed rows to LDS with 16-byte stores instead of transposing
+ * 4-byte ones; every other kernel reads w. Results are bit-identical to the
+ * unpacked call with the same kernel configuration. No reference
+ * counterpart: nert_amd's runner packs the 3x3 initializer weights and
+ * passes them as the FusedConv row's seventh input. */
+int nert_hip_conv_packed_f32(const float* x, const float* w, const float* w_packed, const float* bias,
+                             const float* residual, float* y, const float* w2, const float* bias2, float* y2,
+                             const nert_conv_desc* d, int act, void* stream);
 
 /* ---------------------------------------------------------- elementwise --- */
 

@@ -38,6 +38,12 @@ namespace {
 struct ConvArgs {
     const float* x;
     const float* w;
+    // W again in the order the 3x3 LDS-patch kernel stores it, or null: per
+    // output channel, blocks of 8 input channels, in a block the taps, in a
+    // tap the 8 channels ([M][C_g / 8][KH * KW][8]); that kernel then copies
+    // it to LDS with 16-byte stores instead of transposing 4-byte ones.
+    // Every other kernel reads `w`.
+    const float* w_packed;
     const float* bias;
     float* y;
     int64_t batch, c, m, group;
@@ -794,7 +800,9 @@ __device__ __forceinline__ ConvArgs PairArgs(const ConvArgs& p, const HaloGeom& 
 
 // Register budget: 128 VGPRs (four waves per SIMD, two workgroups per CU),
 // except with four patch positions per thread, where that would spill.
-template <class Shape, int KH, int KW, int NPOS, bool PAIR = false>
+// PACKED: the weights come from p.w_packed (ConvArgs), copied to LDS with
+// 16-byte stores.
+template <class Shape, int KH, int KW, int NPOS, bool PAIR = false, bool PACKED = false>
 __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKernel(ConvArgs p, HaloGeom h) {
     constexpr int BM = Shape::kBM;
     constexpr int BN = Shape::kBN;
@@ -887,7 +895,7 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
     // (channel-major, taps inside), copied as 16-byte loads; quad
     // e = tid + j * THREADS is row e / kQuadsRow, floats 4 * (e % kQuadsRow)...
     // The host guarantees 16-byte alignment (C_g a multiple of 4).
-    const __amdgpu_buffer_rsrc_t wr = MakeRsrc(p.w, static_cast<uint32_t>(p.m * p.kg * 4));
+    const __amdgpu_buffer_rsrc_t wr = MakeRsrc(PACKED ? p.w_packed : p.w, static_cast<uint32_t>(p.m * p.kg * 4));
     uint32_t avoff[kAQuads];
 #pragma unroll
     for (int j = 0; j < kAQuads; ++j) {
@@ -972,17 +980,24 @@ __global__ __launch_bounds__(Shape::kThreads, NPOS >= 4 ? 2 : 4) void HaloConvKe
                 }
             }
         }
-        // Weight float k of a row slice is channel k / kTaps, tap k % kTaps.
+        // Weight float k of a row slice is channel k / kTaps, tap k % kTaps;
+        // packed, it is 8-channel group k / (8 kTaps), tap k % (8 kTaps) / 8,
+        // channel k % 8 of the group, so a quad is 4 channels of one tap.
 #pragma unroll
         for (int j = 0; j < kAQuads; ++j) {
             const int e = tid + j * THREADS;
             if (e < BM * kQuadsRow) {
                 float* row = as + (e / kQuadsRow) * kAPitch;
                 const int k0 = (e % kQuadsRow) * 4;
+                if constexpr (PACKED) {
+                    const int in8 = k0 % (8 * kTaps);
+                    *reinterpret_cast<nert_floatx4*>(row + (in8 / 8) * BK + (k0 / (8 * kTaps)) * 8 + in8 % 8) = av[j];
+                } else {
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int k = k0 + q;
-                    row[(k % kTaps) * BK + k / kTaps] = av[j][q];
+                    for (int q = 0; q < 4; ++q) {
+                        const int k = k0 + q;
+                        row[(k % kTaps) * BK + k / kTaps] = av[j][q];
+                    }
                 }
             }
         }
@@ -1235,12 +1250,21 @@ using HaloShapeM16 = TileShape<64, 128, 16, 2, 4>;
 using HaloShapeQ16 = TileShape<64, 64, 16, 2, 2>;
 using HaloShapeN16 = TileShape<32, 128, 16, 1, 4>;
 
+template <class Shape, int NPOS, bool PACKED>
+void LaunchHaloPacked(const ConvArgs& p, const HaloGeom& h, dim3 grid, size_t lds, hipStream_t stream) {
+    if (h.w2 != nullptr) {
+        HaloConvKernel<Shape, 3, 3, NPOS, true, PACKED><<<grid, Shape::kThreads, lds, stream>>>(p, h);
+    } else {
+        HaloConvKernel<Shape, 3, 3, NPOS, false, PACKED><<<grid, Shape::kThreads, lds, stream>>>(p, h);
+    }
+}
+
 template <class Shape, int NPOS>
 void LaunchHaloPos(const ConvArgs& p, const HaloGeom& h, dim3 grid, size_t lds, hipStream_t stream) {
-    if (h.w2 != nullptr) {
-        HaloConvKernel<Shape, 3, 3, NPOS, true><<<grid, Shape::kThreads, lds, stream>>>(p, h);
+    if (p.w_packed != nullptr) {
+        LaunchHaloPacked<Shape, NPOS, true>(p, h, grid, lds, stream);
     } else {
-        HaloConvKernel<Shape, 3, 3, NPOS><<<grid, Shape::kThreads, lds, stream>>>(p, h);
+        LaunchHaloPacked<Shape, NPOS, false>(p, h, grid, lds, stream);
     }
 }
 
@@ -1261,22 +1285,21 @@ void LaunchHalo(const ConvArgs& p, const HaloGeom& h, dim3 grid, size_t lds, int
 // process for the shape's kernels; false when the runtime refuses.
 constexpr int kHaloMaxLds16 = 80 * 1024;
 
+template <class Shape, bool PAIR, bool PACKED>
+bool AllowHaloLdsFor() {
+    const auto raise = [](const void* kernel) {
+        return hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kHaloMaxLds16) == hipSuccess;
+    };
+    return raise(reinterpret_cast<const void*>(&HaloConvKernel<Shape, 3, 3, 1, PAIR, PACKED>)) &&
+           raise(reinterpret_cast<const void*>(&HaloConvKernel<Shape, 3, 3, 2, PAIR, PACKED>)) &&
+           raise(reinterpret_cast<const void*>(&HaloConvKernel<Shape, 3, 3, 4, PAIR, PACKED>));
+}
+
 template <class Shape>
 bool AllowHaloLds() {
     static const bool allowed = [] {
-        bool ok = true;
-        ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(&HaloConvKernel<Shape, 3, 3, 1>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kHaloMaxLds16) == hipSuccess;
-        ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(&HaloConvKernel<Shape, 3, 3, 2>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kHaloMaxLds16) == hipSuccess;
-        ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(&HaloConvKernel<Shape, 3, 3, 4>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kHaloMaxLds16) == hipSuccess;
-        ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(&HaloConvKernel<Shape, 3, 3, 1, true>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kHaloMaxLds16) == hipSuccess;
-        ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(&HaloConvKernel<Shape, 3, 3, 2, true>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kHaloMaxLds16) == hipSuccess;
-        ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(&HaloConvKernel<Shape, 3, 3, 4, true>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kHaloMaxLds16) == hipSuccess;
+        const bool ok = AllowHaloLdsFor<Shape, false, false>() && AllowHaloLdsFor<Shape, true, false>() &&
+                        AllowHaloLdsFor<Shape, false, true>() && AllowHaloLdsFor<Shape, true, true>();
         if (!ok) {
             (void)hipGetLastError();
         }
@@ -2885,40 +2908,69 @@ extern "C" int nert_hip_conv_fused_f32(const float* x, const float* w, const flo
     });
 }
 
+namespace nert_hip {
+
+// nert_hip_conv_pair_f32's work for the arguments of its 3x3 convolution.
+void RunConvPair(const ConvArgs& p, const float* w2, const float* bias2, float* y2, const nert_conv_desc* d,
+                 void* stream) {
+    // The 1x1 convolution: same input, stride and output shape, kernel 1,
+    // pad 0, dilation 1.
+    nert_conv_desc d2 = *d;
+    for (int i = 0; i < 3; ++i) {
+        d2.kernel[i] = 1;
+        d2.pad[i] = 0;
+        d2.dilation[i] = 1;
+    }
+    const ConvArgs p2 = MakeConvArgs(p.x, w2, bias2, nullptr, y2, &d2, 0);
+    if (p.group != 1 || p.k_d != 1 || p.k_h != 3 || p.k_w != 3 || p.p_h != 1 || p.p_w != 1 || p.d_h != 1 ||
+        p.d_w != 1) {
+        throw Error("conv pair: the first convolution must be 3x3 with pad 1, dilation 1, group 1");
+    }
+    for (int i = 0; i < 3; ++i) {
+        const int64_t in = d->in[i];
+        const int64_t expect = (in - 1) / d->stride[i] + 1;
+        if (d->out[i] != expect) {
+            throw Error("conv pair: the output shape is not that of both convolutions");
+        }
+    }
+    if (p.n_total == 0 || p.mg == 0) {
+        return;
+    }
+    hipStream_t s = StreamOr(stream);
+    if (TryHaloPair(p, HaloPair{w2, bias2, y2}, s)) {
+        return;
+    }
+    RunConv(p, s);
+    RunConv(p2, s);
+}
+
+} // namespace nert_hip
+
 extern "C" int nert_hip_conv_pair_f32(const float* x, const float* w, const float* bias, const float* residual,
                                       float* y, const float* w2, const float* bias2, float* y2,
                                       const nert_conv_desc* d, int act, void* stream) {
     return nert_hip::Guard([&] {
-        const nert_hip::ConvArgs p = nert_hip::MakeConvArgs(x, w, bias, residual, y, d, act);
-        // The 1x1 convolution: same input, stride and output shape, kernel
-        // 1, pad 0, dilation 1.
-        nert_conv_desc d2 = *d;
-        for (int i = 0; i < 3; ++i) {
-            d2.kernel[i] = 1;
-            d2.pad[i] = 0;
-            d2.dilation[i] = 1;
+        nert_hip::RunConvPair(nert_hip::MakeConvArgs(x, w, bias, residual, y, d, act), w2, bias2, y2, d, stream);
+    });
+}
+
+extern "C" int nert_hip_conv_packed_f32(const float* x, const float* w, const float* w_packed, const float* bias,
+                                        const float* residual, float* y, const float* w2, const float* bias2,
+                                        float* y2, const nert_conv_desc* d, int act, void* stream) {
+    return nert_hip::Guard([&] {
+        nert_hip::ConvArgs p = nert_hip::MakeConvArgs(x, w, bias, residual, y, d, act);
+        if (w_packed == nullptr) {
+            throw nert_hip::Error("conv packed: the packed weights are null");
         }
-        const nert_hip::ConvArgs p2 = nert_hip::MakeConvArgs(x, w2, bias2, nullptr, y2, &d2, 0);
-        if (p.group != 1 || p.k_d != 1 || p.k_h != 3 || p.k_w != 3 || p.p_h != 1 || p.p_w != 1 || p.d_h != 1 ||
-            p.d_w != 1) {
-            throw nert_hip::Error("conv pair: the first convolution must be 3x3 with pad 1, dilation 1, group 1");
+        if (p.cg % 8 != 0) {
+            throw nert_hip::Error("conv packed: packed weights need C / group to be a multiple of 8");
         }
-        for (int i = 0; i < 3; ++i) {
-            const int64_t in = d->in[i];
-            const int64_t expect = (in - 1) / d->stride[i] + 1;
-            if (d->out[i] != expect) {
-                throw nert_hip::Error("conv pair: the output shape is not that of both convolutions");
-            }
-        }
-        if (p.n_total == 0 || p.mg == 0) {
+        p.w_packed = w_packed;
+        if (w2 != nullptr) {
+            nert_hip::RunConvPair(p, w2, bias2, y2, d, stream);
             return;
         }
-        hipStream_t s = nert_hip::StreamOr(stream);
-        if (nert_hip::TryHaloPair(p, nert_hip::HaloPair{w2, bias2, y2}, s)) {
-            return;
-        }
-        nert_hip::RunConv(p, s);
-        nert_hip::RunConv(p2, s);
+        nert_hip::RunConv(p, nert_hip::StreamOr(stream));
     });
 }
 

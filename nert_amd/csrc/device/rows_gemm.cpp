@@ -530,14 +530,31 @@ int ActivationCode(const Node& node, const std::string& context) {
     return 0;
 }
 
+// The packed copy of W (FusedConv's seventh input): W's shape and dtype,
+// C/group a multiple of 8 (the order is nert_hip_conv_packed_f32's).
+const float* PackedWeights(const std::string& context, const TensorView& w, const TensorView& packed,
+                           const nert_conv_desc& d) {
+    if (packed.dtype != DataType::Float32 || packed.dims != w.dims) {
+        throw InferenceException(context + ": the packed weights must be float32 with the weight's shape");
+    }
+    if ((d.in_channels / d.group) % 8 != 0) {
+        throw InferenceException(context + ": packed weights need C / group to be a multiple of 8");
+    }
+    if (packed.data == nullptr) {
+        throw InferenceException(context + ": null buffer");
+    }
+    return static_cast<const float*>(packed.data);
+}
+
 // FusedConv with a paired 1x1 convolution: inputs X, W, B, Z, W2, B2 (B, Z
-// and B2 may be omitted), outputs Y and Y2.
+// and B2 may be omitted) and optionally W packed, outputs Y and Y2.
 void FusedConvPair(const Node& node, const std::string& context, const Views& inputs, const Views& outputs) {
     const int act = ActivationCode(node, context);
     const bool has_bias = inputs[2].dtype != DataType::Unknown;
     const TensorView* z = inputs[3].dtype != DataType::Unknown ? &inputs[3] : nullptr;
     Views main_inputs(inputs.begin(), inputs.begin() + (has_bias ? 3 : 2));
     const ConvCall c = CheckConv(node, context, main_inputs, has_bias, z, Views{outputs[0]});
+    const float* packed = inputs.size() == 7 ? PackedWeights(context, inputs[1], inputs[6], c.d) : nullptr;
     const TensorView& w2 = inputs[4];
     const TensorView& b2 = inputs[5];
     const TensorView& y2 = outputs[1];
@@ -561,12 +578,22 @@ void FusedConvPair(const Node& node, const std::string& context, const Views& in
     if (w2.data == nullptr || y2.data == nullptr || (has_b2 && b2.data == nullptr)) {
         throw InferenceException(context + ": null buffer");
     }
-    CheckStatus(nert_hip_conv_pair_f32(static_cast<const float*>(inputs[0].data),
-                                       static_cast<const float*>(inputs[1].data), c.bias, c.residual,
-                                       static_cast<float*>(outputs[0].data), static_cast<const float*>(w2.data),
-                                       has_b2 ? static_cast<const float*>(b2.data) : nullptr,
-                                       static_cast<float*>(y2.data), &d, act, Stream()),
-                context);
+    if (packed != nullptr) {
+        CheckStatus(nert_hip_conv_packed_f32(static_cast<const float*>(inputs[0].data),
+                                             static_cast<const float*>(inputs[1].data), packed, c.bias, c.residual,
+                                             static_cast<float*>(outputs[0].data),
+                                             static_cast<const float*>(w2.data),
+                                             has_b2 ? static_cast<const float*>(b2.data) : nullptr,
+                                             static_cast<float*>(y2.data), &d, act, Stream()),
+                    context);
+    } else {
+        CheckStatus(nert_hip_conv_pair_f32(static_cast<const float*>(inputs[0].data),
+                                           static_cast<const float*>(inputs[1].data), c.bias, c.residual,
+                                           static_cast<float*>(outputs[0].data), static_cast<const float*>(w2.data),
+                                           has_b2 ? static_cast<const float*>(b2.data) : nullptr,
+                                           static_cast<float*>(y2.data), &d, act, Stream()),
+                    context);
+    }
     AfterRow(outputs, context);
 }
 
@@ -593,11 +620,31 @@ void Conv(const Node& node, const Views& inputs, const Views& outputs) {
 // outputs it also computes Y2 = Conv(X, W2, B2) for a 1x1 W2 at the node's
 // strides with pad 0, which the runner pairs with a 3x3 pad-1 conv of the
 // same input (a ResNet block's downsampling shortcut): one launch for both
-// (nert_hip_conv_pair_f32).
+// (nert_hip_conv_pair_f32). A seventh input is W again in the packed order
+// of nert_hip_conv_packed_f32 (the runner packs 3x3 initializer weights
+// once); without a pair, W2 and B2 are then omitted and there is one output.
 void FusedConv(const Node& node, const Views& inputs, const Views& outputs) {
     const std::string context = "FusedConv (node '" + node.name + "')";
-    if (inputs.size() == 6 && outputs.size() == 2) {
+    const bool paired = (inputs.size() == 6 || (inputs.size() == 7 && inputs[4].dtype != DataType::Unknown)) &&
+                        outputs.size() == 2;
+    if (paired) {
         FusedConvPair(node, context, inputs, outputs);
+        return;
+    }
+    if (inputs.size() == 7 && outputs.size() == 1 && inputs[4].dtype == DataType::Unknown &&
+        inputs[5].dtype == DataType::Unknown) {
+        const int act = ActivationCode(node, context);
+        const bool has_bias = inputs[2].dtype != DataType::Unknown;
+        const TensorView* z = inputs[3].dtype != DataType::Unknown ? &inputs[3] : nullptr;
+        Views conv_inputs(inputs.begin(), inputs.begin() + (has_bias ? 3 : 2));
+        const ConvCall c = CheckConv(node, context, conv_inputs, has_bias, z, outputs);
+        const float* packed = PackedWeights(context, inputs[1], inputs[6], c.d);
+        CheckStatus(nert_hip_conv_packed_f32(static_cast<const float*>(inputs[0].data),
+                                             static_cast<const float*>(inputs[1].data), packed, c.bias, c.residual,
+                                             static_cast<float*>(outputs[0].data), nullptr, nullptr, nullptr, &c.d,
+                                             act, Stream()),
+                    context);
+        AfterRow(outputs, context);
         return;
     }
     if (inputs.size() < 2 || inputs.size() > 4 || outputs.size() != 1) {

@@ -282,6 +282,38 @@ def pair_downsample_convs(g: Graph) -> Graph:
     return Graph(nodes=nodes, initializers=g.initializers, inputs=g.inputs, outputs=g.outputs, tensors=g.tensors)
 
 
+def pack_conv_weights(g: Graph) -> Graph:
+    """Gives every 3x3 Conv or FusedConv whose weight is a float32
+    initializer with C/group a multiple of 8 a second copy of that weight in
+    the order the 3x3 LDS-patch kernel stores it -- per output channel,
+    blocks of 8 input channels, in a block the 9 taps, in a tap the 8
+    channels: packed[m][b][t][j] = W[m][8 b + j][t] -- as the FusedConv row's
+    seventh input (X, W, B, Z, W2, B2, W packed; the omitted ones empty),
+    which runs nert_hip_conv_packed_f32. The kernel then copies the weights
+    to LDS with 16-byte stores instead of transposing 4-byte ones. The copy
+    is made once, here; the results are bit-identical."""
+    initializers = dict(g.initializers)
+    tensors = dict(g.tensors)
+    nodes = []
+    for n in g.nodes:
+        w_name = n.inputs[1] if len(n.inputs) > 1 else ""
+        w = g.initializers.get(w_name)
+        fits = n.op in ("Conv", "FusedConv") and len(n.inputs) <= 6 and w is not None and w.dtype == np.float32 and \
+            w.ndim == 4 and w.shape[2:] == (3, 3) and w.shape[1] % 8 == 0
+        if not fits:
+            nodes.append(n)
+            continue
+        name = w_name + ":packed"
+        if name not in initializers:
+            m, cg = w.shape[0], w.shape[1]
+            packed = np.ascontiguousarray(w.reshape(m, cg // 8, 8, 9).transpose(0, 1, 3, 2)).reshape(w.shape)
+            initializers[name] = packed
+            tensors[name] = (packed.dtype, tuple(packed.shape))
+        ins = list(n.inputs) + [""] * (6 - len(n.inputs)) + [name]
+        nodes.append(Node("FusedConv", ins, list(n.outputs), dict(n.attrs), n.name))
+    return Graph(nodes=nodes, initializers=initializers, inputs=g.inputs, outputs=g.outputs, tensors=tensors)
+
+
 def _scalar(g: Graph, name: str) -> float | None:
     """The value of a float32 scalar initializer (shape () or (1,)), else None."""
     v = g.initializers.get(name)
@@ -591,24 +623,28 @@ class _PackedNode:
         self.err = C.create_string_buffer(1024)
 
 
-def fuse_rows(g: Graph, attention: bool = True, pairs: bool = True) -> Graph:
+def fuse_rows(g: Graph, attention: bool = True, pairs: bool = True, packed: bool = True) -> Graph:
     """The runner's fusions in order: Conv chains, 3x3 convs paired with
-    their 1x1 downsampling shortcuts (when `pairs`), attention blocks (when
-    `attention`), MatMul chains, residual Add + LayerNorm. All but the pairs'
-    1x1 outputs and the attention blocks are bit-identical to the separate
-    rows; those two sum in another order, within the rows' tolerance."""
+    their 1x1 downsampling shortcuts (when `pairs`), packed 3x3 weights (when
+    `packed`), attention blocks (when `attention`), MatMul chains, residual
+    Add + LayerNorm. All but the pairs' 1x1 outputs and the attention blocks
+    are bit-identical to the separate rows; those two sum in another order,
+    within the rows' tolerance."""
     g = fuse_conv_chains(g)
     if pairs:
         g = pair_downsample_convs(g)
+    if packed:
+        g = pack_conv_weights(g)
     if attention:
         g = fuse_attention(g)
     return fuse_add_layernorm(fuse_matmul_chains(g))
 
 
 class Program:
-    def __init__(self, g: Graph, fuse: bool = True, views: bool = True, attention: bool = True, pairs: bool = True):
+    def __init__(self, g: Graph, fuse: bool = True, views: bool = True, attention: bool = True, pairs: bool = True,
+                 packed: bool = True):
         if fuse:
-            g = fuse_rows(g, attention, pairs)
+            g = fuse_rows(g, attention, pairs, packed)
         self.alias: dict[str, tuple[str, int]] = {}
         if views:
             g, self.alias = alias_views(g)

@@ -775,3 +775,67 @@ def test_patch_conv_every_gemm_candidate(gpu, monkeypatch, candidate, xs, ws, st
     x, w, b = uniform(xs, seed=80), uniform(ws, seed=81), uniform((ws[0],), seed=82)
     attrs = {"strides": strides}
     assert_parity("Conv", [x, w, b], [(_conv_out(xs, ws, attrs), F)], attrs)
+
+
+_PACKED = """
+import json, os, sys
+import numpy as np
+sys.path.insert(0, {root!r})
+from nert_amd.device import DeviceArray, run_node
+x, w, b, w2, b2 = (np.load(p) for p in {ins!r})
+a = json.loads({attrs!r})
+m, cg = w.shape[:2]
+wp = np.ascontiguousarray(w.reshape(m, cg // 8, 8, 9).transpose(0, 1, 3, 2)).reshape(w.shape)
+dev = lambda v: DeviceArray.from_host(v)
+shape = [x.shape[0], m] + [(x.shape[2 + i] + 2 - 3) // a["strides"][i] + 1 for i in range(2)]
+out = {{}}
+for cand in {cands!r}:
+    os.environ["NERT_HIP_CONV_CANDIDATE"] = str(cand)
+    for packed in (False, True):
+        y = DeviceArray(shape, np.float32)
+        ins = [dev(x), dev(w), dev(b)] + ([None, None, None, dev(wp)] if packed else [])
+        run_node("FusedConv", ins, [y], a)
+        out[f"single_{{cand}}_{{int(packed)}}"] = y.to_host()
+        y, y2 = DeviceArray(shape, np.float32), DeviceArray(shape, np.float32)
+        ins = [dev(x), dev(w), dev(b), None, dev(w2), dev(b2)] + ([dev(wp)] if packed else [])
+        run_node("FusedConv", ins, [y, y2], a)
+        out[f"pair_{{cand}}_{{int(packed)}}"] = y.to_host()
+        out[f"pair2_{{cand}}_{{int(packed)}}"] = y2.to_host()
+np.savez({out!r}, **out)
+"""
+
+
+@pytest.mark.parametrize("xs,m,stride", [((2, 64, 20, 20), 64, 1), ((2, 32, 15, 13), 48, 2), ((1, 16, 9, 9), 32, 1)])
+def test_conv_packed_weights_bit_identical(gpu, tmp_path, xs, m, stride):
+    """FusedConv with W also given packed (seventh input, the 3x3 LDS-patch
+    kernel's order) against the same row without it, single and paired with
+    a 1x1 shortcut, under every 3x3 configuration forced in turn (8- and
+    16-channel blocks, split and tail pieces; tuning off): bit-identical;
+    the tuned result matches the restatement."""
+    import json
+    import os
+    import subprocess
+    import sys
+
+    attrs = {"pads": [1, 1, 1, 1], "strides": [stride, stride], "activation": "Relu"}
+    x = randn(xs, seed=140)
+    w = randn((m, xs[1], 3, 3), seed=141, scale=0.05)
+    b = randn((m,), seed=142, scale=0.1)
+    w2 = randn((m, xs[1], 1, 1), seed=143, scale=0.1)
+    b2 = randn((m,), seed=144, scale=0.1)
+    ins = []
+    for k, v in (("x", x), ("w", w), ("b", b), ("w2", w2), ("b2", b2)):
+        ins.append(str(tmp_path / f"{k}.npy"))
+        np.save(ins[-1], v)
+    out = str(tmp_path / "out.npz")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, NERT_HIP_CONV_TUNE="0", NERT_HIP_TUNE_TABLE=os.devnull)
+    cands = list(range(33))
+    subprocess.run([sys.executable, "-c", _PACKED.format(root=root, ins=ins, attrs=json.dumps(attrs), out=out,
+                                                          cands=cands)], env=env, check=True, timeout=120)
+    r = np.load(out)
+    for cand in cands:
+        for what in ("single", "pair", "pair2"):
+            assert np.array_equal(r[f"{what}_{cand}_0"], r[f"{what}_{cand}_1"]), (what, cand)
+    want = restate.conv(x, w, b, attrs["strides"], None, attrs["pads"], 1, "NOTSET")
+    compare(r["single_0_1"], np.where(want > 0, want, np.float32(0)).astype(F), what="packed FusedConv")

@@ -4,7 +4,7 @@ import numpy as np
 
 from nert_amd import workloads
 from nert_amd.graph import Graph
-from nert_amd.runner import fuse_conv_chains, pair_downsample_convs, plan_arena
+from nert_amd.runner import fuse_conv_chains, pack_conv_weights, pair_downsample_convs, plan_arena
 
 F = np.float32
 
@@ -47,6 +47,47 @@ def test_resnet18_downsample_pairs():
         assert g.tensors[n.outputs[0]][1] == g.tensors[n.outputs[1]][1]
     _valid_order(f)
     assert len(f.nodes) == len(fuse_conv_chains(g).nodes) - 3
+
+
+def test_pack_conv_weights():
+    """3x3 convs with C/group a multiple of 8 get W in the packed order as a
+    seventh input: packed[m][b][t][j] = W[m][8 b + j][t]; pairs keep their
+    six inputs before it; other convs are left as they are."""
+    g, _ = workloads.resnet18(batch=2)
+    f = pack_conv_weights(pair_downsample_convs(fuse_conv_chains(g)))
+    packed = [n for n in f.nodes if n.op == "FusedConv" and len(n.inputs) == 7]
+    # 17 3x3 convs of the 20 (the stem is 7x7 with C = 3; the pairs' 1x1s ride along)
+    assert len(packed) == 16 and sum(1 for n in packed if n.inputs[4]) == 3
+    for n in packed:
+        w = g.initializers[n.inputs[1]]
+        p = f.initializers[n.inputs[6]]
+        assert p.shape == w.shape and p.dtype == w.dtype and f.tensors[n.inputs[6]] == (p.dtype, p.shape)
+        m, cg = w.shape[:2]
+        # brute force over every element, against the formula
+        flat = p.reshape(m, -1)
+        for b in range(cg // 8):
+            for t in range(9):
+                for j in range(8):
+                    assert np.array_equal(flat[:, (b * 9 + t) * 8 + j], w[:, 8 * b + j, t // 3, t % 3])
+        if not n.inputs[4]:
+            assert n.inputs[4:6] == ["", ""] and len(n.outputs) == 1
+    assert [n.outputs for n in f.nodes] == [n.outputs for n in pair_downsample_convs(fuse_conv_chains(g)).nodes]
+    stem = f.nodes[0]
+    assert stem.op == "FusedConv" and len(stem.inputs) < 7
+    _valid_order(f)
+    # a grouped 3x3 conv with 4 channels per group and a plain Conv with 8
+    h = Graph()
+    x = h.add_input("x", F, (1, 16, 6, 6))
+    wa = h.add_initializer("wa", np.arange(16 * 4 * 9, dtype=F).reshape(16, 4, 3, 3))
+    wb = h.add_initializer("wb", np.arange(8 * 16 * 9, dtype=F).reshape(8, 16, 3, 3))
+    (a,) = h.add_node("Conv", [x, wa], [("a", F, (1, 16, 6, 6))], {"pads": [1, 1, 1, 1], "group": 4})
+    (b,) = h.add_node("Conv", [a, wb], [("b", F, (1, 8, 6, 6))], {"pads": [1, 1, 1, 1]})
+    h.outputs = [b]
+    k = pack_conv_weights(h)
+    assert k.nodes[0].op == "Conv" and k.nodes[0].inputs == [x, wa]
+    assert k.nodes[1].op == "FusedConv" and k.nodes[1].inputs == [a, wb, "", "", "", "", "wb:packed"]
+    assert k.nodes[1].attrs == {"pads": [1, 1, 1, 1]}
+    assert k.initializers["wb:packed"].reshape(8, 2, 9, 8)[5, 1, 4, 3] == h.initializers[wb][5, 11, 1, 1]
 
 
 def _pair_graph(pads2=(0, 0, 0, 0), stride2=(2, 2), m2=8, between=False):
