@@ -16,9 +16,10 @@
 // row's K largest are among the chunks' candidates. The row's last chunk
 // workgroup to finish (a zero-kept counter per row) then merges them
 // (MergeTop): the candidates' own threshold for rank K splits them into keys
-// in the result and keys tied on the threshold's 24 bits, ranked among
+// in the result and keys tied on the threshold's bits, ranked among
 // themselves in LDS (or radix-selected past an LDS capacity); the K keys are
-// ranked (all keys are unique) and written out. When a chunk had more
+// ranked (all keys are unique; by a counting sort on the threshold's bins
+// when it stopped at 12 bits) and written out. When a chunk had more
 // candidates than its slots hold, the merge reads the row again. Without the
 // counters (NERT_HIP_SPLIT_FIXUP=0) the merge is a second launch, one
 // workgroup per row.
@@ -147,6 +148,7 @@ constexpr int kBins = 4096;          // 12-bit digits
 constexpr int kWgCand = 1024;        // candidate keys a chunk workgroup keeps
 constexpr int kBatch = 16;           // candidate keys per merging thread held in registers
 constexpr int kTieCap = 2048;        // keys tied on 24 bits that the merge ranks in LDS
+constexpr uint32_t kMergeTieBin = 256; // the merge's threshold stops at 12 bits when its bin holds this many
 constexpr int kChunkQuads = 6;       // 16-byte loads per thread and chunk (all issued up front)
 constexpr int kChunkMax = kFT * 4 * kChunkQuads;
 constexpr int kMergeKeys = kFT * kBatch; // candidates per row the merge aims for
@@ -274,6 +276,45 @@ __device__ __forceinline__ void BlockRange(uint32_t hi, uint32_t lo, uint32_t* t
     __syncthreads(); // the next call may overwrite the results
 }
 
+// h[b] := the number of keys in the bins above b, for kBins LDS counts
+// (kFT threads, kBins / kFT bins each from the top down; barriers).
+__device__ __forceinline__ void SuffixAbove(uint32_t* h) {
+    constexpr int kPer = kBins / kFT;
+    __shared__ uint32_t wave_sum[kFT / 64];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    uint32_t c[kPer];
+    uint32_t local = 0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        c[j] = h[kBins - 1 - kPer * t - j];
+        local += c[j];
+    }
+    uint32_t incl = local;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(incl, off, 64);
+        if (lane >= off) {
+            incl += y;
+        }
+    }
+    if (lane == 63) {
+        wave_sum[wave] = incl;
+    }
+    __syncthreads();
+    for (int w = 0; w < wave; ++w) {
+        incl += wave_sum[w];
+    }
+    uint32_t run = incl - local;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        h[kBins - 1 - kPer * t - j] = run;
+        run += c[j];
+    }
+    __syncthreads();
+}
+
 // The threshold of a set of keys for rank `need`, on a window of 24 key
 // bits fitted to the set's orderable values, which lie in [bottom, top]:
 // every key shares the key bits above bit L + 24, where L = 20 + s and s is
@@ -282,14 +323,19 @@ __device__ __forceinline__ void BlockRange(uint32_t hi, uint32_t lo, uint32_t* t
 // `above1` keys above it), the next 12 bits of the keys in t1 give bin t2;
 // returns L and sets *floor = (top's bits above the window) << 24 | t1 << 12
 // | t2, so that (key >> L) > *floor holds for fewer than `need` keys and
-// (key >> L) >= *floor for at least `need`. A window fitted to the values
-// spreads them over the bins (few LDS adds to one address), however narrow
-// their range. `visit(f)` calls f(key, valid) for each thread's share of
-// the set, the same in every call; `h` is kBins words of LDS. Run by the
-// whole workgroup; contains barriers.
+// (key >> L) >= *floor for at least `need`. When bin t1 holds at most
+// `max_in_bin` keys and the keys from t1 up at most `max_total`, the second
+// level is skipped: then it returns L + 12 and *floor = (top's bits above
+// the window) << 12 | t1, with the same two properties, sets *coarse, and
+// leaves the first level's counts in `h`. A window fitted to
+// the values spreads them over the bins (few LDS adds to one address),
+// however narrow their range. `visit(f)` calls f(key, valid) for each
+// thread's share of the set, the same in every call; `h` is kBins words of
+// LDS. Run by the whole workgroup; contains barriers.
 template <typename Visit>
 __device__ __forceinline__ int ThresholdInRange(uint32_t* h, uint32_t need, Visit visit, uint32_t top, uint32_t bottom,
-                                                uint64_t* floor) {
+                                                uint64_t* floor, uint32_t max_in_bin, uint32_t max_total,
+                                                bool* coarse = nullptr) {
     const uint32_t diff = top ^ bottom;
     const int width = diff == 0 ? 0 : 32 - __clz(static_cast<int>(diff));
     const int L = 20 + (width > 12 ? width - 12 : 0);
@@ -305,6 +351,21 @@ __device__ __forceinline__ int ThresholdInRange(uint32_t* h, uint32_t need, Visi
     __syncthreads();
     uint32_t above1 = 0;
     const uint32_t t1 = BlockTopSelect(h, kBins, need, &above1);
+    // top's bits above the window (none when the window reaches the top bit;
+    // a 64-bit shift would be undefined).
+    const uint64_t common = L + 24 < 64 ? (static_cast<uint64_t>(top) << 32) >> (L + 24) : 0;
+    const uint32_t in_bin = h[t1];
+    __syncthreads(); // every thread has read h[t1] before the clear below
+    if (coarse != nullptr) {
+        *coarse = false;
+    }
+    if (in_bin <= max_in_bin && above1 + in_bin <= max_total) {
+        *floor = (common << 12) | t1;
+        if (coarse != nullptr) {
+            *coarse = true;
+        }
+        return L + 12;
+    }
     for (int b = threadIdx.x; b < kBins; b += kFT) {
         h[b] = 0;
     }
@@ -317,9 +378,6 @@ __device__ __forceinline__ int ThresholdInRange(uint32_t* h, uint32_t need, Visi
     __syncthreads();
     uint32_t above2 = 0;
     const uint32_t t2 = BlockTopSelect(h, kBins, need - above1, &above2);
-    // top's bits above the window (none when the window reaches the top bit;
-    // a 64-bit shift would be undefined).
-    const uint64_t common = L + 24 < 64 ? (static_cast<uint64_t>(top) << 32) >> (L + 24) : 0;
     *floor = (common << 24) | (static_cast<uint64_t>(t1) << 12) | t2;
     return L;
 }
@@ -440,7 +498,7 @@ __device__ __forceinline__ void ChunkTop(const float* __restrict__ x, const RowG
             [&](auto f) {
                 visit([&](uint64_t key, bool valid) { f(key, valid && static_cast<uint32_t>(key >> 32) >= low); });
             },
-            top, bottom, &floor);
+            top, bottom, &floor, 0xFFFFFFFFu, static_cast<uint32_t>(kWgCand));
         bottom = static_cast<uint32_t>((floor << L) >> 32);
     }
     // Candidates of this thread (bit e of `pass` for element e), then their
@@ -521,6 +579,8 @@ __device__ __forceinline__ void MergeTop(const float* __restrict__ x, float* val
     __shared__ uint32_t total_s;
     __shared__ uint32_t fits_s;
     __shared__ uint32_t overflow_s;
+    __shared__ uint32_t top_s;
+    __shared__ uint32_t bottom_s;
     __shared__ uint32_t n_fin;
     __shared__ uint32_t n_ties;
     // Chunk c's candidates go to threads c * T .. c * T + T - 1, kBatch
@@ -540,22 +600,42 @@ __device__ __forceinline__ void MergeTop(const float* __restrict__ x, float* val
         const int slot = member_slot + T * j;
         kv[j] = member && slot < kWgCand ? LoadShared(cand + (wg0 + group) * kWgCand + slot) : 0;
     }
-    if (tid == 0) {
-        fits_s = 1;
-        overflow_s = 0;
-        n_fin = 0;
-        n_ties = 0;
+    // Wave 0 reads every chunk's stats and reduces them (whether the
+    // candidates fit the groups' registers, whether a chunk overflowed its
+    // slots, their value range) for one barrier.
+    if (wave == 0) {
+        bool fits = true;
+        bool overflow = false;
+        uint32_t hi = 0;
+        uint32_t lo = 0xFFFFFFFFu;
+        for (int c = lane; c < chunks; c += 64) {
+            const ChunkStats st = LoadStats(stats + wg0 + c);
+            fits = fits && st.count <= static_cast<uint32_t>(kWgCand) && st.count <= static_cast<uint32_t>(T * kBatch);
+            overflow = overflow || st.count > static_cast<uint32_t>(kWgCand);
+            hi = st.top > hi ? st.top : hi;
+            lo = st.bottom < lo ? st.bottom : lo;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const uint32_t h2 = __shfl_xor(hi, off, 64);
+            const uint32_t l2 = __shfl_xor(lo, off, 64);
+            hi = h2 > hi ? h2 : hi;
+            lo = l2 < lo ? l2 : lo;
+        }
+        const bool all_fit = __all(fits);
+        const bool any_overflow = __any(overflow);
+        if (lane == 0) {
+            fits_s = all_fit ? 1u : 0u;
+            overflow_s = any_overflow ? 1u : 0u;
+            top_s = hi;
+            bottom_s = lo;
+            n_fin = 0;
+            n_ties = 0;
+        }
     }
     for (uint32_t i = tid; i < k; i += kFT) {
         fin[i] = uint64_t{0xFFFFFFFFu}; // a key of index 0: every index read back stays in the row
         rank_s[i] = 0;
-    }
-    __syncthreads();
-    if (member && (cs.count > static_cast<uint32_t>(kWgCand) || cs.count > static_cast<uint32_t>(T * kBatch))) {
-        fits_s = 0;
-    }
-    if (member && cs.count > static_cast<uint32_t>(kWgCand)) {
-        overflow_s = 1;
     }
     __syncthreads();
     const bool in_regs = fits_s != 0;
@@ -643,12 +723,69 @@ __device__ __forceinline__ void MergeTop(const float* __restrict__ x, float* val
     uint32_t range_top = 0;
     uint32_t range_bottom = 0;
     if (in_regs) {
-        BlockRange(cs.top, cs.bottom, &range_top, &range_bottom);
+        range_top = top_s;
+        range_bottom = bottom_s;
     } else {
         VisitRange(source, &range_top, &range_bottom);
     }
     uint64_t top = 0;
-    const int L = ThresholdInRange(h, k, source, range_top, range_bottom, &top);
+    bool coarse = false;
+    const int L = ThresholdInRange(h, k, source, range_top, range_bottom, &top, kMergeTieBin, 0xFFFFFFFFu, &coarse);
+    if (coarse) {
+        // A counting sort on the threshold's bins: keys above the threshold
+        // bin t1 go straight to the slots of their bin, bins in descending
+        // order (h[b] becomes the count above b, then each key takes the
+        // next slot of its bin), so a key's rank is its bin's first slot
+        // plus the count of larger keys in its bin; the keys in t1 (at most
+        // kMergeTieBin) are ranked among themselves after them.
+        const uint32_t t1 = static_cast<uint32_t>(top & 0xFFF);
+        SuffixAbove(h);
+        const uint32_t fin0 = h[t1]; // keys above the threshold, fewer than K
+        source([&](uint64_t key, bool valid) {
+            if (!valid) {
+                return;
+            }
+            if ((key >> L) > top) {
+                fin[atomicAdd(&h[static_cast<uint32_t>(key >> L) & 0xFFF], 1u)] = key;
+            } else if ((key >> L) == top) {
+                ties[atomicAdd(&n_ties, 1u)] = key;
+            }
+        });
+        __syncthreads();
+        const uint32_t need = k - fin0;
+        const uint32_t nt = n_ties;
+        for (uint32_t i = tid; i < nt; i += kFT) {
+            const uint64_t key = ties[i];
+            uint32_t rank = 0;
+            for (uint32_t j = 0; j < nt; ++j) {
+                rank += ties[j] > key ? 1u : 0u;
+            }
+            if (rank < need) {
+                fin[fin0 + rank] = key;
+            }
+        }
+        __syncthreads();
+        const int64_t o = row / g.inner;
+        const int64_t n = row - o * g.inner;
+        for (uint32_t i = tid; i < k; i += kFT) {
+            const uint64_t key = fin[i];
+            uint32_t rank = i;
+            if (i < fin0) {
+                // The bin's slots: [h[b + 1] (0 for the top bin), h[b]).
+                const uint32_t b = static_cast<uint32_t>(key >> L) & 0xFFF;
+                const uint32_t first = b + 1 < static_cast<uint32_t>(kBins) ? h[b + 1] : 0u;
+                const uint32_t end = h[b];
+                rank = first;
+                for (uint32_t q = first; q < end; ++q) {
+                    rank += fin[q] > key ? 1u : 0u;
+                }
+            }
+            const int64_t dst = (o * g.k + rank) * g.inner + n;
+            values[dst] = ValueOf(x, g, row, key);
+            indices[dst] = IndexOf(key);
+        }
+        return;
+    }
     source([&](uint64_t key, bool valid) {
         if (!valid) {
             return;
