@@ -7,16 +7,19 @@
 // Reshape/Transpose/Split/Squeeze copies around them
 // (src/kernels/mat_mul.cpp, mul.cpp, softmax.cpp, transpose.cpp, split.cpp).
 //
-// One wave per (batch, head, block of 32 queries) streams over the keys in
-// blocks of 32 with the running-maximum form of the softmax (the kernel's
+// One wave per (batch, head, block of 16 queries) streams over the keys in
+// blocks of 16 with the running-maximum form of the softmax (the kernel's
 // comment has the lane layout): scores, probabilities and the output block
 // stay in registers, with no LDS and no barrier. Q and K fragments are
-// 16-byte loads: lane half h holds dims 8j + 4h .. 8j + 4h + 3 of its row,
-// so one load feeds four MFMA steps (the same pairing for both operands, so
-// the sum over the 64 dims is the dot product). Keys past the sequence read
-// K and V as 0 (buffer range checks) and get probability 0. Workgroups of
-// one (batch, head) share its K and V: the XCD-aware order puts all its
-// query blocks on one XCD (one L2) when batch x heads % 8 == 0.
+// 16-byte loads: lane group g holds dims 16 g .. 16 g + 15 of its row, so
+// one load feeds four MFMA steps (the same dims for both operands, so the
+// sum over the 64 dims is the dot product). 16 queries a wave instead of 32
+// make twice the waves at under half the registers (four waves per SIMD
+// instead of two): the ViT's 2496 waves fit the machine in one round, at
+// most three per SIMD. Keys past the sequence read K and V as 0 (buffer
+// range checks) and get probability 0. Workgroups of one (batch, head)
+// share its K and V: the XCD-aware order puts all its query blocks on one
+// XCD (one L2) when batch x heads % 8 == 0.
 //
 // Numerics: fp32 MFMA accumulation for both products (the reference sums in
 // double and rounds once), the softmax in the running-maximum form with
@@ -32,7 +35,7 @@ namespace nert_hip {
 namespace {
 
 constexpr int kHeadDim = 64;
-constexpr int kQueries = 32;   // queries per workgroup: one MFMA row block
+constexpr int kQueries = 16;   // queries per workgroup: one 16x16 MFMA block
 
 struct AttnArgs {
     const float* q;
@@ -41,40 +44,46 @@ struct AttnArgs {
     float* out;
     int32_t seq;
     int32_t heads;
-    int32_t key_blocks;  // ceil(seq / 32)
-    int32_t q_blocks;    // ceil(seq / 32)
+    int32_t key_blocks;  // ceil(seq / 16)
+    int32_t q_blocks;    // ceil(seq / 16)
     int32_t xcd;         // 1: batch * heads % 8 == 0, XCD-aware order
     int32_t in_b, in_t, in_h;    // Q/K/V strides (floats): batch, token, head
     int32_t out_b, out_t, out_h; // output strides (floats)
     float scale;
 };
 
-// Any sequence length, one wave per (batch, head, block of 32 queries),
-// streaming over 32-key blocks with the running-maximum form of the softmax:
-// per block, S^T = K Q^T (A = K rows, B = Q^T), so lane (c, h) holds query
-// c's scores for keys 8 (e / 4) + 4 h + e % 4 of the block; the block
-// maximum is the lane's own 16 values and one shuffle with lane c + 32; the
-// running output is rescaled by exp(m_old - m_new) and the block's
-// probabilities accumulate into O^T = V^T P^T, whose B operand is exactly
-// the probabilities the lane holds (lane half h supplies keys 8 j + 4 h + qq
-// at MFMA step (j, qq)) and whose accumulators all belong to query c, so the
-// rescale needs no data from other lanes. The next block's K and V are
-// loaded before the current block's 64 MFMAs. K and V are read with buffer
-// loads whose range check returns 0 past the last key (no clamped addresses,
-// no selects); only the last, partial block masks scores. The exponentials
-// are the hardware exp2 of scores pre-multiplied by scale * log2 e (relative
-// error a few 1e-6 at the score ranges here, against the separate rows'
-// expf of the rounded scaled score); the total is kept per lane in double
-// and the halves combined at the end; outputs are divided once.
+// Any sequence length, one wave per (batch, head, block of 16 queries),
+// streaming over 16-key blocks with the running-maximum form of the softmax,
+// on the 16x16x4 fp32 MFMA (lane l = 16 g + n: operand row/column n, K slice
+// g; result rows 4 g .. 4 g + 3 of column n). Per key block:
+//   S^T = K Q^T in 16 steps; step s takes dims 16 g + s from lane group g,
+//   so lane (n, g) loads dims 16 g .. 16 g + 15 of its key row (K) and query
+//   row (Q) as four 16-byte loads, and ends with the scores of query n for
+//   keys 4 g .. 4 g + 3 of the block;
+//   O^T += V^T P^T in 4 steps per 16-dim block; step t takes key 4 g + t
+//   from lane group g, which is exactly the probability the lane already
+//   holds (its score r = t), so no data moves between lanes; V rows come in
+//   as 4-byte loads, dims 16 b + n.
+// The block maximum of query n is its lane's 4 scores and two shuffles
+// (lanes n, n + 16, n + 32, n + 48), and every output accumulator of a lane
+// belongs to its query, so the rescale by exp(m_old - m_new) is lane-local.
+// The next block's K and V are loaded before the current block's 32 MFMAs.
+// K and V are read with buffer loads whose range check returns 0 past the
+// last key (the whole byte offset in the VGPR offset); only the last,
+// partial block masks scores. The exponentials are the hardware exp2 of
+// scores pre-multiplied by scale * log2 e (relative error a few 1e-6 at the
+// score ranges here, against the separate rows' expf of the rounded scaled
+// score); the total is kept per lane in double and the four lanes of a
+// query combined at the end; outputs are divided once.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t AttnRsrc(const float* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), static_cast<short>(0), static_cast<int>(bytes),
                                              static_cast<int>(0x00020000)); // raw dword buffer (gfx9 family)
 }
 
-__global__ __launch_bounds__(64, 2) void AttentionFlashKernel(AttnArgs a) {
+__global__ __launch_bounds__(64, 4) void AttentionFlashKernel(AttnArgs a) {
     const int lane = threadIdx.x;
-    const int half = lane >> 5;
-    const int c = lane & 31;
+    const int g = lane >> 4;
+    const int n = lane & 15;
     int bh;
     int qb;
     if (a.xcd) {
@@ -95,98 +104,120 @@ __global__ __launch_bounds__(64, 2) void AttentionFlashKernel(AttnArgs a) {
     const __amdgpu_buffer_rsrc_t vr = AttnRsrc(a.v + in_base, slice);
     const uint32_t row_bytes = static_cast<uint32_t>(a.in_t) * 4;
 
-    nert_floatx4 qf[8];
+    // Q: query qb * 16 + n (the last one for queries past the sequence,
+    // whose outputs are not stored), dims 16 g .. 16 g + 15.
+    float qf[16];
     {
-        const float* row = a.q + in_base + static_cast<int64_t>(min(qb * kQueries + c, last)) * a.in_t + 4 * half;
+        const float* row =
+            a.q + in_base + static_cast<int64_t>(min(qb * kQueries + n, last)) * a.in_t + 16 * g;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            qf[j] = *reinterpret_cast<const nert_floatx4*>(row + 8 * j);
+        for (int t = 0; t < 4; ++t) {
+            const nert_floatx4 x = *reinterpret_cast<const nert_floatx4*>(row + 4 * t);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                qf[4 * t + i] = x[i];
+            }
         }
     }
-    // K: row kb * 32 + c, dims 8 j + 4 h ..; V: rows kb * 32 + 4 h + 8 (e / 4)
-    // + e % 4, dims c and 32 + c. Rows past the sequence read as 0.
-    const uint32_t k_lane = static_cast<uint32_t>(c) * row_bytes + 16u * half;
-    const uint32_t v_lane = static_cast<uint32_t>(4 * half) * row_bytes + 4u * c;
-    // The whole byte offset goes in the VGPR offset (soffset stays 0): the
-    // range check of a raw buffer load covers the VGPR offset and the
-    // instruction offset, not the scalar offset.
-    const auto load = [&](int kb, nert_floatx4* kf, float* v0, float* v1) {
-        const uint32_t blk = static_cast<uint32_t>(kb) * 32u * row_bytes;
-        const uint32_t kv = k_lane + blk;
-        const uint32_t vv = v_lane + blk;
+    // K: row kb * 16 + n, dims 16 g ..; V: rows kb * 16 + 4 g + t, dims
+    // 16 d + n. Rows past the sequence read as 0. The whole byte offset goes
+    // in the VGPR offset (soffset stays 0): the range check of a raw buffer
+    // load covers the VGPR offset and the instruction offset, not the scalar
+    // offset.
+    const uint32_t k_lane = static_cast<uint32_t>(n) * row_bytes + 64u * g;
+    const uint32_t v_lane = static_cast<uint32_t>(4 * g) * row_bytes + 4u * n;
+    const auto load_k = [&](int kb, float* kf) {
+        const uint32_t kv = k_lane + static_cast<uint32_t>(kb) * 16u * row_bytes;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            kf[j] = __builtin_bit_cast(nert_floatx4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                         kr, static_cast<int>(kv + 32u * j), 0, 0));
-        }
+        for (int t = 0; t < 4; ++t) {
+            const nert_floatx4 x = __builtin_bit_cast(
+                nert_floatx4, __builtin_amdgcn_raw_buffer_load_b128(kr, static_cast<int>(kv + 16u * t), 0, 0));
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const uint32_t off = vv + static_cast<uint32_t>(8 * (e >> 2) + (e & 3)) * row_bytes;
-            v0[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vr, static_cast<int>(off), 0, 0));
-            v1[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vr, static_cast<int>(off + 128u),
-                                                                                   0, 0));
+            for (int i = 0; i < 4; ++i) {
+                kf[4 * t + i] = x[i];
+            }
         }
     };
-    nert_floatx4 kf[8];
-    float v0[16];
-    float v1[16];
-    load(0, kf, v0, v1);
-    nert_floatx16 o0;
-    nert_floatx16 o1;
+    const auto load_v = [&](int kb, float* vf) {
+        const uint32_t vv = v_lane + static_cast<uint32_t>(kb) * 16u * row_bytes;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        o0[e] = 0.0f;
-        o1[e] = 0.0f;
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                vf[4 * d + t] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(
+                               vr, static_cast<int>(vv + static_cast<uint32_t>(t) * row_bytes + 64u * d), 0, 0));
+            }
+        }
+    };
+    const auto scores = [&](const float* kf) {
+        nert_floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[t], qf[t], acc, 0, 0, 0);
+        }
+        return acc;
+    };
+    // Software pipeline: block kb + 1's score MFMAs are issued before block
+    // kb's softmax, which they do not depend on, so the matrix pipe works
+    // while the wave runs the softmax; K runs two blocks ahead, V one.
+    const int blocks = a.key_blocks;
+    float kf[16];
+    float vf[16];
+    load_k(0, kf);
+    load_v(0, vf);
+    nert_floatx4 s_next = scores(kf);
+    load_k(min(1, blocks - 1), kf);
+    nert_floatx4 o[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            o[d][r] = 0.0f;
+        }
     }
     constexpr float kLog2e = 1.4426950408889634f;
     const float scale2 = a.scale * kLog2e; // scores in log2 units
     float m = -__builtin_huge_valf();       // running maximum (log2 units)
     double total = 0.0;
-    const int blocks = a.key_blocks;
-    const int full = a.seq / 32; // blocks with no key past the sequence
+    const int full = a.seq / 16; // blocks with no key past the sequence
     for (int kb = 0; kb < blocks; ++kb) {
-        nert_floatx4 kn[8];
-        float n0[16];
-        float n1[16];
-        load(min(kb + 1, blocks - 1), kn, n0, n1);
-        nert_floatx16 s;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            s[e] = 0.0f;
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-#pragma unroll
-            for (int qq = 0; qq < 4; ++qq) {
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j][qq], qf[j][qq], s, 0, 0, 0);
-            }
-        }
+        nert_floatx4 s = s_next;
+        // kf holds block kb + 1's keys (loaded last iteration): its scores
+        // go in now, then block kb + 2's keys and block kb + 1's values load.
+        s_next = scores(kf);
+        float kn[16];
+        float vn[16];
+        load_k(min(kb + 2, blocks - 1), kn);
+        load_v(min(kb + 1, blocks - 1), vn);
         // Scores in log2 units (scale * log2 e in one multiply) for exp2.
         if (kb < full) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                s[e] *= scale2;
+            for (int r = 0; r < 4; ++r) {
+                s[r] *= scale2;
             }
         } else {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int key = kb * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
-                s[e] = key < a.seq ? s[e] * scale2 : -__builtin_huge_valf();
+            for (int r = 0; r < 4; ++r) {
+                const int key = kb * 16 + 4 * g + r;
+                s[r] = key < a.seq ? s[r] * scale2 : -__builtin_huge_valf();
             }
         }
         float bm = m;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            bm = s[e] > bm ? s[e] : bm;
+        for (int r = 0; r < 4; ++r) {
+            bm = s[r] > bm ? s[r] : bm;
         }
         {
-            const float o = __shfl_xor(bm, 32, 64);
-            bm = o > bm ? o : bm;
+            float o2 = __shfl_xor(bm, 16, 64);
+            bm = o2 > bm ? o2 : bm;
+            o2 = __shfl_xor(bm, 32, 64);
+            bm = o2 > bm ? o2 : bm;
         }
         // Key 0 opens the scan (block 0): a NaN there stays the maximum, as
         // the reference's peak rule keeps a NaN first element.
         if (kb == 0) {
-            const float first = __shfl(s[0], c, 64);
+            const float first = __shfl(s[0], n, 64);
             if (first != first) {
                 bm = first;
             }
@@ -195,58 +226,54 @@ __global__ __launch_bounds__(64, 2) void AttentionFlashKernel(AttnArgs a) {
         m = bm;
         float part = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            s[e] = __builtin_amdgcn_exp2f(s[e] - m);
-            part += s[e];
+        for (int r = 0; r < 4; ++r) {
+            s[r] = __builtin_amdgcn_exp2f(s[r] - m);
+            part += s[r];
         }
         total = total * static_cast<double>(alpha) + static_cast<double>(part);
         // Once the maxima settle the factor is 1 in every lane: skip the
         // multiplies then (a wave-uniform test).
         if (__any(alpha != 1.0f)) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                o0[e] *= alpha;
-                o1[e] *= alpha;
+            for (int d = 0; d < 4; ++d) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    o[d][r] *= alpha;
+                }
             }
         }
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(v0[e], s[e], o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(v1[e], s[e], o1, 0, 0, 0);
+        for (int d = 0; d < 4; ++d) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[4 * d + t], s[t], o[d], 0, 0, 0);
+            }
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            kf[j] = kn[j];
-        }
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            v0[e] = n0[e];
-            v1[e] = n1[e];
+        for (int t = 0; t < 16; ++t) {
+            kf[t] = kn[t];
+            vf[t] = vn[t];
         }
     }
+    total += __shfl_xor(total, 16, 64);
     total += __shfl_xor(total, 32, 64);
     const float inv = static_cast<float>(1.0 / total);
-    // o0[e] = O[query c][dim 8 (e / 4) + 4 h + e % 4], o1 the same + 32:
-    // four runs of four consecutive dims per block, 16-byte stores.
-    const int query = qb * kQueries + c;
+    // o[d][r] = O[query n][dim 16 d + 4 g + r]: one 16-byte store per block.
+    const int query = qb * kQueries + n;
     if (query < a.seq) {
         float* op = a.out + static_cast<int64_t>(b) * a.out_b + static_cast<int64_t>(h) * a.out_h +
-                    static_cast<int64_t>(query) * a.out_t + 4 * half;
+                    static_cast<int64_t>(query) * a.out_t + 4 * g;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            nert_floatx4 x0;
-            nert_floatx4 x1;
+        for (int d = 0; d < 4; ++d) {
+            nert_floatx4 x;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                x0[i] = o0[4 * j + i] * inv;
-                x1[i] = o1[4 * j + i] * inv;
+            for (int r = 0; r < 4; ++r) {
+                x[r] = o[d][r] * inv;
             }
-            *reinterpret_cast<nert_floatx4*>(op + 8 * j) = x0;
-            *reinterpret_cast<nert_floatx4*>(op + 32 + 8 * j) = x1;
+            *reinterpret_cast<nert_floatx4*>(op + 16 * d) = x;
         }
     }
 }
-
 
 } // namespace
 } // namespace nert_hip
@@ -286,7 +313,7 @@ int nert_hip_attention_f32(const float* q, const float* k, const float* v, float
         // Keys past the sequence must fall beyond a (batch, head) slice's last
         // row (the loads' range check reads them as 0): tokens at least a
         // head's width apart, and the byte offsets of the last key block's
-        // rows (up to 31 rows past the sequence) under 2^32, so no offset
+        // rows (up to 15 rows past the sequence) under 2^32, so no offset
         // wraps back into the slice.
         if (in_strides[1] < head_dim) {
             throw Error("attention: token stride shorter than head_dim");
@@ -304,7 +331,7 @@ int nert_hip_attention_f32(const float* q, const float* k, const float* v, float
             in_strides[2] >= lim || out_strides[0] >= lim || out_strides[1] >= lim || out_strides[2] >= lim) {
             throw Error("attention: tensors beyond 2^31 elements");
         }
-        const int64_t blocks = (seq + 31) / 32;
+        const int64_t blocks = (seq + kQueries - 1) / kQueries;
         const int64_t groups = batch * heads * blocks;
         if (groups >= lim) {
             throw Error("attention: too many workgroups");
