@@ -796,30 +796,32 @@ for cand in {cands!r}:
         ins = [dev(x), dev(w), dev(b)] + ([None, None, None, dev(wp)] if packed else [])
         run_node("FusedConv", ins, [y], a)
         out[f"single_{{cand}}_{{int(packed)}}"] = y.to_host()
-        y, y2 = DeviceArray(shape, np.float32), DeviceArray(shape, np.float32)
-        ins = [dev(x), dev(w), dev(b), None, dev(w2), dev(b2)] + ([dev(wp)] if packed else [])
-        run_node("FusedConv", ins, [y, y2], a)
-        out[f"pair_{{cand}}_{{int(packed)}}"] = y.to_host()
-        out[f"pair2_{{cand}}_{{int(packed)}}"] = y2.to_host()
+        if a.get("group", 1) == 1:
+            y, y2 = DeviceArray(shape, np.float32), DeviceArray(shape, np.float32)
+            ins = [dev(x), dev(w), dev(b), None, dev(w2), dev(b2)] + ([dev(wp)] if packed else [])
+            run_node("FusedConv", ins, [y, y2], a)
+            out[f"pair_{{cand}}_{{int(packed)}}"] = y.to_host()
+            out[f"pair2_{{cand}}_{{int(packed)}}"] = y2.to_host()
 np.savez({out!r}, **out)
 """
 
 
-@pytest.mark.parametrize("xs,m,stride", [((2, 64, 20, 20), 64, 1), ((2, 32, 15, 13), 48, 2), ((1, 16, 9, 9), 32, 1)])
-def test_conv_packed_weights_bit_identical(gpu, tmp_path, xs, m, stride):
+@pytest.mark.parametrize("xs,m,stride,group", [((2, 64, 20, 20), 64, 1, 1), ((2, 32, 15, 13), 48, 2, 1),
+                                              ((1, 16, 9, 9), 32, 1, 1), ((2, 32, 12, 12), 48, 1, 2)])
+def test_conv_packed_weights_bit_identical(gpu, tmp_path, xs, m, stride, group):
     """FusedConv with W also given packed (seventh input, the 3x3 LDS-patch
-    kernel's order) against the same row without it, single and paired with
-    a 1x1 shortcut, under every 3x3 configuration forced in turn (8- and
-    16-channel blocks, split and tail pieces; tuning off): bit-identical;
-    the tuned result matches the restatement."""
+    kernel's order) against the same row without it, single and (group 1)
+    paired with a 1x1 shortcut, under every 3x3 configuration forced in turn
+    (8- and 16-channel blocks, split and tail pieces, two groups; tuning
+    off): bit-identical; the tuned result matches the restatement."""
     import json
     import os
     import subprocess
     import sys
 
-    attrs = {"pads": [1, 1, 1, 1], "strides": [stride, stride], "activation": "Relu"}
+    attrs = {"pads": [1, 1, 1, 1], "strides": [stride, stride], "activation": "Relu", "group": group}
     x = randn(xs, seed=140)
-    w = randn((m, xs[1], 3, 3), seed=141, scale=0.05)
+    w = randn((m, xs[1] // group, 3, 3), seed=141, scale=0.05)
     b = randn((m,), seed=142, scale=0.1)
     w2 = randn((m, xs[1], 1, 1), seed=143, scale=0.1)
     b2 = randn((m,), seed=144, scale=0.1)
@@ -835,7 +837,7 @@ def test_conv_packed_weights_bit_identical(gpu, tmp_path, xs, m, stride):
                                                           cands=cands)], env=env, check=True, timeout=120)
     r = np.load(out)
     for cand in cands:
-        for what in ("single", "pair", "pair2"):
+        for what in ("single", "pair", "pair2") if group == 1 else ("single",):
             assert np.array_equal(r[f"{what}_{cand}_0"], r[f"{what}_{cand}_1"]), (what, cand)
-    want = restate.conv(x, w, b, attrs["strides"], None, attrs["pads"], 1, "NOTSET")
+    want = restate.conv(x, w, b, attrs["strides"], None, attrs["pads"], group, "NOTSET")
     compare(r["single_0_1"], np.where(want > 0, want, np.float32(0)).astype(F), what="packed FusedConv")
