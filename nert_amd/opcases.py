@@ -97,7 +97,7 @@ K_BIG, K_NEW = 4 * 1024 * 1024, 1024 * 1024
 def _cases() -> list[OpCase]:
     c: list[OpCase] = []
     src = "bench/runtime/main.cpp"
-    # --- the reference's published fixtures ---
+    # --- the reference's fixtures that have a published MI300X figure ---
     c.append(OpCase("gemm_512", "Gemm", [("a", (512, 512), F32, _u(-1, 1)), ("b", (512, 512), F32, _u(-1, 1))],
                     [("y", (512, 512), F32)], "mfma", 2.0 * 512 ** 3, mi300x_ms=0.15, source=f"{src}:337-346"))
     c.append(OpCase("conv_8x16x64x64", "Conv",
